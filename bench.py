@@ -1,0 +1,230 @@
+"""Benchmark of the affine-quantized matmul path on one MI355X.
+
+Headline (the JSON line's `value`): mx.quantized_matmul as a decode GEMV,
+4-bit, group 64, x bf16 [1, 3584] against W [18944, 3584] -- the
+K=3584, N=18944 point of the quantized GEMM sweep, in HBM GB/s of algorithmic
+traffic (packed codes + scales + biases + x + y).  One step is one launch.
+16 weight replicas (611 MB, more than the 256 MB Infinity Cache) are used in
+rotation so every launch streams its weights from HBM.  The timed steps are
+replayed from a HIP graph so the GPU runs them back to back; HIP events on the
+launch stream bracket the timed region.
+
+Also reported: the full sweep M in {1,16,128,2048,8192} x (K,N) in
+{(3584,18944), (18944,3584), (3584,4608)} x bits {4,8} (GB/s, TFLOP/s and the
+fraction of the bounding roofline), and the CPU baseline: the oracle's float32
+restatement of MLX's CPU quantized_matmul loop on the host cores, on a bounded
+sample of the headline workload.
+
+    python bench.py [--steps 256] [--warmup 32] [--no-sweep] [--no-cpu]
+    python bench.py --profile   # eager launches + a copy kernel, for rocprofv3
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+RIDGE = BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # FLOP per byte
+METRIC = "decode tok/s (7B-shape 4-bit, bs=1/32); qmv HBM GB/s and qmm TFLOPS vs peak"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_4bit_K3584_N18944_traffic.txt")
+
+
+def alg_bytes(M: int, N: int, K: int, bits: int) -> int:
+    """Packed codes + bf16 scales/biases + bf16 x + bf16 y."""
+    return N * K * bits // 8 + N * (K // 64) * 4 + 2 * M * K + 2 * M * N
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--replicas", type=int, default=16)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", action="store_true",
+                    help="eager launches of the headline kernel + a 512 MiB copy (rocprofv3 runs)")
+    return ap.parse_args()
+
+
+def make_replicas(mq, torch, N, K, bits, count, seed):
+    """`count` independent quantized copies of W ~ N(0, 0.02), cast to bf16, quantized on GPU."""
+    gen = torch.Generator(device="cuda:0")
+    out = []
+    for r in range(count):
+        gen.manual_seed(seed + r)
+        w = (torch.randn(N, K, generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16)
+        out.append(mq.quantize(w, 64, bits))
+        del w
+    return out
+
+
+def time_graph(torch, launch, n_launch: int, warmup: int, reps: int = 1):
+    """Capture `n_launch` launches (launch(i)) in a HIP graph; return ms per launch."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_launch):
+            launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    ms = start.elapsed_time(end)
+    del g
+    return ms / (n_launch * reps), wall / (n_launch * reps)
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(args, orc, wq, s, b, x, N, K, bits):
+    threads = max(1, min(16, os.cpu_count() or 1))
+    orc.qmm_f32(x, wq, s, b, 64, bits, threads=threads)  # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        orc.qmm_f32(x, wq, s, b, 64, bits, threads=threads)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or calls >= 2000:
+            break
+    gbs = alg_bytes(1, N, K, bits) * calls / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{calls} calls ({el:.1f} s) of the 4-bit K={K} N={N} M=1 qmv: the oracle's "
+                      "float32 restatement of MLX's CPU quantized_matmul loop, OpenMP over rows"}
+
+
+def sweep(mq, torch):
+    rows = []
+    for (K, N) in ((3584, 18944), (18944, 3584), (3584, 4608)):
+        for bits in (4, 8):
+            wbytes = alg_bytes(0, N, K, bits)
+            n_rep = max(1, min(16, math.ceil(640e6 / wbytes)))
+            reps = make_replicas(mq, torch, N, K, bits, n_rep, seed=100)
+            for M in (1, 16, 128, 2048, 8192):
+                gen = torch.Generator(device="cuda:0").manual_seed(1)
+                x = torch.randn(M, K, generator=gen, device="cuda:0").to(torch.bfloat16)
+                flops = 2.0 * M * N * K
+                n_launch = 32 if flops < 2e11 else 8
+
+                def launch(i, x=x, reps=reps):
+                    wq, s, b = reps[i % len(reps)]
+                    mq.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits=bits)
+
+                ms, _ = time_graph(torch, launch, n_launch, warmup=2)
+                by = alg_bytes(M, N, K, bits)
+                gbs = by / (ms * 1e-3) / 1e9
+                tfl = flops / (ms * 1e-3) / 1e12
+                bound = "hbm" if flops / by < RIDGE else "mfma"
+                frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tfl / BF16_PEAK_TFLOPS
+                rows.append({"M": M, "K": K, "N": N, "bits": bits, "us": round(ms * 1e3, 2),
+                             "GBps": round(gbs, 1), "TFLOPs": round(tfl, 2), "bound": bound,
+                             "frac": round(frac, 4)})
+                del x
+            del reps
+            torch.cuda.empty_cache()
+    return rows
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
+              "(the path has no multi-GPU component; see DESIGN.md for how it would shard).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    from oracle import oracle as orc
+
+    K, N, bits, M = 3584, 18944, 4, 1
+    replicas = make_replicas(mq, torch, N, K, bits, args.replicas, seed=0)
+    gen = torch.Generator(device="cuda:0").manual_seed(1)
+    x = torch.randn(M, K, generator=gen, device="cuda:0").to(torch.bfloat16)
+
+    def launch(i):
+        wq, s, b = replicas[i % len(replicas)]
+        mq.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits=bits)
+
+    if args.profile:
+        for i in range(args.warmup + args.steps):
+            launch(i)
+        src = torch.empty(256 * 1024 * 1024, dtype=torch.bfloat16, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # calibration: 512 MiB read + 512 MiB written
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "done", "launches": args.warmup + args.steps,
+                          "copy_bytes_each_way": src.numel() * 2}))
+        return
+
+    ms, wall_ms = time_graph(torch, launch, args.steps, args.warmup)
+    by = alg_bytes(M, N, K, bits)
+    gbs = by / (ms * 1e-3) / 1e9
+    traffic = read_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "ms_per_step_wall": round(wall_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: W ~ N(0,0.02) (seeds 0..15) cast to bf16 and quantized on the GPU; "
+                "x ~ N(0,1) bf16 (seed 1)",
+        "config": {"workload": "quantized_matmul decode GEMV (qmv): 4-bit affine, group 64, "
+                               "x bf16 [1,3584] @ W[18944,3584]^T, 16 rotating weight replicas",
+                   "M": M, "K": K, "N": N, "bits": bits, "group_size": 64,
+                   "bytes_per_step": by},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+    }
+    if not args.no_sweep:
+        line["sweep"] = sweep(mq, torch)
+    if not args.no_cpu:
+        wq, s, b = replicas[0]
+        line["cpu_baseline"] = cpu_baseline(
+            args, orc, wq.cpu().numpy().view("uint32"), s.cpu().view(torch.int16).numpy().view("uint16"),
+            b.cpu().view(torch.int16).numpy().view("uint16"),
+            x.cpu().view(torch.int16).numpy().view("uint16"), N, K, bits)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+/*
+ * mq.h -- C ABI of libmi355q, the MI355X (gfx950) affine-quantized matmul path.
+ *
+ * Drop-in boundary for the quantized linear layers of the reference's native
+ * MLX worker (huydt84/mlx-server-runtime, python/mlx_worker/native_mlx/).  The
+ * reference reaches this path only through the Python API of the external mlx
+ * 0.31.2 package (python/uv.lock:939-941); each entry point below replaces one
+ * of those calls, with the same tensors and the same argument meaning.
+ *
+ * Conventions
+ *   - All array pointers are DEVICE pointers owned by the caller; the library
+ *     allocates nothing and never synchronizes the host.  Work is enqueued on
+ *     `stream` (NULL = the default stream).
+ *   - bfloat16 data is passed as raw 16-bit patterns (mq_bf16).
+ *   - Weight format (MLX "affine"): wq uint32 [rows, K*bits/32] with codes
+ *     packed LSB-first (code j of a word at bits [j*bits, (j+1)*bits));
+ *     scales and biases bfloat16 [rows, K/group_size]; w = scale*q + bias.
+ *   - Supported here: bits 4 or 8, group_size 64, transpose = 1.  MLX's other
+ *     settings (bits 2/3/5/6, group_size 32/128, transpose = 0) return
+ *     MQ_ERR_UNSUPPORTED; anything MLX itself rejects returns MQ_ERR_INVALID.
+ *   - Pointers that feed 16-byte loads (x, wq, w, out, y rows) must be 16-byte
+ *     aligned.
+ *   - Return value: MQ_OK, or a negative code with a message available from
+ *     mq_last_error() on the calling thread.  Validation happens before any
+ *     launch, so a failed call enqueues nothing.
+ *   - Reentrant: no mutable global state besides the thread-local message.
+ */
+#ifndef MQ_H
+#define MQ_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t mq_bf16; /* raw bfloat16 bits */
+
+#define MQ_OK 0
+#define MQ_ERR_INVALID (-1)     /* arguments MLX would reject too */
+#define MQ_ERR_UNSUPPORTED (-2) /* valid for MLX, not implemented here */
+#define MQ_ERR_HIP (-3)         /* the HIP runtime refused a launch */
+
+/* (major << 16) | minor */
+int mq_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* mq_last_error(void);
+
+/*
+ * mx.quantize(w, group_size, bits, mode="affine") for bfloat16 w [rows, K]:
+ * writes wq [rows, K*bits/32], scales and biases [rows, K/group_size].
+ * Replaces the calls at python/mlx_worker/native_mlx/models/lfm2.py:112-117
+ * and :142-151 and the one nn.quantize makes per layer
+ * (models/qwen2.py:318-324).  Bit-exact with the float32 algorithm.
+ */
+int mq_quantize(const mq_bf16* w, uint32_t* wq, mq_bf16* scales, mq_bf16* biases, int64_t rows,
+                int64_t K, int group_size, int bits, hipStream_t stream);
+
+/*
+ * mx.dequantize(wq, scales, biases, group_size, bits) -> out bfloat16 [rows, K],
+ * out = bf16(bf16(q*scale) + bias).
+ */
+int mq_dequantize(const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases, mq_bf16* out,
+                  int64_t rows, int64_t K, int group_size, int bits, hipStream_t stream);
+
+/*
+ * Quantized embedding lookup: out[i] = dequantize(wq[ids[i]]) for i < n_ids,
+ * the nn.QuantizedEmbedding call behind models/qwen2.py:185 (embed_tokens).
+ * An id outside [0, rows) yields a row of zeros.
+ */
+int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
+                        const mq_bf16* scales, const mq_bf16* biases, int64_t rows, int64_t K,
+                        int group_size, int bits, mq_bf16* out, hipStream_t stream);
+
+/*
+ * mx.quantized_matmul(x, wq, scales, biases, transpose=True, group_size, bits)
+ * plus QuantizedLinear's optional "+ bias":
+ *   y[m, n] = sum_k x[m, k] * (scale*q + bias)[n, k]  (+ bias_vec[n])
+ * x bfloat16 [M, K], wq [N, K*bits/32], bias_vec bfloat16 [N] or NULL,
+ * y bfloat16 [M, N]; float32 accumulation, one rounding at the store.
+ * Replaces every QuantizedLinear call of the model graphs
+ * (models/qwen2.py:76-78,115,134,227; qwen3.py:78-86,115,134,222).
+ * Decode-sized M uses the GEMV kernel, larger M the MFMA kernel.
+ */
+int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                        const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
+                        int64_t N, int64_t K, int group_size, int bits, int transpose,
+                        hipStream_t stream);
+
+/*
+ * mx.gather_qmm(x, wq, scales, biases, lhs_indices, rhs_indices,
+ *               transpose=True, group_size, bits, sorted_indices):
+ *   y[t] = x[lhs[t]] @ dequantize(wq[rhs[t]])^T      for t < T
+ * x bfloat16 [x_batches, M, K]; wq [E, N, K*bits/32]; scales/biases
+ * [E, N, K/group_size]; lhs int32 [T] or NULL (identity, needs x_batches == T);
+ * rhs int32 [T]; y bfloat16 [T, M, N].  sorted_indices is the caller's promise
+ * that rhs is non-decreasing (models/lfm2.py:202-218 sorts when it has >= 64
+ * rows); results do not depend on it.  A t whose lhs/rhs is out of range gets
+ * zeros.  Replaces QuantizedSwitchLinear.__call__ (models/lfm2.py:176-187).
+ */
+int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* rhs_indices,
+                  const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases, mq_bf16* y,
+                  int64_t T, int64_t M, int64_t N, int64_t K, int64_t E, int64_t x_batches,
+                  int group_size, int bits, int transpose, int sorted_indices,
+                  hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MQ_H */

@@ -1,0 +1,84 @@
+"""ctypes binding of libmi355q.so (declarations in include/mq.h).
+
+The library is loaded from this package directory.  There is no fallback: if
+it is missing or cannot be loaded, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmi355q.so")
+
+MQ_OK = 0
+MQ_ERR_INVALID = -1
+MQ_ERR_UNSUPPORTED = -2
+MQ_ERR_HIP = -3
+
+# Every symbol include/mq.h declares (checked by the CPU test suite).
+EXPORTS = (
+    "mq_version",
+    "mq_last_error",
+    "mq_quantize",
+    "mq_dequantize",
+    "mq_embedding_lookup",
+    "mq_quantized_matmul",
+    "mq_gather_qmm",
+)
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+
+class LibraryNotBuilt(RuntimeError):
+    pass
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.mq_version.argtypes = []
+    L.mq_version.restype = _int
+    L.mq_last_error.argtypes = []
+    L.mq_last_error.restype = ctypes.c_char_p
+    L.mq_quantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]
+    L.mq_dequantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]
+    L.mq_embedding_lookup.argtypes = [_p, _i64, _p, _p, _p, _i64, _i64, _int, _int, _p, _p]
+    L.mq_quantized_matmul.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p]
+    L.mq_gather_qmm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                _int, _int, _int, _int, _p]
+    for name in EXPORTS[2:]:
+        getattr(L, name).restype = _int
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise LibraryNotBuilt(
+                        f"{LIB_PATH} is missing: build it with "
+                        "`python mlx-server-runtime_amd/build_lib.py` (no CPU fallback exists)")
+                L = ctypes.CDLL(LIB_PATH)
+                _declare(L)
+                _lib = L
+    return _lib
+
+
+def check(rc: int, op: str) -> None:
+    """Map a C-ABI return code to the exception MLX raises for the same case."""
+    if rc == MQ_OK:
+        return
+    msg = lib().mq_last_error().decode(errors="replace") or f"[{op}] failed (rc={rc})"
+    if rc == MQ_ERR_INVALID:
+        raise ValueError(msg)
+    if rc == MQ_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)

@@ -1,0 +1,254 @@
+"""mx.* quantization ops on torch tensors, executed by libmi355q on the GPU.
+
+Names, argument order and meaning follow the mlx calls the reference's model
+graphs make (python/mlx_worker/native_mlx/models/qwen2.py, lfm2.py):
+
+    quantize(w, group_size=64, bits=4, mode="affine") -> (wq, scales, biases)
+    dequantize(wq, scales, biases, group_size=64, bits=4, mode="affine")
+    quantized_matmul(x, wq, scales, biases, transpose=True, group_size=64, bits=4)
+    gather_qmm(x, wq, scales, biases, lhs_indices=None, rhs_indices=None,
+               transpose=True, group_size=64, bits=4, sorted_indices=False)
+
+Tensors live on a ROCm device: activations, scales and biases are bfloat16;
+packed weights are uint32 (int32 is accepted as the same bits).  Invalid
+arguments raise ValueError like MLX; settings MLX accepts but this backend
+does not implement (bits other than 4/8, group sizes other than 64,
+transpose=False, non-affine modes) raise NotImplementedError.  There is no CPU
+or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_CODE_DTYPES = (torch.int32, getattr(torch, "uint32", torch.int32))
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(op: str, **tensors: torch.Tensor | None) -> torch.device:
+    dev = None
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"[{op}] {name} must be a torch.Tensor")
+        if t.device.type != "cuda":
+            raise ValueError(f"[{op}] {name} must be on a ROCm GPU device, got {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"[{op}] all inputs must be on one device ({dev} vs {t.device})")
+    return dev
+
+
+def _check_mode(op: str, mode: str) -> None:
+    if mode != "affine":
+        raise NotImplementedError(f"[{op}] mode={mode!r} is not implemented (affine only)")
+
+
+def _check_bf16(op: str, name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"[{op}] {name} must be bfloat16, got {t.dtype}")
+
+
+def _check_codes(op: str, w: torch.Tensor) -> None:
+    if w.dtype not in _CODE_DTYPES:
+        raise ValueError(f"[{op}] The weight matrix should be uint32 but received {w.dtype}")
+
+
+def _check_quantized(op: str, w, scales, biases, group_size: int, bits: int) -> int:
+    """Validate (w, scales, biases); returns K (unpacked input dimension)."""
+    _check_codes(op, w)
+    _check_bf16(op, "scales", scales)
+    _check_bf16(op, "biases", biases)
+    if scales.shape != biases.shape:
+        raise ValueError(
+            f"[{op}] Scales and biases should have the same shape. Received scales with "
+            f"shape {tuple(scales.shape)} and biases with {tuple(biases.shape)}.")
+    if w.ndim < 2 or w.shape[:-1] != scales.shape[:-1]:
+        raise ValueError(
+            f"[{op}] Weight and scales should have the same batch shape. Received weight "
+            f"with shape {tuple(w.shape)} and scales with {tuple(scales.shape)}.")
+    if bits not in (2, 3, 4, 5, 6, 8):
+        raise ValueError(f"[{op}] The requested number of bits {bits} is not supported. "
+                         "The supported bits are 2, 3, 4, 5, 6 and 8.")
+    if group_size not in (32, 64, 128):
+        raise ValueError(f"[{op}] The requested group size {group_size} is not supported. "
+                         "The supported group sizes are 32, 64 and 128.")
+    K = w.shape[-1] * 32 // bits
+    if w.shape[-1] * 32 % bits or scales.shape[-1] * group_size != K:
+        raise ValueError(
+            f"[{op}] The shapes of the weight and scales are incompatible based on bits and "
+            f"group_size. w.shape() == {tuple(w.shape)} and scales.shape() == "
+            f"{tuple(scales.shape)} with group_size={group_size} and bits={bits}")
+    return K
+
+
+# --------------------------------------------------------------------- ops
+
+
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4, mode: str = "affine"):
+    """mx.quantize for a bfloat16 matrix w[..., K] -> (wq uint32-bits int32, scales, biases).
+
+    Follows mlx.core.quantize as called at models/lfm2.py:112-117,142-151.
+    float32 inputs are rounded to bfloat16 first (scales and biases come out
+    in bfloat16, the dtype the quantized kernels consume).
+    """
+    op = "quantize"
+    _check_mode(op, mode)
+    _require_gpu(op, w=w)
+    if w.ndim < 2:
+        raise ValueError(f"[{op}] The matrix to be quantized must have at least 2 dimensions "
+                         f"but it has only {w.ndim}.")
+    if w.dtype == torch.float32 or w.dtype == torch.float16:
+        w = w.to(torch.bfloat16)
+    _check_bf16(op, "w", w)
+    K = w.shape[-1]
+    if K % group_size:
+        raise ValueError(
+            f"[{op}] The last dimension of the matrix needs to be divisible by the quantization "
+            f"group size {group_size}. However the provided matrix has shape {tuple(w.shape)}")
+    w = w.contiguous()
+    rows = w.numel() // K
+    lead = tuple(w.shape[:-1])
+    wq = torch.empty(lead + (K * bits // 32 if bits in (2, 4, 8) else 0,), dtype=torch.int32,
+                     device=w.device)
+    s = torch.empty(lead + (K // group_size,), dtype=torch.bfloat16, device=w.device)
+    b = torch.empty_like(s)
+    L = _lib.lib()
+    _lib.check(L.mq_quantize(_ptr(w), _ptr(wq), _ptr(s), _ptr(b), rows, K, group_size, bits,
+                             _stream(w)), op)
+    return wq, s, b
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = 64,
+               bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """mx.dequantize -> bfloat16 [..., K]; out = bf16(bf16(q*scale) + bias)."""
+    op = "dequantize"
+    _check_mode(op, mode)
+    _require_gpu(op, w=w, scales=scales, biases=biases)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    w, scales, biases = w.contiguous(), scales.contiguous(), biases.contiguous()
+    rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
+    out = torch.empty(tuple(w.shape[:-1]) + (K,), dtype=torch.bfloat16, device=w.device)
+    L = _lib.lib()
+    _lib.check(L.mq_dequantize(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out), rows, K,
+                               group_size, bits, _stream(w)), op)
+    return out
+
+
+def embedding_lookup(ids: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """Dequantized rows w[ids] -> bfloat16 [*ids.shape, K] (nn.QuantizedEmbedding.__call__)."""
+    op = "embedding_lookup"
+    _require_gpu(op, ids=ids, w=w, scales=scales, biases=biases)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    if w.ndim != 2:
+        raise ValueError(f"[{op}] the embedding table must be 2-D, got {tuple(w.shape)}")
+    flat = ids.reshape(-1).to(torch.int32).contiguous()
+    out = torch.empty(tuple(ids.shape) + (K,), dtype=torch.bfloat16, device=w.device)
+    L = _lib.lib()
+    _lib.check(L.mq_embedding_lookup(_ptr(flat), flat.numel(), _ptr(w.contiguous()),
+                                     _ptr(scales.contiguous()), _ptr(biases.contiguous()),
+                                     w.shape[0], K, group_size, bits, _ptr(out), _stream(w)), op)
+    return out
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4, mode: str = "affine",
+                     bias: torch.Tensor | None = None) -> torch.Tensor:
+    """mx.quantized_matmul(x, w, scales, biases, transpose=True) -> x @ dequantize(w).T.
+
+    ``bias`` (bfloat16 [N]) fuses QuantizedLinear's "+ bias" into the store.
+    """
+    op = "quantized_matmul"
+    _check_mode(op, mode)
+    _require_gpu(op, x=x, w=w, scales=scales, biases=biases, bias=bias)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    _check_bf16(op, "x", x)
+    if w.ndim != 2:
+        raise ValueError(f"[{op}] batched weights are not supported here; got {tuple(w.shape)}")
+    if not transpose:
+        raise NotImplementedError(f"[{op}] transpose=False is not implemented on this backend")
+    if x.ndim < 1 or x.shape[-1] != K:
+        raise ValueError(
+            f"[{op}] Last dimension of first input with shape {tuple(x.shape)} must match "
+            f"second input with shape {(w.shape[0], K)}.")
+    N = w.shape[0]
+    if bias is not None:
+        _check_bf16(op, "bias", bias)
+        if bias.shape != (N,):
+            raise ValueError(f"[{op}] bias must have shape ({N},), got {tuple(bias.shape)}")
+        bias = bias.contiguous()
+    xc = x.contiguous()
+    M = xc.numel() // K
+    y = torch.empty(tuple(x.shape[:-1]) + (N,), dtype=torch.bfloat16, device=x.device)
+    L = _lib.lib()
+    _lib.check(L.mq_quantized_matmul(_ptr(xc), _ptr(w.contiguous()), _ptr(scales.contiguous()),
+                                     _ptr(biases.contiguous()), _ptr(bias), _ptr(y), M, N, K,
+                                     group_size, bits, 1, _stream(x)), op)
+    return y
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               lhs_indices: torch.Tensor | None = None, rhs_indices: torch.Tensor | None = None,
+               transpose: bool = True, group_size: int = 64, bits: int = 4, mode: str = "affine",
+               sorted_indices: bool = False) -> torch.Tensor:
+    """mx.gather_qmm: out[b] = x[lhs[b]] @ dequantize(w[rhs[b]]).T, b over the index batch.
+
+    x is [..., M, K] (its batch dims flattened are what lhs_indices index), w is
+    [..., N, K*bits/32] (batch dims flattened are the experts rhs_indices
+    index).  The output shape is broadcast(lhs_indices, rhs_indices) + [M, N];
+    a missing lhs_indices means "every x batch in order" and broadcasts the same
+    way, as in mlx (models/lfm2.py:176-187, 202-218).
+    """
+    op = "gather_qmm"
+    _check_mode(op, mode)
+    _require_gpu(op, x=x, w=w, scales=scales, biases=biases, lhs_indices=lhs_indices,
+                 rhs_indices=rhs_indices)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    _check_bf16(op, "x", x)
+    if not transpose:
+        raise NotImplementedError(f"[{op}] transpose=False is not implemented on this backend")
+    if x.ndim < 2 or x.shape[-1] != K:
+        raise ValueError(f"[{op}] x must be [..., M, {K}], got {tuple(x.shape)}")
+    M = x.shape[-2]
+    N = w.shape[-2]
+    E = math.prod(w.shape[:-2])
+    x_batch = tuple(x.shape[:-2])
+    n_xb = math.prod(x_batch)
+    dev = x.device
+    if rhs_indices is None:
+        rhs_indices = torch.arange(E, device=dev).reshape(tuple(w.shape[:-2]))
+    if lhs_indices is None:
+        lhs_full = torch.arange(n_xb, device=dev).reshape(x_batch)
+    else:
+        lhs_full = lhs_indices
+    for name, t in (("lhs_indices", lhs_full), ("rhs_indices", rhs_indices)):
+        if t.dtype.is_floating_point or t.dtype == torch.bool:
+            raise ValueError(f"[{op}] {name} must be an integer array, got {t.dtype}")
+    out_batch = torch.broadcast_shapes(tuple(lhs_full.shape), tuple(rhs_indices.shape))
+    T = math.prod(out_batch)
+    rhs_flat = rhs_indices.expand(out_batch).reshape(-1).to(torch.int32).contiguous()
+    identity = lhs_indices is None and tuple(out_batch) == x_batch
+    lhs_flat = None if identity else lhs_full.expand(out_batch).reshape(-1).to(torch.int32).contiguous()
+    xc = x.contiguous()
+    y = torch.empty(tuple(out_batch) + (M, N), dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    _lib.check(L.mq_gather_qmm(_ptr(xc), _ptr(lhs_flat), _ptr(rhs_flat), _ptr(w.contiguous()),
+                               _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(y), T, M,
+                               N, K, E, n_xb, group_size, bits, 1, int(bool(sorted_indices)),
+                               _stream(x)), op)
+    return y

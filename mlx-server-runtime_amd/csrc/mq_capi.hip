@@ -1,0 +1,187 @@
+// C ABI of libmi355q: argument validation, then dispatch to the kernels.
+// Declarations and the reference interface each entry point replaces are in
+// include/mq.h.
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/mq.h"
+#include "mq_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return MQ_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MQ_ERR_HIP, "[%s] HIP launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+// Checks shared by every entry point, in the order MLX reports them.
+int check_quant(const char* op, int64_t K, int group_size, int bits) {
+  if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8)
+    return fail(MQ_ERR_INVALID,
+                "[%s] The requested number of bits %d is not supported. The supported bits are "
+                "2, 3, 4, 5, 6 and 8.",
+                op, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(MQ_ERR_INVALID,
+                "[%s] The requested group size %d is not supported. The supported group sizes "
+                "are 32, 64 and 128.",
+                op, group_size);
+  if (bits != 4 && bits != 8)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] bits=%d is not implemented on this backend (4 or 8).",
+                op, bits);
+  if (group_size != 64)
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] group_size=%d is not implemented on this backend (64).", op, group_size);
+  if (K <= 0 || K % group_size != 0)
+    return fail(MQ_ERR_INVALID,
+                "[%s] The last dimension of the matrix needs to be divisible by the "
+                "quantization group size %d. However the provided matrix has %lld columns.",
+                op, group_size, (long long)K);
+  if (K >= kMaxDim) return fail(MQ_ERR_INVALID, "[%s] K=%lld is too large.", op, (long long)K);
+  return MQ_OK;
+}
+
+int check_dim(const char* op, const char* name, int64_t v) {
+  if (v < 0 || v >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] %s=%lld is out of range.", op, name, (long long)v);
+  return MQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mq_version(void) { return (1 << 16) | 0; }
+
+const char* mq_last_error(void) { return g_err; }
+
+int mq_quantize(const mq_bf16* w, uint32_t* wq, mq_bf16* scales, mq_bf16* biases, int64_t rows,
+                int64_t K, int group_size, int bits, hipStream_t stream) {
+  const char* op = "quantize";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (rows == 0) return ok();
+  if (!w || !wq || !scales || !biases) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(w) || !aligned16(wq))
+    return fail(MQ_ERR_INVALID, "[%s] w and wq must be 16-byte aligned.", op);
+  return hip_status(mq::launch_quantize(w, wq, scales, biases, rows, K, bits, stream), op);
+}
+
+int mq_dequantize(const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases, mq_bf16* out,
+                  int64_t rows, int64_t K, int group_size, int bits, hipStream_t stream) {
+  const char* op = "dequantize";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (rows == 0) return ok();
+  if (!wq || !scales || !biases || !out) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(wq) || !aligned16(out))
+    return fail(MQ_ERR_INVALID, "[%s] wq and out must be 16-byte aligned.", op);
+  return hip_status(
+      mq::launch_dequantize(wq, scales, biases, nullptr, rows, rows, out, K, bits, stream), op);
+}
+
+int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
+                        const mq_bf16* scales, const mq_bf16* biases, int64_t rows, int64_t K,
+                        int group_size, int bits, mq_bf16* out, hipStream_t stream) {
+  const char* op = "embedding_lookup";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (int rc = check_dim(op, "n_ids", n_ids)) return rc;
+  if (n_ids == 0) return ok();
+  if (!ids || !wq || !scales || !biases || !out)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(wq) || !aligned16(out))
+    return fail(MQ_ERR_INVALID, "[%s] wq and out must be 16-byte aligned.", op);
+  return hip_status(
+      mq::launch_dequantize(wq, scales, biases, ids, n_ids, rows, out, K, bits, stream), op);
+}
+
+int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                        const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
+                        int64_t N, int64_t K, int group_size, int bits, int transpose,
+                        hipStream_t stream) {
+  const char* op = "quantized_matmul";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", N)) return rc;
+  if (!transpose)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] transpose=False is not implemented on this backend.",
+                op);
+  if (M == 0 || N == 0) return ok();
+  if (!x || !wq || !scales || !biases || !y) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(wq))
+    return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
+  if ((M + 127) / 128 > 65535)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] M=%lld exceeds the launch grid (8388480 rows).", op,
+                (long long)M);
+  hipError_t e;
+  if (M <= mq::qmv_max_rows(K, bits)) {
+    const mq::GatherMap g{nullptr, nullptr, 1, 1, 1};
+    e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g, stream);
+  } else {
+    e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
+  }
+  return hip_status(e, op);
+}
+
+int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* rhs_indices,
+                  const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases, mq_bf16* y,
+                  int64_t T, int64_t M, int64_t N, int64_t K, int64_t E, int64_t x_batches,
+                  int group_size, int bits, int transpose, int sorted_indices,
+                  hipStream_t stream) {
+  const char* op = "gather_qmm";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "T", T)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", N)) return rc;
+  if (int rc = check_dim(op, "E", E)) return rc;
+  if (int rc = check_dim(op, "x_batches", x_batches)) return rc;
+  if (!transpose)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] transpose=False is not implemented on this backend.",
+                op);
+  if (T * M >= kMaxDim) return fail(MQ_ERR_INVALID, "[%s] T*M is too large.", op);
+  if (!lhs_indices && x_batches != T)
+    return fail(MQ_ERR_INVALID, "[%s] without lhs_indices x must have T=%lld batches, got %lld.",
+                op, (long long)T, (long long)x_batches);
+  if (T == 0 || M == 0 || N == 0) return ok();
+  if (E == 0) return fail(MQ_ERR_INVALID, "[%s] the expert table is empty.", op);
+  if (!x || !rhs_indices || !wq || !scales || !biases || !y)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(wq))
+    return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
+  if ((T * M + 127) / 128 > 65535)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] T*M=%lld exceeds the launch grid (8388480 rows).", op,
+                (long long)(T * M));
+  hipError_t e;
+  // Few rows: one GEMV block row per (t, N tile); each t streams its expert.
+  // Many rows: MFMA tiles over the (expert-sorted) rows.
+  if (M <= mq::qmv_max_rows(K, bits) && T <= 65535 && (T * M <= 64 || !sorted_indices)) {
+    const mq::GatherMap g{lhs_indices, rhs_indices, T, E, x_batches};
+    e = mq::launch_qmv(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
+  } else {
+    e = mq::launch_gather_qmm_rows(x, lhs_indices, rhs_indices, wq, scales, biases, y, T * M, N,
+                                   K, E, x_batches * M, (int)M, bits, stream);
+  }
+  return hip_status(e, op);
+}
+
+}  // extern "C"

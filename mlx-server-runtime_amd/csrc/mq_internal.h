@@ -1,0 +1,44 @@
+// Launchers shared between the kernel translation units and the C-ABI.
+// Every launcher assumes its arguments were validated by the C-ABI layer
+// (mq_capi.hip) and only enqueues work on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mq {
+
+struct GatherMap {
+  const int32_t* lhs;   // x batch per output batch (nullptr: identity)
+  const int32_t* rhs;   // expert per output batch (nullptr: single matrix)
+  int64_t T;            // output batches (1 for a plain matmul)
+  int64_t E;            // experts
+  int64_t x_batches;    // batches in x
+};
+
+hipError_t launch_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
+                           int64_t rows, int64_t K, int bits, hipStream_t stream);
+hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                             const int32_t* row_ids, int64_t n_out_rows, int64_t n_rows,
+                             uint16_t* out, int64_t K, int bits, hipStream_t stream);
+
+// y[t][m][n] = x[lhs[t]][m] . dequant(w[rhs[t]][n]) (+ bias[n]), M <= qmv_max_rows(K).
+int qmv_max_rows(int64_t K, int bits);
+hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                      const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                      int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
+
+// MFMA path, any M.
+hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                      const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                      int64_t N, int64_t K, int bits, hipStream_t stream);
+// MFMA gather over flattened rows r = t*rows_per_batch + m: x row
+// lhs[t]*rows_per_batch + m (x_rows rows in x) times expert rhs[t]; the rows of
+// one expert inside a row tile share one pass over the weights.
+hipError_t launch_gather_qmm_rows(const uint16_t* x, const int32_t* lhs, const int32_t* rhs,
+                                  const uint32_t* wq, const uint16_t* scales,
+                                  const uint16_t* biases, uint16_t* y, int64_t rows, int64_t N,
+                                  int64_t K, int64_t E, int64_t x_rows, int rows_per_batch,
+                                  int bits, hipStream_t stream);
+
+}  // namespace mq

@@ -1,0 +1,164 @@
+// Affine quantize / dequantize kernels for gfx950.
+//
+// quantize: mx.quantize(w, group_size=64, bits, mode="affine") as called by
+//   QuantizedSwitchLinear (python/mlx_worker/native_mlx/models/lfm2.py:142-151)
+//   and by nn.quantize (models/qwen2.py:318-324).  Bit-exact with the float32
+//   algorithm: min/max per group, scale = max((max-min)/(2^b-1), 1e-7) signed
+//   toward the larger-magnitude edge, edge refit so that 0.0 is exact, codes
+//   rint((w-bias)/scale) clamped to [0, 2^b-1].
+// dequantize: mx.dequantize -- out = bf16(bf16(q*s) + b), the two rounded
+//   element-wise ops MLX evaluates in the bfloat16 output dtype.  With a row
+//   index list it is the quantized embedding lookup (models/qwen2.py:185).
+//
+// Layout: one group of 64 bf16 weights = 128 contiguous bytes.  quantize gives
+// each group to 8 lanes (16 bytes each, one coalesced 128-byte segment per
+// group); dequantize gives each lane one 16-byte chunk of packed codes.
+#include "mq_common.h"
+#include "mq_internal.h"
+
+namespace mq {
+namespace {
+
+template <int BITS>
+__global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restrict__ w,
+                                                       uint32_t* __restrict__ wq,
+                                                       uint16_t* __restrict__ scales,
+                                                       uint16_t* __restrict__ biases,
+                                                       int64_t n_groups) {
+  const int64_t gid = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  const bool ok = gid < n_groups;
+  u32x4_t v = {0u, 0u, 0u, 0u};
+  if (ok) v = *reinterpret_cast<const u32x4_t*>(w + gid * kGroup + sub * 8);
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = lo_bf16(v[i]);
+    f[2 * i + 1] = hi_bf16(v[i]);
+  }
+  float w_max = f[0], w_min = f[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) {
+    w_max = (w_max < f[i]) ? f[i] : w_max;
+    w_min = (f[i] < w_min) ? f[i] : w_min;
+  }
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) {
+    const float omax = __shfl_xor(w_max, off, 64);
+    const float omin = __shfl_xor(w_min, off, 64);
+    w_max = (w_max < omax) ? omax : w_max;
+    w_min = (omin < w_min) ? omin : w_min;
+  }
+  const float n_bins = (float)((1 << BITS) - 1);
+  const bool mask = fabsf(w_min) > fabsf(w_max);
+  float scale = (w_max - w_min) / n_bins;
+  scale = (scale < 1e-7f) ? 1e-7f : scale;
+  scale = mask ? scale : -scale;
+  const float edge = mask ? w_min : w_max;
+  const float q0 = __builtin_rintf(edge / scale);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+  uint32_t code[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float q = __builtin_rintf((f[i] - bias) / scale);
+    q = (q < 0.0f) ? 0.0f : q;
+    q = (q > n_bins) ? n_bins : q;
+    code[i] = (uint32_t)q;
+  }
+  if (!ok) return;
+  if constexpr (BITS == 4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) word |= code[i] << (4 * i);
+    wq[gid * 8 + sub] = word;
+  } else {
+    u32x2_t words;
+    words[0] = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+    words[1] = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+    *reinterpret_cast<u32x2_t*>(wq + gid * 16 + sub * 2) = words;
+  }
+  if (sub == 0) {
+    scales[gid] = (uint16_t)f32_to_bf16_bits(scale);
+    biases[gid] = (uint16_t)f32_to_bf16_bits(bias);
+  }
+}
+
+// bf16(bf16(q*s) + b)
+__device__ __forceinline__ float deq_two_round(uint32_t q, float s, float b) {
+  const float t = (float)(__bf16)((float)q * s);
+  return t + b;
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void dequantize_kernel(
+    const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const int32_t* __restrict__ row_ids, int64_t n_out_rows,
+    int64_t n_rows, uint16_t* __restrict__ out, int64_t K) {
+  constexpr int EPC = 128 / BITS;  // elements per 16-byte chunk
+  const int64_t cpr = K / EPC;     // chunks per row
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= n_out_rows * cpr) return;
+  const int64_t orow = idx / cpr;
+  const int64_t c = idx - orow * cpr;
+  int64_t srow = orow;
+  if (row_ids) srow = row_ids[orow];
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(out + orow * K + c * EPC);
+  if (srow < 0 || srow >= n_rows) {  // an id outside the table reads as zeros
+#pragma unroll
+    for (int i = 0; i < EPC / 8; ++i) dst[i] = u32x4_t{0u, 0u, 0u, 0u};
+    return;
+  }
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wq + srow * (K * BITS / 32) + c * 4);
+  const int64_t g = srow * (K / kGroup) + (c * EPC) / kGroup;
+  const float s = bf16_bits_to_f32(scales[g]);
+  const float b = bf16_bits_to_f32(biases[g]);
+  uint32_t packed[EPC / 2];
+#pragma unroll
+  for (int i = 0; i < EPC / 2; ++i) {
+    const int e0 = 2 * i;
+    const uint32_t word0 = v[(e0 * BITS) / 32];
+    const uint32_t q0 = (word0 >> ((e0 * BITS) % 32)) & ((1u << BITS) - 1u);
+    const uint32_t q1 = (word0 >> ((e0 * BITS) % 32 + BITS)) & ((1u << BITS) - 1u);
+    packed[i] = pack_bf16x2(deq_two_round(q0, s, b), deq_two_round(q1, s, b));
+  }
+#pragma unroll
+  for (int i = 0; i < EPC / 8; ++i)
+    dst[i] = u32x4_t{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+}
+
+}  // namespace
+
+hipError_t launch_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
+                           int64_t rows, int64_t K, int bits, hipStream_t stream) {
+  const int64_t n_groups = rows * (K / kGroup);
+  if (n_groups == 0) return hipSuccess;
+  const dim3 grid((unsigned)((n_groups + 31) / 32));
+  if (bits == 4)
+    hipLaunchKernelGGL(quantize_kernel<4>, grid, dim3(256), 0, stream, w, wq, scales, biases,
+                       n_groups);
+  else
+    hipLaunchKernelGGL(quantize_kernel<8>, grid, dim3(256), 0, stream, w, wq, scales, biases,
+                       n_groups);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                             const int32_t* row_ids, int64_t n_out_rows, int64_t n_rows,
+                             uint16_t* out, int64_t K, int bits, hipStream_t stream) {
+  const int64_t total = n_out_rows * (K * bits / 128);
+  if (total == 0) return hipSuccess;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (bits == 4)
+    hipLaunchKernelGGL(dequantize_kernel<4>, grid, dim3(256), 0, stream, wq, scales, biases,
+                       row_ids, n_out_rows, n_rows, out, K);
+  else
+    hipLaunchKernelGGL(dequantize_kernel<8>, grid, dim3(256), 0, stream, wq, scales, biases,
+                       row_ids, n_out_rows, n_rows, out, K);
+  return hipGetLastError();
+}
+
+}  // namespace mq

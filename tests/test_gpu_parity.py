@@ -1,0 +1,342 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars:
+* quantize, dequantize, embedding lookup: bit-exact (integer codes and
+  bfloat16 bit patterns).
+* quantized_matmul / gather_qmm: norm-wise relative error
+  max|y - ref| / max|ref| <= 1e-2 (bfloat16 output, float32 accumulation),
+  where ref is the oracle's double-precision contraction with the exact
+  dequantized weights.  TOL below is that bound.
+Full BASELINE-sized shapes are checked directly where the oracle is fast
+(M = 1) and on a sample of rows otherwise (rows of the output depend only on
+their own row of x).
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import normwise_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+DEV = "cuda:0"
+
+
+def bf16_dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint16).view(np.int16)).view(
+        torch.bfloat16).to(DEV)
+
+
+def u32_dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).to(DEV)
+
+
+def bits_host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def u32_host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+def rand_bf16(orc, rng, shape, std):
+    return orc.f32_to_bf16(rng.normal(0, std, shape).astype(np.float32))
+
+
+def quantized(orc, rng, N, K, bits, std=0.02):
+    w = rand_bf16(orc, rng, (N, K), std)
+    return orc.quantize(w, 64, bits)
+
+
+def assert_close(y_dev, ref, tol=TOL):
+    y = bits_host(y_dev)
+    from oracle.oracle import bf16_to_f32
+
+    err = normwise_rel_err(bf16_to_f32(y), ref)
+    assert err <= tol, f"norm-wise relative error {err:.3e} > {tol}"
+    return err
+
+
+# ----------------------------------------------------------- quantize / deq
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("shape", [(37, 256), (5, 3584), (3, 64)])
+def test_quantize_bit_exact(mq, orc, bits, shape):
+    rng = np.random.default_rng(100 + bits)
+    w = rand_bf16(orc, rng, shape, 0.02)
+    w[0, :64] = 0                              # zero group
+    w[-1, -64:] = orc.f32_to_bf16(np.float32(0.0125))  # constant group
+    if shape[1] >= 128:
+        w[0, 64:128] = orc.f32_to_bf16(np.abs(rng.normal(0, 1, 64)).astype(np.float32))
+    wq, s, b = mq.quantize(bf16_dev(w), 64, bits)
+    rq, rs, rb = orc.quantize(w, 64, bits)
+    assert np.array_equal(u32_host(wq), rq)
+    assert np.array_equal(bits_host(s), rs)
+    assert np.array_equal(bits_host(b), rb)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("shape", [(37, 256), (64, 3584), (1, 64)])
+def test_dequantize_bit_exact(mq, orc, bits, shape):
+    rng = np.random.default_rng(200 + bits)
+    wq, s, b = quantized(orc, rng, *shape, bits)
+    out = mq.dequantize(u32_dev(wq), bf16_dev(s), bf16_dev(b), 64, bits)
+    assert np.array_equal(bits_host(out), orc.dequantize(wq, s, b, 64, bits))
+
+
+def test_dequantize_rounds_twice_on_gpu(mq):
+    wq = np.full((1, 8), 0x33333333, np.uint32)
+    s = np.array([[0x3F81]], np.uint16)   # 1.0078125
+    b = np.array([[0xBC00]], np.uint16)   # -0.0078125
+    out = bits_host(mq.dequantize(u32_dev(wq), bf16_dev(s), bf16_dev(b), 64, 4))
+    assert np.all(out == 0x4042)          # 3.03125
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_embedding_lookup_bit_exact(mq, orc, bits):
+    rng = np.random.default_rng(300 + bits)
+    wq, s, b = quantized(orc, rng, 50, 256, bits)
+    ids = np.array([[3, 0, 49], [7, 7, 12]], np.int32)
+    out = mq.embedding_lookup(torch.from_numpy(ids).to(DEV), u32_dev(wq), bf16_dev(s),
+                              bf16_dev(b), 64, bits)
+    ref = orc.dequantize(wq, s, b, 64, bits)[ids.reshape(-1)].reshape(2, 3, 256)
+    assert np.array_equal(bits_host(out), ref)
+    bad = mq.embedding_lookup(torch.tensor([50, -1], device=DEV), u32_dev(wq), bf16_dev(s),
+                              bf16_dev(b), 64, bits)
+    assert np.all(bits_host(bad) == 0)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_kat_fixtures_on_gpu(mq, orc, bits):
+    kat = dict(np.load(os.path.join(GOLDEN, f"kat_affine_b{bits}.npz"), allow_pickle=False))
+    wq, s, b = mq.quantize(bf16_dev(kat["w"]), 64, bits)
+    assert np.array_equal(u32_host(wq), kat["wq"])
+    chk = kat["scale_checked"]
+    assert np.array_equal(bits_host(s)[chk], kat["scales"][chk])
+    assert np.array_equal(bits_host(b), kat["biases"])
+    deq = mq.dequantize(u32_dev(kat["wq"]), bf16_dev(kat["scales"]), bf16_dev(kat["biases"]),
+                        64, bits)
+    assert np.array_equal(orc.bf16_to_f32(bits_host(deq)), orc.bf16_to_f32(kat["deq"]))
+    y = mq.quantized_matmul(bf16_dev(kat["x"]), u32_dev(kat["wq"]), bf16_dev(kat["scales"]),
+                            bf16_dev(kat["biases"]), True, 64, bits)
+    assert_close(y, kat["y"])
+    gy = mq.gather_qmm(bf16_dev(kat["gx"]), u32_dev(kat["gwq"]), bf16_dev(kat["gscales"]),
+                       bf16_dev(kat["gbiases"]), rhs_indices=torch.from_numpy(kat["rhs"]).to(DEV),
+                       group_size=64, bits=bits)
+    assert_close(gy, kat["gy"])
+
+
+# ------------------------------------------------------------ matmul
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 16, 33, 128, 130])
+@pytest.mark.parametrize("KN", [(256, 200), (1024, 384)])
+def test_quantized_matmul_parity(mq, orc, bits, M, KN):
+    K, N = KN
+    rng = np.random.default_rng(1000 * bits + M + K)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits,
+                            bias=bf16_dev(bias))
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    assert_close(y, orc.qmm(x, wq, s, b, 64, bits, bias=bias))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_matmul_leading_dims_and_stream(mq, orc, bits):
+    rng = np.random.default_rng(77)
+    wq, s, b = quantized(orc, rng, 96, 192, bits)
+    x = rand_bf16(orc, rng, (2, 3, 192), 1.0)
+    side = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(side):
+        y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64,
+                                bits)
+    side.synchronize()
+    assert y.shape == (2, 3, 96)
+    assert_close(y, orc.qmm(x.reshape(6, 192), wq, s, b, 64, bits).reshape(2, 3, 96))
+
+
+def test_quantized_matmul_empty_and_errors(mq, orc):
+    rng = np.random.default_rng(5)
+    wq, s, b = quantized(orc, rng, 64, 128, 4)
+    y = mq.quantized_matmul(torch.zeros(0, 128, dtype=torch.bfloat16, device=DEV), u32_dev(wq),
+                            bf16_dev(s), bf16_dev(b))
+    assert y.shape == (0, 64)
+    with pytest.raises(ValueError):
+        mq.quantized_matmul(torch.zeros(1, 64, dtype=torch.bfloat16, device=DEV), u32_dev(wq),
+                            bf16_dev(s), bf16_dev(b))
+    with pytest.raises(NotImplementedError):
+        mq.quantized_matmul(torch.zeros(1, 128, dtype=torch.bfloat16, device=DEV), u32_dev(wq),
+                            bf16_dev(s), bf16_dev(b), transpose=False)
+
+
+def test_quantized_matmul_deterministic(mq, orc):
+    rng = np.random.default_rng(6)
+    wq, s, b = quantized(orc, rng, 512, 1024, 4)
+    x = bf16_dev(rand_bf16(orc, rng, (64, 1024), 1.0))
+    args = (u32_dev(wq), bf16_dev(s), bf16_dev(b))
+    y1 = bits_host(mq.quantized_matmul(x, *args))
+    y2 = bits_host(mq.quantized_matmul(x, *args))
+    assert np.array_equal(y1, y2)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("KN", [(3584, 18944), (18944, 3584), (3584, 4608)])
+def test_decode_shapes_full_size(mq, orc, bits, KN):
+    """M = 1 at the benchmark shapes (the whole output checked)."""
+    K, N = KN
+    rng = np.random.default_rng(4242 + bits + K)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (1, K), 1.0)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
+    assert_close(y, orc.qmm(x, wq, s, b, 64, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [16, 2048])
+def test_prefill_shape_sampled_rows(mq, orc, bits, M):
+    """K=3584, N=18944 at large M: sampled output rows against the oracle."""
+    K, N = 3584, 18944
+    rng = np.random.default_rng(5151 + M + bits)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
+    rows = np.unique(np.r_[0, M - 1, rng.integers(0, M, 6)])
+    assert_close(y[torch.from_numpy(rows).to(DEV)], orc.qmm(x[rows], wq, s, b, 64, bits))
+
+
+# ------------------------------------------------------------ gather_qmm
+
+
+def _experts(orc, rng, E, N, K, bits):
+    w = rand_bf16(orc, rng, (E, N, K), 0.02)
+    return orc.quantize(w, 64, bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("T,sorted_", [(5, False), (64, True), (300, True), (300, False)])
+def test_gather_qmm_parity(mq, orc, bits, T, sorted_):
+    rng = np.random.default_rng(9000 + T + bits)
+    E, N, K = 16, 192, 512
+    wq, s, b = _experts(orc, rng, E, N, K, bits)
+    rhs = rng.integers(0, E, T).astype(np.int32)
+    if sorted_:
+        rhs = np.sort(rhs)
+    x = rand_bf16(orc, rng, (T, 1, K), 1.0)
+    y = mq.gather_qmm(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b),
+                      rhs_indices=torch.from_numpy(rhs).to(DEV), group_size=64, bits=bits,
+                      sorted_indices=sorted_)
+    assert y.shape == (T, 1, N)
+    assert_close(y, orc.gather_qmm(x, wq, s, b, rhs, group_size=64, bits=bits))
+
+
+@pytest.mark.parametrize("M", [1, 3, 12])
+def test_gather_qmm_lhs_broadcast(mq, orc, M):
+    """SwitchGLU's unsorted call: x [B, L, 1, M, K] against indices [B, L, k]."""
+    rng = np.random.default_rng(31 + M)
+    E, N, K, B, L, k = 8, 128, 256, 2, 3, 4
+    wq, s, b = _experts(orc, rng, E, N, K, 4)
+    x = rand_bf16(orc, rng, (B, L, 1, M, K), 1.0)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(B * L)]).reshape(B, L, k).astype(np.int32)
+    y = mq.gather_qmm(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b),
+                      rhs_indices=torch.from_numpy(idx).to(DEV), group_size=64, bits=4)
+    assert y.shape == (B, L, k, M, N)
+    lhs = np.repeat(np.arange(B * L), k).astype(np.int32)
+    ref = orc.gather_qmm(x.reshape(B * L, M, K), wq, s, b, idx.reshape(-1), lhs_indices=lhs)
+    assert_close(y.reshape(-1, M, N), ref)
+
+
+def test_gather_qmm_out_of_range_rows_are_zero(mq, orc):
+    rng = np.random.default_rng(44)
+    E, N, K = 4, 64, 128
+    wq, s, b = _experts(orc, rng, E, N, K, 4)
+    for T in (3, 200):
+        rhs = np.sort(rng.integers(0, E, T)).astype(np.int32)
+        rhs[-1] = E  # out of range
+        x = rand_bf16(orc, rng, (T, 1, K), 1.0)
+        y = mq.gather_qmm(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b),
+                          rhs_indices=torch.from_numpy(rhs).to(DEV), sorted_indices=True)
+        yh = bits_host(y)
+        assert np.all(yh[-1] == 0)
+        ref = orc.gather_qmm(x[:-1], wq, s, b, rhs[:-1])
+        assert_close(y[:-1], ref)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_moe_shape_prefill_sampled(mq, orc, bits):
+    """Qwen3-30B-A3B expert shape (E=128, N=768, K=2048), 2048 sorted rows."""
+    rng = np.random.default_rng(777 + bits)
+    E, N, K, T = 128, 768, 2048, 2048
+    wq, s, b = _experts(orc, rng, E, N, K, bits)
+    rhs = np.sort(rng.integers(0, E, T)).astype(np.int32)
+    x = rand_bf16(orc, rng, (T, 1, K), 1.0)
+    y = mq.gather_qmm(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b),
+                      rhs_indices=torch.from_numpy(rhs).to(DEV), bits=bits, sorted_indices=True)
+    rows = np.unique(np.r_[0, T - 1, rng.integers(0, T, 10)])
+    ref = orc.gather_qmm(x[rows], wq, s, b, rhs[rows], bits=bits)
+    assert_close(y[torch.from_numpy(rows).to(DEV)], ref)
+
+
+# ------------------------------------------------------------ modules
+
+
+def test_switch_glu_matches_dense_reference(mq, orc):
+    """SwitchGLU (models/lfm2.py:193-218) vs a float32 torch reference built from
+    the exactly dequantized expert weights; both the sorted (>= 64 rows) and the
+    unsorted path."""
+    rng = np.random.default_rng(55)
+    E, H, I, k = 16, 256, 128, 4
+    mods = []
+    dense = []
+    for (n, kk) in ((I, H), (I, H), (H, I)):
+        wq, s, b = _experts(orc, rng, E, n, kk, 4)
+        mods.append(mq.nn.QuantizedSwitchLinear(u32_dev(wq), bf16_dev(s), bf16_dev(b)))
+        dense.append(torch.from_numpy(orc.dequantize(wq, s, b, 64, 4, exact=True)).float())
+    glu = mq.nn.SwitchGLU(*mods)
+    for B, L in ((1, 2), (4, 8)):  # 8 and 128 routed rows
+        xh = rand_bf16(orc, rng, (B, L, H), 1.0)
+        idx = np.stack([rng.permutation(E)[:k] for _ in range(B * L)]).reshape(B, L, k)
+        y = glu(bf16_dev(xh), torch.from_numpy(idx.astype(np.int64)).to(DEV))
+        assert y.shape == (B, L, k, H)
+        xf = torch.from_numpy(orc.bf16_to_f32(xh))
+        ref = torch.empty(B, L, k, H)
+        for bb in range(B):
+            for ll in range(L):
+                for j in range(k):
+                    e = idx[bb, ll, j]
+                    g = dense[0][e] @ xf[bb, ll]
+                    u = dense[1][e] @ xf[bb, ll]
+                    h = torch.nn.functional.silu(g) * u
+                    ref[bb, ll, j] = dense[2][e] @ h
+        yf = y.float().cpu()
+        err = float((yf - ref).abs().max() / ref.abs().max())
+        assert err <= 3 * TOL, err  # three chained bfloat16 matmuls
+
+
+def test_quantized_linear_module(mq, orc):
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(256, 96, bias=True).to(DEV)
+    ql = mq.nn.QuantizedLinear.from_linear(lin, 64, 4)
+    x = torch.randn(3, 256, device=DEV).to(torch.bfloat16)
+    y = ql(x)
+    wq, s, b = (u32_host(ql.weight), bits_host(ql.scales), bits_host(ql.biases))
+    ref = orc.qmm(bits_host(x), wq, s, b, 64, 4, bias=bits_host(ql.bias))
+    assert_close(y, ref)
+    # nn.quantize swaps modules in place
+    seq = torch.nn.Sequential(torch.nn.Linear(128, 64, bias=False), torch.nn.Embedding(10, 128)).to(DEV)
+    mq.nn.quantize(seq, 64, 8)
+    assert isinstance(seq[0], mq.nn.QuantizedLinear) and seq[0].bits == 8
+    assert isinstance(seq[1], mq.nn.QuantizedEmbedding)
+    e = seq[1](torch.tensor([1, 2], device=DEV))
+    assert e.shape == (2, 128)
+    assert seq[1].as_linear(e).shape == (2, 10)

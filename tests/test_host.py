@@ -1,0 +1,112 @@
+"""Host-side checks that need no GPU.
+
+* libmi355q.so loads and exports every function include/mq.h declares;
+* the C ABI rejects what MLX rejects (MQ_ERR_INVALID), flags what this backend
+  does not implement (MQ_ERR_UNSUPPORTED), and returns before any launch, so
+  these calls run without a device (null pointers are never dereferenced);
+* the Python layer maps the codes to ValueError / NotImplementedError and
+  refuses CPU tensors instead of falling back to a CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "mq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mq_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_abi():
+    assert declared_functions() == sorted([
+        "mq_version", "mq_last_error", "mq_quantize", "mq_dequantize", "mq_embedding_lookup",
+        "mq_quantized_matmul", "mq_gather_qmm"])
+
+
+def test_library_exports_every_declared_symbol(mq):
+    L = mq._lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    assert set(mq._lib.EXPORTS) == set(declared_functions())
+    assert mq.version() == (1, 0)
+
+
+def _L(mq):
+    return mq._lib.lib()
+
+
+def test_capi_invalid_and_unsupported_codes(mq):
+    L = _L(mq)
+    null = None
+    qmm = L.mq_quantized_matmul
+    # bits MLX does not know -> invalid; bits MLX knows but not here -> unsupported
+    assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 7, 1, null) == -1
+    assert b"supported bits" in L.mq_last_error()
+    assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 2, 1, null) == -2
+    assert qmm(null, null, null, null, null, null, 1, 8, 64, 48, 4, 1, null) == -1
+    assert qmm(null, null, null, null, null, null, 1, 8, 64, 32, 4, 1, null) == -2
+    assert qmm(null, null, null, null, null, null, 1, 8, 96, 64, 4, 1, null) == -1
+    assert b"divisible" in L.mq_last_error()
+    assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 4, 0, null) == -2
+    assert qmm(null, null, null, null, null, null, -1, 8, 64, 64, 4, 1, null) == -1
+    # empty problems succeed without touching memory
+    assert qmm(null, null, null, null, null, null, 0, 8, 64, 64, 4, 1, null) == 0
+    assert L.mq_last_error() == b""
+    # non-empty with null pointers -> invalid, nothing launched
+    assert qmm(null, null, null, null, null, null, 2, 8, 64, 64, 4, 1, null) == -1
+    assert b"null pointer" in L.mq_last_error()
+    # misaligned x
+    buf = ctypes.create_string_buffer(4096)
+    base = (ctypes.addressof(buf) + 15) & ~15
+    assert qmm(base + 2, base, base, base, null, base, 1, 8, 64, 64, 4, 1, null) == -1
+    assert b"aligned" in L.mq_last_error()
+
+
+def test_capi_gather_validation(mq):
+    L = _L(mq)
+    g = L.mq_gather_qmm
+    null = None
+    # without lhs the x batch count must equal T
+    assert g(null, null, null, null, null, null, null, 4, 1, 8, 64, 2, 3, 64, 4, 1, 0, null) == -1
+    assert g(null, null, null, null, null, null, null, 0, 1, 8, 64, 2, 0, 64, 4, 1, 0, null) == 0
+    assert g(null, null, null, null, null, null, null, 2, 1, 8, 64, 0, 2, 64, 4, 1, 0, null) == -1
+    assert g(null, null, null, null, null, null, null, 2, 1, 8, 64, 1, 2, 64, 8, 0, 0, null) == -2
+
+
+def test_capi_quantize_dequantize_validation(mq):
+    L = _L(mq)
+    null = None
+    assert L.mq_quantize(null, null, null, null, 4, 100, 64, 4, null) == -1
+    assert L.mq_quantize(null, null, null, null, 0, 128, 64, 4, null) == 0
+    assert L.mq_dequantize(null, null, null, null, 4, 128, 64, 6, null) == -2
+    assert L.mq_embedding_lookup(null, 3, null, null, null, 10, 128, 64, 4, null, null) == -1
+
+
+def test_python_layer_refuses_cpu_tensors(mq):
+    x = torch.zeros(1, 64, dtype=torch.bfloat16)
+    w = torch.zeros(8, 8, dtype=torch.int32)
+    s = torch.zeros(8, 1, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        mq.quantized_matmul(x, w, s, s)
+    with pytest.raises(ValueError, match="GPU"):
+        mq.quantize(torch.zeros(8, 64, dtype=torch.bfloat16))
+
+
+def test_python_layer_error_mapping(mq):
+    with pytest.raises(ValueError):
+        mq._lib.check(-1, "x")
+    with pytest.raises(NotImplementedError):
+        mq._lib.check(-2, "x")
+    with pytest.raises(RuntimeError):
+        mq._lib.check(-3, "x")
+    mq._lib.check(0, "x")
