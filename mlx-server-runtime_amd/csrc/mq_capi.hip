@@ -3,6 +3,8 @@
 // include/mq.h.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 
 #include "../../include/mq.h"
 #include "mq_internal.h"
@@ -32,6 +34,21 @@ int hip_status(hipError_t e, const char* what) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+// GEMV kernel for decode-sized M.  Measured on MI355X: the dot2 kernel streams
+// large matrices faster at M <= 2 (its 256-byte row segments per load beat the
+// matrix-core kernel's 64-byte ones), the matrix-core kernel wins everywhere
+// else (its VALU cost does not grow with M).  MQ_GEMV=dot2|mfma forces one.
+bool use_matrix_core_gemv(int64_t M, int64_t N, int64_t K) {
+  static const int forced = [] {
+    const char* v = getenv("MQ_GEMV");
+    if (v && strcmp(v, "dot2") == 0) return 1;
+    if (v && strcmp(v, "mfma") == 0) return 2;
+    return 0;
+  }();
+  if (forced) return forced == 2;
+  return !(M <= 2 && N * K >= ((int64_t)1 << 25));
+}
 
 // Checks shared by every entry point, in the order MLX reports them.
 int check_quant(const char* op, int64_t K, int group_size, int bits) {
@@ -134,9 +151,12 @@ int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* sca
     return fail(MQ_ERR_UNSUPPORTED, "[%s] M=%lld exceeds the launch grid (8388480 rows).", op,
                 (long long)M);
   hipError_t e;
-  if (M <= mq::qmv_max_rows(K, bits)) {
-    const mq::GatherMap g{nullptr, nullptr, 1, 1, 1};
-    e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g, stream);
+  const mq::GatherMap g1{nullptr, nullptr, 1, 1, 1};
+  if (mq::qmvm_fits(M, N, K, bits, 1) &&
+      (use_matrix_core_gemv(M, N, K) || !mq::qmv_fits(M, N, K, bits, 1))) {
+    e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
+  } else if (mq::qmv_fits(M, N, K, bits, 1)) {
+    e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
   } else {
     e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
   }
@@ -174,8 +194,12 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
   hipError_t e;
   // Few rows: one GEMV block row per (t, N tile); each t streams its expert.
   // Many rows: MFMA tiles over the (expert-sorted) rows.
-  if (M <= mq::qmv_max_rows(K, bits) && T <= 65535 && (T * M <= 64 || !sorted_indices)) {
-    const mq::GatherMap g{lhs_indices, rhs_indices, T, E, x_batches};
+  const mq::GatherMap g{lhs_indices, rhs_indices, T, E, x_batches};
+  const bool few = T * M <= 64 || !sorted_indices;
+  if (few && mq::qmvm_fits(M, N, K, bits, T) &&
+      (use_matrix_core_gemv(M, N, K) || !mq::qmv_fits(M, N, K, bits, T))) {
+    e = mq::launch_qmvm(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
+  } else if (few && mq::qmv_fits(M, N, K, bits, T)) {
     e = mq::launch_qmv(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
   } else {
     e = mq::launch_gather_qmm_rows(x, lhs_indices, rhs_indices, wq, scales, biases, y, T * M, N,

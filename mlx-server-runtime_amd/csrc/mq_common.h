@@ -60,6 +60,60 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, true));
+}
+
+// Sum over aligned groups of WIDTH consecutive lanes with DPP (no LDS traffic).
+// WIDTH <= 16: every lane of the group holds the total.  WIDTH 32: lanes 16-31
+// of each 32-lane half hold it.  WIDTH 64: lane 63 holds it.
+template <int WIDTH>
+__device__ __forceinline__ float dpp_group_sum(float v) {
+  if constexpr (WIDTH >= 2) v += dpp_f32<0xb1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (WIDTH >= 4) v += dpp_f32<0x4e>(v);   // quad_perm [2,3,0,1]
+  if constexpr (WIDTH >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror
+  if constexpr (WIDTH >= 16) v += dpp_f32<0x140>(v); // row_mirror
+  if constexpr (WIDTH >= 32) v += dpp_f32<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  if constexpr (WIDTH >= 64) v += dpp_f32<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// Lane (within its WIDTH group) that holds dpp_group_sum's result.
+template <int WIDTH>
+constexpr int dpp_sum_lane() {
+  return WIDTH <= 16 ? 0 : WIDTH - 1;
+}
+
+// LDS-only barrier: waits for this wave's LDS operations, not its global loads.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Raw buffer access (gfx9 descriptor: 32-bit byte range, stride 0).  A load
+// whose offset lies outside [0, bytes) returns zeros without touching memory,
+// so tails need no clamping; all addressing is a 32-bit lane offset plus
+// compile-time immediates off an SGPR base.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kBufNT = 2;  // cache policy bit: non-temporal (streamed once)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, 0x00020000);
+}
+template <int AUX = 0>
+__device__ __forceinline__ u32x4_t buf_load16(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, AUX));
+}
+__device__ __forceinline__ u32x2_t buf_load8(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load2(rsrc_t r, uint32_t voff) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0));
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;  // an offset no descriptor here covers
+
 // Non-temporal 16-byte load (weights are streamed once per call).
 __device__ __forceinline__ u32x4_t load_stream_u4(const u32x4_t* p) {
   return __builtin_nontemporal_load(p);

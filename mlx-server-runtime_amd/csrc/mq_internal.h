@@ -22,11 +22,20 @@ hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* scales, const u
                              const int32_t* row_ids, int64_t n_out_rows, int64_t n_rows,
                              uint16_t* out, int64_t K, int bits, hipStream_t stream);
 
-// y[t][m][n] = x[lhs[t]][m] . dequant(w[rhs[t]][n]) (+ bias[n]), M <= qmv_max_rows(K).
-int qmv_max_rows(int64_t K, int bits);
+// y[t][m][n] = x[lhs[t]][m] . dequant(w[rhs[t]][n]) (+ bias[n]); valid when
+// qmv_fits(M, N, K, bits, T) (at most 8 rows, x staged within the LDS budget).
+bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                       int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
+
+// Same contract on the matrix cores for M <= 8 (4-bit) / 16 (8-bit); valid
+// when qmvm_fits(M, N, K, bits, T) (K a multiple of 256, at most 12 chunks
+// per lane).
+bool qmvm_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
+hipError_t launch_qmvm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                       int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
 
 // MFMA path, any M.
 hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

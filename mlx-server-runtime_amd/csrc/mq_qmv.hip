@@ -6,21 +6,27 @@
 // (models/lfm2.py:176-187).
 //
 // HBM-bound: every weight byte is read once.  Design for gfx950:
-//  * a row of W is TPR lanes wide; lane i reads 16-byte chunks i, i+TPR, ...
-//    (32 4-bit or 16 8-bit codes per chunk), R rows per lane slot, all loads
-//    of a slot issued before any math;
-//  * x is staged once per block in LDS, structure-of-arrays by 16-byte block
-//    so that consecutive lanes read consecutive LDS addresses; for 4-bit it is
-//    stored in "pair order" (x0,x4),(x1,x5),(x2,x6),(x3,x7) per 8 elements,
-//    together with the sum of x over every chunk;
-//  * 4-bit: (word >> 4t) & 0x000F000F | 0x43004300 is a pair of bfloat16
-//    numbers 128+q (exact), fed to v_dot2_f32_bf16 against the x pair; per
-//    chunk the result d = sum x*(128+q) turns into the group contribution
-//    s*d + (b - 128*s)*sum(x), the same value as sum x*(s*q+b);
-//  * 8-bit: v_cvt_f32_ubyte{0..3} + fma in float32, then s*d + b*sum(x);
-//  * partial sums are reduced across the TPR lanes of a row with lane
-//    shuffles; float32 accumulation throughout, one bfloat16 rounding at the
-//    store (+ optional bias, QuantizedLinear's "+ bias" fused).
+//  * a weight row is TPR lanes wide; lane l owns 16-byte chunks l, l+TPR, ...
+//    (32 4-bit or 16 8-bit codes per chunk), up to S chunks for each of its R
+//    rows.  Loads are issued in the order they are consumed -- x, this block's
+//    scales and biases, then every weight chunk of the lane -- so waiting for x
+//    (vmcnt counts in issue order) never waits for weights, and the
+//    contraction of chunk j overlaps the arrival of chunks j+1.. ;
+//  * x is staged once per block in LDS as [m][slot][unit][lane] (16-byte
+//    units): consecutive lanes read consecutive addresses, and every slot/unit
+//    offset is a compile-time immediate.  Chunk sums of x and the interleaved
+//    (scale | bias << 16) words sit next to it.  Past the end of a row the LDS
+//    holds zeros, so padded lanes contribute 0 with no per-lane test;
+//  * 4-bit: ((word >> 4t) & 0x000F000F) | 0x43004300 (one v_and_or_b32 after
+//    the shift) is a pair of bfloat16 numbers 128+q, exact, contracted with an
+//    x pair by v_dot2_f32_bf16 (x stored pair-permuted: (x0,x4),(x1,x5),...);
+//    the chunk result d = sum x*(128+q) becomes s*d + (b - 128*s)*sum(x),
+//    equal to sum x*(s*q+b);
+//  * 8-bit: bytes -> float (v_cvt_f32_ubyte) -> bfloat16 pairs (exact for
+//    q <= 255) -> v_dot2_f32_bf16 against natural x pairs; then s*d + b*sum(x);
+//  * per-row partial sums are reduced across the TPR lanes with DPP (LDS across
+//    waves when TPR > 64); float32 throughout, one bfloat16 rounding at the
+//    store, where QuantizedLinear's "+ bias" is fused.
 #include "mq_common.h"
 #include "mq_internal.h"
 
@@ -30,27 +36,47 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kQmvLdsBudget = 48 * 1024;
 
-template <int BITS, int TPR, int R, int MT>
+// Opaque register constants: the mask in an SGPR and the bfloat16 magic in a
+// VGPR let ((w >> s) & mask) | magic select v_and_or_b32 (gfx9 VOP3 encodings
+// take no literal and at most one scalar operand).
+struct Nibble {
+  uint32_t mask, magic;
+  __device__ __forceinline__ Nibble() {
+    __asm__ volatile("s_mov_b32 %0, 0xf000f" : "=s"(mask));
+    __asm__ volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+  }
+  __device__ __forceinline__ uint32_t pair(uint32_t w) const { return (w & mask) | magic; }
+};
+
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool SBW>
 __global__ __launch_bounds__(kBlock) void qmv_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
     const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, int64_t E,
     int64_t x_batches) {
-  constexpr int EPC = 128 / BITS;  // elements per 16-byte chunk
-  constexpr int UPC = EPC / 8;     // 8-element units per chunk (4 or 2)
-  constexpr int SLOTS = kBlock / TPR;
+  constexpr int EPC = 128 / BITS;      // elements per 16-byte chunk
+  constexpr int UPC = EPC / 8;         // 8-element units per chunk (4 or 2)
+  constexpr int CPG = kGroup / EPC;    // chunks per group (2 or 4)
+  constexpr int SLOTS = kBlock / TPR;  // row slots per block
+  constexpr int RPB = SLOTS * R;       // rows per block
+  constexpr int WPR = TPR > 64 ? TPR / 64 : 1;  // waves per row (TPR > 64)
   extern __shared__ u32x4_t smem[];
+  __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : 1];
 
-  const int C = K / EPC;  // chunks per row
-  const int G = K / kGroup;
+  const int C = K / EPC;                // chunks per row
+  const int G = K / kGroup;             // groups per row
+  const int NJ = (C + TPR - 1) / TPR;   // slots used (<= S)
+  const int CP = NJ * TPR;              // chunks per row, padded
+  const int GP = CP / CPG;              // groups per row, padded
   const int64_t t = blockIdx.y;
   int64_t xb = t, e = 0;
   if (lhs) xb = lhs[t];
   if (rhs) e = rhs[t];
   const int slot = threadIdx.x / TPR;
   const int lane = threadIdx.x % TPR;
-  const int row0 = (blockIdx.x * SLOTS + slot) * R;
+  const int rb0 = blockIdx.x * RPB;
+  const int row0 = rb0 + slot * R;
   y += t * (int64_t)M * N;
   if (xb < 0 || xb >= x_batches || e < 0 || e >= E) {  // index outside the tables: zeros
     if (lane == 0)
@@ -59,138 +85,268 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
           if (row0 + r < N) y[(int64_t)m * N + row0 + r] = 0;
     return;
   }
-  x += xb * (int64_t)M * K;
-  wq += e * (int64_t)N * (K * BITS / 32);
-  scales += e * (int64_t)N * G;
-  biases += e * (int64_t)N * G;
+  // ---- 1. loads through buffer descriptors (out-of-range reads return 0):
+  // x, the block's scales/biases (contiguous: the block's rows are
+  // consecutive), then every weight chunk of this lane.  Waiting for x and the
+  // scales (vmcnt counts in issue order) does not wait for the weights, so the
+  // contraction below overlaps their arrival.
+  const int rows_here = min(RPB, N - rb0);
+  const rsrc_t xrs = make_rsrc(x + xb * (int64_t)M * K, (uint64_t)M * K * 2);
+  const rsrc_t wrs = make_rsrc(wq + (e * (int64_t)N + rb0) * (C * 4), (uint64_t)rows_here * C * 16);
+  const int64_t sb0 = e * (int64_t)N * G + (int64_t)rb0 * G;
+  const int n_sb = rows_here * G;  // <= RPB*G <= 1024 entries
+  const rsrc_t srs = make_rsrc(scales + sb0, (uint64_t)n_sb * 2);
+  const rsrc_t brs = make_rsrc(biases + sb0, (uint64_t)n_sb * 2);
 
-  // ---- issue the first slot's weight loads before staging x
-  int rowc[R];
+  const int x_units = MT * CP * UPC;  // padded 8-element units of x
+  u32x4_t xr[XU];
 #pragma unroll
-  for (int r = 0; r < R; ++r) rowc[r] = min(row0 + r, N - 1);  // clamp: loads stay in bounds
-  const u32x4_t* wrow[R];
+  for (int k = 0; k < XU; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    const int m = MT == 1 ? 0 : i / (CP * UPC);
+    const int u = i - m * (CP * UPC);  // unit within the row
+    const bool real = m < M && u < C * UPC;
+    xr[k] = buf_load16(xrs, real ? (uint32_t)(m * K + u * 8) * 2 : kOutOfRange);
+  }
+  // SBW (G % 4 == 0): 4 groups per 8-byte load, one per thread; else 16-bit loads.
+  u32x2_t sv[4], bv[4];
+  if constexpr (SBW) {
+    sv[0] = buf_load8(srs, threadIdx.x * 8);
+    bv[0] = buf_load8(brs, threadIdx.x * 8);
+  } else {
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    wrow[r] = reinterpret_cast<const u32x4_t*>(wq + (int64_t)rowc[r] * (C * 4));
+    for (int k = 0; k < 4; ++k) {
+      sv[k][0] = buf_load2(srs, (threadIdx.x + k * kBlock) * 2);
+      bv[k][0] = buf_load2(brs, (threadIdx.x + k * kBlock) * 2);
+    }
+  }
+  __asm__ volatile("" ::: "memory");  // keep the weight loads after these
 
-  // ---- stage x: unit u (8 elements) of row m -> smem[(m*UPC + u%UPC)*C + u/UPC]
-  float* xsum = reinterpret_cast<float*>(smem + MT * UPC * C);
-  for (int i = threadIdx.x; i < MT * (K / 8); i += kBlock) {
-    const int m = i / (K / 8);
-    const int u = i - m * (K / 8);
-    u32x4_t v = {0u, 0u, 0u, 0u};
-    if (m < M) v = *reinterpret_cast<const u32x4_t*>(x + (int64_t)m * K + u * 8);
+  u32x4_t wv[S][R];
+#pragma unroll
+  for (int j = 0; j < S; ++j)
+#pragma unroll
+    for (int r = 0; r < R; ++r)  // chunks past the row end are multiplied by zero x
+      wv[j][r] = buf_load16<kBufNT>(wrs, (uint32_t)(((slot * R + r) * C + lane + j * TPR) * 16));
+
+  // ---- 2. LDS: x as [m][slot j][unit h][lane] (4-bit pair-permuted), chunk
+  // sums [m][chunk], (scale | bias << 16) as [row][group]; zeros past the row.
+  u32x4_t* xl = smem;
+  float* xsum = reinterpret_cast<float*>(smem + MT * CP * UPC);
+  uint32_t* sb = reinterpret_cast<uint32_t*>(xsum + MT * CP);
+#pragma unroll
+  for (int k = 0; k < XU; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (k * kBlock >= x_units) break;  // uniform
+    const int m = MT == 1 ? 0 : i / (CP * UPC);
+    const int u = i - m * (CP * UPC);
+    const int c = u / UPC, h = u % UPC;
+    u32x4_t v = xr[k];
     float s8 = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s8 += lo_bf16(v[j]) + hi_bf16(v[j]);
+    for (int q = 0; q < 4; ++q) s8 += lo_bf16(v[q]) + hi_bf16(v[q]);
     if constexpr (BITS == 4) {
       const u32x4_t p = {(v[0] & 0xffffu) | (v[2] << 16), (v[0] >> 16) | (v[2] & 0xffff0000u),
                          (v[1] & 0xffffu) | (v[3] << 16), (v[1] >> 16) | (v[3] & 0xffff0000u)};
       v = p;
     }
-    smem[(m * UPC + u % UPC) * C + u / UPC] = v;
-    s8 = lane_group_sum<UPC>(s8);
-    if (u % UPC == 0) xsum[m * C + u / UPC] = s8;
+    s8 += dpp_f32<0xb1>(s8);  // the UPC (2 or 4) consecutive units of a chunk
+    if constexpr (UPC == 4) s8 += dpp_f32<0x4e>(s8);
+    if (i < x_units) {
+      xl[((m * NJ + c / TPR) * UPC + h) * TPR + c % TPR] = v;
+      if (h == 0) xsum[m * CP + c] = s8;
+    }
   }
-  __syncthreads();
+  if constexpr (SBW) {
+    const int i = threadIdx.x * 4;
+    if (i < RPB * G) {  // entries past rows_here were read as zeros
+      const int rl = i / G, g = i - rl * G;
+      *reinterpret_cast<u32x4_t*>(sb + rl * GP + g) =
+          u32x4_t{(sv[0][0] & 0xffffu) | (bv[0][0] << 16), (sv[0][0] >> 16) | (bv[0][0] & 0xffff0000u),
+                  (sv[0][1] & 0xffffu) | (bv[0][1] << 16), (sv[0][1] >> 16) | (bv[0][1] & 0xffff0000u)};
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = threadIdx.x + k * kBlock;
+      if (i < RPB * G) {
+        const int rl = i / G;
+        sb[rl * GP + (i - rl * G)] = sv[k][0] | (bv[k][0] << 16);
+      }
+    }
+  }
+  if (GP > G) {
+    for (int i = threadIdx.x; i < RPB * (GP - G); i += kBlock) {  // padded groups read as 0
+      const int rl = i / (GP - G);
+      sb[rl * GP + G + (i - rl * (GP - G))] = 0u;
+    }
+  }
+  lds_barrier();
 
+  // ---- 3. contract ----
+  const Nibble nib;
   float acc[R][MT];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 
-  const int n_slots = (C + TPR - 1) / TPR;
-  for (int j = 0; j < n_slots; ++j) {
-    const int c = lane + j * TPR;
-    const bool valid = c < C;
-    const int cc = valid ? c : C - 1;
-    u32x4_t wv[R];
+  const u32x4_t* xlane = xl + lane;
+  const float* xslane = xsum + lane;
+  const uint32_t* sblane = sb + slot * R * GP + lane / CPG;
 #pragma unroll
-    for (int r = 0; r < R; ++r) wv[r] = load_stream_u4(wrow[r] + cc);
-    const int g = (cc * EPC) / kGroup;
-    float sc[R], bi[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      sc[r] = bf16_bits_to_f32(scales[(int64_t)rowc[r] * G + g]);
-      bi[r] = bf16_bits_to_f32(biases[(int64_t)rowc[r] * G + g]);
-      if (!valid) sc[r] = bi[r] = 0.f;
-    }
+  for (int j = 0; j < S; ++j) {
+    if (j >= NJ) break;  // uniform
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       if (m >= M) break;
-      const float xs = xsum[m * C + cc];
+      const float xs = xslane[m * CP + j * TPR];
       u32x4_t xv[UPC];
 #pragma unroll
-      for (int h = 0; h < UPC; ++h) xv[h] = smem[(m * UPC + h) * C + cc];
+      for (int h = 0; h < UPC; ++h) xv[h] = xlane[((m * NJ + j) * UPC + h) * TPR];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
+        const uint32_t sbv = sblane[r * GP + j * (TPR / CPG)];
+        const float sc = lo_bf16(sbv), bi = hi_bf16(sbv);
         float d = 0.f;
         if constexpr (BITS == 4) {
 #pragma unroll
           for (int wi = 0; wi < 4; ++wi) {
-            const uint32_t wd = wv[r][wi];
-#pragma unroll
-            for (int sh = 0; sh < 4; ++sh) {
-              const uint32_t p = ((wd >> (4 * sh)) & 0x000F000Fu) | 0x43004300u;
-              d = dot2_bf16(p, xv[wi][sh], d);
-            }
+            const uint32_t wd = wv[j][r][wi];
+            d = dot2_bf16(nib.pair(wd), xv[wi][0], d);
+            d = dot2_bf16(nib.pair(wd >> 4), xv[wi][1], d);
+            d = dot2_bf16(nib.pair(wd >> 8), xv[wi][2], d);
+            d = dot2_bf16(nib.pair(wd >> 12), xv[wi][3], d);
           }
-          acc[r][m] = fmaf(sc[r], d, acc[r][m]);
-          acc[r][m] = fmaf(fmaf(-128.f, sc[r], bi[r]), xs, acc[r][m]);
+          acc[r][m] = fmaf(sc, d, acc[r][m]);
+          acc[r][m] = fmaf(fmaf(-128.f, sc, bi), xs, acc[r][m]);
         } else {
 #pragma unroll
           for (int wi = 0; wi < 4; ++wi) {
-            const uint32_t wd = wv[r][wi];
-            const uint32_t xa = xv[wi / 2][(wi % 2) * 2];
-            const uint32_t xb2 = xv[wi / 2][(wi % 2) * 2 + 1];
-            d = fmaf(lo_bf16(xa), ubyte_f32<0>(wd), d);
-            d = fmaf(hi_bf16(xa), ubyte_f32<1>(wd), d);
-            d = fmaf(lo_bf16(xb2), ubyte_f32<2>(wd), d);
-            d = fmaf(hi_bf16(xb2), ubyte_f32<3>(wd), d);
+            const uint32_t wd = wv[j][r][wi];
+            d = dot2_bf16(pack_bf16x2(ubyte_f32<0>(wd), ubyte_f32<1>(wd)),
+                          xv[wi / 2][(wi % 2) * 2], d);
+            d = dot2_bf16(pack_bf16x2(ubyte_f32<2>(wd), ubyte_f32<3>(wd)),
+                          xv[wi / 2][(wi % 2) * 2 + 1], d);
           }
-          acc[r][m] = fmaf(sc[r], d, acc[r][m]);
-          acc[r][m] = fmaf(bi[r], xs, acc[r][m]);
+          acc[r][m] = fmaf(sc, d, acc[r][m]);
+          acc[r][m] = fmaf(bi, xs, acc[r][m]);
         }
       }
     }
   }
 
+  // ---- 4. reduce across the TPR lanes of each row, store ----
+  constexpr int W = TPR < 64 ? TPR : 64;
+  constexpr int SUM_LANE = dpp_sum_lane<W>();
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = row0 + r;
-    const float add = (bias && row < N) ? bf16_bits_to_f32(bias[row]) : 0.f;
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float v = lane_group_sum<TPR>(acc[r][m]);
-      if (lane == 0 && m < M && row < N)
-        y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(v + add);
+    for (int m = 0; m < MT; ++m) acc[r][m] = dpp_group_sum<W>(acc[r][m]);
+
+  if constexpr (WPR == 1) {
+    if (lane % W == SUM_LANE) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row >= N) continue;
+        const float add = bias ? bf16_bits_to_f32(bias[row]) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          if (m < M) y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(acc[r][m] + add);
+      }
+    }
+  } else {
+    const int wave = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) red[(wave * R + r) * MT + m] = acc[r][m];
+    }
+    __syncthreads();
+    if (lane == 0) {
+      const int w0 = slot * WPR;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row >= N) continue;
+        const float add = bias ? bf16_bits_to_f32(bias[row]) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          float v = 0.f;
+#pragma unroll
+          for (int w = 0; w < WPR; ++w) v += red[((w0 + w) * R + r) * MT + m];
+          if (m < M) y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(v + add);
+        }
+      }
     }
   }
 }
 
-template <int BITS, int TPR, int R, int MT>
+template <int BITS, int TPR>
+size_t lds_bytes(int64_t MT, int64_t K, int R) {
+  constexpr int EPC = 128 / BITS;
+  const int64_t C = K / EPC;
+  const int64_t CP = (C + TPR - 1) / TPR * TPR;
+  const int64_t GP = CP / (kGroup / EPC);
+  const int64_t RPB = (kBlock / TPR) * R;
+  return (size_t)(MT * CP * 16 * (EPC / 8) + MT * CP * 4 + RPB * GP * 4);
+}
+
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool SBW>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                const GatherMap& g, hipStream_t stream) {
-  constexpr int EPC = 128 / BITS;
-  const int64_t C = K / EPC;
-  const size_t lds = (size_t)MT * K * 2 + (size_t)MT * C * 4;
   const int64_t rows_per_block = (kBlock / TPR) * R;
+  const size_t lds = lds_bytes<BITS, TPR>(MT, K, R);
   const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)g.T);
-  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, MT>), grid, dim3(kBlock), lds, stream, x, wq, s, b,
-                     bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E, g.x_batches);
+  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, SBW>), grid, dim3(kBlock), lds, stream, x,
+                     wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E, g.x_batches);
   return hipGetLastError();
 }
 
-template <int BITS, int TPR, int R>
+template <int BITS, int TPR, int R, int S, int MT>
+hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                  const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                  const GatherMap& g, hipStream_t stream) {
+  constexpr int EPC = 128 / BITS;
+  const int64_t CP = (K / EPC + TPR - 1) / TPR * TPR;
+  const int64_t units = (MT * CP * (EPC / 8) + kBlock - 1) / kBlock;  // x units per thread
+  if ((K / kGroup) % 4 != 0) {  // scales loaded 16 bits at a time (generic row width only)
+    if constexpr (TPR == 256) {
+      if (units <= 12)
+        return run<BITS, TPR, R, S, MT, 12, false>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    }
+    return hipErrorInvalidValue;  // pick_tpr routes these shapes to TPR 256
+  }
+  if (units <= 2) return run<BITS, TPR, R, S, MT, 2, true>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 4) return run<BITS, TPR, R, S, MT, 4, true>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 12) return run<BITS, TPR, R, S, MT, 12, true>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  return hipErrorInvalidValue;  // excluded by qmv_fits
+}
+
+template <int BITS, int TPR, int R, int S>
 hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                   const GatherMap& g, hipStream_t stream) {
-  if (M <= 1) return run<BITS, TPR, R, 1>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 2) return run<BITS, TPR, R, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 4) return run<BITS, TPR, R, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  return run<BITS, TPR, R, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 1) return run_xu<BITS, TPR, R, S, 1>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 2) return run_xu<BITS, TPR, R, S, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 4) return run_xu<BITS, TPR, R, S, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  return run_xu<BITS, TPR, R, S, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+}
+
+constexpr int kTprs[] = {16, 32, 64, 128, 256};
+
+// Lanes per row: the narrowest whose lanes own at most 8 chunks each, widened
+// while the grid has fewer than 2 blocks per CU.  Rows whose group count is
+// not a multiple of 4 use the generic 256-lane width.
+int pick_tpr(int64_t C, int64_t N, int64_t T, int64_t G) {
+  if (G % 4 != 0) return 256;  // 16-bit scale loads: one generic configuration
+  int pick = 0;
+  while (pick < 4 && (C + kTprs[pick] - 1) / kTprs[pick] > 8) ++pick;
+  while (pick < 4 && ((N * kTprs[pick]) / kBlock) * T < 512) ++pick;
+  return kTprs[pick];
 }
 
 template <int BITS>
@@ -199,25 +355,40 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
                     const GatherMap& g, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t C = K / EPC;
-  // Lane-per-row shapes tried in order: enough chunks per lane to keep loads
-  // in flight, enough blocks (x output batches) to fill 256 CUs.
-  auto blocks = [&](int tpr, int r) { return ((N * tpr) / (kBlock * r)) * g.T; };
-  if ((C + 15) / 16 <= 8 && blocks(16, 2) >= 1024)
-    return run_mt<BITS, 16, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if ((C + 31) / 32 <= 8 && blocks(32, 2) >= 1024)
-    return run_mt<BITS, 32, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if ((C + 63) / 64 <= 8 && blocks(64, 2) >= 1024)
-    return run_mt<BITS, 64, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  return run_mt<BITS, 64, 1>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  const int tpr = pick_tpr(C, N, g.T, K / kGroup);
+  const int slots = (int)((C + tpr - 1) / tpr);
+  switch (tpr) {
+    case 16:
+      if (slots <= 2) return run_mt<BITS, 16, 1, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 4) return run_mt<BITS, 16, 1, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots == 7) return run_mt<BITS, 16, 1, 7>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 16, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    case 32:
+      if (slots == 7) return run_mt<BITS, 32, 1, 7>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 32, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    case 64:
+      return run_mt<BITS, 64, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    case 128:
+      return run_mt<BITS, 128, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    default:
+      if (slots <= 8) return run_mt<BITS, 256, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return hipErrorInvalidValue;  // excluded by qmv_fits
+  }
 }
 
 }  // namespace
 
-int qmv_max_rows(int64_t K, int bits) {
-  const int64_t per_row = K * 2 + (K / (128 / bits)) * 4;  // staged x + chunk sums
-  for (int mt = 8; mt >= 1; mt >>= 1)
-    if (mt * per_row <= kQmvLdsBudget) return mt;
-  return 0;
+bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T) {
+  if (M < 1 || M > 8 || T > 65535) return false;
+  const int epc = 128 / bits;
+  const int64_t C = K / epc;
+  if (C > 8 * 256) return false;  // more chunks than one block's lanes can own
+  const int tpr = pick_tpr(C, N, T, K / kGroup);
+  const int64_t CP = (C + tpr - 1) / tpr * tpr;
+  const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int64_t lds = mt * CP * 2 * epc + mt * CP * 4 + (kBlock / tpr) * (CP / (kGroup / epc)) * 4;
+  const int64_t units = mt * CP * (epc / 8);  // x units staged per block
+  return lds <= kQmvLdsBudget && units <= 12 * kBlock;
 }
 
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
