@@ -178,11 +178,16 @@ def main():
         mq.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits=bits)
 
     if args.profile:
+        # Counter calibration first: a plain 128 MiB -> 128 MiB copy whose source
+        # was pushed out of the 256 MB Infinity Cache by a 1 GiB fill, so that
+        # FETCH_SIZE / WRITE_SIZE of the copy correspond to known HBM bytes.
+        src = torch.empty(64 * 1024 * 1024, dtype=torch.bfloat16, device="cuda:0").fill_(1)
+        flush = torch.empty(512 * 1024 * 1024, dtype=torch.bfloat16, device="cuda:0").fill_(2)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        del flush
         for i in range(args.warmup + args.steps):
             launch(i)
-        src = torch.empty(256 * 1024 * 1024, dtype=torch.bfloat16, device="cuda:0").fill_(1)
-        dst = torch.empty_like(src)
-        dst.copy_(src)  # calibration: 512 MiB read + 512 MiB written
         torch.cuda.synchronize()
         print(json.dumps({"profile": "done", "launches": args.warmup + args.steps,
                           "copy_bytes_each_way": src.numel() * 2}))
