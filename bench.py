@@ -55,7 +55,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", action="store_true",
-                    help="eager launches of the headline kernel + a 512 MiB copy (rocprofv3 runs)")
+                    help="eager launches of the headline kernel + a 128 MiB copy (rocprofv3 runs)")
+    ap.add_argument("--profile-shape", default=None, metavar="M,K,N,BITS",
+                    help="eager launches of quantized_matmul at one shape (rocprofv3 runs)")
     return ap.parse_args()
 
 
@@ -167,6 +169,18 @@ def main():
 
     mq = importlib.import_module("mlx-server-runtime_amd")
     from oracle import oracle as orc
+
+    if args.profile_shape:
+        pM, pK, pN, pbits = (int(v) for v in args.profile_shape.split(","))
+        reps = make_replicas(mq, torch, pN, pK, pbits, 2, seed=0)
+        px = torch.randn(pM, pK, generator=torch.Generator(device="cuda:0").manual_seed(1),
+                         device="cuda:0").to(torch.bfloat16)
+        for i in range(args.warmup + args.steps):
+            wq, s, b = reps[i % 2]
+            mq.quantized_matmul(px, wq, s, b, transpose=True, group_size=64, bits=pbits)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_shape": [pM, pK, pN, pbits], "launches": args.warmup + args.steps}))
+        return
 
     K, N, bits, M = 3584, 18944, 4, 1
     replicas = make_replicas(mq, torch, N, K, bits, args.replicas, seed=0)

@@ -215,6 +215,23 @@ def test_prefill_shape_sampled_rows(mq, orc, bits, M):
     assert_close(y[torch.from_numpy(rows).to(DEV)], orc.qmm(x[rows], wq, s, b, 64, bits))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_large_tiles_ragged_edges(mq, orc, bits):
+    """M and N that are not multiples of the 256-row tiles, with enough tiles
+    (5 x 26) for the large-tile kernel: rows of the last, partial M tile and
+    the last, partial N tile are among those checked."""
+    M, N, K = 1100, 6500, 512
+    rng = np.random.default_rng(616 + bits)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits,
+                            bias=bf16_dev(bias))
+    rows = np.unique(np.r_[0, 255, 256, 1023, 1024, M - 1, rng.integers(0, M, 8)])
+    assert_close(y[torch.from_numpy(rows).to(DEV)],
+                 orc.qmm(x[rows], wq, s, b, 64, bits, bias=bias))
+
+
 # ------------------------------------------------------------ gather_qmm
 
 
