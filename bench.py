@@ -126,6 +126,19 @@ def cpu_baseline(args, orc, wq, s, b, x, N, K, bits):
                       "float32 restatement of MLX's CPU quantized_matmul loop, OpenMP over rows"}
 
 
+def hbm_floor(torch, nbytes: int, count: int = 16):
+    """Device-to-device copies moving `nbytes` in total (half read, half written),
+    `count` rotating sources so every copy reads from HBM: what one launch of a
+    plain streaming kernel of the GEMV's size achieves."""
+    half = nbytes // 4  # bf16 elements per direction
+    srcs = [torch.empty(half, dtype=torch.bfloat16, device="cuda:0").fill_(i) for i in range(count)]
+    dst = torch.empty(half, dtype=torch.bfloat16, device="cuda:0")
+    ms, _ = time_graph(torch, lambda i: dst.copy_(srcs[i % count]), 256, warmup=8)
+    del srcs, dst
+    return {"kind": "device copy (torch copy_), one launch per step", "bytes": 4 * half,
+            "us": round(ms * 1e3, 3), "GBps": round(4 * half / (ms * 1e-3) / 1e9, 1)}
+
+
 def sweep(mq, torch):
     rows = []
     for (K, N) in ((3584, 18944), (18944, 3584), (3584, 4608)):
@@ -234,6 +247,7 @@ def main():
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
     }
+    line["hbm_floor"] = hbm_floor(torch, by)
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
     if not args.no_cpu:

@@ -33,6 +33,13 @@
  * zero-exactness property of the edge refit, one-hot and all-zero-code
  * matmul identities, and numpy matmul of the dequantized matrix.
  *
+ * Parity unpinned against MLX itself (only an import of mlx could pin these,
+ * and mlx is absent): the rounding sequence of mx.dequantize (restated here
+ * as bf16(bf16(q*s) + b), MLX's op-graph order), the tie-breaking and refit
+ * of mx.quantize on weights that are not on the quantization grid, and the
+ * accumulation order of MLX's CPU quantized_matmul.  The restatement itself
+ * is pinned by the checks above.
+ *
  * Build: oracle/Makefile (gcc, -ffp-contract=off so no multiply-add is fused:
  * every float operation below rounds exactly once, as written).
  */
