@@ -83,11 +83,15 @@ int check_dim(const char* op, const char* name, int64_t v) {
   return MQ_OK;
 }
 
-// MQ_QMM=tile128 forces the 128x128-tile MFMA kernel for every large M (A/B runs).
-bool force_tile128() {
-  static const bool v = [] {
+// GEMM kernel for M above the GEMV range: the register-dequant 256x256 kernel
+// where it fits, else the LDS-dequant 256x256 kernel, else the 128x128 one.
+// MQ_QMM=tile128|lds256 forces one of the latter two (A/B runs).
+int gemm_override() {
+  static const int v = [] {
     const char* e = getenv("MQ_QMM");
-    return e && strcmp(e, "tile128") == 0;
+    if (e && strcmp(e, "tile128") == 0) return 1;
+    if (e && strcmp(e, "lds256") == 0) return 2;
+    return 0;
   }();
   return v;
 }
@@ -166,7 +170,9 @@ int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* sca
     e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
   } else if (mq::qmv_fits(M, N, K, bits, 1)) {
     e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
-  } else if (mq::qmm2_fits(M, N, K, bits) && !force_tile128()) {
+  } else if (mq::qmm3_fits(M, N, K, bits) && gemm_override() == 0) {
+    e = mq::launch_qmm3(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
+  } else if (mq::qmm2_fits(M, N, K, bits) && gemm_override() != 1) {
     e = mq::launch_qmm2(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
   } else {
     e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);

@@ -43,6 +43,13 @@ hipError_t launch_qmm2(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, hipStream_t stream);
 
+// 256x256-tile MFMA path with weights dequantized in registers (qmm3_fits:
+// K a multiple of 512, >= 128 tiles, 32-bit offsets).
+bool qmm3_fits(int64_t M, int64_t N, int64_t K, int bits);
+hipError_t launch_qmm3(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                       int64_t N, int64_t K, int bits, hipStream_t stream);
+
 // MFMA path, any M.
 hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,

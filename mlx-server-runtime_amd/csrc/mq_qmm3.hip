@@ -1,0 +1,267 @@
+// Large-M quantized matmul, weights dequantized straight into MFMA registers:
+//   y[m, n] = sum_k x[m, k] * (s*q + b)[n, k]  (+ bias[n])
+// mx.quantized_matmul(x, w, scales, biases, transpose=True) for prefill-sized
+// M (python/mlx_worker/native_mlx/models/qwen2.py:76-78,115,134,227).
+//
+// MFMA-bound.  A 512-thread block owns a 256x256 output tile and walks K in
+// steps of 64 (one quantization group).  Each of the 8 waves (2 along M x 4
+// along N) computes a 128x64 sub-tile with 4x2 v_mfma_f32_32x32x16_bf16 per
+// 16-wide k slice.
+//
+// * x never passes through registers on its way in: each step's 256x64 tile is
+//   copied HBM -> LDS by buffer_load_dwordx4 ... lds (every lane writes 16
+//   bytes at M0 + 16*lane), two steps ahead, into one of three 32 KiB stages.
+//   Rows are 128 bytes with the 16-byte chunk index XOR-ed with (row >> 1) & 7,
+//   so a fragment read of 32 rows hits 16 distinct 4-bank groups per half wave.
+// * Weights never pass through LDS: for the MFMA B operand, lane l holds the
+//   8 codes of column l % 32 for k-slice ks of its half (l / 32).  The k order
+//   inside a group is permuted (A and B agree on it, so the product is
+//   unchanged): half h takes k = 32h + 8ks .. 32h + 8ks + 7, which makes a
+//   lane's codes for the whole step one contiguous 16-byte (4-bit) or 32-byte
+//   (8-bit) load.  Codes are loaded one step ahead and dequantized
+//   (fma(s, q, b), one bfloat16 rounding) right before their MFMAs, so the
+//   dequantization of one wave runs under the other wave's MFMAs.
+// * Scales and biases for 8 groups of the block's 256 columns (16 bytes per
+//   column and array) are DMA-ed into LDS two steps before they are needed.
+// One barrier per step; the wait before it covers only the DMA of the next
+// step's x tile, never the prefetches issued in the current step.
+#include "mq_common.h"
+#include "mq_internal.h"
+
+namespace mq {
+namespace {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int kThreads = 512;
+constexpr int kXStage = BM * BK * 2;             // 32 KiB of x per step
+constexpr int kSbChunk = 8;                      // groups per scale/bias chunk
+constexpr int kSbArray = BN * kSbChunk * 2;      // 4 KiB: one array, one chunk
+constexpr int kSbBytes = 2 * kSbArray;           // scales + biases of a chunk
+constexpr int kSbBase = 3 * kXStage;             // after the three x stages
+constexpr int kLds = kSbBase + 2 * kSbBytes;     // 112 KiB
+
+typedef __attribute__((address_space(3))) void lds_t;
+
+__device__ __forceinline__ void dma16(rsrc_t r, lds_t* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+}
+
+// End of a step: this thread's DMA of step kt+1 (issued one step earlier) has
+// landed once at most N memory operations -- the ones issued this step -- are
+// outstanding; then the whole block syncs.
+template <int N>
+__device__ __forceinline__ void step_barrier() {
+  if constexpr (N == 6) __asm__ volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 7) __asm__ volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 8) __asm__ volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 9) __asm__ volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else static_assert(N >= 6 && N <= 9, "unexpected count");
+}
+
+// 8 codes (one MFMA B fragment) -> bf16(fma(s, q, b)), k order preserved.
+template <int BITS>
+__device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, float b) {
+  u32x4_t o;
+  if constexpr (BITS == 4) {
+    // byte t of w0 = q[2t] | q[2t+1] << 4.  The empty asm keeps the two masks
+    // as two instructions feeding v_cvt_f32_ubyte0..3 (otherwise each code
+    // becomes its own bit-field extract).
+    uint32_t lo = w0 & 0x0F0F0F0Fu, hi = (w0 >> 4) & 0x0F0F0F0Fu;
+    __asm__("" : "+v"(lo), "+v"(hi));
+    o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+    o[1] = pack_bf16x2(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+    o[2] = pack_bf16x2(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+    o[3] = pack_bf16x2(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
+    (void)w1;
+  } else {
+    o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w0), b), fmaf(s, ubyte_f32<1>(w0), b));
+    o[1] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w0), b), fmaf(s, ubyte_f32<3>(w0), b));
+    o[2] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w1), b), fmaf(s, ubyte_f32<1>(w1), b));
+    o[3] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w1), b), fmaf(s, ubyte_f32<3>(w1), b));
+  }
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    int tiles_m) {
+  extern __shared__ u32x4_t smem[];
+  char* const lds = reinterpret_cast<char*>(smem);
+  const int tid = threadIdx.x;
+  const int l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int h = l >> 5;
+
+  // ---- tile order: XCD-contiguous runs, M fastest within a weight column ----
+  const int nblk = gridDim.x;
+  const int per_xcd = nblk / 8, rem = nblk % 8;
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const int tile = (xcd < rem ? xcd * (per_xcd + 1) : rem * (per_xcd + 1) + (xcd - rem) * per_xcd) + slot;
+  const int bm = tile % tiles_m, bn = tile / tiles_m;
+  const int m0 = bm * BM, n0 = bn * BN;
+
+  const int G = K / kGroup;
+  const int KT = K / BK;
+  const rsrc_t xrs = make_rsrc(x, (uint64_t)M * K * 2);
+  const rsrc_t wrs = make_rsrc(wq, (uint64_t)N * K * BITS / 8);
+  const rsrc_t srs = make_rsrc((wave & 1) ? biases : scales, (uint64_t)N * G * 2);
+
+  // x DMA: wave w, op i fills rows (4w + i)*8 .. +7 of a stage (1 KiB); lane l
+  // writes physical chunk l % 8 of row l / 8, i.e. logical chunk (l%8) ^ f(row).
+  uint32_t xoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (wave * 4 + i) * 8 + (l >> 3);
+    const int chunk = (l & 7) ^ ((row >> 1) & 7);
+    xoff[i] = m0 + row < M ? (uint32_t)((m0 + row) * K + chunk * 8) * 2 : kOutOfRange;
+  }
+  // Codes: column n0 + wn*64 + 32j + l%32, half h of each group.
+  constexpr int CB = BITS * 4;  // code bytes per lane per step: 16 (4-bit) / 32 (8-bit)
+  constexpr int NC = BITS == 4 ? 2 : 4;  // 16-byte code loads per lane per step
+  uint32_t coff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn * 64 + j * 32 + (l & 31);
+    coff[j] = n < N ? (uint32_t)(n * (K * BITS / 8) + h * CB) : kOutOfRange;
+  }
+  // Scale/bias DMA: wave w loads array (w & 1) for columns (w >> 1)*64 + l.
+  uint32_t soff;
+  {
+    const int n = n0 + (wave >> 1) * 64 + l;
+    soff = n < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
+  }
+  const int sb_dst = kSbBase + (wave & 1) * kSbArray + (wave >> 1) * 1024;
+  // A fragment rows wm*128 + 32i + l%32; logical chunk 4h + ks.
+  uint32_t aoff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    aoff[ks] = (uint32_t)((wm * 128 + (l & 31)) * 128 + (((h * 4 + ks) ^ ((l >> 1) & 7)) * 16));
+  uint32_t sbr[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) sbr[j] = kSbBase + (wn * 64 + j * 32 + (l & 31)) * 16;
+
+  auto dma_x = [&](int kt, int stage) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(xrs, (lds_t*)(lds + stage * kXStage + (wave * 4 + i) * 1024), xoff[i] + kt * (BK * 2));
+  };
+  auto dma_sb = [&](int chunk, int buf) {
+    dma16(srs, (lds_t*)(lds + sb_dst + buf * kSbBytes), soff + chunk * (kSbChunk * 2));
+  };
+  auto load_codes = [&](u32x4_t (&cw)[2][NC / 2], int kt) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int p = 0; p < NC / 2; ++p) cw[j][p] = buf_load16(wrs, coff[j] + kt * (BK * BITS / 8) + p * 16);
+  };
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  u32x4_t cw[2][2][NC / 2];
+  // ---- prologue: scale chunk 0, x steps 0 and 1, codes of step 0 ----
+  dma_sb(0, 0);
+  dma_x(0, 0);
+  dma_x(1, 1);
+  load_codes(cw[0], 0);
+  step_barrier<4 + NC>();
+
+  int st = 0;  // stage holding x of the current step
+  for (int c = 0; c < KT / kSbChunk; ++c) {
+#pragma unroll
+    for (int u = 0; u < kSbChunk; ++u) {
+      const int kt = c * kSbChunk + u;
+      load_codes(cw[(u + 1) & 1], kt + 1);
+      dma_x(kt + 2, st == 0 ? 2 : st - 1);
+      if (u == kSbChunk - 2) dma_sb(c + 1, (c + 1) & 1);
+
+      const int cb = (c & 1) * kSbBytes;
+      float sc[2], bi[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        sc[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(lds + sbr[j] + cb + u * 2));
+        bi[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(lds + sbr[j] + cb + kSbArray + u * 2));
+      }
+      const char* xs = lds + st * kXStage;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8_t a[4], bq[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a[i] = *reinterpret_cast<const bf16x8_t*>(xs + aoff[ks] + i * 4096);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const u32x4_t& q = cw[u & 1][j][BITS == 4 ? 0 : ks >> 1];
+          if constexpr (BITS == 4)
+            bq[j] = dequant8<4>(q[ks], 0u, sc[j], bi[j]);
+          else
+            bq[j] = dequant8<8>(q[(ks & 1) * 2], q[(ks & 1) * 2 + 1], sc[j], bi[j]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bq[j], acc[i][j], 0, 0, 0);
+      }
+      if (u == kSbChunk - 2) step_barrier<5 + NC>();
+      else step_barrier<4 + NC>();
+      st = st == 2 ? 0 : st + 1;
+    }
+  }
+  // The prefetches of the last steps (past K, unused) must land before the
+  // block's LDS is released.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4 ----
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + wn * 64 + j * 32 + (l & 31);
+    if (n >= N) continue;
+    const float add = bias ? bf16_bits_to_f32(bias[n]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
+        if (m < M) y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][v] + add);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+bool qmm3_fits(int64_t M, int64_t N, int64_t K, int bits) {
+  // 32-bit buffer offsets (with room for the kOutOfRange marker) for x, the
+  // codes and the scales; whole 8-group scale chunks; >= 128 tiles.
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int64_t lim = (int64_t)1 << 31;
+  return K % (kSbChunk * kGroup) == 0 && M * K * 2 < lim && N * K * bits / 8 < lim &&
+         N * (K / kGroup) * 2 < lim && tiles >= 128 && tiles < lim;
+}
+
+hipError_t launch_qmm3(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                       int64_t N, int64_t K, int bits, hipStream_t stream) {
+  if (M == 0 || N == 0) return hipSuccess;
+  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  auto kern = bits == 4 ? qmm3_kernel<4> : qmm3_kernel<8>;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), kLds, stream, x, wq, scales, biases, bias, y,
+                     (int)M, (int)N, (int)K, tiles_m);
+  return hipGetLastError();
+}
+
+}  // namespace mq
