@@ -19,10 +19,10 @@
 //   unchanged): half h takes k = 32h + 8ks .. 32h + 8ks + 7, which makes a
 //   lane's codes for the whole step one contiguous 16-byte (4-bit) or 32-byte
 //   (8-bit) load.  Codes are loaded one step ahead and dequantized
-//   (fma(s, q, b), one bfloat16 rounding) right before their MFMAs, so the
-//   dequantization of one wave runs under the other wave's MFMAs.
+//   (fma(s, q, b), one bfloat16 rounding) one k-slice ahead of their MFMAs,
+//   so the dequantization runs under the MFMAs.
 // * Scales and biases for 8 groups of the block's 256 columns (16 bytes per
-//   column and array) are DMA-ed into LDS two steps before they are needed.
+//   column and array) are DMA-ed into LDS three steps before they are needed.
 // One barrier per step; the wait before it covers only the DMA of the next
 // step's x tile, never the prefetches issued in the current step.
 #include "mq_common.h"
@@ -59,13 +59,18 @@ __device__ __forceinline__ void step_barrier() {
 }
 
 // 8 codes (one MFMA B fragment) -> bf16(fma(s, q, b)), k order preserved.
+// Codes go through v_cvt_f32_ubyte0..3, nibbles after two masks spread them
+// over bytes.  (A variant that built fp16 1024 + q by OR-ing codes into a
+// mantissa and scaled them with v_fma_mix_f32 used 25% fewer VALU
+// instructions but gave intermittently wrong results on MI355X, run to run
+// on identical inputs; it is not used.)
 template <int BITS>
 __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, float b) {
   u32x4_t o;
   if constexpr (BITS == 4) {
     // byte t of w0 = q[2t] | q[2t+1] << 4.  The empty asm keeps the two masks
-    // as two instructions feeding v_cvt_f32_ubyte0..3 (otherwise each code
-    // becomes its own bit-field extract).
+    // as two instructions (otherwise each code becomes its own bit-field
+    // extract).
     uint32_t lo = w0 & 0x0F0F0F0Fu, hi = (w0 >> 4) & 0x0F0F0F0Fu;
     __asm__("" : "+v"(lo), "+v"(hi));
     o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
@@ -81,6 +86,10 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, 
   }
   return __builtin_bit_cast(bf16x8_t, o);
 }
+
+struct GroupAffine {
+  float s, b;
+};
 
 template <int BITS>
 __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
@@ -111,13 +120,14 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
   const rsrc_t srs = make_rsrc((wave & 1) ? biases : scales, (uint64_t)N * G * 2);
 
   // x DMA: wave w, op i fills rows (4w + i)*8 .. +7 of a stage (1 KiB); lane l
-  // writes physical chunk l % 8 of row l / 8, i.e. logical chunk (l%8) ^ f(row).
+  // writes physical chunk l % 8 of row l / 8, i.e. logical chunk (l%8) ^ f(row)
+  // with f(row) = (row >> 1) & 7.  Rows past M, and steps past K on the last
+  // row, lie beyond the descriptor's M*K*2 bytes and read as zeros.
   uint32_t xoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = (wave * 4 + i) * 8 + (l >> 3);
-    const int chunk = (l & 7) ^ ((row >> 1) & 7);
-    xoff[i] = m0 + row < M ? (uint32_t)((m0 + row) * K + chunk * 8) * 2 : kOutOfRange;
+    xoff[i] = (uint32_t)((m0 + row) * K + (((l & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
   }
   // Codes: column n0 + wn*64 + 32j + l%32, half h of each group.
   constexpr int CB = BITS * 4;  // code bytes per lane per step: 16 (4-bit) / 32 (8-bit)
@@ -135,11 +145,10 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
     soff = n < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
   }
   const int sb_dst = kSbBase + (wave & 1) * kSbArray + (wave >> 1) * 1024;
-  // A fragment rows wm*128 + 32i + l%32; logical chunk 4h + ks.
-  uint32_t aoff[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    aoff[ks] = (uint32_t)((wm * 128 + (l & 31)) * 128 + (((h * 4 + ks) ^ ((l >> 1) & 7)) * 16));
+  // A fragment rows wm*128 + 32i + l%32; logical chunk 4h + ks, stored at
+  // (4h + ks) ^ f: only bits 4-5 of the byte offset depend on ks, so the
+  // k-slice ks reads at aoff ^ (ks << 4).
+  const uint32_t aoff = (uint32_t)((wm * 128 + (l & 31)) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
   uint32_t sbr[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) sbr[j] = kSbBase + (wn * 64 + j * 32 + (l & 31)) * 16;
@@ -147,7 +156,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
   auto dma_x = [&](int kt, int stage) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dma16(xrs, (lds_t*)(lds + stage * kXStage + (wave * 4 + i) * 1024), xoff[i] + kt * (BK * 2));
+      dma16(xrs, (lds_t*)(lds + stage * kXStage + (wave * 4 + i) * 1024),
+            xoff[i] + kt * (BK * 2));
   };
   auto dma_sb = [&](int chunk, int buf) {
     dma16(srs, (lds_t*)(lds + sb_dst + buf * kSbBytes), soff + chunk * (kSbChunk * 2));
@@ -168,51 +178,79 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   u32x4_t cw[2][2][NC / 2];
+  auto dequant_frag = [&](const u32x4_t (&q)[2][NC / 2], int j, int ks, const GroupAffine& g) {
+    const u32x4_t& w = q[j][BITS == 4 ? 0 : ks >> 1];
+    if constexpr (BITS == 4) return dequant8<4>(w[ks], 0u, g.s, g.b);
+    else return dequant8<8>(w[(ks & 1) * 2], w[(ks & 1) * 2 + 1], g.s, g.b);
+  };
+  auto read_sb = [&](int buf, int grp, GroupAffine (&g)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const char* p = lds + sbr[j] + buf * kSbBytes + grp * 2;
+      g[j].s = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+      g[j].b = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + kSbArray));
+    }
+  };
+
   // ---- prologue: scale chunk 0, x steps 0 and 1, codes of step 0 ----
   dma_sb(0, 0);
   dma_x(0, 0);
   dma_x(1, 1);
   load_codes(cw[0], 0);
   step_barrier<4 + NC>();
+  // B fragments of k-slice 0 are always dequantized one step early, at the end
+  // of the previous step, so each step opens with MFMAs instead of VALU.
+  GroupAffine ga[2];
+  read_sb(0, 0, ga);
+  bf16x8_t b0[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
 
   int st = 0;  // stage holding x of the current step
   for (int c = 0; c < KT / kSbChunk; ++c) {
 #pragma unroll
     for (int u = 0; u < kSbChunk; ++u) {
       const int kt = c * kSbChunk + u;
+      const uint32_t xa = st * kXStage + aoff;
+      bf16x8_t a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8_t*>(lds + xa + i * 4096);
       load_codes(cw[(u + 1) & 1], kt + 1);
       dma_x(kt + 2, st == 0 ? 2 : st - 1);
-      if (u == kSbChunk - 2) dma_sb(c + 1, (c + 1) & 1);
+      if (u == kSbChunk - 3) dma_sb(c + 1, (c + 1) & 1);
 
-      const int cb = (c & 1) * kSbBytes;
-      float sc[2], bi[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        sc[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(lds + sbr[j] + cb + u * 2));
-        bi[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(lds + sbr[j] + cb + kSbArray + u * 2));
-      }
-      const char* xs = lds + st * kXStage;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        bf16x8_t a[4], bq[2];
+        bf16x8_t bq[2], an[4];
+        if (ks < 3) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          a[i] = *reinterpret_cast<const bf16x8_t*>(xs + aoff[ks] + i * 4096);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const u32x4_t& q = cw[u & 1][j][BITS == 4 ? 0 : ks >> 1];
-          if constexpr (BITS == 4)
-            bq[j] = dequant8<4>(q[ks], 0u, sc[j], bi[j]);
-          else
-            bq[j] = dequant8<8>(q[(ks & 1) * 2], q[(ks & 1) * 2 + 1], sc[j], bi[j]);
+          for (int i = 0; i < 4; ++i)
+            an[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ ((ks + 1) << 4)) + i * 4096);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bq[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b0[j], acc[i][j], 0, 0, 0);
+        if (ks < 3) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[u & 1], j, ks + 1, ga[j]);
+        } else {
+          // next step: its scales (the next chunk's buffer after the last
+          // step of a chunk, DMA-ed three steps ago) and its first k-slice
+          if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
+          else read_sb(c & 1, u + 1, ga);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[(u + 1) & 1], j, 0, ga[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) b0[j] = bq[j];
+        if (ks < 3) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) a[i] = an[i];
+        }
       }
-      if (u == kSbChunk - 2) step_barrier<5 + NC>();
+      if (u == kSbChunk - 3) step_barrier<5 + NC>();
       else step_barrier<4 + NC>();
       st = st == 2 ? 0 : st + 1;
     }

@@ -191,6 +191,23 @@ def test_quantized_matmul_deterministic(mq, orc):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+def test_large_tiles_deterministic(mq, orc, bits):
+    """The 256x256-tile kernels (DMA staging, register dequantization) give
+    bit-identical results run to run: no stage is read before it is filled."""
+    rng = np.random.default_rng(17 + bits)
+    M, N, K = 2048, 4096, 1024  # 8 x 16 tiles
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = bf16_dev(rand_bf16(orc, rng, (M, K), 1.0))
+    args = (u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
+    first = mq.quantized_matmul(x, *args)
+    for _ in range(6):
+        assert torch.equal(mq.quantized_matmul(x, *args).view(torch.int16), first.view(torch.int16))
+    rows = np.array([0, 777, M - 1])
+    assert_close(first[torch.from_numpy(rows).to(DEV)],
+                 orc.qmm(bits_host(x)[rows], wq, s, b, 64, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("KN", [(3584, 18944), (18944, 3584), (3584, 4608)])
 def test_decode_shapes_full_size(mq, orc, bits, KN):
     """M = 1 at the benchmark shapes (the whole output checked)."""
@@ -203,7 +220,7 @@ def test_decode_shapes_full_size(mq, orc, bits, KN):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M", [16, 2048])
+@pytest.mark.parametrize("M", [16, 2048, 8192])
 def test_prefill_shape_sampled_rows(mq, orc, bits, M):
     """K=3584, N=18944 at large M: sampled output rows against the oracle."""
     K, N = 3584, 18944
