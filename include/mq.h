@@ -28,6 +28,7 @@
 #ifndef MQ_H
 #define MQ_H
 
+#include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
@@ -82,12 +83,36 @@ int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
  * y bfloat16 [M, N]; float32 accumulation, one rounding at the store.
  * Replaces every QuantizedLinear call of the model graphs
  * (models/qwen2.py:76-78,115,134,227; qwen3.py:78-86,115,134,222).
- * Decode-sized M uses the GEMV kernel, larger M the MFMA kernel.
+ * Decode-sized M uses the GEMV kernels, larger M the MFMA kernels; this
+ * entry point never splits K (see mq_quantized_matmul_ws).
  */
 int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
                         const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
                         int64_t N, int64_t K, int group_size, int bits, int transpose,
                         hipStream_t stream);
+
+/*
+ * Workspace, in bytes, that mq_quantized_matmul_ws can use for this shape
+ * (0 = none).  Shapes with few output columns and a long K (the down
+ * projection at small M) split K over blocks and need float32 partial sums.
+ * MLX allocates such temporaries internally; this library allocates nothing,
+ * so the caller provides them.  No counterpart in the reference: it serves
+ * the same mx.quantized_matmul call sites as mq_quantized_matmul.
+ */
+size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size, int bits);
+
+/*
+ * mq_quantized_matmul with a caller-owned device workspace (16-byte aligned,
+ * `workspace_bytes` long; NULL/0 allowed).  With at least
+ * mq_quantized_matmul_workspace() bytes, K may be split over blocks; with
+ * less it runs unsplit.  Results are identical run to run either way (the
+ * partial sums are added in a fixed order).  Calls that share a workspace
+ * must be ordered on one stream.
+ */
+int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                           const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
+                           int64_t N, int64_t K, int group_size, int bits, int transpose,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
  * mx.gather_qmm(x, wq, scales, biases, lhs_indices, rhs_indices,

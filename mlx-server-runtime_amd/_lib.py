@@ -26,6 +26,8 @@ EXPORTS = (
     "mq_dequantize",
     "mq_embedding_lookup",
     "mq_quantized_matmul",
+    "mq_quantized_matmul_workspace",
+    "mq_quantized_matmul_ws",
     "mq_gather_qmm",
 )
 
@@ -50,10 +52,14 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_dequantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]
     L.mq_embedding_lookup.argtypes = [_p, _i64, _p, _p, _p, _i64, _i64, _int, _int, _p, _p]
     L.mq_quantized_matmul.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p]
+    L.mq_quantized_matmul_workspace.argtypes = [_i64, _i64, _i64, _int, _int]
+    L.mq_quantized_matmul_ws.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int,
+                                         _p, ctypes.c_size_t, _p]
     L.mq_gather_qmm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _int, _int, _int, _int, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
+    L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t
 
 
 def lib() -> ctypes.CDLL:

@@ -196,9 +196,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     M = xc.numel() // K
     y = torch.empty(tuple(x.shape[:-1]) + (N,), dtype=torch.bfloat16, device=x.device)
     L = _lib.lib()
-    _lib.check(L.mq_quantized_matmul(_ptr(xc), _ptr(w.contiguous()), _ptr(scales.contiguous()),
-                                     _ptr(biases.contiguous()), _ptr(bias), _ptr(y), M, N, K,
-                                     group_size, bits, 1, _stream(x)), op)
+    ws_bytes = L.mq_quantized_matmul_workspace(M, N, K, group_size, bits) if M and N else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.check(L.mq_quantized_matmul_ws(_ptr(xc), _ptr(w.contiguous()), _ptr(scales.contiguous()),
+                                        _ptr(biases.contiguous()), _ptr(bias), _ptr(y), M, N, K,
+                                        group_size, bits, 1, _ptr(ws), ws_bytes, _stream(x)), op)
     return y
 
 

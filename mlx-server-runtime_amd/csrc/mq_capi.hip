@@ -96,6 +96,13 @@ int gemm_override() {
   return v;
 }
 
+// Skinny MFMA kernel for M above the GEMV range and up to two 128-row tiles.
+// MQ_QMM=tile128 turns it off (A/B runs).
+bool use_skinny(int64_t M, int64_t N, int64_t K, int bits) {
+  return M <= 256 && gemm_override() != 1 && !mq::qmvm_fits(M, N, K, bits, 1) &&
+         !mq::qmv_fits(M, N, K, bits, 1) && mq::qmms_fits(M, N, K, bits);
+}
+
 }  // namespace
 
 extern "C" {
@@ -145,10 +152,26 @@ int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
       mq::launch_dequantize(wq, scales, biases, ids, n_ids, rows, out, K, bits, stream), op);
 }
 
+size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size,
+                                     int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
+  if (!use_skinny(M, N, K, bits)) return 0;
+  return mq::qmms_workspace_bytes(M, N, K, bits);
+}
+
 int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
                         const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
                         int64_t N, int64_t K, int group_size, int bits, int transpose,
                         hipStream_t stream) {
+  return mq_quantized_matmul_ws(x, wq, scales, biases, bias_vec, y, M, N, K, group_size, bits,
+                                transpose, nullptr, 0, stream);
+}
+
+int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                           const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
+                           int64_t N, int64_t K, int group_size, int bits, int transpose,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const char* op = "quantized_matmul";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
@@ -170,6 +193,11 @@ int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* sca
     e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
   } else if (mq::qmv_fits(M, N, K, bits, 1)) {
     e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
+  } else if (use_skinny(M, N, K, bits)) {
+    if (workspace && !aligned16(workspace))
+      return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
+    e = mq::launch_qmms(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
+                        workspace_bytes, stream);
   } else if (mq::qmm3_fits(M, N, K, bits) && gemm_override() == 0) {
     e = mq::launch_qmm3(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
   } else if (mq::qmm2_fits(M, N, K, bits) && gemm_override() != 1) {

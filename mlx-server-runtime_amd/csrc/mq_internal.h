@@ -50,6 +50,17 @@ hipError_t launch_qmm3(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, hipStream_t stream);
 
+// Skinny MFMA path (M up to a few hundred): weights streamed once per M tile
+// of up to 128 rows; K split over blocks through a float32 workspace when the
+// tiles alone cannot fill the GPU (qmms_workspace_bytes > 0).  Without a large
+// enough workspace it runs unsplit.
+bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits);
+size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits);
+hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
 // MFMA path, any M.
 hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,

@@ -23,8 +23,8 @@
 //   so the dequantization runs under the MFMAs.
 // * Scales and biases for 8 groups of the block's 256 columns (16 bytes per
 //   column and array) are DMA-ed into LDS three steps before they are needed.
-// One barrier per step; the wait before it covers only the DMA of the next
-// step's x tile, never the prefetches issued in the current step.
+// One barrier per step; the wait before it covers the DMAs of earlier steps
+// (the next step's x tile), never those issued in the current step.
 #include "mq_common.h"
 #include "mq_internal.h"
 
@@ -46,16 +46,15 @@ __device__ __forceinline__ void dma16(rsrc_t r, lds_t* dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
 }
 
-// End of a step: this thread's DMA of step kt+1 (issued one step earlier) has
-// landed once at most N memory operations -- the ones issued this step -- are
-// outstanding; then the whole block syncs.
+// End of a step: wait until at most N memory operations are outstanding, N
+// being the number of DMA operations issued in this step, then sync the
+// block.  vmcnt retires in issue order and the DMAs (LDS writes) never move
+// across this asm, so every DMA of earlier steps -- in particular the next
+// step's x tile -- has landed whatever the compiler did with the register
+// loads (it may move those across the asm: they read __restrict__ memory).
 template <int N>
 __device__ __forceinline__ void step_barrier() {
-  if constexpr (N == 6) __asm__ volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 7) __asm__ volatile("s_waitcnt vmcnt(7) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 8) __asm__ volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 9) __asm__ volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else static_assert(N >= 6 && N <= 9, "unexpected count");
+  __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // 8 codes (one MFMA B fragment) -> bf16(fma(s, q, b)), k order preserved.
@@ -193,11 +192,11 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
   };
 
   // ---- prologue: scale chunk 0, x steps 0 and 1, codes of step 0 ----
+  load_codes(cw[0], 0);
   dma_sb(0, 0);
   dma_x(0, 0);
   dma_x(1, 1);
-  load_codes(cw[0], 0);
-  step_barrier<4 + NC>();
+  step_barrier<4>();
   // B fragments of k-slice 0 are always dequantized one step early, at the end
   // of the previous step, so each step opens with MFMAs instead of VALU.
   GroupAffine ga[2];
@@ -250,8 +249,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
           for (int i = 0; i < 4; ++i) a[i] = an[i];
         }
       }
-      if (u == kSbChunk - 3) step_barrier<5 + NC>();
-      else step_barrier<4 + NC>();
+      if (u == kSbChunk - 3) step_barrier<5>();
+      else step_barrier<4>();
       st = st == 2 ? 0 : st + 1;
     }
   }

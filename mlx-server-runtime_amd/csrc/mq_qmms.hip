@@ -1,0 +1,305 @@
+// Skinny quantized matmul on the matrix cores (M up to a few hundred rows):
+//   y[m, n] = sum_k x[m, k] * (s*q + b)[n, k]  (+ bias[n])
+// mx.quantized_matmul(x, w, scales, biases, transpose=True) for batched decode
+// and short prefill chunks (python/mlx_worker/native_mlx/models/qwen2.py:
+// 76-78,115,134,227; the scheduler caps a prefill chunk at 256 rows,
+// python/mlx_worker/scheduler.py:567).
+//
+// Every weight is read from HBM and dequantized exactly once per M tile, so
+// for M <= 128 the kernel streams the codes like a GEMV while the matrix
+// cores do the arithmetic.  A 256-thread block owns 128 columns (32 per
+// wave) and an M tile of 32*MI rows (MI = 1, 2, 4), and walks K in steps of
+// one quantization group:
+// * x tiles (32*MI rows x 64) are copied HBM -> LDS by buffer_load_dwordx4
+//   ... lds two steps ahead into three stages, rows of 128 bytes with the
+//   16-byte chunk index XOR-ed with (row >> 1) & 7.
+// * For v_mfma_f32_32x32x16_bf16's B operand lane l holds column l % 32 and,
+//   in k-slice ks, the 8 codes k = 32h + 8ks .. +7 of its half h = l / 32
+//   (A reads x with the same k order), so a lane's codes for a step are one
+//   contiguous 16-byte (4-bit) or 32-byte (8-bit) load, issued a step ahead
+//   and dequantized (fma(s, q, b), one bfloat16 rounding) in registers.
+// * Scales and biases come 8 groups at a time (16 bytes per column and
+//   array), a chunk ahead.
+// When the N x M tiles alone cannot fill the GPU (few columns, long K: the
+// down projection), K is split over blocks in whole 8-group chunks; each
+// split writes float32 partial sums to a caller-provided workspace and
+// splitk_reduce adds them in a fixed order (results do not depend on timing).
+#include <algorithm>
+
+#include "mq_common.h"
+#include "mq_internal.h"
+
+namespace mq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int BN = 128;
+constexpr int BK = 64;
+constexpr int kChunk = 8;  // groups per scale/bias load
+
+typedef __attribute__((address_space(3))) void lds_t;
+
+__device__ __forceinline__ void dma16(rsrc_t r, lds_t* dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
+}
+
+// End of a step: wait until at most N memory operations are outstanding, N
+// being the number of x DMA operations issued in this step, then sync the
+// block.  vmcnt retires in issue order and the DMAs (LDS writes) never move
+// across this asm, so every DMA of earlier steps -- in particular the next
+// step's x tile -- has landed whatever the compiler did with the register
+// loads (it may move those across the asm: they read __restrict__ memory).
+template <int N>
+__device__ __forceinline__ void step_barrier() {
+  __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int BITS>
+__device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, float b) {
+  u32x4_t o;
+  if constexpr (BITS == 4) {
+    // byte t of w0 = q[2t] | q[2t+1] << 4; the empty asm keeps two masks
+    // feeding v_cvt_f32_ubyte0..3 instead of one bit-field extract per code.
+    uint32_t lo = w0 & 0x0F0F0F0Fu, hi = (w0 >> 4) & 0x0F0F0F0Fu;
+    __asm__("" : "+v"(lo), "+v"(hi));
+    o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+    o[1] = pack_bf16x2(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+    o[2] = pack_bf16x2(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+    o[3] = pack_bf16x2(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
+    (void)w1;
+  } else {
+    o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w0), b), fmaf(s, ubyte_f32<1>(w0), b));
+    o[1] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w0), b), fmaf(s, ubyte_f32<3>(w0), b));
+    o[2] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w1), b), fmaf(s, ubyte_f32<1>(w1), b));
+    o[3] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w1), b), fmaf(s, ubyte_f32<3>(w1), b));
+  }
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+template <int BITS, int MI, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void qmms_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
+    int M, int N, int K, int tiles_n, int tiles_m, int chunks_per_split) {
+  constexpr int BM = 32 * MI;
+  constexpr int kXStage = BM * BK * 2;
+  constexpr int CB = BITS * 4;           // code bytes per lane per step
+  constexpr int NC = BITS == 4 ? 1 : 2;  // 16-byte code loads per lane per step
+  extern __shared__ u32x4_t smem[];
+  char* const lds = reinterpret_cast<char*>(smem);
+  const int l = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = l >> 5;
+
+  int blk = blockIdx.x;
+  const int tn = blk % tiles_n;
+  blk /= tiles_n;
+  const int tm = blk % tiles_m;
+  const int split = blk / tiles_m;
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int KT = K / BK;
+  const int G = K / kGroup;
+  const int c_begin = split * chunks_per_split;
+  const int c_end = min(KT / kChunk, c_begin + chunks_per_split);
+
+  const rsrc_t xrs = make_rsrc(x, (uint64_t)M * K * 2);
+  const rsrc_t wrs = make_rsrc(wq, (uint64_t)N * K * BITS / 8);
+  const rsrc_t srs = make_rsrc(scales, (uint64_t)N * G * 2);
+  const rsrc_t brs = make_rsrc(biases, (uint64_t)N * G * 2);
+
+  // x DMA: op i of wave w fills rows (4i + w)*8 .. +7 (1 KiB); lane l writes
+  // physical chunk l % 8 of row l / 8, logical chunk (l % 8) ^ ((row >> 1) & 7).
+  // Rows past M lie beyond the descriptor and read as zeros.
+  uint32_t xoff[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int row = (i * 4 + wave) * 8 + (l >> 3);
+    xoff[i] = (uint32_t)((m0 + row) * K + (((l & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
+  }
+  // This lane's column; columns past N lie beyond the descriptors (zeros).
+  const int n = n0 + wave * 32 + (l & 31);
+  const uint32_t coff = (uint32_t)n * (uint32_t)(K * BITS / 8) + h * CB;
+  const uint32_t soff = (uint32_t)n * (uint32_t)G * 2;
+  // A fragment: row 32i + l % 32, logical chunk 4h + ks at (4h + ks) ^ f(row).
+  const uint32_t aoff = (uint32_t)((l & 31) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
+
+  auto dma_x = [&](int kt, int stage) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+      dma16(xrs, (lds_t*)(lds + stage * kXStage + (i * 4 + wave) * 1024), xoff[i] + kt * (BK * 2));
+  };
+  auto load_codes = [&](u32x4_t (&cw)[NC], int kt) {
+#pragma unroll
+    for (int p = 0; p < NC; ++p) cw[p] = buf_load16(wrs, coff + kt * (BK * BITS / 8) + p * 16);
+  };
+
+  f32x16_t acc[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
+
+  // ---- prologue ----
+  const int kt0 = c_begin * kChunk;
+  u32x4_t sv = buf_load16(srs, soff + c_begin * 16), bv = buf_load16(brs, soff + c_begin * 16);
+  u32x4_t cw[2][NC];
+  load_codes(cw[0], kt0);
+  dma_x(kt0, 0);
+  dma_x(kt0 + 1, 1);
+  step_barrier<MI>();
+
+  int st = 0;
+  for (int c = c_begin; c < c_end; ++c) {
+    u32x4_t svn, bvn;
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int kt = c * kChunk + u;
+      if (u == 0) {
+        svn = buf_load16(srs, soff + (c + 1) * 16);
+        bvn = buf_load16(brs, soff + (c + 1) * 16);
+      }
+      load_codes(cw[(u + 1) & 1], kt + 1);
+      dma_x(kt + 2, st == 0 ? 2 : st - 1);
+
+      const float s = bf16_bits_to_f32((sv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
+      const float b = bf16_bits_to_f32((bv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
+      const uint32_t xa = st * kXStage + aoff;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8_t a[MI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          a[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ (ks << 4)) + i * 4096);
+        const u32x4_t& q = cw[u & 1][BITS == 4 ? 0 : ks >> 1];
+        bf16x8_t bq;
+        if constexpr (BITS == 4) bq = dequant8<4>(q[ks], 0u, s, b);
+        else bq = dequant8<8>(q[(ks & 1) * 2], q[(ks & 1) * 2 + 1], s, b);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bq, acc[i], 0, 0, 0);
+      }
+      step_barrier<MI>();
+      st = st == 2 ? 0 : st + 1;
+    }
+    sv = svn;
+    bv = bvn;
+  }
+  // Prefetches past the split's range must land before the LDS is released.
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue: D[m][n], lane holds column l % 32, rows 8(v/4) + 4(l/32) + v%4 ----
+  if (n >= N) return;
+  const float add = (!PARTIAL && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
+      if (m < M) {
+        if constexpr (PARTIAL)
+          partial[((int64_t)split * M + m) * N + n] = acc[i][v];
+        else
+          y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][v] + add);
+      }
+    }
+  }
+}
+
+// y[m, n] = bf16(sum over splits of partial[s, m, n] (in split order) + bias[n])
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ partial, int S,
+                                                     const uint16_t* __restrict__ bias,
+                                                     uint16_t* __restrict__ y, int64_t MN, int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  float acc = 0.f;
+  for (int s = 0; s < S; ++s) acc += partial[s * MN + i];
+  if (bias) acc += bf16_bits_to_f32(bias[i % N]);
+  y[i] = (uint16_t)f32_to_bf16_bits(acc);
+}
+
+struct Plan {
+  int mi, tiles_n, tiles_m, splits, chunks_per_split;
+};
+
+Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
+  Plan p;
+  p.mi = M <= 32 ? 1 : M <= 64 ? 2 : 4;
+  p.tiles_n = (int)((N + BN - 1) / BN);
+  p.tiles_m = (int)((M + 32 * p.mi - 1) / (32 * p.mi));
+  const int chunks = (int)(K / (BK * kChunk));
+  const int64_t base = (int64_t)p.tiles_n * p.tiles_m;
+  int64_t splits = 1;
+  if (can_split && base < 256) {
+    // Aim for one block per CU (256 CUs); a split keeps >= 2 chunks, and the
+    // partial sums (written once, read once) stay under half the weight bytes.
+    const int64_t weight_bytes = N * K * bits / 8;
+    splits = std::min<int64_t>({(256 + base - 1) / base, chunks / 2,
+                                weight_bytes / (16 * M * N)});
+  }
+  if (splits < 1) splits = 1;
+  p.chunks_per_split = (int)((chunks + splits - 1) / splits);
+  p.splits = (chunks + p.chunks_per_split - 1) / p.chunks_per_split;
+  return p;
+}
+
+template <int BITS, int MI, bool PARTIAL>
+hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+               const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
+               int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
+  const int lds = 3 * 32 * MI * BK * 2;
+  const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
+  hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL>), grid, dim3(kThreads), lds, stream, x, wq,
+                     scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
+                     p.tiles_m, p.chunks_per_split);
+  return hipGetLastError();
+}
+
+template <int BITS, bool PARTIAL>
+hipError_t run_mi(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                  const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
+                  int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
+  switch (p.mi) {
+    case 1: return run<BITS, 1, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
+    case 2: return run<BITS, 2, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
+    default: return run<BITS, 4, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
+  }
+}
+
+}  // namespace
+
+bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits) {
+  const int64_t lim = (int64_t)1 << 31;
+  // whole 8-group chunks; 32-bit offsets with room for the tiles' overhang
+  return K % (BK * kChunk) == 0 && M >= 1 && (M + 128) * K * 2 < lim &&
+         (N + BN) * K * bits / 8 < lim && (N + BN) * (K / kGroup) * 2 < lim;
+}
+
+size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits) {
+  const Plan p = plan(M, N, K, bits, true);
+  return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+}
+
+hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  if (M == 0 || N == 0) return hipSuccess;
+  Plan p = plan(M, N, K, bits, true);
+  if (p.splits > 1 && (!workspace || workspace_bytes < (size_t)p.splits * M * N * sizeof(float)))
+    p = plan(M, N, K, bits, false);
+  if (p.splits == 1)
+    return bits == 4 ? run_mi<4, false>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream)
+                     : run_mi<8, false>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+  float* part = static_cast<float*>(workspace);
+  hipError_t e = bits == 4
+                     ? run_mi<4, true>(x, wq, scales, biases, bias, y, part, M, N, K, p, stream)
+                     : run_mi<8, true>(x, wq, scales, biases, bias, y, part, M, N, K, p, stream);
+  if (e != hipSuccess) return e;
+  const int64_t MN = M * N;
+  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream, part,
+                     p.splits, bias, y, MN, (int)N);
+  return hipGetLastError();
+}
+
+}  // namespace mq

@@ -24,13 +24,14 @@ HEADER = os.path.join(ROOT, "include", "mq.h")
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mq_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mq_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_abi():
     assert declared_functions() == sorted([
         "mq_version", "mq_last_error", "mq_quantize", "mq_dequantize", "mq_embedding_lookup",
-        "mq_quantized_matmul", "mq_gather_qmm"])
+        "mq_quantized_matmul", "mq_quantized_matmul_workspace", "mq_quantized_matmul_ws",
+        "mq_gather_qmm"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -43,6 +44,21 @@ def test_library_exports_every_declared_symbol(mq):
 
 def _L(mq):
     return mq._lib.lib()
+
+
+def test_workspace_query(mq):
+    """Workspace sizes are pure host arithmetic: float32 partials for split-K
+    shapes (few columns, long K), none for wide or GEMV shapes."""
+    L = _L(mq)
+    q = L.mq_quantized_matmul_workspace
+    down = q(64, 3584, 18944, 64, 4)          # 28 column tiles: K is split
+    assert down > 0 and down % (64 * 3584 * 4) == 0
+    assert q(128, 18944, 3584, 64, 4) == 0    # 148 column tiles: no split
+    assert q(1, 3584, 18944, 64, 4) == 0      # GEMV
+    assert q(4096, 3584, 18944, 64, 4) == 0   # large-M kernels
+    assert q(64, 3584, 18944, 64, 3) == 0     # unsupported bits
+    assert q(64, 3584, 18900, 64, 4) == 0     # K not a group multiple
+    assert q(0, 3584, 18944, 64, 4) == 0
 
 
 def test_capi_invalid_and_unsupported_codes(mq):
