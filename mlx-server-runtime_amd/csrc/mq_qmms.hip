@@ -11,13 +11,15 @@
 // wave) and an M tile of 32*MI rows (MI = 1, 2, 4), and walks K in steps of
 // one quantization group:
 // * x tiles (32*MI rows x 64) are copied HBM -> LDS by buffer_load_dwordx4
-//   ... lds two steps ahead into three stages, rows of 128 bytes with the
+//   ... lds three steps ahead into four stages, rows of 128 bytes with the
 //   16-byte chunk index XOR-ed with (row >> 1) & 7.
 // * For v_mfma_f32_32x32x16_bf16's B operand lane l holds column l % 32 and,
 //   in k-slice ks, the 8 codes k = 32h + 8ks .. +7 of its half h = l / 32
 //   (A reads x with the same k order), so a lane's codes for a step are one
-//   contiguous 16-byte (4-bit) or 32-byte (8-bit) load, issued a step ahead
-//   and dequantized (fma(s, q, b), one bfloat16 rounding) in registers.
+//   contiguous 16-byte (4-bit) or 32-byte (8-bit) load, issued four steps
+//   ahead (a GEMV-sized M has little work per step, so the loads in flight
+//   must cover the memory latency) and dequantized (fma(s, q, b), one
+//   bfloat16 rounding) in registers.
 // * Scales and biases come 8 groups at a time (16 bytes per column and
 //   array), a chunk ahead.
 // When the N x M tiles alone cannot fill the GPU (few columns, long K: the
@@ -35,7 +37,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int BN = 128;
 constexpr int BK = 64;
-constexpr int kChunk = 8;  // groups per scale/bias load
+constexpr int kChunk = 8;     // groups per scale/bias load
+constexpr int kPrefetch = 4;  // steps of codes in flight per lane (divides kChunk)
+constexpr int kStages = 4;    // x stages: the DMA runs 3 steps ahead
 
 typedef __attribute__((address_space(3))) void lds_t;
 
@@ -44,11 +48,12 @@ __device__ __forceinline__ void dma16(rsrc_t r, lds_t* dst, uint32_t voff) {
 }
 
 // End of a step: wait until at most N memory operations are outstanding, N
-// being the number of x DMA operations issued in this step, then sync the
-// block.  vmcnt retires in issue order and the DMAs (LDS writes) never move
-// across this asm, so every DMA of earlier steps -- in particular the next
-// step's x tile -- has landed whatever the compiler did with the register
-// loads (it may move those across the asm: they read __restrict__ memory).
+// being the number of x DMA operations issued in this step and the one
+// before, then sync the block.  vmcnt retires in issue order and the DMAs
+// (LDS writes) never move across this asm, so every older DMA -- in
+// particular the next step's x tile -- has landed whatever the compiler did
+// with the register loads (it may move those across the asm: they read
+// __restrict__ memory).
 template <int N>
 __device__ __forceinline__ void step_barrier() {
   __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
@@ -140,16 +145,18 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
 
-  // ---- prologue ----
+  // ---- prologue: codes of the first kPrefetch steps, x of the first 3 ----
   const int kt0 = c_begin * kChunk;
   u32x4_t sv = buf_load16(srs, soff + c_begin * 16), bv = buf_load16(brs, soff + c_begin * 16);
-  u32x4_t cw[2][NC];
-  load_codes(cw[0], kt0);
+  u32x4_t cw[kPrefetch][NC];
+#pragma unroll
+  for (int p = 0; p < kPrefetch; ++p) load_codes(cw[p], kt0 + p);
   dma_x(kt0, 0);
   dma_x(kt0 + 1, 1);
-  step_barrier<MI>();
+  dma_x(kt0 + 2, 2);
+  step_barrier<2 * MI>();
 
-  int st = 0;
+  int st = 0;  // stage of the current step's x tile
   for (int c = c_begin; c < c_end; ++c) {
     u32x4_t svn, bvn;
 #pragma unroll
@@ -159,28 +166,30 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
         svn = buf_load16(srs, soff + (c + 1) * 16);
         bvn = buf_load16(brs, soff + (c + 1) * 16);
       }
-      load_codes(cw[(u + 1) & 1], kt + 1);
-      dma_x(kt + 2, st == 0 ? 2 : st - 1);
+      dma_x(kt + 3, (st + 3) & 3);
 
       const float s = bf16_bits_to_f32((sv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
       const float b = bf16_bits_to_f32((bv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
       const uint32_t xa = st * kXStage + aoff;
+      u32x4_t (&q)[NC] = cw[u % kPrefetch];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         bf16x8_t a[MI];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
           a[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ (ks << 4)) + i * 4096);
-        const u32x4_t& q = cw[u & 1][BITS == 4 ? 0 : ks >> 1];
+        const u32x4_t& w = q[BITS == 4 ? 0 : ks >> 1];
         bf16x8_t bq;
-        if constexpr (BITS == 4) bq = dequant8<4>(q[ks], 0u, s, b);
-        else bq = dequant8<8>(q[(ks & 1) * 2], q[(ks & 1) * 2 + 1], s, b);
+        if constexpr (BITS == 4) bq = dequant8<4>(w[ks], 0u, s, b);
+        else bq = dequant8<8>(w[(ks & 1) * 2], w[(ks & 1) * 2 + 1], s, b);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
           acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bq, acc[i], 0, 0, 0);
       }
-      step_barrier<MI>();
-      st = st == 2 ? 0 : st + 1;
+      // refill the slot just consumed with the codes kPrefetch steps ahead
+      load_codes(q, kt + kPrefetch);
+      step_barrier<2 * MI>();
+      st = (st + 1) & 3;
     }
     sv = svn;
     bv = bvn;
@@ -230,11 +239,14 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   const int chunks = (int)(K / (BK * kChunk));
   const int64_t base = (int64_t)p.tiles_n * p.tiles_m;
   int64_t splits = 1;
-  if (can_split && base < 256) {
-    // Aim for one block per CU (256 CUs); a split keeps >= 2 chunks, and the
-    // partial sums (written once, read once) stay under half the weight bytes.
+  // Blocks wanted: 4 per CU (256 CUs) for one 32-row M tile, fewer for
+  // taller tiles, which carry more work per step.
+  const int64_t want = 1024 / p.mi;
+  if (can_split && base < want) {
+    // The partial sums (written once, read once) stay under half the weight
+    // bytes.
     const int64_t weight_bytes = N * K * bits / 8;
-    splits = std::min<int64_t>({(256 + base - 1) / base, chunks / 2,
+    splits = std::min<int64_t>({(want + base - 1) / base, chunks,
                                 weight_bytes / (16 * M * N)});
   }
   if (splits < 1) splits = 1;
@@ -247,7 +259,7 @@ template <int BITS, int MI, bool PARTIAL>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
-  const int lds = 3 * 32 * MI * BK * 2;
+  const int lds = kStages * 32 * MI * BK * 2;
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
   hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL>), grid, dim3(kThreads), lds, stream, x, wq,
                      scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
