@@ -35,6 +35,10 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kQmvLdsBudget = 48 * 1024;
+// Scale + bias DMA operations per wave: 2 arrays of ceil((RPB*G + GP) / 2)
+// words, at most 16 64-word operations each (RPB*G <= 2048 entries: a block
+// owns at most 256 * 8 chunks), over 4 waves.
+constexpr int kSbOpsPerWave = 8;
 
 // Opaque register constants: the mask in an SGPR and the bfloat16 magic in a
 // VGPR let ((w >> s) & mask) | magic select v_and_or_b32 (gfx9 VOP3 encodings
@@ -48,11 +52,14 @@ struct Nibble {
   __device__ __forceinline__ uint32_t pair(uint32_t w) const { return (w & mask) | magic; }
 };
 
-template <int BITS, int TPR, int R, int S, int MT, int XU, bool SBW>
+template <int BITS, int TPR, int R, int S, int MT, int XU>
+// The input pointers are deliberately not __restrict__: with it the compiler
+// may move their loads across the inline-asm barriers below (it proves the
+// asm cannot touch restrict memory), which breaks the issue order the waits
+// rely on.
 __global__ __launch_bounds__(kBlock) void qmv_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
+    const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+    const uint16_t* bias, uint16_t* y, int M, int N, int K,
     const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, int64_t E,
     int64_t x_batches) {
   constexpr int EPC = 128 / BITS;      // elements per 16-byte chunk
@@ -108,19 +115,35 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
     const bool real = m < M && u < C * UPC;
     xr[k] = buf_load16(xrs, real ? (uint32_t)(m * K + u * 8) * 2 : kOutOfRange);
   }
-  // SBW (G % 4 == 0): 4 groups per 8-byte load, one per thread; else 16-bit loads.
-  u32x2_t sv[4], bv[4];
-  if constexpr (SBW) {
-    sv[0] = buf_load8(srs, threadIdx.x * 8);
-    bv[0] = buf_load8(brs, threadIdx.x * 8);
-  } else {
+  // Scales and biases go straight to LDS (buffer_load ... lds, 4 bytes per
+  // lane) and are waited for only before the epilogue: under the weight
+  // traffic of the whole grid they arrive late, and the dot products do not
+  // need them.  Entries past the block's rows read as zeros.
+  u32x4_t* xl = smem;
+  float* xsum = reinterpret_cast<float*>(smem + MT * CP * UPC);
+  uint16_t* sl = reinterpret_cast<uint16_t*>(xsum + MT * CP);  // [RPB*G + GP] scales
+  const int sb_words = (RPB * G + GP + 1) / 2;                 // 32-bit words per array
+  uint16_t* bl = sl + 2 * ((sb_words + 63) / 64 * 64);          // biases, same layout
+  {
+    // A fixed number of operations per wave (the largest any shape needs;
+    // extra ones repeat the last), so the compiler's wait for x above counts
+    // exactly: x was issued before these and the weights.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
+    const int ops = (sb_words + 63) / 64;  // wave-wide 4-byte DMA operations per array
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      sv[k][0] = buf_load2(srs, (threadIdx.x + k * kBlock) * 2);
-      bv[k][0] = buf_load2(brs, (threadIdx.x + k * kBlock) * 2);
+    for (int q = 0; q < kSbOpsPerWave; ++q) {
+      const int o = min(wave + q * (kBlock / 64), 2 * ops - 1);
+      const bool is_b = o >= ops;
+      const int oo = is_b ? o - ops : o;
+      uint16_t* dst = (is_b ? bl : sl) + oo * 128;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_b ? brs : srs,
+                                               (__attribute__((address_space(3))) void*)dst, 4,
+                                               (uint32_t)(oo * 64 + ln) * 4, 0, 0, 0);
     }
   }
-  __asm__ volatile("" ::: "memory");  // keep the weight loads after these
+  // Keep the weight loads after these: vmcnt retires in issue order, so x and
+  // the scales must be issued first for their waits not to wait for weights.
+  __asm__ volatile("" ::: "memory");
 
   u32x4_t wv[S][R];
 #pragma unroll
@@ -129,11 +152,8 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
     for (int r = 0; r < R; ++r)  // chunks past the row end are multiplied by zero x
       wv[j][r] = buf_load16<kBufNT>(wrs, (uint32_t)(((slot * R + r) * C + lane + j * TPR) * 16));
 
-  // ---- 2. LDS: x as [m][slot j][unit h][lane] (4-bit pair-permuted), chunk
-  // sums [m][chunk], (scale | bias << 16) as [row][group]; zeros past the row.
-  u32x4_t* xl = smem;
-  float* xsum = reinterpret_cast<float*>(smem + MT * CP * UPC);
-  uint32_t* sb = reinterpret_cast<uint32_t*>(xsum + MT * CP);
+  // ---- 2. LDS: x as [m][slot j][unit h][lane] (4-bit pair-permuted) and
+  // chunk sums [m][chunk]; zeros past the row.
 #pragma unroll
   for (int k = 0; k < XU; ++k) {
     const int i = threadIdx.x + k * kBlock;
@@ -157,30 +177,6 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
       if (h == 0) xsum[m * CP + c] = s8;
     }
   }
-  if constexpr (SBW) {
-    const int i = threadIdx.x * 4;
-    if (i < RPB * G) {  // entries past rows_here were read as zeros
-      const int rl = i / G, g = i - rl * G;
-      *reinterpret_cast<u32x4_t*>(sb + rl * GP + g) =
-          u32x4_t{(sv[0][0] & 0xffffu) | (bv[0][0] << 16), (sv[0][0] >> 16) | (bv[0][0] & 0xffff0000u),
-                  (sv[0][1] & 0xffffu) | (bv[0][1] << 16), (sv[0][1] >> 16) | (bv[0][1] & 0xffff0000u)};
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = threadIdx.x + k * kBlock;
-      if (i < RPB * G) {
-        const int rl = i / G;
-        sb[rl * GP + (i - rl * G)] = sv[k][0] | (bv[k][0] << 16);
-      }
-    }
-  }
-  if (GP > G) {
-    for (int i = threadIdx.x; i < RPB * (GP - G); i += kBlock) {  // padded groups read as 0
-      const int rl = i / (GP - G);
-      sb[rl * GP + G + (i - rl * (GP - G))] = 0u;
-    }
-  }
   lds_barrier();
 
   // ---- 3. contract ----
@@ -193,21 +189,20 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
 
   const u32x4_t* xlane = xl + lane;
   const float* xslane = xsum + lane;
-  const uint32_t* sblane = sb + slot * R * GP + lane / CPG;
+  // Straight-line over all S chunks and MT rows so that the wait before chunk
+  // j covers chunks <= j only: rows m >= M are zeros in LDS; chunks past NJ
+  // (only when S > NJ) read a valid chunk and are masked out.
+  float dsum[S][R][MT];
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    if (j >= NJ) break;  // uniform
+    const int jj = j < NJ ? j : NJ - 1;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      if (m >= M) break;
-      const float xs = xslane[m * CP + j * TPR];
       u32x4_t xv[UPC];
 #pragma unroll
-      for (int h = 0; h < UPC; ++h) xv[h] = xlane[((m * NJ + j) * UPC + h) * TPR];
+      for (int h = 0; h < UPC; ++h) xv[h] = xlane[((m * NJ + jj) * UPC + h) * TPR];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint32_t sbv = sblane[r * GP + j * (TPR / CPG)];
-        const float sc = lo_bf16(sbv), bi = hi_bf16(sbv);
         float d = 0.f;
         if constexpr (BITS == 4) {
 #pragma unroll
@@ -218,8 +213,6 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
             d = dot2_bf16(nib.pair(wd >> 8), xv[wi][2], d);
             d = dot2_bf16(nib.pair(wd >> 12), xv[wi][3], d);
           }
-          acc[r][m] = fmaf(sc, d, acc[r][m]);
-          acc[r][m] = fmaf(fmaf(-128.f, sc, bi), xs, acc[r][m]);
         } else {
 #pragma unroll
           for (int wi = 0; wi < 4; ++wi) {
@@ -229,7 +222,32 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
             d = dot2_bf16(pack_bf16x2(ubyte_f32<2>(wd), ubyte_f32<3>(wd)),
                           xv[wi / 2][(wi % 2) * 2 + 1], d);
           }
-          acc[r][m] = fmaf(sc, d, acc[r][m]);
+        }
+        dsum[j][r][m] = j < NJ ? d : 0.f;
+        __asm__ volatile("" ::"v"(dsum[j][r][m]));  // computed before the barrier below
+      }
+    }
+  }
+  // The scale/bias DMA of every wave has landed (nothing else is in flight).
+  __asm__ volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  const uint16_t* slane = sl + slot * R * G + lane / CPG;
+  const uint16_t* blane = bl + slot * R * G + lane / CPG;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    if (j >= NJ) break;  // uniform; past the dot products
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m >= M) break;
+      const float xs = xslane[m * CP + j * TPR];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float sc = bf16_bits_to_f32(slane[r * G + j * (TPR / CPG)]);
+        const float bi = bf16_bits_to_f32(blane[r * G + j * (TPR / CPG)]);
+        if constexpr (BITS == 4) {
+          acc[r][m] = fmaf(sc, dsum[j][r][m], acc[r][m]);
+          acc[r][m] = fmaf(fmaf(-128.f, sc, bi), xs, acc[r][m]);
+        } else {
+          acc[r][m] = fmaf(sc, dsum[j][r][m], acc[r][m]);
           acc[r][m] = fmaf(bi, xs, acc[r][m]);
         }
       }
@@ -284,24 +302,27 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   }
 }
 
-template <int BITS, int TPR>
-size_t lds_bytes(int64_t MT, int64_t K, int R) {
-  constexpr int EPC = 128 / BITS;
-  const int64_t C = K / EPC;
-  const int64_t CP = (C + TPR - 1) / TPR * TPR;
-  const int64_t GP = CP / (kGroup / EPC);
-  const int64_t RPB = (kBlock / TPR) * R;
-  return (size_t)(MT * CP * 16 * (EPC / 8) + MT * CP * 4 + RPB * GP * 4);
+// x units, chunk sums, then scales and biases: each array ceil((RPB*G + GP) / 2)
+// words rounded up to whole 64-lane DMA operations.
+int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R) {
+  const int epc = 128 / bits;
+  const int64_t C = K / epc;
+  const int64_t CP = (C + tpr - 1) / tpr * tpr;
+  const int64_t G = K / kGroup;
+  const int64_t GP = CP / (kGroup / epc);
+  const int64_t RPB = (kBlock / tpr) * R;
+  const int64_t sb_words = (RPB * G + GP + 1) / 2;
+  return MT * CP * 16 * (epc / 8) + MT * CP * 4 + 2 * ((sb_words + 63) / 64) * 256;
 }
 
-template <int BITS, int TPR, int R, int S, int MT, int XU, bool SBW>
+template <int BITS, int TPR, int R, int S, int MT, int XU>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                const GatherMap& g, hipStream_t stream) {
   const int64_t rows_per_block = (kBlock / TPR) * R;
-  const size_t lds = lds_bytes<BITS, TPR>(MT, K, R);
+  const size_t lds = (size_t)lds_bytes(BITS, TPR, MT, K, R);
   const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)g.T);
-  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, SBW>), grid, dim3(kBlock), lds, stream, x,
+  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU>), grid, dim3(kBlock), lds, stream, x,
                      wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E, g.x_batches);
   return hipGetLastError();
 }
@@ -313,16 +334,9 @@ hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, cons
   constexpr int EPC = 128 / BITS;
   const int64_t CP = (K / EPC + TPR - 1) / TPR * TPR;
   const int64_t units = (MT * CP * (EPC / 8) + kBlock - 1) / kBlock;  // x units per thread
-  if ((K / kGroup) % 4 != 0) {  // scales loaded 16 bits at a time (generic row width only)
-    if constexpr (TPR == 256) {
-      if (units <= 12)
-        return run<BITS, TPR, R, S, MT, 12, false>(x, wq, s, b, bias, y, M, N, K, g, stream);
-    }
-    return hipErrorInvalidValue;  // pick_tpr routes these shapes to TPR 256
-  }
-  if (units <= 2) return run<BITS, TPR, R, S, MT, 2, true>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (units <= 4) return run<BITS, TPR, R, S, MT, 4, true>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (units <= 12) return run<BITS, TPR, R, S, MT, 12, true>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 2) return run<BITS, TPR, R, S, MT, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 4) return run<BITS, TPR, R, S, MT, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 12) return run<BITS, TPR, R, S, MT, 12>(x, wq, s, b, bias, y, M, N, K, g, stream);
   return hipErrorInvalidValue;  // excluded by qmv_fits
 }
 
@@ -339,10 +353,8 @@ hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, cons
 constexpr int kTprs[] = {16, 32, 64, 128, 256};
 
 // Lanes per row: the narrowest whose lanes own at most 8 chunks each, widened
-// while the grid has fewer than 2 blocks per CU.  Rows whose group count is
-// not a multiple of 4 use the generic 256-lane width.
-int pick_tpr(int64_t C, int64_t N, int64_t T, int64_t G) {
-  if (G % 4 != 0) return 256;  // 16-bit scale loads: one generic configuration
+// while the grid has fewer than 2 blocks per CU.
+int pick_tpr(int64_t C, int64_t N, int64_t T) {
   int pick = 0;
   while (pick < 4 && (C + kTprs[pick] - 1) / kTprs[pick] > 8) ++pick;
   while (pick < 4 && ((N * kTprs[pick]) / kBlock) * T < 512) ++pick;
@@ -355,7 +367,7 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
                     const GatherMap& g, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t C = K / EPC;
-  const int tpr = pick_tpr(C, N, g.T, K / kGroup);
+  const int tpr = pick_tpr(C, N, g.T);
   const int slots = (int)((C + tpr - 1) / tpr);
   switch (tpr) {
     case 16:
@@ -383,12 +395,12 @@ bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T) {
   const int epc = 128 / bits;
   const int64_t C = K / epc;
   if (C > 8 * 256) return false;  // more chunks than one block's lanes can own
-  const int tpr = pick_tpr(C, N, T, K / kGroup);
+  if ((K / kGroup) % 2 != 0) return false;  // scales move in 4-byte words
+  const int tpr = pick_tpr(C, N, T);
   const int64_t CP = (C + tpr - 1) / tpr * tpr;
   const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-  const int64_t lds = mt * CP * 2 * epc + mt * CP * 4 + (kBlock / tpr) * (CP / (kGroup / epc)) * 4;
   const int64_t units = mt * CP * (epc / 8);  // x units staged per block
-  return lds <= kQmvLdsBudget && units <= 12 * kBlock;
+  return lds_bytes(bits, tpr, mt, K, 1) <= kQmvLdsBudget && units <= 12 * kBlock;
 }
 
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
