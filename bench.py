@@ -11,7 +11,9 @@ launch stream bracket the timed region.
 
 Also reported: the full sweep M in {1,16,128,2048,8192} x (K,N) in
 {(3584,18944), (18944,3584), (3584,4608)} x bits {4,8} (GB/s, TFLOP/s and the
-fraction of the bounding roofline), and the CPU baseline: the oracle's float32
+fraction of the bounding roofline; for 4-bit M >= 128 also a dense bf16 GEMM
+of the same shape through torch.matmul, for scale), and the CPU baseline: the
+oracle's float32
 restatement of MLX's CPU quantized_matmul loop on the host cores, on a bounded
 sample of the headline workload.
 
@@ -146,6 +148,10 @@ def sweep(mq, torch):
             wbytes = alg_bytes(0, N, K, bits)
             n_rep = max(1, min(16, math.ceil(640e6 / wbytes)))
             reps = make_replicas(mq, torch, N, K, bits, n_rep, seed=100)
+            wdt = None
+            if bits == 4:
+                wq0, s0, b0 = reps[0]
+                wdt = mq.dequantize(wq0, s0, b0, 64, bits).t().contiguous()  # [K, N] bf16
             for M in (1, 16, 128, 2048, 8192):
                 gen = torch.Generator(device="cuda:0").manual_seed(1)
                 x = torch.randn(M, K, generator=gen, device="cuda:0").to(torch.bfloat16)
@@ -162,11 +168,18 @@ def sweep(mq, torch):
                 tfl = flops / (ms * 1e-3) / 1e12
                 bound = "hbm" if flops / by < RIDGE else "mfma"
                 frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tfl / BF16_PEAK_TFLOPS
-                rows.append({"M": M, "K": K, "N": N, "bits": bits, "us": round(ms * 1e3, 2),
-                             "GBps": round(gbs, 1), "TFLOPs": round(tfl, 2), "bound": bound,
-                             "frac": round(frac, 4)})
+                row = {"M": M, "K": K, "N": N, "bits": bits, "us": round(ms * 1e3, 2),
+                       "GBps": round(gbs, 1), "TFLOPs": round(tfl, 2), "bound": bound,
+                       "frac": round(frac, 4)}
+                if bits == 4 and M >= 128:
+                    # For scale: a dense bf16 GEMM of the same shape through
+                    # torch.matmul (hipBLASLt) on the dequantized weights.
+                    dms, _ = time_graph(torch, lambda i, x=x: torch.matmul(x, wdt), n_launch, warmup=2)
+                    row["dense_bf16_us"] = round(dms * 1e3, 2)
+                    row["dense_bf16_TFLOPs"] = round(flops / (dms * 1e-3) / 1e12, 2)
+                rows.append(row)
                 del x
-            del reps
+            del reps, wdt
             torch.cuda.empty_cache()
     return rows
 

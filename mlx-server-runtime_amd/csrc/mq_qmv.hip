@@ -149,8 +149,9 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
 #pragma unroll
   for (int j = 0; j < S; ++j)
 #pragma unroll
-    for (int r = 0; r < R; ++r)  // chunks past the row end are multiplied by zero x
-      wv[j][r] = buf_load16<kBufNT>(wrs, (uint32_t)(((slot * R + r) * C + lane + j * TPR) * 16));
+    for (int r = 0; r < R; ++r)  // slots past NJ read nothing (out of range: zeros)
+      wv[j][r] = buf_load16<kBufNT>(
+          wrs, j < NJ ? (uint32_t)(((slot * R + r) * C + lane + j * TPR) * 16) : kOutOfRange);
 
   // ---- 2. LDS: x as [m][slot j][unit h][lane] (4-bit pair-permuted) and
   // chunk sums [m][chunk]; zeros past the row.
@@ -370,19 +371,29 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
   const int tpr = pick_tpr(C, N, g.T);
   const int slots = (int)((C + tpr - 1) / tpr);
   switch (tpr) {
+    // Chunk slots per lane S: the instantiated S >= NJ closest to it (slots
+    // past NJ cost arithmetic on zeros, not memory traffic).  The S values
+    // cover the model shapes exactly: K = 3584 / 18944 / 2048 / 768 at 4 and
+    // 8 bits.
     case 16:
       if (slots <= 2) return run_mt<BITS, 16, 1, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 3) return run_mt<BITS, 16, 1, 3>(x, wq, s, b, bias, y, M, N, K, g, stream);
       if (slots <= 4) return run_mt<BITS, 16, 1, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots == 7) return run_mt<BITS, 16, 1, 7>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 7) return run_mt<BITS, 16, 1, 7>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return run_mt<BITS, 16, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
     case 32:
-      if (slots == 7) return run_mt<BITS, 32, 1, 7>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 4) return run_mt<BITS, 32, 1, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 7) return run_mt<BITS, 32, 1, 7>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return run_mt<BITS, 32, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
     case 64:
+      if (slots <= 5) return run_mt<BITS, 64, 1, 5>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return run_mt<BITS, 64, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
     case 128:
+      if (slots <= 5) return run_mt<BITS, 128, 1, 5>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return run_mt<BITS, 128, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
     default:
+      if (slots <= 3) return run_mt<BITS, 256, 1, 3>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 5) return run_mt<BITS, 256, 1, 5>(x, wq, s, b, bias, y, M, N, K, g, stream);
       if (slots <= 8) return run_mt<BITS, 256, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return hipErrorInvalidValue;  // excluded by qmv_fits
   }
