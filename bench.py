@@ -120,7 +120,7 @@ def cpu_baseline(args, orc, wq, s, b, x, N, K, bits):
         orc.qmm_f32(x, wq, s, b, 64, bits, threads=threads)
         calls += 1
         el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or calls >= 2000:
+        if el >= args.cpu_seconds or calls >= 20000:
             break
     gbs = alg_bytes(1, N, K, bits) * calls / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
