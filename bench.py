@@ -12,12 +12,14 @@ launch stream bracket the timed region.
 Also reported: the full sweep M in {1,16,128,2048,8192} x (K,N) in
 {(3584,18944), (18944,3584), (3584,4608)} x bits {4,8} (GB/s, TFLOP/s and the
 fraction of the bounding roofline; for 4-bit M >= 128 also a dense bf16 GEMM
-of the same shape through torch.matmul, for scale), and the CPU baseline: the
+of the same shape through torch.matmul, for scale), greedy decode of the
+Qwen2.5-7B-shaped 4-bit model (random init) at batch 1 and 32 in tokens/s,
+and the CPU baseline: the
 oracle's float32
 restatement of MLX's CPU quantized_matmul loop on the host cores, on a bounded
 sample of the headline workload.
 
-    python bench.py [--steps 256] [--warmup 32] [--no-sweep] [--no-cpu]
+    python bench.py [--steps 256] [--warmup 32] [--no-sweep] [--no-cpu] [--no-decode]
     python bench.py --profile   # eager launches + a copy kernel, for rocprofv3
 """
 
@@ -55,6 +57,7 @@ def parse():
     ap.add_argument("--replicas", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", action="store_true",
                     help="eager launches of the headline kernel + a 128 MiB copy (rocprofv3 runs)")
@@ -139,6 +142,42 @@ def hbm_floor(torch, nbytes: int, count: int = 16):
     del srcs, dst
     return {"kind": "device copy (torch copy_), one launch per step", "bytes": 4 * half,
             "us": round(ms * 1e3, 3), "GBps": round(4 * half / (ms * 1e-3) / 1e9, 1)}
+
+
+def decode_bench(torch, batch: int, prompt_len: int, n_new: int):
+    """Greedy decode of the Qwen2.5-7B-shaped 4-bit model (random init): prefill
+    `prompt_len` tokens per row, then `n_new` graph-replayed decode steps."""
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config.qwen25_7b(bits=4)
+    model = q2.Qwen2Model.random(cfg, seed=0, device="cuda:0")
+    gen = torch.Generator(device="cuda:0").manual_seed(2)
+    prompt = torch.randint(0, cfg.vocab_size, (batch, prompt_len), generator=gen, device="cuda:0")
+    model.generate(prompt[:, :16], 4)  # warm-up: kernels, graph capture path
+    torch.cuda.synchronize()
+    cache = q2.KVCache(cfg, batch, prompt_len + n_new, "cuda:0")
+    t0 = time.perf_counter()
+    logits = model.prefill(prompt, cache)
+    torch.cuda.synchronize()
+    t_prefill = time.perf_counter() - t0
+    cos, sin = q2.rope_tables(cfg, prompt_len + n_new, "cuda:0")
+    tok = logits.float().argmax(-1)
+    pos = torch.full((batch,), prompt_len, dtype=torch.int64, device="cuda:0")
+    g, static_logits = model._capture(lambda: model.decode_step(tok, pos, cache, cos, sin))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(n_new):
+        g.replay()
+        tok.copy_(static_logits.float().argmax(-1))
+        pos.add_(1)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    del model, cache, g
+    torch.cuda.empty_cache()
+    return {"batch": batch, "prompt_len": prompt_len, "new_tokens": n_new,
+            "decode_tok_s": round(batch * n_new / (ms * 1e-3), 1),
+            "ms_per_decode_step": round(ms / n_new, 3),
+            "prefill_tok_s": round(batch * prompt_len / t_prefill, 1)}
 
 
 def sweep(mq, torch):
@@ -261,6 +300,10 @@ def main():
                      "traffic": traffic},
     }
     line["hbm_floor"] = hbm_floor(torch, by)
+    if not args.no_decode:
+        # Qwen2.5-7B shape, 4-bit: batch 1 (512-token prompt, 128 tokens) and
+        # batch 32 (1024-token prompts, 256 tokens).
+        line["decode"] = [decode_bench(torch, 1, 512, 128), decode_bench(torch, 32, 1024, 256)]
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
     if not args.no_cpu:

@@ -1,0 +1,87 @@
+"""Float32 reference of the Qwen2 decoder for the GPU parity tests.
+
+Test infrastructure only.  It restates the reference's graph
+(python/mlx_worker/native_mlx/models/qwen2.py:47-227) in float32 end to end
+-- RMSNorm, linears, RoPE, attention, SiLU, residuals -- on the *dequantized*
+weights of a mlx-server-runtime_amd.qwen2.Qwen2Model, so it differs from the
+model under test only by the latter's bfloat16 activations.  Weights are
+dequantized with the library's dequantize (bit-exact with the oracle, checked
+by test_gpu_parity.py) one layer at a time.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def _deq(mq, ql) -> torch.Tensor:
+    return mq.dequantize(ql.wq, ql.scales, ql.biases, ql.group_size, ql.bits).float()
+
+
+def _linear(mq, ql, x):
+    y = x @ _deq(mq, ql).t()
+    if ql.bias is not None:
+        y = y + ql.bias.float()
+    return y
+
+
+def _rms(x, w, eps):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+
+def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = False
+                     ) -> torch.Tensor:
+    """tokens [B, S] (positions 0..S-1) -> float32 logits [B, S, vocab], causal.
+
+    With bf16_activations, values are rounded to bfloat16 wherever the model
+    under test stores bfloat16 (norm outputs, linear outputs, the residual
+    stream, the SiLU product), isolating the kernels' own arithmetic."""
+    from importlib import import_module
+
+    r = (lambda t: t.to(torch.bfloat16).float()) if bf16_activations else (lambda t: t)
+
+    q2 = import_module("mlx-server-runtime_amd.qwen2")
+    c = model.cfg
+    B, S = tokens.shape
+    d, nh, nkv = c.head_dim, c.num_attention_heads, c.num_key_value_heads
+    cos, sin = q2.rope_tables(c, S, tokens.device)
+    causal = torch.full((S, S), float("-inf"), device=tokens.device).triu(1)
+    e = model.embed
+    h = mq.embedding_lookup(tokens.reshape(-1).to(torch.int32), e.wq, e.scales, e.biases,
+                            e.group_size, e.bits).float().reshape(B, S, c.hidden_size)
+    for layer in model.layers:
+        x = r(_rms(h, layer.input_norm, c.rms_norm_eps))
+        qkv = r(_linear(mq, layer.qkv, x))
+        q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
+        q = q2.apply_rope(q.reshape(B, S, nh, d).transpose(1, 2), cos, sin)
+        k = q2.apply_rope(k.reshape(B, S, nkv, d).transpose(1, 2), cos, sin)
+        v = v.reshape(B, S, nkv, d).transpose(1, 2)
+        rep = nh // nkv
+        k, v = k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1)
+        s = q @ k.transpose(-1, -2).contiguous() * d ** -0.5 + causal
+        a = r((torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B, S, nh * d))
+        h = r(h + r(_linear(mq, layer.o, a)))
+        x = r(_rms(h, layer.post_norm, c.rms_norm_eps))
+        gu = r(_linear(mq, layer.gate_up, x))
+        act = r(r(F.silu(gu[..., :c.intermediate_size])) * gu[..., c.intermediate_size:])
+        h = r(h + r(_linear(mq, layer.down, act)))
+    h = r(_rms(h, model.final_norm, c.rms_norm_eps))
+    head = model.lm_head if model.lm_head is not None else model.embed
+    return h @ _deq(mq, head).t()
+
+
+def greedy_agreement(ref_logits: torch.Tensor, prompt_len: int, tokens: torch.Tensor):
+    """Teacher-forced check of greedy tokens.  tokens [B, n] were generated after
+    a prompt of prompt_len; ref_logits [B, prompt_len + n - 1 (or more), vocab].
+    Returns (matches, n, worst), worst = the largest reference margin
+    (ref top logit - ref logit of the chosen token) over mismatches, in units
+    of that position's logit standard deviation (0 if all match)."""
+    B, n = tokens.shape
+    lg = ref_logits[:, prompt_len - 1:prompt_len - 1 + n]
+    top = lg.argmax(-1)
+    match = (top == tokens)
+    chosen = lg.gather(-1, tokens.unsqueeze(-1)).squeeze(-1)
+    margin = (lg.max(-1).values - chosen) / lg.std(-1)
+    worst = float(margin[~match].max()) if (~match).any() else 0.0
+    return int(match.sum()), B * n, worst
