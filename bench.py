@@ -144,22 +144,42 @@ def hbm_floor(torch, nbytes: int, count: int = 16):
             "us": round(ms * 1e3, 3), "GBps": round(4 * half / (ms * 1e-3) / 1e9, 1)}
 
 
-def decode_bench(torch, batch: int, prompt_len: int, n_new: int):
+def _weight_bytes(model) -> int:
+    """Bytes of every quantized linear a decode step streams (not the embedding,
+    of which a step reads one row per sequence)."""
+    total = 0
+    linears = [ql for layer in model.layers
+               for ql in (layer.qkv, layer.o, layer.gate_up, layer.down)]
+    linears.append(model.lm_head if model.lm_head is not None else model.embed)
+    for ql in linears:
+        for t in (ql.wq, ql.scales, ql.biases, ql.bias):
+            if t is not None:
+                total += t.numel() * t.element_size()
+    return total
+
+
+def decode_bench(torch, batch: int, prompt_len: int, n_new: int, prefix_len: int = 0):
     """Greedy decode of the Qwen2.5-7B-shaped 4-bit model (random init): prefill
-    `prompt_len` tokens per row, then `n_new` graph-replayed decode steps."""
+    `prompt_len` tokens per row (the first `prefix_len` shared by every row and
+    prefilled once into shared pages), then `n_new` graph-replayed decode steps
+    over the paged KV cache (pages of 16)."""
     q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
     cfg = q2.Qwen2Config.qwen25_7b(bits=4)
     model = q2.Qwen2Model.random(cfg, seed=0, device="cuda:0")
     gen = torch.Generator(device="cuda:0").manual_seed(2)
     prompt = torch.randint(0, cfg.vocab_size, (batch, prompt_len), generator=gen, device="cuda:0")
-    model.generate(prompt[:, :16], 4)  # warm-up: kernels, graph capture path
+    if prefix_len:
+        prompt[:, :prefix_len] = prompt[0, :prefix_len]
+    model.generate(prompt[:, :32], 4, prefix_len=16 if prefix_len else 0)  # warm-up
     torch.cuda.synchronize()
-    cache = q2.KVCache(cfg, batch, prompt_len + n_new, "cuda:0")
+    cache = model.new_cache(batch, prompt_len + n_new, prefix_len)
     t0 = time.perf_counter()
-    logits = model.prefill(prompt, cache)
+    if prefix_len:
+        model.prefill(prompt[:1, :prefix_len], cache, rows=torch.zeros(1, dtype=torch.long))
+    logits = model.prefill(prompt[:, prefix_len:], cache, start=prefix_len)
     torch.cuda.synchronize()
     t_prefill = time.perf_counter() - t0
-    cos, sin = q2.rope_tables(cfg, prompt_len + n_new, "cuda:0")
+    cos, sin = q2.rope_tables(cfg, cache.capacity, "cuda:0")
     tok = logits.float().argmax(-1)
     pos = torch.full((batch,), prompt_len, dtype=torch.int64, device="cuda:0")
     g, static_logits = model._capture(lambda: model.decode_step(tok, pos, cache, cos, sin))
@@ -172,12 +192,20 @@ def decode_bench(torch, batch: int, prompt_len: int, n_new: int):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
+    wbytes = _weight_bytes(model)
+    kv_per_pos = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
+    step_bytes = wbytes + batch * kv_per_pos * (prompt_len + (n_new + 1) / 2)
+    step_s = ms * 1e-3 / n_new
     del model, cache, g
     torch.cuda.empty_cache()
-    return {"batch": batch, "prompt_len": prompt_len, "new_tokens": n_new,
+    return {"batch": batch, "prompt_len": prompt_len, "shared_prefix": prefix_len,
+            "new_tokens": n_new, "page_size": 16,
             "decode_tok_s": round(batch * n_new / (ms * 1e-3), 1),
             "ms_per_decode_step": round(ms / n_new, 3),
-            "prefill_tok_s": round(batch * prompt_len / t_prefill, 1)}
+            "hbm_bytes_per_step": int(step_bytes),
+            "hbm_frac": round(step_bytes / step_s / 8e12, 3),
+            "prefill_ms": round(t_prefill * 1e3, 1),
+            "prefill_tok_s": round(batch * (prompt_len - prefix_len) / t_prefill, 1)}
 
 
 def sweep(mq, torch):
@@ -303,7 +331,8 @@ def main():
     if not args.no_decode:
         # Qwen2.5-7B shape, 4-bit: batch 1 (512-token prompt, 128 tokens) and
         # batch 32 (1024-token prompts, 256 tokens).
-        line["decode"] = [decode_bench(torch, 1, 512, 128), decode_bench(torch, 32, 1024, 256)]
+        line["decode"] = [decode_bench(torch, 1, 512, 128),
+                          decode_bench(torch, 32, 1024, 256, prefix_len=256)]
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
     if not args.no_cpu:

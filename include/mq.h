@@ -131,6 +131,79 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
                   int group_size, int bits, int transpose, int sorted_indices,
                   hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Decoder step around the quantized linears (models/qwen2.py:47-163).
+ * KV pages are the reference's layout (cache.py:686-695): per layer,
+ * bfloat16 [num_pages, page_size, n_kv_heads, head_dim].  A sequence's pages
+ * are its row of an int32 page table [batch, pages_per_seq]; position p of
+ * sequence b lives in slot page_table[b][p / page_size] * page_size +
+ * p % page_size (cache.py:459-471).  positions int64 [batch] holds each
+ * sequence's current token position, in device memory so that a captured
+ * step replays with new values.  Out-of-range positions and page ids are
+ * clamped into the cache (wrong values, never an access outside it).
+ * ------------------------------------------------------------------------ */
+
+/*
+ * nn.RMSNorm (models/qwen2.py:140-145,187; mx.fast.rms_norm), optionally
+ * fused with the residual add before it (qwen2.py:158-163):
+ *   h = residual ? bf16(x + residual) : x      (h stored to residual_out)
+ *   out = bf16(h * rsqrt(mean(h^2) + eps) * weight)   float32 arithmetic
+ * x, residual, residual_out, out bfloat16 [rows, dim]; weight bfloat16 [dim];
+ * residual and residual_out are both NULL or both set.  dim % 8 == 0, <= 8192.
+ */
+int mq_rms_norm(const mq_bf16* x, const mq_bf16* residual, mq_bf16* residual_out,
+                const mq_bf16* weight, mq_bf16* out, int64_t rows, int64_t dim, float eps,
+                hipStream_t stream);
+
+/*
+ * mx.fast.rope(traditional=False) of q and k for one token per sequence
+ * (models/qwen2.py:93-108) and the paged KV append of that token
+ * (cache.py:485-520, PagedBatchReservation.stage_layer):
+ *   qkv bfloat16 [batch, (n_heads + 2 n_kv_heads) * head_dim] (q | k | v heads),
+ *   q_out bfloat16 [batch, n_heads, head_dim] = rope(q),
+ *   k_pages[slot] = rope(k), v_pages[slot] = v        (bfloat16)
+ * cos/sin float32 [positions, head_dim / 2], row p = cos/sin(p * theta^(-2i/d)).
+ */
+int mq_rope_kv_append(const mq_bf16* qkv, const int64_t* positions, const int32_t* page_table,
+                      int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                      const float* cos_table, const float* sin_table, mq_bf16* q_out,
+                      mq_bf16* k_pages, mq_bf16* v_pages, int64_t batch, int n_heads,
+                      int n_kv_heads, int head_dim, hipStream_t stream);
+
+/*
+ * Workspace, in bytes, for mq_paged_decode_attention (0 = unsupported shape).
+ * Positions are split over blocks; each split leaves float32 partials.  No
+ * counterpart in the reference (MLX allocates temporaries internally).
+ */
+size_t mq_paged_decode_attention_workspace(int64_t batch, int n_heads, int n_kv_heads,
+                                           int head_dim, int64_t pages_per_seq,
+                                           int64_t page_size);
+
+/*
+ * Attention of one query token per sequence over its cached positions
+ * 0..positions[b] (causal, grouped-query: query head h reads KV head
+ * h / (n_heads / n_kv_heads)).  Replaces PagedLayerAttentionContext
+ * .append_and_attend's gather of the pages into dense rows plus
+ * mx.fast.scaled_dot_product_attention for a decode step
+ * (attention.py:206-298).  q bfloat16 [batch, n_heads, head_dim];
+ * out bfloat16 [batch, n_heads * head_dim]; float32 softmax and accumulation.
+ * head_dim 64 or 128, 1-8 query heads per KV head.
+ */
+int mq_paged_decode_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq_bf16* v_pages,
+                              const int32_t* page_table, int64_t pages_per_seq, int64_t page_size,
+                              int64_t num_pages, const int64_t* positions, int64_t batch,
+                              int n_heads, int n_kv_heads, int head_dim, float scale,
+                              void* workspace, size_t workspace_bytes, mq_bf16* out,
+                              hipStream_t stream);
+
+/*
+ * silu(gate) * up of the MLP (models/qwen2.py:43-44,132-133) on the fused
+ * gate|up projection: gate_up bfloat16 [rows, 2 * inter], out bfloat16
+ * [rows, inter] = bf16(bf16(gate * sigmoid(gate)) * up).  inter % 8 == 0.
+ */
+int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inter,
+                hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,13 +7,15 @@ Import by its directory name (it contains dashes):
     y = mq.quantized_matmul(x, wq, scales, biases, transpose=True, group_size=64, bits=4)
 
 Ops (mx.* names): quantize, dequantize, quantized_matmul, gather_qmm,
-embedding_lookup.  Modules (mlx.nn names): nn.QuantizedLinear,
+embedding_lookup.  Decoder-step ops (decode_ops): rms_norm, rope_kv_append,
+paged_decode_attention, silu_mul over a PagedKV cache; qwen2: the Qwen2-shaped
+decoder with greedy decode.  Modules (mlx.nn names): nn.QuantizedLinear,
 nn.QuantizedEmbedding, nn.QuantizedSwitchLinear, nn.SwitchGLU, nn.quantize.
 Everything runs in the gfx950 HIP library libmi355q.so built by build_lib.py;
 there is no CPU fallback.
 """
 
-from . import _lib, core, nn
+from . import _lib, core, decode_ops, nn
 from .core import dequantize, embedding_lookup, gather_qmm, quantize, quantized_matmul
 
 
@@ -26,5 +28,5 @@ def version() -> tuple[int, int]:
     return v >> 16, v & 0xFFFF
 
 
-__all__ = ["core", "nn", "quantize", "dequantize", "quantized_matmul", "gather_qmm",
+__all__ = ["core", "decode_ops", "nn", "quantize", "dequantize", "quantized_matmul", "gather_qmm",
            "embedding_lookup", "library_path", "version"]

@@ -253,4 +253,116 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
   return hip_status(e, op);
 }
 
+int mq_rms_norm(const mq_bf16* x, const mq_bf16* residual, mq_bf16* residual_out,
+                const mq_bf16* weight, mq_bf16* out, int64_t rows, int64_t dim, float eps,
+                hipStream_t stream) {
+  const char* op = "rms_norm";
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (!mq::rmsnorm_supported(dim))
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] dim=%lld is not supported (a multiple of 8, <= 8192).",
+                op, (long long)dim);
+  if (!residual != !residual_out)
+    return fail(MQ_ERR_INVALID, "[%s] residual and residual_out go together.", op);
+  if (rows == 0) return ok();
+  if (!x || !weight || !out) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) ||
+      (residual && (!aligned16(residual) || !aligned16(residual_out))))
+    return fail(MQ_ERR_INVALID, "[%s] every buffer must be 16-byte aligned.", op);
+  return hip_status(
+      mq::launch_rmsnorm(x, residual, residual_out, weight, out, rows, dim, eps, stream), op);
+}
+
+namespace {
+int check_pages(const char* op, int64_t B, int n_heads, int n_kv_heads, int64_t pages_per_seq,
+                int64_t page_size, int64_t num_pages) {
+  if (int rc = check_dim(op, "batch", B)) return rc;
+  if (B > 65535) return fail(MQ_ERR_UNSUPPORTED, "[%s] batch=%lld > 65535.", op, (long long)B);
+  if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads)
+    return fail(MQ_ERR_INVALID, "[%s] query heads must be divisible by KV heads (%d, %d).", op,
+                n_heads, n_kv_heads);
+  if (page_size <= 0 || pages_per_seq <= 0 || num_pages <= 0)
+    return fail(MQ_ERR_INVALID, "[%s] page_size, pages_per_seq and num_pages must be > 0.", op);
+  if (pages_per_seq * page_size >= kMaxDim || num_pages >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] the page table is too large.", op);
+  return MQ_OK;
+}
+}  // namespace
+
+int mq_rope_kv_append(const mq_bf16* qkv, const int64_t* positions, const int32_t* page_table,
+                      int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                      const float* cos_table, const float* sin_table, mq_bf16* q_out,
+                      mq_bf16* k_pages, mq_bf16* v_pages, int64_t batch, int n_heads,
+                      int n_kv_heads, int head_dim, hipStream_t stream) {
+  const char* op = "rope_kv_append";
+  if (int rc = check_pages(op, batch, n_heads, n_kv_heads, pages_per_seq, page_size, num_pages))
+    return rc;
+  if (head_dim <= 0 || head_dim % 2)
+    return fail(MQ_ERR_INVALID, "[%s] head_dim=%d must be even.", op, head_dim);
+  if (batch == 0) return ok();
+  if (!qkv || !positions || !page_table || !cos_table || !sin_table || !q_out || !k_pages ||
+      !v_pages)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  return hip_status(mq::launch_rope_append(qkv, positions, page_table, pages_per_seq, page_size,
+                                           num_pages, cos_table, sin_table, q_out, k_pages,
+                                           v_pages, batch, n_heads, n_kv_heads, head_dim, stream),
+                    op);
+}
+
+size_t mq_paged_decode_attention_workspace(int64_t batch, int n_heads, int n_kv_heads,
+                                           int head_dim, int64_t pages_per_seq,
+                                           int64_t page_size) {
+  if (batch <= 0 || batch > 65535 || pages_per_seq <= 0 || page_size <= 0 ||
+      pages_per_seq * page_size >= kMaxDim ||
+      !mq::decode_attention_supported(n_heads, n_kv_heads, head_dim))
+    return 0;
+  return mq::decode_attention_workspace(batch, n_heads, n_kv_heads, head_dim,
+                                        pages_per_seq * page_size);
+}
+
+int mq_paged_decode_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq_bf16* v_pages,
+                              const int32_t* page_table, int64_t pages_per_seq, int64_t page_size,
+                              int64_t num_pages, const int64_t* positions, int64_t batch,
+                              int n_heads, int n_kv_heads, int head_dim, float scale,
+                              void* workspace, size_t workspace_bytes, mq_bf16* out,
+                              hipStream_t stream) {
+  const char* op = "paged_decode_attention";
+  if (int rc = check_pages(op, batch, n_heads, n_kv_heads, pages_per_seq, page_size, num_pages))
+    return rc;
+  if (!mq::decode_attention_supported(n_heads, n_kv_heads, head_dim))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] head_dim=%d with %d query heads per KV head is not supported (64 or 128; "
+                "1-8).",
+                op, head_dim, n_kv_heads > 0 ? n_heads / n_kv_heads : 0);
+  if (batch == 0) return ok();
+  const size_t need = mq::decode_attention_workspace(batch, n_heads, n_kv_heads, head_dim,
+                                                     pages_per_seq * page_size);
+  if (!workspace || workspace_bytes < need)
+    return fail(MQ_ERR_INVALID, "[%s] the workspace needs %zu bytes, got %zu.", op, need,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!q || !k_pages || !v_pages || !page_table || !positions || !out)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(q) || !aligned16(k_pages) || !aligned16(v_pages) || !aligned16(workspace))
+    return fail(MQ_ERR_INVALID, "[%s] q, the pages and the workspace must be 16-byte aligned.",
+                op);
+  return hip_status(mq::launch_decode_attention(q, k_pages, v_pages, page_table, pages_per_seq,
+                                                page_size, num_pages, positions, batch, n_heads,
+                                                n_kv_heads, head_dim, scale,
+                                                static_cast<float*>(workspace), out, stream),
+                    op);
+}
+
+int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inter,
+                hipStream_t stream) {
+  const char* op = "silu_mul";
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (inter <= 0 || inter % 8 || inter >= kMaxDim)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] the width %lld must be a positive multiple of 8.", op,
+                (long long)inter);
+  if (rows == 0) return ok();
+  if (!gate_up || !out) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(gate_up) || !aligned16(out))
+    return fail(MQ_ERR_INVALID, "[%s] buffers must be 16-byte aligned.", op);
+  return hip_status(mq::launch_silu_mul(gate_up, out, rows, inter, stream), op);
+}
+
 }  // extern "C"

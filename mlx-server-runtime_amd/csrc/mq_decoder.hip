@@ -1,0 +1,455 @@
+// Decoder-step kernels around the quantized linears of the Qwen2 graph
+// (python/mlx_worker/native_mlx/models/qwen2.py:47-163), fused so that a
+// decode step is a handful of launches instead of dozens of elementwise ones:
+//
+//  * rmsnorm_kernel      nn.RMSNorm (qwen2.py:140-145, 187), optionally after
+//                        the residual add before it (qwen2.py:158-163):
+//                        h = bf16(x + r) is written out, and
+//                        out = bf16(h * rsqrt(mean(h^2) + eps) * w) in float32;
+//  * rope_append_kernel  mx.fast.rope (traditional=False) on q and k of one
+//                        token per sequence (qwen2.py:93-108), q rounded to
+//                        bfloat16, k and v written into the paged cache at the
+//                        token's slot (cache.py:459-471: slot = page * page_size
+//                        + pos % page_size);
+//  * attn_split_kernel   attention of one query token per sequence over its
+//    + attn_combine      cached positions 0..pos (attention.py:206-298: the
+//                        reference gathers the pages into dense rows and calls
+//                        scaled_dot_product_attention).  Query heads that share
+//                        a KV head are scored together; the positions are split
+//                        over blocks (partial max, sum and weighted values per
+//                        split, float32), and a second kernel combines them;
+//  * silu_mul_kernel     silu(gate) * up (qwen2.py:43-44, 132-133).
+//
+// KV pages are the reference's layout (cache.py:686-695): per layer
+// bfloat16 [num_pages, page_size, kv_heads, head_dim]; a sequence's pages are
+// listed in its row of an int32 page table [B, pages_per_seq].
+#include <algorithm>
+
+#include "mq_common.h"
+#include "mq_internal.h"
+
+namespace mq {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float bf16r(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+// Positions and page ids come from device memory the host does not inspect;
+// clamping them keeps a bad table or position inside the cache (wrong values
+// in, wrong values out, never an access outside the buffers).
+__device__ __forceinline__ int64_t clamp_index(int64_t v, int64_t n) {
+  return v < 0 ? 0 : (v >= n ? n - 1 : v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// One row per block, 8 elements (16 bytes) per thread and pass; dim <= 8192.
+constexpr int kNormMaxUnits = 4;
+
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res_in,
+    uint16_t* __restrict__ res_out, const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+    int dim, float eps) {
+  __shared__ float red[kThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int units = dim / 8;
+  u32x4_t hv[kNormMaxUnits];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormMaxUnits; ++k) {
+    const int u = threadIdx.x + k * kThreads;
+    if (u < units) {
+      u32x4_t v = reinterpret_cast<const u32x4_t*>(x + row * dim)[u];
+      if (res_in) {
+        const u32x4_t r = reinterpret_cast<const u32x4_t*>(res_in + row * dim)[u];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          v[q] = pack_bf16x2(lo_bf16(v[q]) + lo_bf16(r[q]), hi_bf16(v[q]) + hi_bf16(r[q]));
+        reinterpret_cast<u32x4_t*>(res_out + row * dim)[u] = v;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = lo_bf16(v[q]), b = hi_bf16(v[q]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+      hv[k] = v;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; ++i) ss += red[i];
+  const float inv = rsqrtf(ss / (float)dim + eps);
+#pragma unroll
+  for (int k = 0; k < kNormMaxUnits; ++k) {
+    const int u = threadIdx.x + k * kThreads;
+    if (u < units) {
+      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(w)[u];
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pack_bf16x2(lo_bf16(hv[k][q]) * inv * lo_bf16(wv[q]),
+                           hi_bf16(hv[k][q]) * inv * hi_bf16(wv[q]));
+      reinterpret_cast<u32x4_t*>(out + row * dim)[u] = o;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- RoPE + append
+// One sequence per block.  qkv bf16 [B, (nh + 2 nkv) * d] (q heads, k heads,
+// v heads); q_out bf16 [B, nh, d]; cos/sin float32 [positions, d/2].
+__global__ __launch_bounds__(kThreads) void rope_append_kernel(
+    const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
+    const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages,
+    int nh, int nkv, int d) {
+  const int64_t b = blockIdx.x;
+  const int64_t p = clamp_index(pos[b], (int64_t)pages_per_seq * page_size);
+  const int64_t page = clamp_index(page_table[b * pages_per_seq + p / page_size], num_pages);
+  const int64_t slot = page * page_size + p % page_size;
+  const int half = d / 2;
+  const uint16_t* row = qkv + b * (int64_t)(nh + 2 * nkv) * d;
+  const float* cs = cos_t + p * half;
+  const float* sn = sin_t + p * half;
+  for (int e = threadIdx.x; e < (nh + nkv) * half; e += kThreads) {
+    const int hh = e / half, i = e % half;
+    const float x1 = bf16_bits_to_f32(row[hh * d + i]);
+    const float x2 = bf16_bits_to_f32(row[hh * d + i + half]);
+    const uint16_t o1 = (uint16_t)f32_to_bf16_bits(x1 * cs[i] - x2 * sn[i]);
+    const uint16_t o2 = (uint16_t)f32_to_bf16_bits(x2 * cs[i] + x1 * sn[i]);
+    uint16_t* dst = hh < nh ? q_out + (b * nh + hh) * (int64_t)d
+                            : k_pages + (slot * nkv + (hh - nh)) * (int64_t)d;
+    dst[i] = o1;
+    dst[i + half] = o2;
+  }
+  for (int e = threadIdx.x; e < nkv * d; e += kThreads)
+    v_pages[slot * nkv * (int64_t)d + e] = row[(nh + nkv) * d + e];
+}
+
+// ---------------------------------------------------------------- attention
+// Grid (splits, nkv, B), 256 threads.  A cached row of one KV head (D bf16,
+// 2D bytes) is read by D/8 lanes, 16 bytes each, so a block covers
+// 2048/D positions per pass (16 at D = 128, 32 at D = 64).  REP query heads
+// share the KV head.
+//
+// Partials per (b, kv head, split), float32: m[REP], s[REP], acc[REP][D].
+constexpr int kMaxChunk = 512;
+
+template <int REP, int D>
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pages,
+    const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table,
+    int pages_per_seq, int page_size, int num_pages, const int64_t* __restrict__ pos,
+    float* __restrict__ part, int nkv, int chunk, float scale) {
+  constexpr int LANES = D / 8;               // lanes per cached row
+  constexpr int PASS = kThreads / LANES;     // positions per pass
+  __shared__ float sc[REP][kMaxChunk];
+  __shared__ float stat[2][REP];
+  __shared__ float red[kThreads / 64][REP][D];
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int splits = gridDim.x;
+  const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
+  const int l0 = split * chunk;
+  const int n = min(L - l0, chunk);
+  float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
+  float* ps = pm + REP;
+  float* pa = ps + REP;
+  if (n <= 0) {  // past the sequence: an empty split
+    if (threadIdx.x < REP) {
+      pm[threadIdx.x] = -INFINITY;
+      ps[threadIdx.x] = 0.f;
+    }
+    return;
+  }
+  const int sub = threadIdx.x % LANES, slot_in_pass = threadIdx.x / LANES;
+  const int nh = nkv * REP;
+  const int32_t* table = page_table + b * pages_per_seq;
+
+  // this lane's 8 dims of every query head, pre-scaled
+  float qr[REP][8];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const u32x4_t v =
+        reinterpret_cast<const u32x4_t*>(q + (b * nh + kvh * REP + r) * (int64_t)D)[sub];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      qr[r][2 * t] = lo_bf16(v[t]) * scale;
+      qr[r][2 * t + 1] = hi_bf16(v[t]) * scale;
+    }
+  }
+
+  // scores
+  for (int i0 = 0; i0 < n; i0 += PASS) {
+    const int i = i0 + slot_in_pass;
+    const int l = l0 + min(i, n - 1);
+    const int64_t slot = clamp_index(table[l / page_size], num_pages) * page_size + l % page_size;
+    const u32x4_t kv =
+        reinterpret_cast<const u32x4_t*>(k_pages + (slot * nkv + kvh) * (int64_t)D)[sub];
+    float kf[8];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      kf[2 * t] = lo_bf16(kv[t]);
+      kf[2 * t + 1] = hi_bf16(kv[t]);
+    }
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      float dot = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) dot = fmaf(qr[r][t], kf[t], dot);
+      dot = dpp_group_sum<LANES>(dot);
+      if (sub == 0 && i < n) sc[r][i] = dot;
+    }
+  }
+  __syncthreads();
+
+  // softmax numerators: wave w takes heads w, w + 4, ...
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int r = wave; r < REP; r += kThreads / 64) {
+    float m = -INFINITY;
+    for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[r][i]);
+    m = wave_max(m);
+    float s = 0.f;
+    for (int i = lane; i < n; i += 64) {
+      const float e = __expf(sc[r][i] - m);
+      sc[r][i] = e;
+      s += e;
+    }
+    s = wave_sum(s);
+    if (lane == 0) {
+      stat[0][r] = m;
+      stat[1][r] = s;
+    }
+  }
+  __syncthreads();
+
+  // weighted values: the same lane mapping as the scores
+  float acc[REP][8];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
+  for (int i0 = 0; i0 < n; i0 += PASS) {
+    const int i = i0 + slot_in_pass;
+    if (i < n) {
+      const int l = l0 + i;
+      const int64_t slot = clamp_index(table[l / page_size], num_pages) * page_size + l % page_size;
+      const u32x4_t vv =
+          reinterpret_cast<const u32x4_t*>(v_pages + (slot * nkv + kvh) * (int64_t)D)[sub];
+      float vf[8];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        vf[2 * t] = lo_bf16(vv[t]);
+        vf[2 * t + 1] = hi_bf16(vv[t]);
+      }
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const float p = sc[r][i];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(p, vf[t], acc[r][t]);
+      }
+    }
+  }
+  // sum the position slots of each wave (lanes sub, sub + LANES, ...), then
+  // the 4 waves through LDS
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      float v = acc[r][t];
+#pragma unroll
+      for (int off = LANES; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+      if (lane < LANES) red[wave][r][8 * sub + t] = v;
+    }
+  __syncthreads();
+  for (int e = threadIdx.x; e < REP * D; e += kThreads) {
+    const int r = e / D, dd = e % D;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) v += red[w][r][dd];
+    pa[e] = v;
+  }
+  if (threadIdx.x < REP) {
+    pm[threadIdx.x] = stat[0][threadIdx.x];
+    ps[threadIdx.x] = stat[1][threadIdx.x];
+  }
+}
+
+// Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over splits of the
+// partials rescaled to the common max, divided by the rescaled sum.
+template <int REP, int D>
+__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ part,
+                                                         uint16_t* __restrict__ out, int nkv,
+                                                         int splits) {
+  const int hh = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int kvh = hh / REP, r = hh % REP;
+  const int dd = threadIdx.x;
+  const float* base = part + (b * nkv + kvh) * splits * (int64_t)(REP * (D + 2));
+  float m = -INFINITY;
+  for (int s = 0; s < splits; ++s) m = fmaxf(m, base[s * (REP * (D + 2)) + r]);
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    const float* p = base + s * (REP * (D + 2));
+    const float ms = p[r];
+    if (ms == -INFINITY) continue;
+    const float f = __expf(ms - m);
+    den = fmaf(f, p[REP + r], den);
+    num = fmaf(f, p[2 * REP + r * D + dd], num);
+  }
+  out[(b * nkv * REP + hh) * (int64_t)D + dd] = (uint16_t)f32_to_bf16_bits(num / den);
+}
+
+// ---------------------------------------------------------------- SiLU * up
+// gu bf16 [rows, 2 * inter] = (gate | up) -> out bf16 [rows, inter]
+//   = bf16(bf16(silu(gate)) * up)
+__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                            uint16_t* __restrict__ out,
+                                                            int64_t rows, int inter) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // 8-element unit
+  const int upr = inter / 8;
+  if (i >= rows * upr) return;
+  const int64_t r = i / upr, u = i % upr;
+  const u32x4_t g = reinterpret_cast<const u32x4_t*>(gu + r * 2 * inter)[u];
+  const u32x4_t up = reinterpret_cast<const u32x4_t*>(gu + r * 2 * inter + inter)[u];
+  u32x4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float g0 = lo_bf16(g[q]), g1 = hi_bf16(g[q]);
+    const float s0 = bf16r(g0 / (1.f + __expf(-g0))), s1 = bf16r(g1 / (1.f + __expf(-g1)));
+    o[q] = pack_bf16x2(s0 * lo_bf16(up[q]), s1 * hi_bf16(up[q]));
+  }
+  reinterpret_cast<u32x4_t*>(out + r * inter)[u] = o;
+}
+
+// Positions per split: whole passes of 32 (one or two passes of the kernel),
+// at most kMaxChunk, and enough splits for about 512 blocks over the chip.
+int attn_chunk(int64_t B, int nkv, int64_t capacity) {
+  const int64_t blocks = B * nkv;
+  int64_t splits = (512 + blocks - 1) / blocks;
+  splits = std::max<int64_t>(1, std::min<int64_t>(splits, (capacity + 31) / 32));
+  int64_t chunk = (capacity + splits - 1) / splits;
+  chunk = (chunk + 31) / 32 * 32;
+  return (int)std::min<int64_t>(chunk, kMaxChunk);
+}
+
+}  // namespace
+
+bool rmsnorm_supported(int64_t dim) {
+  return dim > 0 && dim % 8 == 0 && dim <= 8 * kThreads * kNormMaxUnits;
+}
+
+bool decode_attention_supported(int nh, int nkv, int d) {
+  return (d == 64 || d == 128) && nkv > 0 && nh % nkv == 0 && nh / nkv >= 1 && nh / nkv <= 8;
+}
+
+size_t decode_attention_workspace(int64_t B, int nh, int nkv, int d, int64_t capacity) {
+  const int rep = nh / nkv;
+  const int64_t chunk = attn_chunk(B, nkv, capacity);
+  const int64_t splits = (capacity + chunk - 1) / chunk;
+  return (size_t)(B * nkv * splits * rep * (d + 2)) * sizeof(float);
+}
+
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* res_out,
+                          const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim, float eps,
+                          hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, stream, x, res_in,
+                     res_out, w, out, (int)dim, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int32_t* page_table,
+                              int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                              const float* cos_t,
+                              const float* sin_t, uint16_t* q_out, uint16_t* k_pages,
+                              uint16_t* v_pages, int64_t B, int nh, int nkv, int d,
+                              hipStream_t stream) {
+  if (B == 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)B), dim3(kThreads), 0, stream, qkv, pos,
+                     page_table, (int)pages_per_seq, (int)page_size, (int)num_pages, cos_t, sin_t,
+                     q_out, k_pages, v_pages, nh, nkv, d);
+  return hipGetLastError();
+}
+
+namespace {
+template <int D>
+hipError_t launch_attention_d(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                              const int32_t* page_table, int pages_per_seq, int page_size,
+                              int num_pages, const int64_t* pos, int64_t B, int nh, int nkv,
+                              float scale, float* workspace, uint16_t* out, int chunk, int splits,
+                              hipStream_t stream) {
+  const dim3 grid((unsigned)splits, (unsigned)nkv, (unsigned)B);
+  const dim3 cgrid((unsigned)nh, (unsigned)B);
+#define MQ_ATTN(REP)                                                                            \
+  case REP:                                                                                     \
+    hipLaunchKernelGGL((attn_split_kernel<REP, D>), grid, dim3(kThreads), 0, stream, q,        \
+                       k_pages, v_pages, page_table, pages_per_seq, page_size, num_pages, pos,  \
+                       workspace, nkv, chunk, scale);                                           \
+    hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,    \
+                       out, nkv, splits);                                                       \
+    break;
+  switch (nh / nkv) {
+    MQ_ATTN(1)
+    MQ_ATTN(2)
+    MQ_ATTN(3)
+    MQ_ATTN(4)
+    MQ_ATTN(5)
+    MQ_ATTN(6)
+    MQ_ATTN(7)
+    MQ_ATTN(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef MQ_ATTN
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
+                                   const uint16_t* v_pages, const int32_t* page_table,
+                                   int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                                   const int64_t* pos, int64_t B, int nh, int nkv, int d,
+                                   float scale, float* workspace, uint16_t* out,
+                                   hipStream_t stream) {
+  if (B == 0) return hipSuccess;
+  const int64_t capacity = pages_per_seq * page_size;
+  const int chunk = attn_chunk(B, nkv, capacity);
+  const int splits = (int)((capacity + chunk - 1) / chunk);
+  if (d == 64)
+    return launch_attention_d<64>(q, k_pages, v_pages, page_table, (int)pages_per_seq,
+                                  (int)page_size, (int)num_pages, pos, B, nh, nkv, scale,
+                                  workspace, out, chunk, splits, stream);
+  if (d == 128)
+    return launch_attention_d<128>(q, k_pages, v_pages, page_table, (int)pages_per_seq,
+                                   (int)page_size, (int)num_pages, pos, B, nh, nkv, scale,
+                                   workspace, out, chunk, splits, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter,
+                           hipStream_t stream) {
+  const int64_t units = rows * (inter / 8);
+  if (units == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((units + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, gu, out, rows, (int)inter);
+  return hipGetLastError();
+}
+
+}  // namespace mq

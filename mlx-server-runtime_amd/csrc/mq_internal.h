@@ -74,4 +74,27 @@ hipError_t launch_gather_qmm_rows(const uint16_t* x, const int32_t* lhs, const i
                                   int64_t K, int64_t E, int64_t x_rows, int rows_per_batch,
                                   int bits, hipStream_t stream);
 
+// Decoder-step kernels (mq_decoder.hip).  KV pages: bfloat16
+// [num_pages, page_size, nkv, head_dim]; page table int32 [B, pages_per_seq];
+// pos int64 [B] is the position of each sequence's current token.
+bool rmsnorm_supported(int64_t dim);
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* res_out,
+                          const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim, float eps,
+                          hipStream_t stream);
+hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int32_t* page_table,
+                              int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                              const float* cos_t, const float* sin_t, uint16_t* q_out,
+                              uint16_t* k_pages, uint16_t* v_pages, int64_t B, int nh, int nkv,
+                              int d, hipStream_t stream);
+bool decode_attention_supported(int nh, int nkv, int d);
+size_t decode_attention_workspace(int64_t B, int nh, int nkv, int d, int64_t capacity);
+hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
+                                   const uint16_t* v_pages, const int32_t* page_table,
+                                   int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                                   const int64_t* pos, int64_t B, int nh, int nkv, int d,
+                                   float scale, float* workspace, uint16_t* out,
+                                   hipStream_t stream);
+hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter,
+                           hipStream_t stream);
+
 }  // namespace mq

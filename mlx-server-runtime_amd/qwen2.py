@@ -17,9 +17,15 @@ every linear layer and the token embedding running through libmi355q:
 Two equivalent rearrangements keep the weights MLX's and the arithmetic the
 same: q/k/v are concatenated into one quantized matrix (and gate/up into
 another) so each is one launch, which is exact because the output columns of
-a quantized matmul are independent.  Activations are bfloat16; RMSNorm, RoPE,
-the softmax and the KV cache are float32.  The decode step is captured once
-in a HIP graph and replayed per token (inputs live in static device buffers).
+a quantized matmul are independent.  Activations and the paged KV cache are
+bfloat16 (as in the reference, cache.py:659-695); RMSNorm, RoPE, the softmax
+and every accumulation are float32.  A decode step is ten launches per layer
+(QKV GEMV, RoPE + KV append, split attention + combine, o GEMV, residual add +
+RMSNorm, gate|up GEMV, SiLU * up, down GEMV, residual add + RMSNorm), captured
+once in a HIP graph and replayed per token (inputs live in static device
+buffers).  Prefill runs the same linears as GEMMs and float32 attention over
+the pages (the reference's dense-row gather, attention.py:264-298), so a
+prompt may start after a prefix already in the cache (prefix sharing).
 Weights can be random-initialised at the reference's 7B shape
 (Qwen2Config.qwen25_7b) for benchmarking.
 """
@@ -33,6 +39,8 @@ import torch
 import torch.nn.functional as F
 
 from . import core
+from .decode_ops import PagedKV, paged_decode_attention, rope_kv_append, silu_mul
+from .decode_ops import rms_norm as fused_rms_norm
 
 
 @dataclass(frozen=True)
@@ -106,13 +114,6 @@ class Layer:
     down: QLinear              # [hidden, intermediate]
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """nn.RMSNorm: float32 x * rsqrt(mean(x^2) + eps) * weight, stored in x's dtype."""
-    xf = x.float()
-    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()
-    return y.to(x.dtype)
-
-
 def rope_tables(cfg: Qwen2Config, max_len: int, device) -> tuple[torch.Tensor, torch.Tensor]:
     """cos/sin [max_len, head_dim/2] of mx.fast.rope (traditional=False, base=theta)."""
     half = cfg.head_dim // 2
@@ -127,18 +128,6 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     half = x.shape[-1] // 2
     x1, x2 = x[..., :half], x[..., half:]
     return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1)
-
-
-class KVCache:
-    """Dense float32 KV cache [layers][B, kv_heads, max_len, head_dim]."""
-
-    def __init__(self, cfg: Qwen2Config, batch: int, max_len: int, device):
-        shape = (batch, cfg.num_key_value_heads, max_len, cfg.head_dim)
-        self.k = [torch.zeros(shape, dtype=torch.float32, device=device)
-                  for _ in range(cfg.num_hidden_layers)]
-        self.v = [torch.zeros(shape, dtype=torch.float32, device=device)
-                  for _ in range(cfg.num_hidden_layers)]
-        self.max_len = max_len
 
 
 class Qwen2Model:
@@ -178,97 +167,125 @@ class Qwen2Model:
         return cls(cfg, embed, layers, final_norm, lm_head)
 
     # ------------------------------------------------------------ pieces
+    def new_cache(self, batch: int, max_len: int, prefix_len: int = 0,
+                  page_size: int = 16) -> PagedKV:
+        """Paged KV for `batch` sequences of up to max_len positions.  With
+        prefix_len > 0 (a multiple of page_size) every sequence's first
+        prefix_len positions map to the same pages: a shared prompt prefix that
+        is prefilled once (the reference's prefix-cache hit, prefix_cache.py:364)."""
+        c = self.cfg
+        dev = self.final_norm.device
+        per = -(-max_len // page_size)
+        if prefix_len % page_size or prefix_len > max_len:
+            raise ValueError(f"prefix_len {prefix_len} must be a multiple of page_size "
+                             f"{page_size} and at most max_len {max_len}")
+        shared = prefix_len // page_size
+        own = per - shared
+        table = torch.empty(batch, per, dtype=torch.int32)
+        table[:, :shared] = torch.arange(shared, dtype=torch.int32)
+        table[:, shared:] = shared + torch.arange(batch * own, dtype=torch.int32).reshape(batch, own)
+        return PagedKV(c.num_hidden_layers, shared + batch * own, page_size,
+                       c.num_key_value_heads, c.head_dim, table, dev)
+
     def _embed(self, ids: torch.Tensor) -> torch.Tensor:
         e = self.embed
         return core.embedding_lookup(ids.to(torch.int32), e.wq, e.scales, e.biases,
                                      e.group_size, e.bits)
 
-    def _logits(self, h: torch.Tensor) -> torch.Tensor:
-        h = rms_norm(h, self.final_norm, self.cfg.rms_norm_eps)
+    def _head(self, x: torch.Tensor) -> torch.Tensor:
+        """LM head on final-normed activations (untied, or the tied embedding's as_linear)."""
         if self.lm_head is None:
             e = self.embed
-            return core.quantized_matmul(h, e.wq, e.scales, e.biases, True, e.group_size, e.bits)
-        return self.lm_head(h)
+            return core.quantized_matmul(x, e.wq, e.scales, e.biases, True, e.group_size, e.bits)
+        return self.lm_head(x)
 
-    def _split_qkv(self, qkv: torch.Tensor):
-        c = self.cfg
-        d = c.head_dim
-        nq, nkv = c.num_attention_heads * d, c.num_key_value_heads * d
-        return qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
+    def _next_norm(self, li: int) -> torch.Tensor:
+        return (self.layers[li + 1].input_norm if li + 1 < len(self.layers)
+                else self.final_norm)
 
-    def _mlp(self, layer: Layer, x: torch.Tensor) -> torch.Tensor:
-        gu = layer.gate_up(x)
-        inter = self.cfg.intermediate_size
-        return layer.down(F.silu(gu[..., :inter]) * gu[..., inter:])
+    def _ffn(self, li: int, h: torch.Tensor, o: torch.Tensor):
+        """Second half of layer li after its o_proj output o: returns (x, h) where
+        h is the updated residual stream and x the next layer's normed input
+        (the final norm after the last layer)."""
+        layer, eps = self.layers[li], self.cfg.rms_norm_eps
+        x, h = fused_rms_norm(o, layer.post_norm, eps, residual=h)
+        m = layer.down(silu_mul(layer.gate_up(x)))
+        return fused_rms_norm(m, self._next_norm(li), eps, residual=h)
 
     # ------------------------------------------------------------ prefill
-    def prefill(self, ids: torch.Tensor, cache: KVCache, all_positions: bool = False
-                ) -> torch.Tensor:
-        """ids [B, T] (positions 0..T-1 of every row) -> logits [B, vocab] of position T-1
-        (or [B, T, vocab] with all_positions); fills cache positions 0..T-1."""
+    def prefill(self, ids: torch.Tensor, cache: PagedKV, start: int = 0,
+                rows: torch.Tensor | None = None, all_positions: bool = False) -> torch.Tensor:
+        """ids [B, T] at positions start..start+T-1 of cache rows `rows` (default
+        0..B-1), attending to the cached positions 0..start-1 as well ->
+        logits [B, vocab] of the last position (or [B, T, vocab] with all_positions);
+        writes K/V of the new positions into the pages."""
         c = self.cfg
         B, T = ids.shape
-        d, nh, nkv = c.head_dim, c.num_attention_heads, c.num_key_value_heads
-        cos, sin = rope_tables(c, T, ids.device)
-        causal = torch.full((T, T), float("-inf"), device=ids.device).triu(1)
-        h = self._embed(ids.reshape(-1)).reshape(B, T, c.hidden_size)
-        for li, layer in enumerate(self.layers):
-            x = rms_norm(h, layer.input_norm, c.rms_norm_eps)
-            q, k, v = self._split_qkv(layer.qkv(x))
-            q = apply_rope(q.float().reshape(B, T, nh, d).transpose(1, 2), cos, sin)
-            k = apply_rope(k.float().reshape(B, T, nkv, d).transpose(1, 2), cos, sin)
-            v = v.float().reshape(B, T, nkv, d).transpose(1, 2)
-            cache.k[li][:, :, :T] = k
-            cache.v[li][:, :, :T] = v
-            rep = nh // nkv
-            kk = k.repeat_interleave(rep, dim=1)
-            vv = v.repeat_interleave(rep, dim=1)
-            s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + causal
-            a = torch.matmul(torch.softmax(s, dim=-1), vv)
-            a = a.transpose(1, 2).reshape(B, T, nh * d).to(torch.bfloat16)
-            h = h + layer.o(a)
-            h = h + self._mlp(layer, rms_norm(h, layer.post_norm, c.rms_norm_eps))
-        return self._logits(h if all_positions else h[:, -1])
-
-    # ------------------------------------------------------------ decode
-    def decode_step(self, tok: torch.Tensor, pos: torch.Tensor, cache: KVCache,
-                    cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-        """One token per row: tok [B] int, pos [B] int64 (its position) -> logits [B, vocab].
-        Static shapes only (graph-capturable): the cache is read over max_len with a mask."""
-        c = self.cfg
-        B = tok.shape[0]
+        dev = ids.device
         d, nh, nkv = c.head_dim, c.num_attention_heads, c.num_key_value_heads
         rep = nh // nkv
-        cs, sn = cos[pos][:, None, None, :], sin[pos][:, None, None, :]  # [B,1,1,D/2]
-        idx = pos.view(B, 1, 1, 1).expand(B, nkv, 1, d)
-        keep = (torch.arange(cache.max_len, device=tok.device)[None, :] <= pos[:, None])
-        mask = torch.where(keep, 0.0, float("-inf"))[:, None, None, :]  # [B,1,1,L]
-        h = self._embed(tok)
+        S = start + T
+        rows = torch.arange(B, device=dev) if rows is None else rows.to(dev).long()
+        cos, sin = rope_tables(c, S, dev)
+        cs, sn = cos[start:], sin[start:]
+        pos = torch.arange(start, S, device=dev)
+        slots = cache.slots(rows.repeat_interleave(T), pos.repeat(B))
+        # query i (position start + i) sees keys 0..start + i
+        causal = torch.full((T, S), float("-inf"), device=dev).triu(start + 1)
+        h = self._embed(ids.reshape(-1)).reshape(B, T, c.hidden_size)
+        x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
-            x = rms_norm(h, layer.input_norm, c.rms_norm_eps)
-            q, k, v = self._split_qkv(layer.qkv(x))
-            q = apply_rope(q.float().reshape(B, nh, 1, d), cs, sn)
-            k = apply_rope(k.float().reshape(B, nkv, 1, d), cs, sn)
-            cache.k[li].scatter_(2, idx, k)
-            cache.v[li].scatter_(2, idx, v.float().reshape(B, nkv, 1, d))
-            qg = q.reshape(B, nkv, rep, d)
-            s = torch.matmul(qg, cache.k[li].transpose(-1, -2)) * (d ** -0.5) + mask
-            a = torch.matmul(torch.softmax(s, dim=-1), cache.v[li])  # [B, nkv, rep, d]
-            h = h + layer.o(a.reshape(B, nh * d).to(torch.bfloat16))
-            h = h + self._mlp(layer, rms_norm(h, layer.post_norm, c.rms_norm_eps))
-        return self._logits(h)
+            qkv = layer.qkv(x)
+            q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
+            q = apply_rope(q.float().reshape(B, T, nh, d).transpose(1, 2), cs, sn)
+            k = apply_rope(k.float().reshape(B, T, nkv, d).transpose(1, 2), cs, sn)
+            k = k.to(torch.bfloat16)
+            v = v.reshape(B, T, nkv, d).transpose(1, 2)
+            cache.write(li, slots, k.transpose(1, 2).reshape(B * T, nkv, d),
+                        v.transpose(1, 2).reshape(B * T, nkv, d))
+            if start:
+                k, v = cache.gather_rows(li, rows, S)
+            q = q.to(torch.bfloat16).float()
+            kk = k.float().repeat_interleave(rep, dim=1)
+            vv = v.float().repeat_interleave(rep, dim=1)
+            s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + causal
+            a = torch.matmul(torch.softmax(s, dim=-1), vv)
+            o = layer.o(a.transpose(1, 2).reshape(B, T, nh * d).to(torch.bfloat16))
+            x, h = self._ffn(li, h, o)
+        return self._head(x if all_positions else x[:, -1])
+
+    # ------------------------------------------------------------ decode
+    def decode_step(self, tok: torch.Tensor, pos: torch.Tensor, cache: PagedKV,
+                    cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """One token per sequence: tok [B] int, pos [B] int64 (its position, on the
+        device) -> logits [B, vocab].  Static shapes only, so it can be captured."""
+        c = self.cfg
+        d, nh = c.head_dim, c.num_attention_heads
+        h = self._embed(tok)
+        x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
+        for li, layer in enumerate(self.layers):
+            q = rope_kv_append(layer.qkv(x), pos, cache, li, cos, sin, nh)
+            a = paged_decode_attention(q, cache, li, pos, d ** -0.5)
+            x, h = self._ffn(li, h, layer.o(a))
+        return self._head(x)
 
     def generate(self, prompt: torch.Tensor, n_new: int, max_len: int | None = None,
-                 use_graph: bool = True, logits_out: list | None = None) -> torch.Tensor:
+                 use_graph: bool = True, logits_out: list | None = None,
+                 prefix_len: int = 0, page_size: int = 16) -> torch.Tensor:
         """Greedy decode: prompt [B, T] -> new tokens [B, n_new] (int64).  With
-        logits_out, each step's logits [B, vocab] are appended to it."""
+        logits_out, each step's logits [B, vocab] are appended to it.  With
+        prefix_len > 0 the rows' first prefix_len prompt tokens are equal (the
+        caller's promise): they are prefilled once, from row 0, into pages every
+        row shares, and each row prefills only its own suffix."""
         B, T = prompt.shape
         dev = prompt.device
         max_len = max_len or (T + n_new)
-        cache = KVCache(self.cfg, B, max_len, dev)
-        cos, sin = rope_tables(self.cfg, max_len, dev)
+        cache = self.new_cache(B, max_len, prefix_len, page_size)
+        cos, sin = rope_tables(self.cfg, cache.capacity, dev)
         out = torch.empty(B, n_new, dtype=torch.int64, device=dev)
-        logits = self.prefill(prompt, cache)
+        if prefix_len:
+            self.prefill(prompt[:1, :prefix_len], cache, rows=torch.zeros(1, dtype=torch.long))
+        logits = self.prefill(prompt[:, prefix_len:], cache, start=prefix_len)
         if logits_out is not None:
             logits_out.append(logits.clone())
         out[:, 0] = logits.float().argmax(-1)
@@ -305,5 +322,4 @@ class Qwen2Model:
         return g, static_logits
 
 
-__all__ = ["Qwen2Config", "Qwen2Model", "KVCache", "QLinear", "rms_norm", "rope_tables",
-           "apply_rope"]
+__all__ = ["Qwen2Config", "Qwen2Model", "QLinear", "rope_tables", "apply_rope"]

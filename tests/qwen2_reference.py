@@ -35,7 +35,8 @@ def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
     """tokens [B, S] (positions 0..S-1) -> float32 logits [B, S, vocab], causal.
 
     With bf16_activations, values are rounded to bfloat16 wherever the model
-    under test stores bfloat16 (norm outputs, linear outputs, the residual
+    under test -- and the reference's MLX graph -- stores bfloat16 (norm
+    outputs, linear outputs, q and k after RoPE, the KV cache, the residual
     stream, the SiLU product), isolating the kernels' own arithmetic."""
     from importlib import import_module
 
@@ -54,8 +55,8 @@ def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
         x = r(_rms(h, layer.input_norm, c.rms_norm_eps))
         qkv = r(_linear(mq, layer.qkv, x))
         q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
-        q = q2.apply_rope(q.reshape(B, S, nh, d).transpose(1, 2), cos, sin)
-        k = q2.apply_rope(k.reshape(B, S, nkv, d).transpose(1, 2), cos, sin)
+        q = r(q2.apply_rope(q.reshape(B, S, nh, d).transpose(1, 2), cos, sin))
+        k = r(q2.apply_rope(k.reshape(B, S, nkv, d).transpose(1, 2), cos, sin))
         v = v.reshape(B, S, nkv, d).transpose(1, 2)
         rep = nh // nkv
         k, v = k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1)

@@ -1,0 +1,250 @@
+"""Decoder-step kernels (decode_ops: rms_norm, rope_kv_append,
+paged_decode_attention, silu_mul) against float32 PyTorch restatements of the
+reference's ops on the same inputs.
+
+Bounds: outputs are bfloat16 of a float32 result, so an element may differ from
+the float32 restatement by one bfloat16 step (at most 2^-7 relative) where the
+two float32 values straddle a rounding boundary; the residual sum and the
+appended V rows are exact.
+"""
+
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    return importlib.import_module("mlx-server-runtime_amd.decode_ops")
+
+
+def _gen(seed):
+    return torch.Generator(device=DEV).manual_seed(seed)
+
+
+def _within_one_step(out, ref_f32):
+    """Every element of out (bf16) is within one bf16 step of the float32
+    reference, plus 1e-5 of the largest |ref| for results that cancel to near
+    zero (there float32 rounding order, e.g. fused multiply-adds, dominates)."""
+    ref = ref_f32.float()
+    tol = ref.abs() * 2.0 ** -7 + 1e-5 * ref.abs().max()
+    return bool(((out.float() - ref).abs() <= tol).all())
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 256), (7, 3584), (32, 3584), (3, 8192), (2, 8)])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rms_norm(ops, rows, dim, with_residual):
+    g = _gen(rows * 131 + dim)
+    x = (torch.randn(rows, dim, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(dim, generator=g, device=DEV)).to(torch.bfloat16)
+    eps = 1e-6
+    if with_residual:
+        r = torch.randn(rows, dim, generator=g, device=DEV).to(torch.bfloat16)
+        out, h = ops.rms_norm(x, w, eps, residual=r)
+        h_ref = (x.float() + r.float()).to(torch.bfloat16)
+        assert torch.equal(h, h_ref)
+    else:
+        out = ops.rms_norm(x, w, eps)
+        h_ref = x
+    hf = h_ref.float()
+    ref = hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    assert _within_one_step(out, ref)
+
+
+def test_rms_norm_batched_shape(ops):
+    x = torch.randn(2, 5, 512, generator=_gen(3), device=DEV).to(torch.bfloat16)
+    w = torch.ones(512, dtype=torch.bfloat16, device=DEV)
+    out = ops.rms_norm(x, w, 1e-5)
+    assert out.shape == x.shape
+    ref = ops.rms_norm(x.reshape(10, 512), w, 1e-5).reshape(2, 5, 512)
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 18944), (32, 18944), (5, 8), (3, 768)])
+def test_silu_mul(ops, rows, inter):
+    gu = (torch.randn(rows, 2 * inter, generator=_gen(inter + rows), device=DEV) * 4
+          ).to(torch.bfloat16)
+    out = ops.silu_mul(gu)
+    g, u = gu[:, :inter].float(), gu[:, inter:].float()
+    act = F.silu(g).to(torch.bfloat16).float()
+    assert out.shape == (rows, inter)
+    ref = (act * u).to(torch.bfloat16)
+    # bf16(silu(g)) may land on the neighbouring bf16 value (exp differs in the
+    # last float32 bits), moving the product by at most two bf16 steps
+    d = (out.float() - ref.float()).abs()
+    assert bool((d <= ref.float().abs() * 2.0 ** -6 + 1e-30).all())
+    assert (out == ref).float().mean() > 0.99
+
+
+def _rope_ref(x, cos, sin):
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], -1)
+
+
+def _tables(d, n, theta=1e6):
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config(d * 4, 8, 4, 1, 1, 8, rope_theta=theta)
+    return q2.rope_tables(cfg, n, DEV)
+
+
+def _shuffled_cache(ops, layers, B, pages_per_seq, page_size, nkv, d, seed):
+    """Every row gets its own pages in a random order across the pool."""
+    perm = torch.randperm(B * pages_per_seq, generator=torch.Generator().manual_seed(seed))
+    table = perm.reshape(B, pages_per_seq).to(torch.int32)
+    return ops.PagedKV(layers, B * pages_per_seq, page_size, nkv, d, table, DEV)
+
+
+@pytest.mark.parametrize("B,nh,nkv,d", [(1, 28, 4, 128), (5, 28, 4, 128), (3, 8, 8, 128),
+                                        (2, 32, 4, 128), (3, 14, 2, 64)])
+def test_rope_kv_append(ops, B, nh, nkv, d):
+    ps, per = 16, 5
+    cache = _shuffled_cache(ops, 2, B, per, ps, nkv, d, seed=B)
+    cos, sin = _tables(d, cache.capacity)
+    g = _gen(7 + B)
+    qkv = torch.randn(B, (nh + 2 * nkv) * d, generator=g, device=DEV).to(torch.bfloat16)
+    pos = torch.randint(0, cache.capacity, (B,), generator=g, device=DEV)
+    pos[0] = cache.capacity - 1
+    q = ops.rope_kv_append(qkv, pos, cache, 1, cos, sin, nh)
+    qf = qkv.float()
+    cs, sn = cos[pos][:, None, :], sin[pos][:, None, :]
+    q_ref = _rope_ref(qf[:, :nh * d].reshape(B, nh, d), cs, sn)
+    k_ref = _rope_ref(qf[:, nh * d:(nh + nkv) * d].reshape(B, nkv, d), cs, sn)
+    v_ref = qkv[:, (nh + nkv) * d:].reshape(B, nkv, d)
+    assert _within_one_step(q, q_ref)
+    slots = cache.slots(torch.arange(B, device=DEV), pos)
+    flat_k = cache.k[1].view(-1, nkv, d)
+    flat_v = cache.v[1].view(-1, nkv, d)
+    assert _within_one_step(flat_k[slots], k_ref)
+    assert torch.equal(flat_v[slots], v_ref)
+    # nothing else written: layer 0 untouched, and only B slots of layer 1 nonzero
+    assert not cache.k[0].any() and not cache.v[0].any()
+    assert int((flat_v.abs().sum((1, 2)) > 0).sum()) == B
+
+
+def _attention_ref(q, cache, layer, pos, scale):
+    """float32 softmax(q k^T scale) v per row over its positions 0..pos."""
+    B, nh, d = q.shape
+    rep = nh // cache.kv_heads
+    outs = []
+    for b in range(B):
+        L = int(pos[b]) + 1
+        k, v = cache.gather_rows(layer, torch.tensor([b], device=DEV), L)
+        k = k[0].float().repeat_interleave(rep, 0)  # [nh, L, d]
+        v = v[0].float().repeat_interleave(rep, 0)
+        s = torch.matmul(k, q[b].float().unsqueeze(-1)).squeeze(-1) * scale   # [nh, L]
+        p = torch.softmax(s, -1).unsqueeze(1)                                 # [nh, 1, L]
+        outs.append(torch.matmul(p, v).reshape(nh * d))
+    return torch.stack(outs)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("B,nh,nkv,per,positions", [
+    (1, 28, 4, 40, [639]),                      # 7B heads, batch 1, a full 640-slot row
+    (1, 28, 4, 40, [0]),                        # one cached position
+    (4, 28, 4, 80, [1279, 17, 640, 1000]),     # ragged rows, several splits each
+    (3, 8, 8, 4, [63, 5, 33]),                 # no grouping
+    (2, 32, 4, 7, [100, 111]),                 # 8 query heads per KV head
+    (2, 12, 4, 3, [47, 16]),                   # 3 per KV head
+    (32, 28, 4, 80, None),                     # batch 32 decode at ~1.2K context
+])
+def test_paged_decode_attention(ops, B, nh, nkv, per, positions, d):
+    ps = 16
+    cache = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=per + B)
+    g = _gen(11 + B + nh + d)
+    cache.k[0].copy_(torch.randn(cache.k[0].shape, generator=g, device=DEV).to(torch.bfloat16))
+    cache.v[0].copy_(torch.randn(cache.v[0].shape, generator=g, device=DEV).to(torch.bfloat16))
+    if positions is None:
+        pos = torch.randint(1000, cache.capacity, (B,), generator=g, device=DEV)
+    else:
+        pos = torch.tensor(positions, dtype=torch.int64, device=DEV)
+    q = (torch.randn(B, nh, d, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    scale = d ** -0.5
+    out = ops.paged_decode_attention(q, cache, 0, pos, scale)
+    ref = _attention_ref(q, cache, 0, pos, scale)
+    err = (out.float() - ref).abs().max() / ref.abs().max()
+    assert out.shape == (B, nh * d)
+    assert err < 2.0 ** -7, float(err)
+    again = ops.paged_decode_attention(q, cache, 0, pos, scale)
+    assert torch.equal(out, again)
+
+
+def test_paged_decode_attention_shared_prefix_pages(ops):
+    """Rows that share their first pages (a cached prompt prefix) read them
+    through the table: equal to a cache holding private copies."""
+    d, ps, nkv, nh, B = 128, 16, 4, 28, 3
+    shared, own = 4, 3
+    table = torch.empty(B, shared + own, dtype=torch.int32)
+    table[:, :shared] = torch.arange(shared, dtype=torch.int32)
+    table[:, shared:] = shared + torch.arange(B * own, dtype=torch.int32).reshape(B, own)
+    c1 = ops.PagedKV(1, shared + B * own, ps, nkv, d, table, DEV)
+    g = _gen(5)
+    c1.k[0].copy_(torch.randn(c1.k[0].shape, generator=g, device=DEV).to(torch.bfloat16))
+    c1.v[0].copy_(torch.randn(c1.v[0].shape, generator=g, device=DEV).to(torch.bfloat16))
+    c2 = ops.PagedKV.contiguous(1, B, (shared + own) * ps, nkv, d, DEV, ps)
+    for b in range(B):
+        k, v = c1.gather_rows(0, torch.tensor([b], device=DEV), c1.capacity)
+        n = c1.capacity
+        slots = c2.slots(torch.full((n,), b, device=DEV), torch.arange(n, device=DEV))
+        c2.write(0, slots, k[0].transpose(0, 1), v[0].transpose(0, 1))
+    pos = torch.tensor([70, 111, 64], device=DEV)
+    q = torch.randn(B, nh, d, generator=g, device=DEV).to(torch.bfloat16)
+    a1 = ops.paged_decode_attention(q, c1, 0, pos, 0.1)
+    a2 = ops.paged_decode_attention(q, c2, 0, pos, 0.1)
+    assert torch.equal(a1, a2)
+
+
+def test_decode_ops_in_graph_replays(ops):
+    """A captured rope-append + attention step replays correctly as positions
+    advance (positions live on the device)."""
+    d, nkv, nh, B, ps, per = 128, 4, 28, 2, 16, 4
+    cache = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=9)
+    cos, sin = _tables(d, cache.capacity)
+    g = _gen(21)
+    qkv = torch.randn(B, (nh + 2 * nkv) * d, generator=g, device=DEV).to(torch.bfloat16)
+    pos = torch.zeros(B, dtype=torch.int64, device=DEV)
+
+    def step():
+        q = ops.rope_kv_append(qkv, pos, cache, 0, cos, sin, nh)
+        return ops.paged_decode_attention(q, cache, 0, pos, d ** -0.5), q
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, q_static = step()
+    for i in range(1, 20):
+        pos.fill_(i)
+        qkv.copy_(torch.randn(qkv.shape, generator=g, device=DEV).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _attention_ref(q_static, cache, 0, pos, d ** -0.5)
+        err = (out.float() - ref).abs().max() / ref.abs().max()
+        assert err < 2.0 ** -7, (i, float(err))
+
+
+def test_errors(ops):
+    d, nkv = 128, 4
+    cache = ops.PagedKV.contiguous(1, 2, 32, nkv, d, DEV)
+    pos = torch.zeros(2, dtype=torch.int64, device=DEV)
+    with pytest.raises(NotImplementedError):
+        q = torch.zeros(2, 36, d, dtype=torch.bfloat16, device=DEV)  # 9 per KV head
+        ops.paged_decode_attention(q, cache, 0, pos, 1.0)
+    with pytest.raises(ValueError):
+        q = torch.zeros(2, 28, d, dtype=torch.float32, device=DEV)
+        ops.paged_decode_attention(q, cache, 0, pos, 1.0)
+    with pytest.raises(NotImplementedError):
+        ops.rms_norm(torch.zeros(2, 12, dtype=torch.bfloat16, device=DEV),
+                     torch.ones(12, dtype=torch.bfloat16, device=DEV), 1e-6)
+    with pytest.raises(ValueError):
+        ops.silu_mul(torch.zeros(2, 7, dtype=torch.bfloat16, device=DEV))

@@ -31,7 +31,8 @@ def test_header_declares_the_abi():
     assert declared_functions() == sorted([
         "mq_version", "mq_last_error", "mq_quantize", "mq_dequantize", "mq_embedding_lookup",
         "mq_quantized_matmul", "mq_quantized_matmul_workspace", "mq_quantized_matmul_ws",
-        "mq_gather_qmm"])
+        "mq_gather_qmm", "mq_rms_norm", "mq_rope_kv_append",
+        "mq_paged_decode_attention_workspace", "mq_paged_decode_attention", "mq_silu_mul"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -59,6 +60,51 @@ def test_workspace_query(mq):
     assert q(64, 3584, 18944, 64, 3) == 0     # unsupported bits
     assert q(64, 3584, 18900, 64, 4) == 0     # K not a group multiple
     assert q(0, 3584, 18944, 64, 4) == 0
+
+
+def test_attention_workspace_query(mq):
+    """Float32 partials (max, sum, 128 weighted values per query head) per
+    (sequence, KV head, split of the positions)."""
+    q = _L(mq).mq_paged_decode_attention_workspace
+    per_split = 28 * (128 + 2) * 4
+    bs1 = q(1, 28, 4, 128, 40, 16)             # 640 positions
+    assert bs1 > 0 and bs1 % (4 * per_split) == 0
+    splits = bs1 // (4 * per_split)
+    assert 1 < splits <= 40                      # split over blocks, >= 16 positions each
+    bs32 = q(32, 28, 4, 128, 80, 16)
+    assert bs32 > 0 and bs32 % (32 * 4 * per_split) == 0
+    assert q(1, 28, 4, 64, 40, 16) == bs1 // 130 * 66   # head_dim 64: 64 + 2 floats per head
+    assert q(1, 28, 4, 96, 40, 16) == 0          # head_dim 96: unsupported
+    assert q(1, 36, 4, 128, 40, 16) == 0         # 9 query heads per KV head
+    assert q(0, 28, 4, 128, 40, 16) == 0
+    assert q(1, 28, 4, 128, 0, 16) == 0
+
+
+def test_decoder_entry_validation(mq):
+    """Argument checks run before any device access (null pointers are fine)."""
+    L = _L(mq)
+    null = None
+    assert L.mq_rms_norm(null, null, null, null, null, 4, 12, 1e-6, null) == -2   # dim % 8
+    assert L.mq_rms_norm(null, null, null, null, null, 4, 8200, 1e-6, null) == -2
+    assert L.mq_rms_norm(null, 1, null, null, null, 4, 64, 1e-6, null) == -1     # residual pair
+    assert L.mq_rms_norm(null, null, null, null, null, 0, 64, 1e-6, null) == 0
+    assert L.mq_silu_mul(null, null, 4, 12, null) == -2
+    assert L.mq_silu_mul(null, null, 0, 16, null) == 0
+    att = L.mq_paged_decode_attention
+    assert att(null, null, null, null, 4, 16, 8, null, 2, 30, 4, 128, 1.0, null, 0, null,
+               null) == -1                                                      # 30 % 4
+    assert att(null, null, null, null, 4, 16, 8, null, 2, 28, 4, 96, 1.0, null, 0, null,
+               null) == -2                                                      # head_dim
+    assert att(null, null, null, null, 4, 16, 8, null, 2, 28, 4, 128, 1.0, null, 0, null,
+               null) == -1                                                      # no workspace
+    assert b"workspace" in L.mq_last_error()
+    assert att(null, null, null, null, 0, 16, 8, null, 2, 28, 4, 128, 1.0, null, 0, null,
+               null) == -1                                                      # no pages
+    rope = L.mq_rope_kv_append
+    assert rope(null, null, null, 4, 16, 8, null, null, null, null, null, 2, 28, 4, 127,
+                null) == -1                                                     # odd head_dim
+    assert rope(null, null, null, 4, 16, 8, null, null, null, null, null, 0, 28, 4, 128,
+                null) == 0
 
 
 def test_capi_invalid_and_unsupported_codes(mq):
