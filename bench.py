@@ -63,6 +63,9 @@ def parse():
                     help="eager launches of the headline kernel + a 128 MiB copy (rocprofv3 runs)")
     ap.add_argument("--profile-shape", default=None, metavar="M,K,N,BITS",
                     help="eager launches of quantized_matmul at one shape (rocprofv3 runs)")
+    ap.add_argument("--decode-only", type=int, default=None, metavar="BATCH",
+                    help="only one decode benchmark: 7B at batch 1 or 32, or the MoE model "
+                         "at batch 8 (rocprofv3 runs)")
     return ap.parse_args()
 
 
@@ -144,27 +147,38 @@ def hbm_floor(torch, nbytes: int, count: int = 16):
             "us": round(ms * 1e3, 3), "GBps": round(4 * half / (ms * 1e-3) / 1e9, 1)}
 
 
-def _weight_bytes(model) -> int:
-    """Bytes of every quantized linear a decode step streams (not the embedding,
-    of which a step reads one row per sequence)."""
+def _weight_bytes(model, batch: int) -> int:
+    """Bytes of the quantized weights a decode step streams: every linear (not
+    the embedding, of which a step reads one row per sequence) and, for an
+    expert MLP, the expected number of distinct experts that `batch` tokens
+    route to, E * (1 - (1 - k/E)^batch) per layer (uniform routing)."""
+    def nbytes(*ts):
+        return sum(t.numel() * t.element_size() for t in ts if t is not None)
+
     total = 0
-    linears = [ql for layer in model.layers
-               for ql in (layer.qkv, layer.o, layer.gate_up, layer.down)]
-    linears.append(model.lm_head if model.lm_head is not None else model.embed)
-    for ql in linears:
-        for t in (ql.wq, ql.scales, ql.biases, ql.bias):
-            if t is not None:
-                total += t.numel() * t.element_size()
-    return total
+    for layer in model.layers:
+        for ql in (layer.qkv, layer.o, layer.gate_up, layer.down):
+            if ql is not None:
+                total += nbytes(ql.wq, ql.scales, ql.biases, ql.bias)
+        if layer.moe is not None:
+            m = layer.moe
+            E, k = m.num_experts, m.top_k
+            per_expert = sum(nbytes(qe.wq, qe.scales, qe.biases) for qe in (m.gate_up, m.down)) / E
+            total += nbytes(m.gate.wq, m.gate.scales, m.gate.biases)
+            total += int(E * (1 - (1 - k / E) ** batch) * per_expert)
+    head = model.lm_head if model.lm_head is not None else model.embed
+    return total + nbytes(head.wq, head.scales, head.biases)
 
 
-def decode_bench(torch, batch: int, prompt_len: int, n_new: int, prefix_len: int = 0):
-    """Greedy decode of the Qwen2.5-7B-shaped 4-bit model (random init): prefill
-    `prompt_len` tokens per row (the first `prefix_len` shared by every row and
-    prefilled once into shared pages), then `n_new` graph-replayed decode steps
-    over the paged KV cache (pages of 16)."""
+def decode_bench(torch, batch: int, prompt_len: int, n_new: int, prefix_len: int = 0,
+                 model_name: str = "qwen25_7b"):
+    """Greedy decode of a 4-bit random-init model (Qwen2.5-7B shape, or the
+    Qwen3-30B-A3B MoE shape): prefill `prompt_len` tokens per row (the first
+    `prefix_len` shared by every row and prefilled once into shared pages),
+    then `n_new` graph-replayed decode steps over the paged KV cache (pages of
+    16)."""
     q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
-    cfg = q2.Qwen2Config.qwen25_7b(bits=4)
+    cfg = getattr(q2.Qwen2Config, model_name)(bits=4)
     model = q2.Qwen2Model.random(cfg, seed=0, device="cuda:0")
     gen = torch.Generator(device="cuda:0").manual_seed(2)
     prompt = torch.randint(0, cfg.vocab_size, (batch, prompt_len), generator=gen, device="cuda:0")
@@ -192,13 +206,14 @@ def decode_bench(torch, batch: int, prompt_len: int, n_new: int, prefix_len: int
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
-    wbytes = _weight_bytes(model)
+    wbytes = _weight_bytes(model, batch)
     kv_per_pos = 2 * cfg.num_hidden_layers * cfg.num_key_value_heads * cfg.head_dim * 2
     step_bytes = wbytes + batch * kv_per_pos * (prompt_len + (n_new + 1) / 2)
     step_s = ms * 1e-3 / n_new
     del model, cache, g
     torch.cuda.empty_cache()
-    return {"batch": batch, "prompt_len": prompt_len, "shared_prefix": prefix_len,
+    return {"model": model_name, "batch": batch, "prompt_len": prompt_len,
+            "shared_prefix": prefix_len,
             "new_tokens": n_new, "page_size": 16,
             "decode_tok_s": round(batch * n_new / (ms * 1e-3), 1),
             "ms_per_decode_step": round(ms / n_new, 3),
@@ -275,6 +290,16 @@ def main():
         print(json.dumps({"profile_shape": [pM, pK, pN, pbits], "launches": args.warmup + args.steps}))
         return
 
+    if args.decode_only is not None:
+        if args.decode_only == 1:
+            res = decode_bench(torch, 1, 512, 128)
+        elif args.decode_only == 8:
+            res = decode_bench(torch, 8, 512, 128, model_name="qwen3_30b_a3b")
+        else:
+            res = decode_bench(torch, args.decode_only, 1024, 256, prefix_len=256)
+        print(json.dumps({"decode": res}))
+        return
+
     K, N, bits, M = 3584, 18944, 4, 1
     replicas = make_replicas(mq, torch, N, K, bits, args.replicas, seed=0)
     gen = torch.Generator(device="cuda:0").manual_seed(1)
@@ -332,7 +357,8 @@ def main():
         # Qwen2.5-7B shape, 4-bit: batch 1 (512-token prompt, 128 tokens) and
         # batch 32 (1024-token prompts, 256 tokens).
         line["decode"] = [decode_bench(torch, 1, 512, 128),
-                          decode_bench(torch, 32, 1024, 256, prefix_len=256)]
+                          decode_bench(torch, 32, 1024, 256, prefix_len=256),
+                          decode_bench(torch, 8, 512, 128, model_name="qwen3_30b_a3b")]
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
     if not args.no_cpu:

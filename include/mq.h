@@ -141,6 +141,7 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
  * sequence's current token position, in device memory so that a captured
  * step replays with new values.  Out-of-range positions and page ids are
  * clamped into the cache (wrong values, never an access outside it).
+ * num_pages * page_size and pages_per_seq * page_size are below 2^31.
  * ------------------------------------------------------------------------ */
 
 /*
@@ -163,12 +164,15 @@ int mq_rms_norm(const mq_bf16* x, const mq_bf16* residual, mq_bf16* residual_out
  *   q_out bfloat16 [batch, n_heads, head_dim] = rope(q),
  *   k_pages[slot] = rope(k), v_pages[slot] = v        (bfloat16)
  * cos/sin float32 [positions, head_dim / 2], row p = cos/sin(p * theta^(-2i/d)).
+ * q_norm / k_norm (bfloat16 [head_dim] or NULL): Qwen3's per-head RMSNorm
+ * before RoPE (models/qwen3.py:61-62,84-85), eps norm_eps; head_dim <= 128.
  */
 int mq_rope_kv_append(const mq_bf16* qkv, const int64_t* positions, const int32_t* page_table,
                       int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
-                      const float* cos_table, const float* sin_table, mq_bf16* q_out,
-                      mq_bf16* k_pages, mq_bf16* v_pages, int64_t batch, int n_heads,
-                      int n_kv_heads, int head_dim, hipStream_t stream);
+                      const float* cos_table, const float* sin_table, const mq_bf16* q_norm,
+                      const mq_bf16* k_norm, float norm_eps, mq_bf16* q_out, mq_bf16* k_pages,
+                      mq_bf16* v_pages, int64_t batch, int n_heads, int n_kv_heads, int head_dim,
+                      hipStream_t stream);
 
 /*
  * Workspace, in bytes, for mq_paged_decode_attention (0 = unsupported shape).
@@ -203,6 +207,46 @@ int mq_paged_decode_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq
  */
 int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inter,
                 hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Mixture-of-experts routing around mq_gather_qmm (models/lfm2.py:348-375,
+ * SwitchGLU lfm2.py:193-218 with _gather_sort/_scatter_unsort :613-622).
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Router of Lfm2MoE.__call__ (models/lfm2.py:365-373) after the gate linear:
+ *   gates = softmax(float32(logits)) (+ expert_bias, float32 [E], or NULL)
+ *   indices int32 [tokens, top_k] = the top_k gates' experts (argpartition;
+ *     here in descending gate order, ties to the lower id),
+ *   scores bfloat16 [tokens, top_k] = those gates, divided by
+ *     (their sum + 1e-20) when norm_topk_prob.
+ * logits bfloat16 [tokens, num_experts]; num_experts <= 512, top_k <= 64.
+ */
+int mq_moe_route(const mq_bf16* logits, const float* expert_bias, int64_t tokens,
+                 int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
+                 mq_bf16* scores, hipStream_t stream);
+
+/*
+ * _gather_sort (models/lfm2.py:613-618) as a stable counting sort of the flat
+ * expert ids [n] (n = tokens * top_k): sorted_ids[p] = ids[order[p]],
+ * inverse[order[p]] = p, and rows[p] = order[p] / top_k (the x row that
+ * mq_gather_qmm takes as lhs index; rows may be NULL).  Ids outside
+ * [0, num_experts) sort last, unchanged.  int32 throughout; one block.
+ */
+int mq_moe_sort(const int32_t* expert_ids, int64_t n, int top_k, int num_experts,
+                int32_t* sorted_ids, int32_t* order, int32_t* inverse, int32_t* rows,
+                hipStream_t stream);
+
+/*
+ * _scatter_unsort (models/lfm2.py:621-622) and the score-weighted sum over the
+ * top_k experts (lfm2.py:375):
+ *   out[t, :] = bf16( sum_j bf16(y[r(t, j), :] * scores[t, j]) ),  float32 sum,
+ * r(t, j) = inverse[t * top_k + j] (rows of y in expert order), or
+ * t * top_k + j when inverse is NULL.  y bfloat16 [tokens * top_k, hidden],
+ * out bfloat16 [tokens, hidden], hidden % 8 == 0.
+ */
+int mq_moe_combine(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scores, mq_bf16* out,
+                   int64_t tokens, int top_k, int64_t hidden, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,9 @@ EXPORTS = (
     "mq_paged_decode_attention_workspace",
     "mq_paged_decode_attention",
     "mq_silu_mul",
+    "mq_moe_route",
+    "mq_moe_sort",
+    "mq_moe_combine",
 )
 
 _lock = threading.Lock()
@@ -63,12 +66,15 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_gather_qmm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _int, _int, _int, _int, _p]
     L.mq_rms_norm.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p]
-    L.mq_rope_kv_append.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _int,
-                                    _int, _int, _p]
+    L.mq_rope_kv_append.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, ctypes.c_float,
+                                    _p, _p, _p, _i64, _int, _int, _int, _p]
     L.mq_paged_decode_attention_workspace.argtypes = [_i64, _int, _int, _int, _i64, _i64]
     L.mq_paged_decode_attention.argtypes = [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _int, _int,
                                             _int, ctypes.c_float, _p, ctypes.c_size_t, _p, _p]
     L.mq_silu_mul.argtypes = [_p, _p, _i64, _i64, _p]
+    L.mq_moe_route.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p]
+    L.mq_moe_sort.argtypes = [_p, _i64, _int, _int, _p, _p, _p, _p, _p]
+    L.mq_moe_combine.argtypes = [_p, _p, _p, _p, _i64, _int, _i64, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
     L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t

@@ -282,29 +282,34 @@ int check_pages(const char* op, int64_t B, int n_heads, int n_kv_heads, int64_t 
                 n_heads, n_kv_heads);
   if (page_size <= 0 || pages_per_seq <= 0 || num_pages <= 0)
     return fail(MQ_ERR_INVALID, "[%s] page_size, pages_per_seq and num_pages must be > 0.", op);
-  if (pages_per_seq * page_size >= kMaxDim || num_pages >= kMaxDim)
-    return fail(MQ_ERR_INVALID, "[%s] the page table is too large.", op);
+  if (pages_per_seq * page_size >= kMaxDim || num_pages * page_size >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] the page table is too large (2^31 slots at most).", op);
   return MQ_OK;
 }
 }  // namespace
 
 int mq_rope_kv_append(const mq_bf16* qkv, const int64_t* positions, const int32_t* page_table,
                       int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
-                      const float* cos_table, const float* sin_table, mq_bf16* q_out,
-                      mq_bf16* k_pages, mq_bf16* v_pages, int64_t batch, int n_heads,
-                      int n_kv_heads, int head_dim, hipStream_t stream) {
+                      const float* cos_table, const float* sin_table, const mq_bf16* q_norm,
+                      const mq_bf16* k_norm, float norm_eps, mq_bf16* q_out, mq_bf16* k_pages,
+                      mq_bf16* v_pages, int64_t batch, int n_heads, int n_kv_heads, int head_dim,
+                      hipStream_t stream) {
   const char* op = "rope_kv_append";
   if (int rc = check_pages(op, batch, n_heads, n_kv_heads, pages_per_seq, page_size, num_pages))
     return rc;
   if (head_dim <= 0 || head_dim % 2)
     return fail(MQ_ERR_INVALID, "[%s] head_dim=%d must be even.", op, head_dim);
+  if ((q_norm || k_norm) && head_dim > 128)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] q/k norms need head_dim <= 128, got %d.", op,
+                head_dim);
   if (batch == 0) return ok();
   if (!qkv || !positions || !page_table || !cos_table || !sin_table || !q_out || !k_pages ||
       !v_pages)
     return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
   return hip_status(mq::launch_rope_append(qkv, positions, page_table, pages_per_seq, page_size,
-                                           num_pages, cos_table, sin_table, q_out, k_pages,
-                                           v_pages, batch, n_heads, n_kv_heads, head_dim, stream),
+                                           num_pages, q_norm, k_norm, norm_eps, cos_table,
+                                           sin_table, q_out, k_pages, v_pages, batch, n_heads,
+                                           n_kv_heads, head_dim, stream),
                     op);
 }
 
@@ -363,6 +368,55 @@ int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inte
   if (!aligned16(gate_up) || !aligned16(out))
     return fail(MQ_ERR_INVALID, "[%s] buffers must be 16-byte aligned.", op);
   return hip_status(mq::launch_silu_mul(gate_up, out, rows, inter, stream), op);
+}
+
+int mq_moe_route(const mq_bf16* logits, const float* expert_bias, int64_t tokens,
+                 int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
+                 mq_bf16* scores, hipStream_t stream) {
+  const char* op = "moe_route";
+  if (int rc = check_dim(op, "tokens", tokens)) return rc;
+  if (!mq::moe_route_supported(num_experts, top_k))
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] %d experts, top %d: 1 <= k <= min(E, 64), E <= 512.",
+                op, num_experts, top_k);
+  if (tokens == 0) return ok();
+  if (!logits || !indices || !scores) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  return hip_status(mq::launch_moe_route(logits, expert_bias, tokens, num_experts, top_k,
+                                         norm_topk_prob != 0, indices, scores, stream),
+                    op);
+}
+
+int mq_moe_sort(const int32_t* expert_ids, int64_t n, int top_k, int num_experts,
+                int32_t* sorted_ids, int32_t* order, int32_t* inverse, int32_t* rows,
+                hipStream_t stream) {
+  const char* op = "moe_sort";
+  if (int rc = check_dim(op, "n", n)) return rc;
+  if (top_k < 1) return fail(MQ_ERR_INVALID, "[%s] top_k=%d must be >= 1.", op, top_k);
+  if (!mq::moe_sort_supported(n, num_experts))
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] %d experts (1..512), %lld entries (< 2^30).", op,
+                num_experts, (long long)n);
+  if (n == 0) return ok();
+  if (!expert_ids || !sorted_ids || !order || !inverse)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  return hip_status(mq::launch_moe_sort(expert_ids, n, top_k, num_experts, sorted_ids, order,
+                                        inverse, rows, stream),
+                    op);
+}
+
+int mq_moe_combine(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scores, mq_bf16* out,
+                   int64_t tokens, int top_k, int64_t hidden, hipStream_t stream) {
+  const char* op = "moe_combine";
+  if (int rc = check_dim(op, "tokens", tokens)) return rc;
+  if (top_k < 1 || (int64_t)top_k * tokens >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] top_k=%d is out of range.", op, top_k);
+  if (hidden <= 0 || hidden % 8 || hidden >= kMaxDim)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] hidden=%lld must be a positive multiple of 8.", op,
+                (long long)hidden);
+  if (tokens == 0) return ok();
+  if (!y || !scores || !out) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(y) || !aligned16(out))
+    return fail(MQ_ERR_INVALID, "[%s] y and out must be 16-byte aligned.", op);
+  return hip_status(mq::launch_moe_combine(y, inverse, scores, out, tokens, top_k, hidden, stream),
+                    op);
 }
 
 }  // extern "C"

@@ -111,12 +111,17 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
 }
 
 // ---------------------------------------------------------------- RoPE + append
-// One sequence per block.  qkv bf16 [B, (nh + 2 nkv) * d] (q heads, k heads,
-// v heads); q_out bf16 [B, nh, d]; cos/sin float32 [positions, d/2].
+// One sequence per block, one wave per head (q heads, then k heads), lane i
+// < d/2 holding the rotated pair (i, i + d/2).  qkv bf16 [B, (nh + 2 nkv) * d]
+// (q heads, k heads, v heads); q_out bf16 [B, nh, d]; cos/sin float32
+// [positions, d/2].  With q_norm / k_norm (Qwen3, qwen3.py:61-62,84-85) each
+// head is first RMS-normalised over d with that weight and rounded to
+// bfloat16, as nn.RMSNorm stores it.
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(
     const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
     const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages,
     int nh, int nkv, int d) {
   const int64_t b = blockIdx.x;
@@ -125,18 +130,31 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
   const int64_t slot = page * page_size + p % page_size;
   const int half = d / 2;
   const uint16_t* row = qkv + b * (int64_t)(nh + 2 * nkv) * d;
-  const float* cs = cos_t + p * half;
-  const float* sn = sin_t + p * half;
-  for (int e = threadIdx.x; e < (nh + nkv) * half; e += kThreads) {
-    const int hh = e / half, i = e % half;
-    const float x1 = bf16_bits_to_f32(row[hh * d + i]);
-    const float x2 = bf16_bits_to_f32(row[hh * d + i + half]);
-    const uint16_t o1 = (uint16_t)f32_to_bf16_bits(x1 * cs[i] - x2 * sn[i]);
-    const uint16_t o2 = (uint16_t)f32_to_bf16_bits(x2 * cs[i] + x1 * sn[i]);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int hh = wave; hh < nh + nkv; hh += kThreads / 64) {
+    const uint16_t* norm = hh < nh ? q_norm : k_norm;
     uint16_t* dst = hh < nh ? q_out + (b * nh + hh) * (int64_t)d
                             : k_pages + (slot * nkv + (hh - nh)) * (int64_t)d;
-    dst[i] = o1;
-    dst[i + half] = o2;
+    for (int i0 = 0; i0 < half; i0 += 64) {  // one pass for d <= 128
+      const int i = i0 + lane;
+      float x1 = 0.f, x2 = 0.f;
+      if (i < half) {
+        x1 = bf16_bits_to_f32(row[hh * d + i]);
+        x2 = bf16_bits_to_f32(row[hh * d + i + half]);
+      }
+      if (norm) {  // uniform per wave; d <= 128 so the head is this one pass
+        const float inv = rsqrtf(wave_sum(fmaf(x1, x1, x2 * x2)) / (float)d + eps);
+        if (i < half) {
+          x1 = bf16r(x1 * inv * bf16_bits_to_f32(norm[i]));
+          x2 = bf16r(x2 * inv * bf16_bits_to_f32(norm[i + half]));
+        }
+      }
+      if (i < half) {
+        const float c = cos_t[p * half + i], sn = sin_t[p * half + i];
+        dst[i] = (uint16_t)f32_to_bf16_bits(x1 * c - x2 * sn);
+        dst[i + half] = (uint16_t)f32_to_bf16_bits(x2 * c + x1 * sn);
+      }
+    }
   }
   for (int e = threadIdx.x; e < nkv * d; e += kThreads)
     v_pages[slot * nkv * (int64_t)d + e] = row[(nh + nkv) * d + e];
@@ -144,172 +162,193 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
 
 // ---------------------------------------------------------------- attention
 // Grid (splits, nkv, B), 256 threads.  A cached row of one KV head (D bf16,
-// 2D bytes) is read by D/8 lanes, 16 bytes each, so a block covers
-// 2048/D positions per pass (16 at D = 128, 32 at D = 64).  REP query heads
-// share the KV head.
+// 2D bytes) is read by LANES = D/8 lanes, 16 bytes each.  The block's lane
+// groups take the split's positions round robin, kTile positions per group at
+// a time with the K and V rows of all of them loaded together.  Each group
+// keeps its own running max, sum and weighted values (online softmax), and the
+// groups are merged at the end.  Scores are kept in log2 units
+// (q.k * scale * log2 e), so every exponential is exp2.
 //
-// Partials per (b, kv head, split), float32: m[REP], s[REP], acc[REP][D].
+// Partials per (b, kv head, split), float32: m[REP], s[REP], acc[REP][D];
+// splits past the sequence's end are neither written nor read.
 constexpr int kMaxChunk = 512;
+constexpr int kTile = 4;
+constexpr float kNoScore = -1e30f;  // running max before the first position
 
 template <int REP, int D>
 __global__ __launch_bounds__(kThreads) void attn_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pages,
     const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table,
     int pages_per_seq, int page_size, int num_pages, const int64_t* __restrict__ pos,
-    float* __restrict__ part, int nkv, int chunk, float scale) {
+    float* __restrict__ part, int nkv, int chunk, float scale_log2) {
   constexpr int LANES = D / 8;               // lanes per cached row
-  constexpr int PASS = kThreads / LANES;     // positions per pass
-  __shared__ float sc[REP][kMaxChunk];
-  __shared__ float stat[2][REP];
-  __shared__ float red[kThreads / 64][REP][D];
+  constexpr int GROUPS = kThreads / LANES;   // positions per pass of the block
+  constexpr int WAVES = kThreads / 64;
+  __shared__ int32_t slot_of[kMaxChunk];
+  __shared__ float mrg_m[WAVES][REP], mrg_s[WAVES][REP];
+  __shared__ float mrg_a[WAVES][REP][D];
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int splits = gridDim.x;
   const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
   const int l0 = split * chunk;
   const int n = min(L - l0, chunk);
+  if (n <= 0) return;  // past the sequence's end
   float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
   float* ps = pm + REP;
   float* pa = ps + REP;
-  if (n <= 0) {  // past the sequence: an empty split
-    if (threadIdx.x < REP) {
-      pm[threadIdx.x] = -INFINITY;
-      ps[threadIdx.x] = 0.f;
-    }
-    return;
-  }
-  const int sub = threadIdx.x % LANES, slot_in_pass = threadIdx.x / LANES;
-  const int nh = nkv * REP;
   const int32_t* table = page_table + b * pages_per_seq;
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const int l = l0 + i;
+    slot_of[i] = (int32_t)(clamp_index(table[l / page_size], num_pages) * page_size +
+                           l % page_size);
+  }
+  const int sub = threadIdx.x % LANES, grp = threadIdx.x / LANES;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nh = nkv * REP;
+  // this lane's 8 dims of every query head, as bf16 pairs
+  u32x4_t qv[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+    qv[r] = reinterpret_cast<const u32x4_t*>(q + (b * nh + kvh * REP + r) * (int64_t)D)[sub];
+  __syncthreads();
 
-  // this lane's 8 dims of every query head, pre-scaled
-  float qr[REP][8];
+  float m[REP], s[REP], acc[REP][8];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
-    const u32x4_t v =
-        reinterpret_cast<const u32x4_t*>(q + (b * nh + kvh * REP + r) * (int64_t)D)[sub];
+    m[r] = kNoScore;
+    s[r] = 0.f;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      qr[r][2 * t] = lo_bf16(v[t]) * scale;
-      qr[r][2 * t + 1] = hi_bf16(v[t]) * scale;
-    }
+    for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
   }
-
-  // scores
-  for (int i0 = 0; i0 < n; i0 += PASS) {
-    const int i = i0 + slot_in_pass;
-    const int l = l0 + min(i, n - 1);
-    const int64_t slot = clamp_index(table[l / page_size], num_pages) * page_size + l % page_size;
-    const u32x4_t kv =
-        reinterpret_cast<const u32x4_t*>(k_pages + (slot * nkv + kvh) * (int64_t)D)[sub];
-    float kf[8];
+  const int64_t row_elems = (int64_t)nkv * D;
+  const uint16_t* kb = k_pages + kvh * D + sub * 8;
+  const uint16_t* vb = v_pages + kvh * D + sub * 8;
+  for (int t0 = 0; t0 < n; t0 += GROUPS * kTile) {
+    u32x4_t kr[kTile], vr[kTile];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      kf[2 * t] = lo_bf16(kv[t]);
-      kf[2 * t + 1] = hi_bf16(kv[t]);
+    for (int u = 0; u < kTile; ++u) {
+      const int i = min(t0 + grp + GROUPS * u, n - 1);
+      const int64_t off = (int64_t)slot_of[i] * row_elems;
+      kr[u] = *reinterpret_cast<const u32x4_t*>(kb + off);
+      vr[u] = *reinterpret_cast<const u32x4_t*>(vb + off);
+    }
+    float x[kTile][REP];
+#pragma unroll
+    for (int u = 0; u < kTile; ++u) {
+      const bool valid = t0 + grp + GROUPS * u < n;
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) d = dot2_bf16(qv[r][t], kr[u][t], d);
+        d = dpp_group_sum<LANES>(d);
+        x[u][r] = valid ? d * scale_log2 : -INFINITY;
+      }
     }
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      float dot = 0.f;
+      float mt = x[0][r];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) dot = fmaf(qr[r][t], kf[t], dot);
-      dot = dpp_group_sum<LANES>(dot);
-      if (sub == 0 && i < n) sc[r][i] = dot;
-    }
-  }
-  __syncthreads();
-
-  // softmax numerators: wave w takes heads w, w + 4, ...
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int r = wave; r < REP; r += kThreads / 64) {
-    float m = -INFINITY;
-    for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[r][i]);
-    m = wave_max(m);
-    float s = 0.f;
-    for (int i = lane; i < n; i += 64) {
-      const float e = __expf(sc[r][i] - m);
-      sc[r][i] = e;
-      s += e;
-    }
-    s = wave_sum(s);
-    if (lane == 0) {
-      stat[0][r] = m;
-      stat[1][r] = s;
-    }
-  }
-  __syncthreads();
-
-  // weighted values: the same lane mapping as the scores
-  float acc[REP][8];
+      for (int u = 1; u < kTile; ++u) mt = fmaxf(mt, x[u][r]);
+      const float mn = fmaxf(m[r], mt);
+      const float f = exp2f(m[r] - mn);
+      float psum = 0.f;
 #pragma unroll
-  for (int r = 0; r < REP; ++r)
+      for (int u = 0; u < kTile; ++u) {
+        x[u][r] = exp2f(x[u][r] - mn);  // now the weight p of position u
+        psum += x[u][r];
+      }
+      s[r] = fmaf(s[r], f, psum);
+      m[r] = mn;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
-  for (int i0 = 0; i0 < n; i0 += PASS) {
-    const int i = i0 + slot_in_pass;
-    if (i < n) {
-      const int l = l0 + i;
-      const int64_t slot = clamp_index(table[l / page_size], num_pages) * page_size + l % page_size;
-      const u32x4_t vv =
-          reinterpret_cast<const u32x4_t*>(v_pages + (slot * nkv + kvh) * (int64_t)D)[sub];
+      for (int t = 0; t < 8; ++t) acc[r][t] *= f;
+    }
+#pragma unroll
+    for (int u = 0; u < kTile; ++u) {
       float vf[8];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        vf[2 * t] = lo_bf16(vv[t]);
-        vf[2 * t + 1] = hi_bf16(vv[t]);
+        vf[2 * t] = lo_bf16(vr[u][t]);
+        vf[2 * t + 1] = hi_bf16(vr[u][t]);
       }
 #pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        const float p = sc[r][i];
+      for (int r = 0; r < REP; ++r)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(p, vf[t], acc[r][t]);
+        for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(x[u][r], vf[t], acc[r][t]);
+    }
+  }
+
+  // merge the lane groups of each wave (butterfly: every group ends with the
+  // wave's totals), then the waves through LDS
+#pragma unroll
+  for (int off = LANES; off < 64; off <<= 1) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const float mo = __shfl_xor(m[r], off, 64);
+      const float so = __shfl_xor(s[r], off, 64);
+      const float mn = fmaxf(m[r], mo);
+      const float f1 = exp2f(m[r] - mn), f2 = exp2f(mo - mn);
+      s[r] = s[r] * f1 + so * f2;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[r][t] = acc[r][t] * f1 + __shfl_xor(acc[r][t], off, 64) * f2;
+      m[r] = mn;
+    }
+  }
+  if (lane < LANES) {
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) mrg_a[wave][r][8 * sub + t] = acc[r][t];
+      if (lane == 0) {
+        mrg_m[wave][r] = m[r];
+        mrg_s[wave][r] = s[r];
       }
     }
   }
-  // sum the position slots of each wave (lanes sub, sub + LANES, ...), then
-  // the 4 waves through LDS
-#pragma unroll
-  for (int r = 0; r < REP; ++r)
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      float v = acc[r][t];
-#pragma unroll
-      for (int off = LANES; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-      if (lane < LANES) red[wave][r][8 * sub + t] = v;
-    }
   __syncthreads();
   for (int e = threadIdx.x; e < REP * D; e += kThreads) {
     const int r = e / D, dd = e % D;
-    float v = 0.f;
+    float mx = mrg_m[0][r];
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) v += red[w][r][dd];
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, mrg_m[w][r]);
+    float v = 0.f, sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const float f = exp2f(mrg_m[w][r] - mx);
+      v = fmaf(mrg_a[w][r][dd], f, v);
+      sum = fmaf(mrg_s[w][r], f, sum);
+    }
     pa[e] = v;
-  }
-  if (threadIdx.x < REP) {
-    pm[threadIdx.x] = stat[0][threadIdx.x];
-    ps[threadIdx.x] = stat[1][threadIdx.x];
+    if (dd == 0) {
+      pm[r] = mx;
+      ps[r] = sum;
+    }
   }
 }
 
-// Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over splits of the
-// partials rescaled to the common max, divided by the rescaled sum.
+// Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over the sequence's
+// splits of the partials rescaled to their common max, over the rescaled sum.
 template <int REP, int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ part,
-                                                         uint16_t* __restrict__ out, int nkv,
-                                                         int splits) {
+__global__ __launch_bounds__(D) void attn_combine_kernel(
+    const float* __restrict__ part, const int64_t* __restrict__ pos, int pages_per_seq,
+    int page_size, uint16_t* __restrict__ out, int nkv, int splits, int chunk) {
+  constexpr int STRIDE = REP * (D + 2);
   const int hh = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int kvh = hh / REP, r = hh % REP;
   const int dd = threadIdx.x;
-  const float* base = part + (b * nkv + kvh) * splits * (int64_t)(REP * (D + 2));
-  float m = -INFINITY;
-  for (int s = 0; s < splits; ++s) m = fmaxf(m, base[s * (REP * (D + 2)) + r]);
+  const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
+  const int used = min(splits, (L + chunk - 1) / chunk);
+  const float* base = part + (b * nkv + kvh) * splits * (int64_t)STRIDE;
+  float mx = -INFINITY;
+#pragma unroll 8
+  for (int sp = 0; sp < used; ++sp) mx = fmaxf(mx, base[sp * STRIDE + r]);
   float num = 0.f, den = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float* p = base + s * (REP * (D + 2));
-    const float ms = p[r];
-    if (ms == -INFINITY) continue;
-    const float f = __expf(ms - m);
+#pragma unroll 8
+  for (int sp = 0; sp < used; ++sp) {
+    const float* p = base + sp * STRIDE;
+    const float f = exp2f(p[r] - mx);
     den = fmaf(f, p[REP + r], den);
     num = fmaf(f, p[2 * REP + r * D + dd], num);
   }
@@ -338,11 +377,11 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   reinterpret_cast<u32x4_t*>(out + r * inter)[u] = o;
 }
 
-// Positions per split: whole passes of 32 (one or two passes of the kernel),
-// at most kMaxChunk, and enough splits for about 512 blocks over the chip.
+// Positions per split: a multiple of 32, at most kMaxChunk, and enough
+// splits for about 1024 blocks over the chip.
 int attn_chunk(int64_t B, int nkv, int64_t capacity) {
   const int64_t blocks = B * nkv;
-  int64_t splits = (512 + blocks - 1) / blocks;
+  int64_t splits = (1024 + blocks - 1) / blocks;
   splits = std::max<int64_t>(1, std::min<int64_t>(splits, (capacity + 31) / 32));
   int64_t chunk = (capacity + splits - 1) / splits;
   chunk = (chunk + 31) / 32 * 32;
@@ -377,6 +416,7 @@ hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* r
 
 hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int32_t* page_table,
                               int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                              const uint16_t* q_norm, const uint16_t* k_norm, float eps,
                               const float* cos_t,
                               const float* sin_t, uint16_t* q_out, uint16_t* k_pages,
                               uint16_t* v_pages, int64_t B, int nh, int nkv, int d,
@@ -384,7 +424,7 @@ hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int
   if (B == 0) return hipSuccess;
   hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)B), dim3(kThreads), 0, stream, qkv, pos,
                      page_table, (int)pages_per_seq, (int)page_size, (int)num_pages, cos_t, sin_t,
-                     q_out, k_pages, v_pages, nh, nkv, d);
+                     q_norm, k_norm, eps, q_out, k_pages, v_pages, nh, nkv, d);
   return hipGetLastError();
 }
 
@@ -395,15 +435,16 @@ hipError_t launch_attention_d(const uint16_t* q, const uint16_t* k_pages, const 
                               int num_pages, const int64_t* pos, int64_t B, int nh, int nkv,
                               float scale, float* workspace, uint16_t* out, int chunk, int splits,
                               hipStream_t stream) {
+  const float scale_log2 = scale * 1.4426950408889634f;  // exp(x) = exp2(x log2 e)
   const dim3 grid((unsigned)splits, (unsigned)nkv, (unsigned)B);
   const dim3 cgrid((unsigned)nh, (unsigned)B);
 #define MQ_ATTN(REP)                                                                            \
   case REP:                                                                                     \
     hipLaunchKernelGGL((attn_split_kernel<REP, D>), grid, dim3(kThreads), 0, stream, q,        \
                        k_pages, v_pages, page_table, pages_per_seq, page_size, num_pages, pos,  \
-                       workspace, nkv, chunk, scale);                                           \
+                       workspace, nkv, chunk, scale_log2);                                      \
     hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,    \
-                       out, nkv, splits);                                                       \
+                       pos, pages_per_seq, page_size, out, nkv, splits, chunk);                 \
     break;
   switch (nh / nkv) {
     MQ_ATTN(1)

@@ -83,6 +83,7 @@ hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* res_in, uint16_t* r
                           hipStream_t stream);
 hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int32_t* page_table,
                               int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                              const uint16_t* q_norm, const uint16_t* k_norm, float eps,
                               const float* cos_t, const float* sin_t, uint16_t* q_out,
                               uint16_t* k_pages, uint16_t* v_pages, int64_t B, int nh, int nkv,
                               int d, hipStream_t stream);
@@ -96,5 +97,16 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
                                    hipStream_t stream);
 hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter,
                            hipStream_t stream);
+
+// Mixture-of-experts routing (mq_moe.hip).
+bool moe_route_supported(int E, int k);
+hipError_t launch_moe_route(const uint16_t* logits, const float* expert_bias, int64_t T, int E,
+                            int k, bool normalize, int32_t* indices, uint16_t* scores,
+                            hipStream_t stream);
+bool moe_sort_supported(int64_t n, int E);
+hipError_t launch_moe_sort(const int32_t* ids, int64_t n, int k, int E, int32_t* sorted_ids,
+                           int32_t* order, int32_t* inverse, int32_t* rows, hipStream_t stream);
+hipError_t launch_moe_combine(const uint16_t* y, const int32_t* inverse, const uint16_t* scores,
+                              uint16_t* out, int64_t T, int k, int64_t H, hipStream_t stream);
 
 }  // namespace mq

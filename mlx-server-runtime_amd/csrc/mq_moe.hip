@@ -1,0 +1,243 @@
+// Mixture-of-experts routing around mx.gather_qmm, as the reference's MoE
+// block runs it (python/mlx_worker/native_mlx/models/lfm2.py:348-375 and
+// SwitchGLU, lfm2.py:193-218, 613-622):
+//
+//  * moe_route_kernel    gates = softmax(float32(router logits)) (+ expert
+//                        bias), the top-k experts per token (argpartition:
+//                        here in descending gate order, ties to the lower
+//                        expert id), their gates, optionally renormalised to
+//                        sum 1 (+1e-20), rounded to the activation dtype;
+//  * moe_sort_kernel     the flat (token, slot) pairs ordered by expert
+//                        (_gather_sort: argsort of the flat ids), stable, as
+//                        one counting sort: sorted ids, the order, its
+//                        inverse, and the x row of every sorted pair, which
+//                        gather_qmm takes as lhs indices (so the sorted copy
+//                        of x is never materialised);
+//  * moe_combine_kernel  _scatter_unsort plus the weighting of lfm2.py:375:
+//                        out[t] = sum_j bf16(y[inverse[t*k + j]] * score[t, j]),
+//                        float32 sum, one rounding.
+#include <algorithm>
+
+#include "mq_common.h"
+#include "mq_internal.h"
+
+namespace mq {
+namespace {
+
+// ---------------------------------------------------------------- router
+// One wave per token; E <= kMaxExperts (E / 64 values per lane).
+constexpr int kMaxExperts = 512;
+constexpr int kRouteWaves = 4;
+
+__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
+    const uint16_t* __restrict__ logits, const float* __restrict__ expert_bias, int64_t T, int E,
+    int k, int normalize, int32_t* __restrict__ indices, uint16_t* __restrict__ scores) {
+  constexpr int PER = kMaxExperts / 64;
+  const int64_t t = (int64_t)blockIdx.x * kRouteWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;  // whole waves
+  const uint16_t* row = logits + t * E;
+  float v[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? bf16_bits_to_f32(row[e]) : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    v[j] = lane + 64 * j < E ? __expf(v[j] - mx) : 0.f;
+    sum += v[j];
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) sum += __shfl_xor(sum, off, 64);
+  const float inv = 1.f / sum;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? v[j] * inv + (expert_bias ? expert_bias[e] : 0.f) : -INFINITY;
+  }
+  // k rounds of a wave arg-max (larger gate, then smaller id)
+  float picked = 0.f, total = 0.f;
+  int picked_id = 0;
+  for (int r = 0; r < k; ++r) {
+    float best = -INFINITY;
+    int best_id = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      if (v[j] > best || (v[j] == best && e < best_id)) {
+        best = v[j];
+        best_id = e;
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float ob = __shfl_xor(best, off, 64);
+      const int oi = __shfl_xor(best_id, off, 64);
+      if (ob > best || (ob == best && oi < best_id)) {
+        best = ob;
+        best_id = oi;
+      }
+    }
+    // every lane now holds the round's winner; its owner removes it
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (lane + 64 * j == best_id) v[j] = -INFINITY;
+    if (lane == r) {
+      picked = best;
+      picked_id = best_id;
+    }
+    total += best;
+  }
+  if (lane < k) {
+    float sc = picked;
+    if (normalize) sc = sc / (total + 1e-20f);
+    indices[t * k + lane] = picked_id;
+    scores[t * k + lane] = (uint16_t)f32_to_bf16_bits(sc);
+  }
+}
+
+// ---------------------------------------------------------------- sort
+// One block.  Entries are processed in chunks of kSortThreads, in order; an
+// entry's place is its expert's offset, plus the entries of that expert in
+// earlier chunks, earlier waves of this chunk and earlier lanes of its wave
+// (a match mask built from one ballot per id bit).  Ids outside [0, E) go to
+// a last bucket E, kept as they are (gather_qmm gives such rows zeros).
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kMaxBuckets = kMaxExperts + 1;
+
+__global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
+    const int32_t* __restrict__ ids, int n, int k, int E, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ order, int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
+  __shared__ int offset[kMaxBuckets];
+  __shared__ int wave_count[kSortWaves][kMaxBuckets];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int buckets = E + 1;
+  int bits = 0;
+  while ((1 << bits) < buckets) ++bits;
+  for (int e = tid; e < buckets; e += kSortThreads) offset[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += kSortThreads) {
+    const int id = ids[i];
+    atomicAdd(&offset[(id >= 0 && id < E) ? id : E], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {  // exclusive scan over at most 513 buckets
+    int run = 0;
+    for (int e = 0; e < buckets; ++e) {
+      const int c = offset[e];
+      offset[e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  for (int c0 = 0; c0 < n; c0 += kSortThreads) {
+    for (int e = lane; e < buckets; e += 64) wave_count[wave][e] = 0;
+    const int i = c0 + tid;
+    const bool valid = i < n;
+    int bucket = E;
+    int id = 0;
+    if (valid) {
+      id = ids[i];
+      bucket = (id >= 0 && id < E) ? id : E;
+    }
+    uint64_t match = __ballot(valid);
+    for (int bit = 0; bit < bits; ++bit) {
+      const uint64_t ones = __ballot(valid && ((bucket >> bit) & 1));
+      match &= ((bucket >> bit) & 1) ? ones : ~ones;
+    }
+    const int rank = __popcll(match & below);
+    __syncthreads();  // wave_count cleared by every wave
+    if (valid && rank == __popcll(match) - 1) wave_count[wave][bucket] = rank + 1;
+    __syncthreads();
+    int before = 0;
+    if (valid)
+      for (int w = 0; w < wave; ++w) before += wave_count[w][bucket];
+    if (valid) {
+      const int p = offset[bucket] + before + rank;
+      sorted_ids[p] = id;
+      order[p] = i;
+      inverse[i] = p;
+      if (rows) rows[p] = i / k;
+    }
+    __syncthreads();  // every read of offset / wave_count for this chunk done
+    for (int e = tid; e < buckets; e += kSortThreads) {
+      int add = 0;
+      for (int w = 0; w < kSortWaves; ++w) add += wave_count[w][e];
+      offset[e] += add;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- combine
+// Grid (T, ceil(H / (8 * 256))), 256 threads, 8 elements per thread.
+__global__ __launch_bounds__(256) void moe_combine_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ inverse,
+    const uint16_t* __restrict__ scores, uint16_t* __restrict__ out, int64_t T, int k, int H,
+    int64_t y_rows) {
+  const int64_t t = blockIdx.x;
+  const int u = blockIdx.y * 256 + threadIdx.x;  // 8-element unit of the row
+  if (u >= H / 8) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < k; ++j) {
+    int64_t r = t * k + j;
+    if (inverse) r = inverse[r];
+    r = r < 0 ? 0 : (r >= y_rows ? y_rows - 1 : r);
+    const float sc = bf16_bits_to_f32(scores[t * k + j]);
+    const u32x4_t v = reinterpret_cast<const u32x4_t*>(y + r * H)[u];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc[2 * q] += bf16_bits_to_f32(f32_to_bf16_bits(lo_bf16(v[q]) * sc));
+      acc[2 * q + 1] += bf16_bits_to_f32(f32_to_bf16_bits(hi_bf16(v[q]) * sc));
+    }
+  }
+  u32x4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+  reinterpret_cast<u32x4_t*>(out + t * H)[u] = o;
+}
+
+}  // namespace
+
+bool moe_route_supported(int E, int k) {
+  return E >= 1 && E <= kMaxExperts && k >= 1 && k <= 64 && k <= E;
+}
+
+hipError_t launch_moe_route(const uint16_t* logits, const float* expert_bias, int64_t T, int E,
+                            int k, bool normalize, int32_t* indices, uint16_t* scores,
+                            hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((T + kRouteWaves - 1) / kRouteWaves);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(blocks), dim3(64 * kRouteWaves), 0, stream, logits,
+                     expert_bias, T, E, k, normalize ? 1 : 0, indices, scores);
+  return hipGetLastError();
+}
+
+bool moe_sort_supported(int64_t n, int E) { return E >= 1 && E <= kMaxExperts && n < (1 << 30); }
+
+hipError_t launch_moe_sort(const int32_t* ids, int64_t n, int k, int E, int32_t* sorted_ids,
+                           int32_t* order, int32_t* inverse, int32_t* rows, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, ids, (int)n, k, E,
+                     sorted_ids, order, inverse, rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const uint16_t* y, const int32_t* inverse, const uint16_t* scores,
+                              uint16_t* out, int64_t T, int k, int64_t H, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  const dim3 grid((unsigned)T, (unsigned)((H / 8 + 255) / 256));
+  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, stream, y, inverse, scores, out, T,
+                     k, (int)H, T * k);
+  return hipGetLastError();
+}
+
+}  // namespace mq

@@ -121,10 +121,13 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
 
 
 def rope_kv_append(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, layer: int,
-                   cos: torch.Tensor, sin: torch.Tensor, n_heads: int) -> torch.Tensor:
+                   cos: torch.Tensor, sin: torch.Tensor, n_heads: int,
+                   q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,
+                   norm_eps: float = 1e-6) -> torch.Tensor:
     """qkv bf16 [B, (n_heads + 2 kv_heads) * head_dim] of one token per sequence ->
     q bf16 [B, n_heads, head_dim] after RoPE; rope(k) and v go into the pages at
-    each sequence's position (positions int64 [B], on the device)."""
+    each sequence's position (positions int64 [B], on the device).  q_norm /
+    k_norm (bf16 [head_dim]): Qwen3's per-head RMSNorm before RoPE."""
     op = "rope_kv_append"
     _require_gpu(op, qkv=qkv, positions=positions, cos=cos, sin=sin)
     _check_bf16(op, "qkv", qkv)
@@ -141,12 +144,16 @@ def rope_kv_append(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, l
         raise ValueError(f"[{op}] cos/sin must be float32 [positions, {d // 2}]")
     if cos.shape[0] < cache.capacity or sin.shape != cos.shape:
         raise ValueError(f"[{op}] cos/sin need {cache.capacity} positions")
+    for name, w in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if w is not None and (w.dtype != torch.bfloat16 or w.shape != (d,)):
+            raise ValueError(f"[{op}] {name} must be bfloat16 [{d}]")
     q = torch.empty(B, n_heads, d, dtype=torch.bfloat16, device=qkv.device)
     L = _lib.lib()
     _lib.check(L.mq_rope_kv_append(
         _ptr(qkv.contiguous()), _ptr(positions), _ptr(cache.page_table), cache.pages_per_seq,
-        cache.page_size, cache.num_pages, _ptr(cos.contiguous()), _ptr(sin.contiguous()), _ptr(q),
-        _ptr(cache.k[layer]), _ptr(cache.v[layer]), B, n_heads, nkv, d, _stream(qkv)), op)
+        cache.page_size, cache.num_pages, _ptr(cos.contiguous()), _ptr(sin.contiguous()),
+        _ptr(q_norm), _ptr(k_norm), float(norm_eps), _ptr(q), _ptr(cache.k[layer]),
+        _ptr(cache.v[layer]), B, n_heads, nkv, d, _stream(qkv)), op)
     return q
 
 

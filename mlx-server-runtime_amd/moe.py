@@ -1,0 +1,135 @@
+"""Mixture-of-experts block on gather_qmm, executed by libmi355q.
+
+Restates the reference's top-k routed SwiGLU expert block
+(python/mlx_worker/native_mlx/models/lfm2.py:348-375, SwitchGLU :193-218,
+_gather_sort/_scatter_unsort :613-622):
+
+    route(logits, top_k, norm_topk_prob, expert_bias=None) -> (indices, scores)
+        softmax(float32(logits)) (+ expert_bias), the top_k experts per token,
+        their gates (renormalised to sum 1 when norm_topk_prob), bfloat16
+    expert_sort(indices, num_experts) -> (sorted_ids, order, inverse, rows)
+        stable sort of the flat expert ids; rows[p] = order[p] // top_k is the
+        token whose x feeds sorted pair p (gather_qmm's lhs indices)
+    combine(y, inverse, scores) -> out
+        out[t] = sum_j bf16(y[inverse[t*k + j]] * scores[t, j])
+
+MoEBlock runs them around two gather_qmm calls: the experts' gate and up
+projections concatenated per expert (one call, [E, 2I, H]), SiLU * up, and
+the down projection.  Rows are sorted by expert when tokens * top_k >= 64,
+as in the reference.  There is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib, core
+from .core import _check_bf16, _ptr, _require_gpu, _stream
+from .decode_ops import silu_mul
+
+
+def route(logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
+          expert_bias: torch.Tensor | None = None):
+    """logits bf16 [T, E] -> (indices int32 [T, top_k], scores bf16 [T, top_k])."""
+    op = "moe_route"
+    _require_gpu(op, logits=logits, expert_bias=expert_bias)
+    _check_bf16(op, "logits", logits)
+    T, E = logits.reshape(-1, logits.shape[-1]).shape
+    if expert_bias is not None and (expert_bias.dtype != torch.float32
+                                    or expert_bias.shape != (E,)):
+        raise ValueError(f"[{op}] expert_bias must be float32 [{E}]")
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=logits.device)
+    sc = torch.empty(T, top_k, dtype=torch.bfloat16, device=logits.device)
+    L = _lib.lib()
+    _lib.check(L.mq_moe_route(_ptr(logits.contiguous()), _ptr(expert_bias), T, E, top_k,
+                              int(bool(norm_topk_prob)), _ptr(idx), _ptr(sc), _stream(logits)), op)
+    return idx, sc
+
+
+def expert_sort(indices: torch.Tensor, num_experts: int):
+    """indices int32 [T, k] -> (sorted_ids, order, inverse, rows), each int32 [T*k]."""
+    op = "moe_sort"
+    _require_gpu(op, indices=indices)
+    if indices.dtype != torch.int32:
+        raise ValueError(f"[{op}] indices must be int32, got {indices.dtype}")
+    k = indices.shape[-1]
+    flat = indices.contiguous().reshape(-1)
+    n = flat.numel()
+    outs = [torch.empty(n, dtype=torch.int32, device=flat.device) for _ in range(4)]
+    L = _lib.lib()
+    _lib.check(L.mq_moe_sort(_ptr(flat), n, k, num_experts, *(_ptr(t) for t in outs),
+                             _stream(flat)), op)
+    return tuple(outs)
+
+
+def combine(y: torch.Tensor, inverse: torch.Tensor | None, scores: torch.Tensor) -> torch.Tensor:
+    """y bf16 [T*k, H] (expert order when inverse is given) -> bf16 [T, H]."""
+    op = "moe_combine"
+    _require_gpu(op, y=y, inverse=inverse, scores=scores)
+    _check_bf16(op, "y", y)
+    _check_bf16(op, "scores", scores)
+    T, k = scores.shape
+    H = y.shape[-1]
+    y2 = y.contiguous().reshape(-1, H)
+    if y2.shape[0] != T * k:
+        raise ValueError(f"[{op}] y has {y2.shape[0]} rows, expected {T * k}")
+    if inverse is not None and (inverse.dtype != torch.int32 or inverse.numel() != T * k):
+        raise ValueError(f"[{op}] inverse must be int32 [{T * k}]")
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=y.device)
+    L = _lib.lib()
+    _lib.check(L.mq_moe_combine(_ptr(y2), _ptr(inverse), _ptr(scores.contiguous()), _ptr(out), T,
+                                k, H, _stream(y)), op)
+    return out
+
+
+class QExperts:
+    """Quantized expert bank: wq [E, N, K*bits/32], scales/biases [E, N, K/group]."""
+
+    def __init__(self, wq, scales, biases, group_size=64, bits=4):
+        self.wq, self.scales, self.biases = wq, scales, biases
+        self.group_size, self.bits = group_size, bits
+
+    @property
+    def num_experts(self) -> int:
+        return self.wq.shape[0]
+
+    def __call__(self, x, lhs=None, rhs=None, sorted_indices=False):
+        return core.gather_qmm(x, self.wq, self.scales, self.biases, lhs_indices=lhs,
+                               rhs_indices=rhs, transpose=True, group_size=self.group_size,
+                               bits=self.bits, sorted_indices=sorted_indices)
+
+
+class MoEBlock:
+    """Top-k routed SwiGLU experts (Lfm2MoE.__call__, models/lfm2.py:365-375)."""
+
+    def __init__(self, gate, gate_up: QExperts, down: QExperts, top_k: int,
+                 norm_topk_prob: bool = True, expert_bias: torch.Tensor | None = None):
+        self.gate, self.gate_up, self.down = gate, gate_up, down
+        self.top_k, self.norm_topk_prob, self.expert_bias = top_k, norm_topk_prob, expert_bias
+
+    @property
+    def num_experts(self) -> int:
+        return self.gate_up.num_experts
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """x bf16 [..., H] -> bf16 [..., H]."""
+        shape = x.shape
+        xt = x.reshape(-1, shape[-1])
+        T = xt.shape[0]
+        idx, sc = route(self.gate(xt), self.top_k, self.norm_topk_prob, self.expert_bias)
+        xb = xt.reshape(T, 1, shape[-1])
+        if idx.numel() >= 64:  # the reference sorts at >= 64 pairs (lfm2.py:204)
+            sorted_ids, _, inverse, rows = expert_sort(idx, self.num_experts)
+            gu = self.gate_up(xb, lhs=rows, rhs=sorted_ids, sorted_indices=True)
+            y = self.down(silu_mul(gu), rhs=sorted_ids, sorted_indices=True)
+        else:
+            inverse = None
+            rows = torch.arange(T, device=x.device, dtype=torch.int32).repeat_interleave(
+                self.top_k)
+            flat = idx.reshape(-1)
+            gu = self.gate_up(xb, lhs=rows, rhs=flat)
+            y = self.down(silu_mul(gu), rhs=flat)
+        return combine(y.reshape(T * self.top_k, -1), inverse, sc).reshape(shape)
+
+
+__all__ = ["route", "expert_sort", "combine", "QExperts", "MoEBlock"]

@@ -8,6 +8,9 @@ every linear layer and the token embedding running through libmi355q:
   RoPE (theta from the config), grouped-query attention with scale
   head_dim**-0.5 and a causal mask, o_proj without bias;
 * MLP (qwen2.py:118-133): down(silu(gate(x)) * up(x)), no biases;
+* Qwen3 options (models/qwen3.py:47-117): explicit head_dim, no q/k/v bias,
+  per-head RMSNorm of q and k before RoPE; and the reference's top-k routed
+  expert MLP (models/lfm2.py:348-375, moe.MoEBlock) for Qwen3-MoE shapes;
 * block (qwen2.py:136-163): pre-norm RMSNorm, residual after attention and
   after the MLP; backbone (qwen2.py:166-196): embedding, layers, final RMSNorm;
 * LM head (qwen2.py:199-227): untied quantized linear (or the tied embedding's
@@ -40,6 +43,7 @@ import torch.nn.functional as F
 
 from . import core
 from .decode_ops import PagedKV, paged_decode_attention, rope_kv_append, silu_mul
+from .moe import MoEBlock, QExperts
 from .decode_ops import rms_norm as fused_rms_norm
 
 
@@ -56,10 +60,20 @@ class Qwen2Config:
     tie_word_embeddings: bool = False
     group_size: int = 64
     bits: int = 4
+    # Qwen3 variants (models/qwen3.py:47-66): explicit head_dim, no q/k/v
+    # bias, per-head RMSNorm of q and k; mixture-of-experts MLP (the
+    # reference's MoE block, models/lfm2.py:348-375) when num_experts > 0.
+    head_dim_: int = 0
+    attention_bias: bool = True
+    qk_norm: bool = False
+    num_experts: int = 0
+    num_experts_per_tok: int = 0
+    moe_intermediate_size: int = 0
+    norm_topk_prob: bool = True
 
     @property
     def head_dim(self) -> int:
-        return self.hidden_size // self.num_attention_heads
+        return self.head_dim_ or self.hidden_size // self.num_attention_heads
 
     @classmethod
     def qwen25_7b(cls, bits: int = 4) -> "Qwen2Config":
@@ -67,6 +81,16 @@ class Qwen2Config:
         return cls(hidden_size=3584, intermediate_size=18944, num_attention_heads=28,
                    num_key_value_heads=4, num_hidden_layers=28, vocab_size=152064,
                    rms_norm_eps=1e-6, rope_theta=1e6, bits=bits)
+
+    @classmethod
+    def qwen3_30b_a3b(cls, bits: int = 4) -> "Qwen2Config":
+        """Qwen3-30B-A3B: 48 layers, hidden 2048, 32 Q / 4 KV heads of 128, q/k norms,
+        128 experts, top 8 (renormalised), expert MLP 768, vocab 151936."""
+        return cls(hidden_size=2048, intermediate_size=6144, num_attention_heads=32,
+                   num_key_value_heads=4, num_hidden_layers=48, vocab_size=151936,
+                   rms_norm_eps=1e-6, rope_theta=1e6, bits=bits, head_dim_=128,
+                   attention_bias=False, qk_norm=True, num_experts=128,
+                   num_experts_per_tok=8, moe_intermediate_size=768, norm_topk_prob=True)
 
 
 class QLinear:
@@ -108,10 +132,22 @@ def _concat(parts: list[QLinear]) -> QLinear:
 class Layer:
     input_norm: torch.Tensor   # bfloat16 [hidden]
     post_norm: torch.Tensor    # bfloat16 [hidden]
-    qkv: QLinear               # [(heads + 2 kv_heads) * head_dim, hidden], with bias
+    qkv: QLinear               # [(heads + 2 kv_heads) * head_dim, hidden] (+ bias in Qwen2)
     o: QLinear                 # [hidden, heads * head_dim]
-    gate_up: QLinear           # [2 * intermediate, hidden]
-    down: QLinear              # [hidden, intermediate]
+    gate_up: QLinear | None = None   # [2 * intermediate, hidden] (dense MLP)
+    down: QLinear | None = None      # [hidden, intermediate]
+    q_norm: torch.Tensor | None = None   # bfloat16 [head_dim] (Qwen3)
+    k_norm: torch.Tensor | None = None
+    moe: MoEBlock | None = None          # replaces gate_up / down
+
+
+def _random_experts(gen, E, n_out, n_in, cfg, device, std=0.02) -> QExperts:
+    """E experts of [n_out, n_in], N(0, std), quantized per expert row."""
+    w = (torch.randn(E * n_out, n_in, generator=gen, device=device) * std).to(torch.bfloat16)
+    wq, s, b = core.quantize(w, cfg.group_size, cfg.bits)
+    del w
+    return QExperts(wq.reshape(E, n_out, -1), s.reshape(E, n_out, -1), b.reshape(E, n_out, -1),
+                    cfg.group_size, cfg.bits)
 
 
 def rope_tables(cfg: Qwen2Config, max_len: int, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -148,19 +184,34 @@ class Qwen2Model:
         h, d = cfg.hidden_size, cfg.head_dim
         res_std = 0.02 / math.sqrt(2 * cfg.num_hidden_layers)
         embed = _random_qlinear(gen, cfg.vocab_size, h, cfg, False, device)
+        bias = cfg.attention_bias
         layers = []
         for _ in range(cfg.num_hidden_layers):
-            q = _random_qlinear(gen, cfg.num_attention_heads * d, h, cfg, True, device)
-            k = _random_qlinear(gen, cfg.num_key_value_heads * d, h, cfg, True, device)
-            v = _random_qlinear(gen, cfg.num_key_value_heads * d, h, cfg, True, device)
+            q = _random_qlinear(gen, cfg.num_attention_heads * d, h, cfg, bias, device)
+            k = _random_qlinear(gen, cfg.num_key_value_heads * d, h, cfg, bias, device)
+            v = _random_qlinear(gen, cfg.num_key_value_heads * d, h, cfg, bias, device)
             o = _random_qlinear(gen, h, cfg.num_attention_heads * d, cfg, False, device,
                                 res_std)
-            gate = _random_qlinear(gen, cfg.intermediate_size, h, cfg, False, device)
-            up = _random_qlinear(gen, cfg.intermediate_size, h, cfg, False, device)
-            down = _random_qlinear(gen, h, cfg.intermediate_size, cfg, False, device, res_std)
             ones = torch.ones(h, dtype=torch.bfloat16, device=device)
-            layers.append(Layer(ones, ones.clone(), _concat([q, k, v]), o, _concat([gate, up]),
-                                down))
+            layer = Layer(ones, ones.clone(), _concat([q, k, v]), o)
+            if cfg.qk_norm:  # non-trivial norm weights, so the tests exercise them
+                layer.q_norm, layer.k_norm = (
+                    (1 + 0.1 * torch.randn(d, generator=gen, device=device)).to(torch.bfloat16)
+                    for _ in range(2))
+            if cfg.num_experts:
+                E, inter = cfg.num_experts, cfg.moe_intermediate_size
+                router = _random_qlinear(gen, E, h, cfg, False, device)
+                gate_up = _random_experts(gen, E, 2 * inter, h, cfg, device)  # gate | up rows
+                down = _random_experts(gen, E, h, inter, cfg, device, res_std)
+                layer.moe = MoEBlock(router, gate_up, down, cfg.num_experts_per_tok,
+                                     cfg.norm_topk_prob)
+            else:
+                gate = _random_qlinear(gen, cfg.intermediate_size, h, cfg, False, device)
+                up = _random_qlinear(gen, cfg.intermediate_size, h, cfg, False, device)
+                layer.gate_up = _concat([gate, up])
+                layer.down = _random_qlinear(gen, h, cfg.intermediate_size, cfg, False, device,
+                                             res_std)
+            layers.append(layer)
         final_norm = torch.ones(h, dtype=torch.bfloat16, device=device)
         lm_head = None if cfg.tie_word_embeddings else _random_qlinear(
             gen, cfg.vocab_size, h, cfg, False, device)
@@ -209,7 +260,7 @@ class Qwen2Model:
         (the final norm after the last layer)."""
         layer, eps = self.layers[li], self.cfg.rms_norm_eps
         x, h = fused_rms_norm(o, layer.post_norm, eps, residual=h)
-        m = layer.down(silu_mul(layer.gate_up(x)))
+        m = layer.moe(x) if layer.moe is not None else layer.down(silu_mul(layer.gate_up(x)))
         return fused_rms_norm(m, self._next_norm(li), eps, residual=h)
 
     # ------------------------------------------------------------ prefill
@@ -237,8 +288,12 @@ class Qwen2Model:
         for li, layer in enumerate(self.layers):
             qkv = layer.qkv(x)
             q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
-            q = apply_rope(q.float().reshape(B, T, nh, d).transpose(1, 2), cs, sn)
-            k = apply_rope(k.float().reshape(B, T, nkv, d).transpose(1, 2), cs, sn)
+            q, k = q.reshape(B, T, nh, d), k.reshape(B, T, nkv, d)
+            if layer.q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
+                q = fused_rms_norm(q, layer.q_norm, c.rms_norm_eps)
+                k = fused_rms_norm(k, layer.k_norm, c.rms_norm_eps)
+            q = apply_rope(q.float().transpose(1, 2), cs, sn)
+            k = apply_rope(k.float().transpose(1, 2), cs, sn)
             k = k.to(torch.bfloat16)
             v = v.reshape(B, T, nkv, d).transpose(1, 2)
             cache.write(li, slots, k.transpose(1, 2).reshape(B * T, nkv, d),
@@ -264,7 +319,8 @@ class Qwen2Model:
         h = self._embed(tok)
         x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
-            q = rope_kv_append(layer.qkv(x), pos, cache, li, cos, sin, nh)
+            q = rope_kv_append(layer.qkv(x), pos, cache, li, cos, sin, nh, layer.q_norm,
+                               layer.k_norm, c.rms_norm_eps)
             a = paged_decode_attention(q, cache, li, pos, d ** -0.5)
             x, h = self._ffn(li, h, layer.o(a))
         return self._head(x)

@@ -30,6 +30,43 @@ def _rms(x, w, eps):
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.float()
 
 
+def _deq_experts(mq, qe) -> torch.Tensor:
+    E, N = qe.wq.shape[:2]
+    return mq.dequantize(qe.wq.reshape(E * N, -1), qe.scales.reshape(E * N, -1),
+                         qe.biases.reshape(E * N, -1), qe.group_size, qe.bits
+                         ).float().reshape(E, N, -1)
+
+
+def moe_reference(mq, block, x, r=lambda t: t, indices=None):
+    """Float32 restatement of the routed expert MLP (models/lfm2.py:365-375,
+    SwitchGLU :193-218): softmax router, top-k, renormalised gates, per
+    expert down(silu(gate(x)) * up(x)), gate-weighted sum.  With indices
+    (int [T, k]) the routing choice is taken from there (the gates are still
+    recomputed here), which isolates the expert arithmetic from near-ties."""
+    shape = x.shape
+    xt = x.reshape(-1, shape[-1]).float()
+    gates = torch.softmax(_linear(mq, block.gate, xt), -1)
+    if block.expert_bias is not None:
+        gates = gates + block.expert_bias.float()
+    if indices is None:
+        indices = torch.topk(gates, block.top_k, -1).indices
+    indices = indices.long()
+    sc = gates.gather(-1, indices)
+    if block.norm_topk_prob:
+        sc = sc / (sc.sum(-1, keepdim=True) + 1e-20)
+    sc = r(sc)
+    wgu, wd = _deq_experts(mq, block.gate_up), _deq_experts(mq, block.down)
+    inter = wd.shape[-1]
+    out = torch.zeros_like(xt)
+    for j in range(block.top_k):
+        e = indices[:, j]
+        gu = r(torch.bmm(wgu[e], xt.unsqueeze(-1)).squeeze(-1))        # [T, 2I]
+        act = r(r(F.silu(gu[:, :inter])) * gu[:, inter:])
+        y = r(torch.bmm(wd[e], act.unsqueeze(-1)).squeeze(-1))         # [T, H]
+        out = out + r(y * sc[:, j:j + 1])
+    return out.reshape(shape)
+
+
 def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = False
                      ) -> torch.Tensor:
     """tokens [B, S] (positions 0..S-1) -> float32 logits [B, S, vocab], causal.
@@ -55,8 +92,12 @@ def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
         x = r(_rms(h, layer.input_norm, c.rms_norm_eps))
         qkv = r(_linear(mq, layer.qkv, x))
         q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
-        q = r(q2.apply_rope(q.reshape(B, S, nh, d).transpose(1, 2), cos, sin))
-        k = r(q2.apply_rope(k.reshape(B, S, nkv, d).transpose(1, 2), cos, sin))
+        q, k = q.reshape(B, S, nh, d), k.reshape(B, S, nkv, d)
+        if layer.q_norm is not None:  # Qwen3 per-head RMSNorm (models/qwen3.py:84-85)
+            q = r(_rms(q, layer.q_norm, c.rms_norm_eps))
+            k = r(_rms(k, layer.k_norm, c.rms_norm_eps))
+        q = r(q2.apply_rope(q.transpose(1, 2), cos, sin))
+        k = r(q2.apply_rope(k.transpose(1, 2), cos, sin))
         v = v.reshape(B, S, nkv, d).transpose(1, 2)
         rep = nh // nkv
         k, v = k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1)
@@ -64,6 +105,9 @@ def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
         a = r((torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B, S, nh * d))
         h = r(h + r(_linear(mq, layer.o, a)))
         x = r(_rms(h, layer.post_norm, c.rms_norm_eps))
+        if layer.moe is not None:
+            h = r(h + r(moe_reference(mq, layer.moe, x, r)))
+            continue
         gu = r(_linear(mq, layer.gate_up, x))
         act = r(r(F.silu(gu[..., :c.intermediate_size])) * gu[..., c.intermediate_size:])
         h = r(h + r(_linear(mq, layer.down, act)))

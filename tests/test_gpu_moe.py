@@ -1,0 +1,203 @@
+"""Mixture-of-experts routing kernels (moe.route / expert_sort / combine) and
+the routed expert block (moe.MoEBlock) against PyTorch restatements of the
+reference's MoE block (models/lfm2.py:348-375, SwitchGLU :193-218,
+_gather_sort/_scatter_unsort :613-622), and a Qwen3-MoE-shaped decoder
+against its float32 restatement.
+
+* route: the chosen expert sets equal torch.topk of the float32 softmax; the
+  gates (renormalised or not) are within one bfloat16 step.
+* expert_sort: bit-equal to torch.argsort(stable=True) and its inverse.
+* combine: bit-equal to the sequential float32 sum of bf16(y * score).
+* MoEBlock: norm-wise within 2e-2 of a float32 per-expert restatement with the
+  same routing choice (the activations in between are bfloat16).
+"""
+
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+from qwen2_reference import _linear, greedy_agreement, moe_reference, reference_logits
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def moe():
+    return importlib.import_module("mlx-server-runtime_amd.moe")
+
+
+@pytest.fixture(scope="module")
+def mq():
+    return importlib.import_module("mlx-server-runtime_amd")
+
+
+def _gen(seed):
+    return torch.Generator(device=DEV).manual_seed(seed)
+
+
+@pytest.mark.parametrize("T,E,k,norm", [(37, 128, 8, True), (8, 128, 8, True), (5, 8, 2, False),
+                                        (300, 60, 4, True), (3, 512, 16, False), (1, 4, 4, True)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_route(moe, T, E, k, norm, with_bias):
+    logits = (torch.randn(T, E, generator=_gen(E + T), device=DEV) * 2).to(torch.bfloat16)
+    bias = (torch.randn(E, generator=_gen(1), device=DEV) * 0.01) if with_bias else None
+    idx, sc = moe.route(logits, k, norm, bias)
+    gates = torch.softmax(logits.float(), -1)
+    if bias is not None:
+        gates = gates + bias
+    top = torch.topk(gates, k, -1)
+    assert idx.dtype == torch.int32 and idx.shape == (T, k)
+    assert torch.equal(torch.sort(idx.long(), -1).values, torch.sort(top.indices, -1).values)
+    ref = gates.gather(-1, idx.long())
+    if norm:
+        ref = ref / (ref.sum(-1, keepdim=True) + 1e-20)
+    assert bool(((sc.float() - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-7).all())
+    # descending gate order
+    assert bool((ref[:, :-1] >= ref[:, 1:]).all())
+
+
+@pytest.mark.parametrize("T,k,E", [(8, 8, 128), (4096, 8, 128), (77, 3, 17), (1, 1, 1),
+                                   (2000, 6, 512)])
+def test_expert_sort(moe, T, k, E):
+    ids = torch.randint(0, E, (T, k), generator=_gen(T + k), device=DEV, dtype=torch.int32)
+    sorted_ids, order, inverse, rows = moe.expert_sort(ids, E)
+    flat = ids.reshape(-1).long()
+    ref_order = torch.argsort(flat, stable=True)
+    assert torch.equal(order.long(), ref_order)
+    assert torch.equal(sorted_ids.long(), flat[ref_order])
+    assert torch.equal(inverse.long(), torch.argsort(ref_order, stable=True))
+    assert torch.equal(rows.long(), ref_order // k)
+
+
+def test_expert_sort_out_of_range_ids_go_last(moe):
+    ids = torch.tensor([[3, -1], [7, 0], [8, 3]], dtype=torch.int32, device=DEV)  # E = 8
+    sorted_ids, order, inverse, rows = moe.expert_sort(ids, 8)
+    assert sorted_ids.tolist() == [0, 3, 3, 7, -1, 8]
+    assert order.tolist() == [3, 0, 5, 2, 1, 4]
+    assert rows.tolist() == [1, 0, 2, 1, 0, 2]
+    assert torch.equal(order[inverse.long()].long(), torch.arange(6, device=DEV))
+
+
+@pytest.mark.parametrize("T,k,H", [(8, 8, 2048), (3, 2, 256), (513, 8, 2048), (2, 4, 8)])
+@pytest.mark.parametrize("sorted_rows", [True, False])
+def test_combine(moe, T, k, H, sorted_rows):
+    g = _gen(T * H + k)
+    y = torch.randn(T * k, H, generator=g, device=DEV).to(torch.bfloat16)
+    sc = torch.rand(T, k, generator=g, device=DEV).to(torch.bfloat16)
+    inverse = None
+    src = torch.arange(T * k, device=DEV)
+    if sorted_rows:
+        inverse = torch.randperm(T * k, generator=torch.Generator().manual_seed(T)).to(
+            device=DEV, dtype=torch.int32)
+        src = inverse.long()
+    out = moe.combine(y, inverse, sc)
+    rows = y[src].float().reshape(T, k, H)
+    acc = torch.zeros(T, H, device=DEV)
+    for j in range(k):
+        acc = acc + (rows[:, j] * sc[:, j:j + 1].float()).to(torch.bfloat16).float()
+    assert torch.equal(out, acc.to(torch.bfloat16))
+
+
+def _block(moe, mq, E, k, H, inter, seed=0):
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config(H, 4 * H, 4, 2, 1, 100)
+    g = _gen(seed)
+    router = q2._random_qlinear(g, E, H, cfg, False, DEV)
+    gate_up = q2._random_experts(g, E, 2 * inter, H, cfg, DEV)
+    down = q2._random_experts(g, E, H, inter, cfg, DEV)
+    return moe.MoEBlock(router, gate_up, down, k, True)
+
+
+@pytest.mark.parametrize("T", [3, 8, 512])
+def test_moe_block_vs_float32(moe, mq, T):
+    """T=3: 24 pairs (unsorted path); T=8: 64 pairs (sorted); T=512: 4096 pairs."""
+    E, k, H, inter = 16, 8, 256, 128
+    block = _block(moe, mq, E, k, H, inter)
+    x = torch.randn(T, H, generator=_gen(T), device=DEV).to(torch.bfloat16)
+    out = block(x)
+    idx, _ = moe.route(block.gate(x), k, True)
+    ref = moe_reference(mq, block, x, indices=idx)
+    err = float((out.float() - ref).abs().max() / ref.abs().max())
+    assert err < 2e-2, err
+    # the routing itself: the float32 router's choice matches except at near-ties
+    ref_idx = torch.topk(torch.softmax(_linear(mq, block.gate, x.float()), -1), k, -1).indices
+    same = (torch.sort(idx.long(), -1).values == torch.sort(ref_idx, -1).values).all(-1)
+    assert same.float().mean() >= 0.9
+
+
+def test_moe_block_sorted_equals_unsorted(moe, mq):
+    """Permutation equivariance (models/lfm2.py:202-218): rows routed through
+    the sorted path agree with the same rows through the unsorted path (the
+    kernels differ, so to rounding; a wrong permutation would be O(1))."""
+    E, k, H, inter = 16, 8, 256, 128
+    block = _block(moe, mq, E, k, H, inter, seed=3)
+    x = torch.randn(32, H, generator=_gen(4), device=DEV).to(torch.bfloat16)
+    full = block(x)                        # 256 pairs: sorted
+    parts = torch.cat([block(x[i:i + 2]) for i in range(0, 32, 2)])  # 16 pairs: unsorted
+    assert _nrel(full, parts) < 1e-2
+
+
+def _nrel(a, b):
+    return float((a.float() - b.float()).abs().max() / b.float().abs().max())
+
+
+def _per_position(a, b):
+    """Norm-wise relative error of every (row, position) logit vector."""
+    d = (a.float() - b.float()).abs().amax(-1)
+    return (d / b.float().abs().amax(-1)).flatten()
+
+
+def test_qwen3_moe_small_decoder(mq):
+    """Qwen3-MoE-shaped (q/k norms, 8 experts top 2, renormalised) decoder:
+    graph decode equals eager decode; prefill logits and greedy tokens against
+    the float32 restatement.  Routing is a discrete choice: where two experts'
+    gates nearly tie, the bfloat16 model and the float32 restatement can pick
+    different experts for a token, which moves that position's logits by
+    ~10 % (and, through its K/V, a few later ones).  So the bounds are on the
+    median and on the share of positions near the dense-model error (~1-2 %);
+    with top_k = num_experts (no choice) the error is the dense one."""
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config(256, 512, 4, 2, 2, 1000, head_dim_=64, attention_bias=False,
+                         qk_norm=True, num_experts=8, num_experts_per_tok=2,
+                         moe_intermediate_size=128)
+    m = q2.Qwen2Model.random(cfg, seed=5, device=DEV)
+    B, T, n = 4, 24, 16   # 4 * 2 = 8 pairs per decode step; prefill 192 pairs (sorted)
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=_gen(6), device=DEV)
+    steps = []
+    toks = m.generate(prompt, n, use_graph=False, logits_out=steps)
+    assert torch.equal(toks, m.generate(prompt, n))
+    full = torch.cat([prompt, toks], 1)[:, :-1]
+    ref = reference_logits(mq, m, full)
+    ours = m.prefill(full, m.new_cache(B, full.shape[1]), all_positions=True)
+    e_pre = _per_position(ours, ref)
+    e_dec = _per_position(torch.stack(steps, 1), ours[:, T - 1:T - 1 + n])
+    match, total, worst = greedy_agreement(ref, T, toks)
+    print(f"qwen3-moe small: prefill err median {e_pre.median():.4f}, "
+          f"{(e_pre <= 3e-2).float().mean():.2f} of positions <= 3e-2; decode err median "
+          f"{e_dec.median():.4f}; greedy {match}/{total}, worst margin {worst:.3f}")
+    assert e_pre.median() <= 2.5e-2 and (e_pre <= 3e-2).float().mean() >= 0.75
+    assert e_dec.median() <= 2e-2 and (e_dec <= 3e-2).float().mean() >= 0.75
+    assert match >= 0.8 * total and worst <= 0.3, (match, total, worst)
+
+
+def test_qwen3_dense_with_qk_norm_small_decoder(mq):
+    """The same decoder with a dense MLP (q/k norms only): dense-model bounds."""
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config(256, 512, 4, 2, 2, 1000, head_dim_=64, attention_bias=False,
+                         qk_norm=True)
+    m = q2.Qwen2Model.random(cfg, seed=5, device=DEV)
+    B, T, n = 2, 16, 16
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=_gen(7), device=DEV)
+    steps = []
+    toks = m.generate(prompt, n, use_graph=False, logits_out=steps)
+    full = torch.cat([prompt, toks], 1)[:, :-1]
+    ref = reference_logits(mq, m, full)
+    ours = m.prefill(full, m.new_cache(B, full.shape[1]), all_positions=True)
+    assert _per_position(ours, ref).max() <= 4e-2
+    assert _per_position(torch.stack(steps, 1), ours[:, T - 1:T - 1 + n]).max() <= 3e-2
+    match, total, worst = greedy_agreement(ref, T, toks)
+    assert match >= 0.9 * total and worst <= 0.05, (match, total, worst)

@@ -32,7 +32,8 @@ def test_header_declares_the_abi():
         "mq_version", "mq_last_error", "mq_quantize", "mq_dequantize", "mq_embedding_lookup",
         "mq_quantized_matmul", "mq_quantized_matmul_workspace", "mq_quantized_matmul_ws",
         "mq_gather_qmm", "mq_rms_norm", "mq_rope_kv_append",
-        "mq_paged_decode_attention_workspace", "mq_paged_decode_attention", "mq_silu_mul"])
+        "mq_paged_decode_attention_workspace", "mq_paged_decode_attention", "mq_silu_mul",
+        "mq_moe_route", "mq_moe_sort", "mq_moe_combine"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -101,10 +102,21 @@ def test_decoder_entry_validation(mq):
     assert att(null, null, null, null, 0, 16, 8, null, 2, 28, 4, 128, 1.0, null, 0, null,
                null) == -1                                                      # no pages
     rope = L.mq_rope_kv_append
-    assert rope(null, null, null, 4, 16, 8, null, null, null, null, null, 2, 28, 4, 127,
-                null) == -1                                                     # odd head_dim
-    assert rope(null, null, null, 4, 16, 8, null, null, null, null, null, 0, 28, 4, 128,
-                null) == 0
+    assert rope(null, null, null, 4, 16, 8, null, null, null, null, 1e-6, null, null, null, 2,
+                28, 4, 127, null) == -1                                         # odd head_dim
+    assert rope(null, null, null, 4, 16, 8, null, null, 1, null, 1e-6, null, null, null, 2,
+                28, 4, 256, null) == -2                                         # norm, d > 128
+    assert rope(null, null, null, 4, 16, 8, null, null, null, null, 1e-6, null, null, null, 0,
+                28, 4, 128, null) == 0
+    assert L.mq_moe_route(null, null, 4, 128, 8, 1, null, null, null) == -1    # null pointers
+    assert L.mq_moe_route(null, null, 4, 600, 8, 1, null, null, null) == -2    # too many experts
+    assert L.mq_moe_route(null, null, 4, 8, 9, 1, null, null, null) == -2      # k > E
+    assert L.mq_moe_route(null, null, 0, 128, 8, 1, null, null, null) == 0
+    assert L.mq_moe_sort(null, 64, 8, 128, null, null, null, null, null) == -1
+    assert L.mq_moe_sort(null, 64, 0, 128, null, null, null, null, null) == -1
+    assert L.mq_moe_sort(null, 0, 8, 128, null, null, null, null, null) == 0
+    assert L.mq_moe_combine(null, null, null, null, 4, 8, 2044, null) == -2    # hidden % 8
+    assert L.mq_moe_combine(null, null, null, null, 0, 8, 2048, null) == 0
 
 
 def test_capi_invalid_and_unsupported_codes(mq):
