@@ -234,18 +234,19 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     dev = x.device
     if rhs_indices is None:
         rhs_indices = torch.arange(E, device=dev).reshape(tuple(w.shape[:-2]))
-    if lhs_indices is None:
-        lhs_full = torch.arange(n_xb, device=dev).reshape(x_batch)
-    else:
-        lhs_full = lhs_indices
-    for name, t in (("lhs_indices", lhs_full), ("rhs_indices", rhs_indices)):
-        if t.dtype.is_floating_point or t.dtype == torch.bool:
+    for name, t in (("lhs_indices", lhs_indices), ("rhs_indices", rhs_indices)):
+        if t is not None and (t.dtype.is_floating_point or t.dtype == torch.bool):
             raise ValueError(f"[{op}] {name} must be an integer array, got {t.dtype}")
-    out_batch = torch.broadcast_shapes(tuple(lhs_full.shape), tuple(rhs_indices.shape))
+    lhs_shape = x_batch if lhs_indices is None else tuple(lhs_indices.shape)
+    out_batch = torch.broadcast_shapes(lhs_shape, tuple(rhs_indices.shape))
     T = math.prod(out_batch)
     rhs_flat = rhs_indices.expand(out_batch).reshape(-1).to(torch.int32).contiguous()
-    identity = lhs_indices is None and tuple(out_batch) == x_batch
-    lhs_flat = None if identity else lhs_full.expand(out_batch).reshape(-1).to(torch.int32).contiguous()
+    if lhs_indices is None and tuple(out_batch) == x_batch:
+        lhs_flat = None  # identity: batch t reads x batch t
+    else:
+        lhs_full = (torch.arange(n_xb, device=dev).reshape(x_batch) if lhs_indices is None
+                    else lhs_indices)
+        lhs_flat = lhs_full.expand(out_batch).reshape(-1).to(torch.int32).contiguous()
     xc = x.contiguous()
     y = torch.empty(tuple(out_batch) + (M, N), dtype=torch.bfloat16, device=dev)
     L = _lib.lib()

@@ -111,12 +111,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
 }
 
 // ---------------------------------------------------------------- RoPE + append
-// One sequence per block, one wave per head (q heads, then k heads), lane i
-// < d/2 holding the rotated pair (i, i + d/2).  qkv bf16 [B, (nh + 2 nkv) * d]
-// (q heads, k heads, v heads); q_out bf16 [B, nh, d]; cos/sin float32
-// [positions, d/2].  With q_norm / k_norm (Qwen3, qwen3.py:61-62,84-85) each
-// head is first RMS-normalised over d with that weight and rounded to
-// bfloat16, as nn.RMSNorm stores it.
+// Grid (B, ceil((nh + nkv) / 4) + 1), 256 threads.  Block (b, y) takes heads
+// 4y .. 4y+3 (q heads, then k heads), one wave per head, lane i < d/2 holding
+// the rotated pair (i, i + d/2); the last y copies the v heads.  qkv bf16
+// [B, (nh + 2 nkv) * d] (q heads, k heads, v heads); q_out bf16 [B, nh, d];
+// cos/sin float32 [positions, d/2].  With q_norm / k_norm (Qwen3,
+// qwen3.py:61-62,84-85) each head is first RMS-normalised over d with that
+// weight and rounded to bfloat16, as nn.RMSNorm stores it.
+constexpr int kRopeHeadsPerBlock = kThreads / 64;
+
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(
     const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
     const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
@@ -128,36 +131,39 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
   const int64_t p = clamp_index(pos[b], (int64_t)pages_per_seq * page_size);
   const int64_t page = clamp_index(page_table[b * pages_per_seq + p / page_size], num_pages);
   const int64_t slot = page * page_size + p % page_size;
-  const int half = d / 2;
   const uint16_t* row = qkv + b * (int64_t)(nh + 2 * nkv) * d;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int hh = wave; hh < nh + nkv; hh += kThreads / 64) {
-    const uint16_t* norm = hh < nh ? q_norm : k_norm;
-    uint16_t* dst = hh < nh ? q_out + (b * nh + hh) * (int64_t)d
-                            : k_pages + (slot * nkv + (hh - nh)) * (int64_t)d;
-    for (int i0 = 0; i0 < half; i0 += 64) {  // one pass for d <= 128
-      const int i = i0 + lane;
-      float x1 = 0.f, x2 = 0.f;
+  if ((int)blockIdx.y * kRopeHeadsPerBlock >= nh + nkv) {  // the v heads
+    for (int e = threadIdx.x; e < nkv * d; e += kThreads)
+      v_pages[slot * nkv * (int64_t)d + e] = row[(nh + nkv) * d + e];
+    return;
+  }
+  const int half = d / 2;
+  const int lane = threadIdx.x & 63;
+  const int hh = blockIdx.y * kRopeHeadsPerBlock + (threadIdx.x >> 6);
+  if (hh >= nh + nkv) return;  // whole waves
+  const uint16_t* norm = hh < nh ? q_norm : k_norm;
+  uint16_t* dst = hh < nh ? q_out + (b * nh + hh) * (int64_t)d
+                          : k_pages + (slot * nkv + (hh - nh)) * (int64_t)d;
+  for (int i0 = 0; i0 < half; i0 += 64) {  // one pass for d <= 128
+    const int i = i0 + lane;
+    float x1 = 0.f, x2 = 0.f;
+    if (i < half) {
+      x1 = bf16_bits_to_f32(row[hh * d + i]);
+      x2 = bf16_bits_to_f32(row[hh * d + i + half]);
+    }
+    if (norm) {  // uniform per wave; d <= 128 so the head is this one pass
+      const float inv = rsqrtf(wave_sum(fmaf(x1, x1, x2 * x2)) / (float)d + eps);
       if (i < half) {
-        x1 = bf16_bits_to_f32(row[hh * d + i]);
-        x2 = bf16_bits_to_f32(row[hh * d + i + half]);
-      }
-      if (norm) {  // uniform per wave; d <= 128 so the head is this one pass
-        const float inv = rsqrtf(wave_sum(fmaf(x1, x1, x2 * x2)) / (float)d + eps);
-        if (i < half) {
-          x1 = bf16r(x1 * inv * bf16_bits_to_f32(norm[i]));
-          x2 = bf16r(x2 * inv * bf16_bits_to_f32(norm[i + half]));
-        }
-      }
-      if (i < half) {
-        const float c = cos_t[p * half + i], sn = sin_t[p * half + i];
-        dst[i] = (uint16_t)f32_to_bf16_bits(x1 * c - x2 * sn);
-        dst[i + half] = (uint16_t)f32_to_bf16_bits(x2 * c + x1 * sn);
+        x1 = bf16r(x1 * inv * bf16_bits_to_f32(norm[i]));
+        x2 = bf16r(x2 * inv * bf16_bits_to_f32(norm[i + half]));
       }
     }
+    if (i < half) {
+      const float c = cos_t[p * half + i], sn = sin_t[p * half + i];
+      dst[i] = (uint16_t)f32_to_bf16_bits(x1 * c - x2 * sn);
+      dst[i + half] = (uint16_t)f32_to_bf16_bits(x2 * c + x1 * sn);
+    }
   }
-  for (int e = threadIdx.x; e < nkv * d; e += kThreads)
-    v_pages[slot * nkv * (int64_t)d + e] = row[(nh + nkv) * d + e];
 }
 
 // ---------------------------------------------------------------- attention
@@ -377,14 +383,24 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   reinterpret_cast<u32x4_t*>(out + r * inter)[u] = o;
 }
 
-// Positions per split: a multiple of 32, at most kMaxChunk, and enough
-// splits for about 1024 blocks over the chip.
-int attn_chunk(int64_t B, int nkv, int64_t capacity) {
+// Blocks of attn_split_kernel<REP, 128> one CU holds at once (4-wave blocks;
+// waves per SIMD as the register count allows).
+int attn_blocks_per_cu(int rep) {
+  static const int occ[9] = {0, 8, 5, 4, 4, 4, 2, 3, 2};
+  return occ[rep < 1 ? 1 : rep > 8 ? 8 : rep];
+}
+
+// Positions per split: whole tile passes (64 positions at head_dim 128), at
+// most kMaxChunk, and as many splits as keep every CU busy in one round of
+// blocks (a split is latency-bound, so a second round costs a full split).
+int attn_chunk(int64_t B, int nkv, int rep, int d, int64_t capacity) {
+  const int64_t pass = (int64_t)(kThreads / (d / 8)) * kTile;
   const int64_t blocks = B * nkv;
-  int64_t splits = (1024 + blocks - 1) / blocks;
-  splits = std::max<int64_t>(1, std::min<int64_t>(splits, (capacity + 31) / 32));
+  const int64_t target = 256 * (int64_t)attn_blocks_per_cu(rep);
+  int64_t splits = std::max<int64_t>(1, target / blocks);
+  splits = std::min<int64_t>(splits, (capacity + pass - 1) / pass);
   int64_t chunk = (capacity + splits - 1) / splits;
-  chunk = (chunk + 31) / 32 * 32;
+  chunk = (chunk + pass - 1) / pass * pass;
   return (int)std::min<int64_t>(chunk, kMaxChunk);
 }
 
@@ -400,7 +416,7 @@ bool decode_attention_supported(int nh, int nkv, int d) {
 
 size_t decode_attention_workspace(int64_t B, int nh, int nkv, int d, int64_t capacity) {
   const int rep = nh / nkv;
-  const int64_t chunk = attn_chunk(B, nkv, capacity);
+  const int64_t chunk = attn_chunk(B, nkv, rep, d, capacity);
   const int64_t splits = (capacity + chunk - 1) / chunk;
   return (size_t)(B * nkv * splits * rep * (d + 2)) * sizeof(float);
 }
@@ -422,7 +438,9 @@ hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int
                               uint16_t* v_pages, int64_t B, int nh, int nkv, int d,
                               hipStream_t stream) {
   if (B == 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)B), dim3(kThreads), 0, stream, qkv, pos,
+  const unsigned head_blocks = (unsigned)((nh + nkv + kRopeHeadsPerBlock - 1) / kRopeHeadsPerBlock);
+  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)B, head_blocks + 1), dim3(kThreads), 0,
+                     stream, qkv, pos,
                      page_table, (int)pages_per_seq, (int)page_size, (int)num_pages, cos_t, sin_t,
                      q_norm, k_norm, eps, q_out, k_pages, v_pages, nh, nkv, d);
   return hipGetLastError();
@@ -471,7 +489,7 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
                                    hipStream_t stream) {
   if (B == 0) return hipSuccess;
   const int64_t capacity = pages_per_seq * page_size;
-  const int chunk = attn_chunk(B, nkv, capacity);
+  const int chunk = attn_chunk(B, nkv, nh / nkv, d, capacity);
   const int splits = (int)((capacity + chunk - 1) / chunk);
   if (d == 64)
     return launch_attention_d<64>(q, k_pages, v_pages, page_table, (int)pages_per_seq,

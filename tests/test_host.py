@@ -67,14 +67,15 @@ def test_attention_workspace_query(mq):
     """Float32 partials (max, sum, 128 weighted values per query head) per
     (sequence, KV head, split of the positions)."""
     q = _L(mq).mq_paged_decode_attention_workspace
-    per_split = 28 * (128 + 2) * 4
+    per_split = 7 * (128 + 2) * 4                # one KV head's 7 query heads
     bs1 = q(1, 28, 4, 128, 40, 16)             # 640 positions
     assert bs1 > 0 and bs1 % (4 * per_split) == 0
     splits = bs1 // (4 * per_split)
-    assert 1 < splits <= 40                      # split over blocks, >= 16 positions each
+    assert 1 < splits <= 10                      # split over blocks, >= 64 positions each
     bs32 = q(32, 28, 4, 128, 80, 16)
     assert bs32 > 0 and bs32 % (32 * 4 * per_split) == 0
-    assert q(1, 28, 4, 64, 40, 16) == bs1 // 130 * 66   # head_dim 64: 64 + 2 floats per head
+    d64 = q(1, 28, 4, 64, 40, 16)                # head_dim 64: 64 + 2 floats per head
+    assert d64 > 0 and d64 % (4 * 7 * 66 * 4) == 0
     assert q(1, 28, 4, 96, 40, 16) == 0          # head_dim 96: unsupported
     assert q(1, 36, 4, 128, 40, 16) == 0         # 9 query heads per KV head
     assert q(0, 28, 4, 128, 40, 16) == 0
