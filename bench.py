@@ -238,13 +238,15 @@ def sweep(mq, torch):
                 gen = torch.Generator(device="cuda:0").manual_seed(1)
                 x = torch.randn(M, K, generator=gen, device="cuda:0").to(torch.bfloat16)
                 flops = 2.0 * M * N * K
-                n_launch = 32 if flops < 2e11 else 8
+                # a graph replay has a fixed start-up latency (~0.15 ms): replay
+                # enough launches that it stays under 1 % of the timed region
+                n_launch, replays = (64, 4) if flops < 2e11 else (8, 4)
 
                 def launch(i, x=x, reps=reps):
                     wq, s, b = reps[i % len(reps)]
                     mq.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits=bits)
 
-                ms, _ = time_graph(torch, launch, n_launch, warmup=2)
+                ms, _ = time_graph(torch, launch, n_launch, warmup=2, reps=replays)
                 by = alg_bytes(M, N, K, bits)
                 gbs = by / (ms * 1e-3) / 1e9
                 tfl = flops / (ms * 1e-3) / 1e12
@@ -256,7 +258,8 @@ def sweep(mq, torch):
                 if bits == 4 and M >= 128:
                     # For scale: a dense bf16 GEMM of the same shape through
                     # torch.matmul (hipBLASLt) on the dequantized weights.
-                    dms, _ = time_graph(torch, lambda i, x=x: torch.matmul(x, wdt), n_launch, warmup=2)
+                    dms, _ = time_graph(torch, lambda i, x=x: torch.matmul(x, wdt), n_launch,
+                                        warmup=2, reps=replays)
                     row["dense_bf16_us"] = round(dms * 1e3, 2)
                     row["dense_bf16_TFLOPs"] = round(flops / (dms * 1e-3) / 1e12, 2)
                 rows.append(row)
@@ -270,7 +273,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
-              "(the path has no multi-GPU component; see DESIGN.md for how it would shard).",
+              "(the path has no multi-GPU component; it would shard by heads, K groups and "
+              "experts across one process per GPU).",
               file=sys.stderr)
         sys.exit(2)
     import torch

@@ -7,7 +7,7 @@ Bars:
   max|y - ref| / max|ref| <= 1e-2 (bfloat16 output, float32 accumulation),
   where ref is the oracle's double-precision contraction with the exact
   dequantized weights.  TOL below is that bound.
-Full BASELINE-sized shapes are checked directly where the oracle is fast
+Full-size shapes (the 7B layer widths) are checked directly where the oracle is fast
 (M = 1) and on a sample of rows otherwise (rows of the output depend only on
 their own row of x).
 """
