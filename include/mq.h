@@ -93,8 +93,9 @@ int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* sca
 
 /*
  * Workspace, in bytes, that mq_quantized_matmul_ws can use for this shape
- * (0 = none).  Shapes with few output columns and a long K (the down
- * projection at small M) split K over blocks and need float32 partial sums.
+ * (0 = none).  Shapes whose output tiles cannot fill the GPU and have a long
+ * K (the down projection at small M, and at M = 1-2K prefill chunks) split K
+ * over blocks and need float32 partial sums.
  * MLX allocates such temporaries internally; this library allocates nothing,
  * so the caller provides them.  No counterpart in the reference: it serves
  * the same mx.quantized_matmul call sites as mq_quantized_matmul.

@@ -45,10 +45,17 @@ hipError_t launch_qmm2(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
 
 // 256x256-tile MFMA path with weights dequantized in registers (qmm3_fits:
 // K a multiple of 512, >= 128 tiles, 32-bit offsets).
+// Few tiles and a long K: K is split over blocks through a float32 workspace
+// of qmm3_workspace_bytes (without it the launch runs unsplit).
 bool qmm3_fits(int64_t M, int64_t N, int64_t K, int bits);
+size_t qmm3_workspace_bytes(int64_t M, int64_t N, int64_t K);
 hipError_t launch_qmm3(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, hipStream_t stream);
+                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+// y[i] = bf16(sum over s < splits of partial[s * MN + i] (in order) + bias[i % N])
+hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t* bias,
+                                uint16_t* y, int64_t MN, int64_t N, hipStream_t stream);
 
 // Skinny MFMA path (M up to a few hundred): weights streamed once per M tile
 // of up to 128 rows; K split over blocks through a float32 workspace when the

@@ -25,6 +25,8 @@
 //   column and array) are DMA-ed into LDS three steps before they are needed.
 // One barrier per step; the wait before it covers the DMAs of earlier steps
 // (the next step's x tile), never those issued in the current step.
+#include <algorithm>
+
 #include "mq_common.h"
 #include "mq_internal.h"
 
@@ -94,8 +96,8 @@ template <int BITS>
 __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
-    int tiles_m) {
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
+    int M, int N, int K, int tiles_m, int tiles, int chunks_per_split) {
   extern __shared__ u32x4_t smem[];
   char* const lds = reinterpret_cast<char*>(smem);
   const int tid = threadIdx.x;
@@ -108,12 +110,17 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
   const int nblk = gridDim.x;
   const int per_xcd = nblk / 8, rem = nblk % 8;
   const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  const int tile = (xcd < rem ? xcd * (per_xcd + 1) : rem * (per_xcd + 1) + (xcd - rem) * per_xcd) + slot;
+  const int idx = (xcd < rem ? xcd * (per_xcd + 1) : rem * (per_xcd + 1) + (xcd - rem) * per_xcd) + slot;
+  // With K split, idx = split * tiles + tile: a split's blocks are contiguous.
+  const int tile = idx % tiles, split = idx / tiles;
   const int bm = tile % tiles_m, bn = tile / tiles_m;
   const int m0 = bm * BM, n0 = bn * BN;
 
   const int G = K / kGroup;
   const int KT = K / BK;
+  const int c_begin = split * chunks_per_split;
+  const int c_end = min(KT / kSbChunk, c_begin + chunks_per_split);
+  const int kt0 = c_begin * kSbChunk;
   const rsrc_t xrs = make_rsrc(x, (uint64_t)M * K * 2);
   const rsrc_t wrs = make_rsrc(wq, (uint64_t)N * K * BITS / 8);
   const rsrc_t srs = make_rsrc((wave & 1) ? biases : scales, (uint64_t)N * G * 2);
@@ -191,22 +198,23 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
     }
   };
 
-  // ---- prologue: scale chunk 0, x steps 0 and 1, codes of step 0 ----
-  load_codes(cw[0], 0);
-  dma_sb(0, 0);
-  dma_x(0, 0);
-  dma_x(1, 1);
+  // ---- prologue: this split's first scale chunk, x of its first two steps,
+  // codes of its first step ----
+  load_codes(cw[0], kt0);
+  dma_sb(c_begin, c_begin & 1);
+  dma_x(kt0, 0);
+  dma_x(kt0 + 1, 1);
   step_barrier<4>();
   // B fragments of k-slice 0 are always dequantized one step early, at the end
   // of the previous step, so each step opens with MFMAs instead of VALU.
   GroupAffine ga[2];
-  read_sb(0, 0, ga);
+  read_sb(c_begin & 1, 0, ga);
   bf16x8_t b0[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
 
   int st = 0;  // stage holding x of the current step
-  for (int c = 0; c < KT / kSbChunk; ++c) {
+  for (int c = c_begin; c < c_end; ++c) {
 #pragma unroll
     for (int u = 0; u < kSbChunk; ++u) {
       const int kt = c * kSbChunk + u;
@@ -258,47 +266,77 @@ __global__ __launch_bounds__(kThreads, 1) void qmm3_kernel(
   // block's LDS is released.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4 ----
+  // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4;
+  // a split of K writes float32 partial sums instead ----
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + wn * 64 + j * 32 + (l & 31);
     if (n >= N) continue;
-    const float add = bias ? bf16_bits_to_f32(bias[n]) : 0.f;
+    const float add = (bias && !partial) ? bf16_bits_to_f32(bias[n]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
-        if (m < M) y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][v] + add);
+        if (m >= M) continue;
+        if (partial) partial[((int64_t)split * M + m) * N + n] = acc[i][j][v];
+        else y[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(acc[i][j][v] + add);
       }
     }
   }
+}
+
+// K splits for a launch: 1 when the tiles fill one round of the GPU (one
+// block per CU); otherwise the most splits that keep the grid within one
+// round, each at least 4 scale chunks (2048 K) long.
+int qmm3_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  constexpr int64_t kRound = 256;
+  if (tiles >= kRound / 2) return 1;
+  const int64_t chunks = K / (kSbChunk * kGroup);
+  return (int)std::max<int64_t>(1, std::min(kRound / tiles, chunks / 4));
 }
 
 }  // namespace
 
 bool qmm3_fits(int64_t M, int64_t N, int64_t K, int bits) {
   // 32-bit buffer offsets (with room for the kOutOfRange marker) for x, the
-  // codes and the scales; whole 8-group scale chunks; >= 128 tiles.
+  // codes and the scales; whole 8-group scale chunks; >= 128 tiles, or >= 32
+  // when K is long enough to split over blocks.
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int64_t lim = (int64_t)1 << 31;
   return K % (kSbChunk * kGroup) == 0 && M * K * 2 < lim && N * K * bits / 8 < lim &&
-         N * (K / kGroup) * 2 < lim && tiles >= 128 && tiles < lim;
+         N * (K / kGroup) * 2 < lim && tiles < lim &&
+         (tiles >= 128 || (tiles >= 32 && qmm3_splits(M, N, K) * tiles >= 128));
+}
+
+size_t qmm3_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  const int S = qmm3_splits(M, N, K);
+  return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
 }
 
 hipError_t launch_qmm3(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, hipStream_t stream) {
+                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  const int tiles = tiles_m * tiles_n;
+  const int chunks = (int)(K / (kSbChunk * kGroup));
+  int S = qmm3_splits(M, N, K);
+  if (S > 1 && (!workspace || workspace_bytes < qmm3_workspace_bytes(M, N, K))) S = 1;
+  const int per = (chunks + S - 1) / S;
+  S = (chunks + per - 1) / per;
+  float* part = S > 1 ? static_cast<float*>(workspace) : nullptr;
+  const dim3 grid((unsigned)(tiles * S));
   auto kern = bits == 4 ? qmm3_kernel<4> : qmm3_kernel<8>;
   const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), kLds, stream, x, wq, scales, biases, bias, y,
-                     (int)M, (int)N, (int)K, tiles_m);
-  return hipGetLastError();
+                     part, (int)M, (int)N, (int)K, tiles_m, tiles, per);
+  if (S == 1) return hipGetLastError();
+  return launch_splitk_reduce(part, S, bias, y, M * N, N, stream);
 }
 
 }  // namespace mq

@@ -280,6 +280,13 @@ hipError_t run_mi(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
 
 }  // namespace
 
+hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t* bias,
+                                uint16_t* y, int64_t MN, int64_t N, hipStream_t stream) {
+  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream,
+                     partial, splits, bias, y, MN, (int)N);
+  return hipGetLastError();
+}
+
 bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits) {
   const int64_t lim = (int64_t)1 << 31;
   // whole 8-group chunks; 32-bit offsets with room for the tiles' overhang

@@ -57,7 +57,8 @@ def test_workspace_query(mq):
     assert down > 0 and down % (64 * 3584 * 4) == 0
     assert q(128, 18944, 3584, 64, 4) == 0    # 148 column tiles: no split
     assert q(1, 3584, 18944, 64, 4) == 0      # GEMV
-    assert q(4096, 3584, 18944, 64, 4) == 0   # large-M kernels
+    assert q(4096, 3584, 18944, 64, 4) == 0   # large-M kernels, 224 tiles: no split
+    assert q(2048, 3584, 18944, 64, 4) == 2 * 2048 * 3584 * 4   # 112 tiles: K in 2
     assert q(64, 3584, 18944, 64, 3) == 0     # unsupported bits
     assert q(64, 3584, 18900, 64, 4) == 0     # K not a group multiple
     assert q(0, 3584, 18944, 64, 4) == 0
