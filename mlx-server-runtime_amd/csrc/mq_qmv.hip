@@ -35,6 +35,8 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kQmvLdsBudget = 48 * 1024;
+// Two rows per lane group may use up to 52 KiB: still 3 blocks per CU.
+constexpr int kTwoRowLdsBudget = 52 * 1024;
 // Scale + bias DMA operations per wave: 2 arrays of ceil((RPB*G + GP) / 2)
 // words, at most 16 64-word operations each (RPB*G <= 2048 entries: a block
 // owns at most 256 * 8 chunks), over 4 waves.
@@ -362,6 +364,19 @@ int pick_tpr(int64_t C, int64_t N, int64_t T) {
   return kTprs[pick];
 }
 
+// R = 2 needs its scales to fit the block's LDS DMA budget (RPB * G + GP
+// entries per array, kSbOpsPerWave operations per wave) and the LDS budget.
+bool two_rows(int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t T) {
+  const int epc = 128 / bits;
+  const int64_t C = K / epc, G = K / kGroup;
+  const int64_t CP = (C + tpr - 1) / tpr * tpr, GP = CP / (kGroup / epc);
+  const int64_t rpb = (kBlock / tpr) * 2;
+  const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int64_t sb_words = (rpb * G + GP + 1) / 2;
+  return 2 * ((sb_words + 63) / 64) <= kSbOpsPerWave * (kBlock / 64) &&
+         lds_bytes(bits, tpr, mt, K, 2) <= kTwoRowLdsBudget && (N + rpb - 1) / rpb * T >= 512;
+}
+
 template <int BITS>
 hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
@@ -389,6 +404,11 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
       if (slots <= 5) return run_mt<BITS, 64, 1, 5>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return run_mt<BITS, 64, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
     case 128:
+      // Two rows per lane group when that still leaves 512 blocks: a block
+      // stages all of x (long rows: up to 40 KB), so rows per block divide
+      // that L2 traffic (the down projection: 2.1x less x than weights).
+      if (slots <= 5 && two_rows(BITS, 128, M, N, K, g.T))
+        return run_mt<BITS, 128, 2, 5>(x, wq, s, b, bias, y, M, N, K, g, stream);
       if (slots <= 5) return run_mt<BITS, 128, 1, 5>(x, wq, s, b, bias, y, M, N, K, g, stream);
       return run_mt<BITS, 128, 1, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
     default:
