@@ -202,6 +202,24 @@ int mq_paged_decode_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq
                               hipStream_t stream);
 
 /*
+ * One decode step of a layer's attention after its QKV projection:
+ * mq_rope_kv_append followed by mq_paged_decode_attention (same arguments and
+ * results, bit for bit) with the RoPE (and Qwen3's q/k norms) and the append
+ * of k and v done inside the attention's split kernel -- two launches instead
+ * of three.  Replaces the part of Qwen2Attention.__call__ after the
+ * projections (models/qwen2.py:93-113): rope +
+ * PagedLayerAttentionContext.append_and_attend (attention.py:206-298).  The
+ * workspace is mq_paged_decode_attention_workspace() bytes.
+ */
+int mq_decode_attention_step(const mq_bf16* qkv, const int64_t* positions,
+                             const int32_t* page_table, int64_t pages_per_seq, int64_t page_size,
+                             int64_t num_pages, const float* cos_table, const float* sin_table,
+                             const mq_bf16* q_norm, const mq_bf16* k_norm, float norm_eps,
+                             mq_bf16* k_pages, mq_bf16* v_pages, int64_t batch, int n_heads,
+                             int n_kv_heads, int head_dim, float scale, void* workspace,
+                             size_t workspace_bytes, mq_bf16* out, hipStream_t stream);
+
+/*
  * silu(gate) * up of the MLP (models/qwen2.py:43-44,132-133) on the fused
  * gate|up projection: gate_up bfloat16 [rows, 2 * inter], out bfloat16
  * [rows, inter] = bf16(bf16(gate * sigmoid(gate)) * up).  inter % 8 == 0.

@@ -362,6 +362,41 @@ int mq_paged_decode_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq
                     op);
 }
 
+int mq_decode_attention_step(const mq_bf16* qkv, const int64_t* positions,
+                             const int32_t* page_table, int64_t pages_per_seq, int64_t page_size,
+                             int64_t num_pages, const float* cos_table, const float* sin_table,
+                             const mq_bf16* q_norm, const mq_bf16* k_norm, float norm_eps,
+                             mq_bf16* k_pages, mq_bf16* v_pages, int64_t batch, int n_heads,
+                             int n_kv_heads, int head_dim, float scale, void* workspace,
+                             size_t workspace_bytes, mq_bf16* out, hipStream_t stream) {
+  const char* op = "decode_attention_step";
+  if (int rc = check_pages(op, batch, n_heads, n_kv_heads, pages_per_seq, page_size, num_pages))
+    return rc;
+  if (!mq::decode_attention_supported(n_heads, n_kv_heads, head_dim))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] head_dim=%d with %d query heads per KV head is not supported (64 or 128; "
+                "1-8).",
+                op, head_dim, n_kv_heads > 0 ? n_heads / n_kv_heads : 0);
+  if (batch == 0) return ok();
+  const size_t need = mq::decode_attention_workspace(batch, n_heads, n_kv_heads, head_dim,
+                                                     pages_per_seq * page_size);
+  if (!workspace || workspace_bytes < need)
+    return fail(MQ_ERR_INVALID, "[%s] the workspace needs %zu bytes, got %zu.", op, need,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!qkv || !positions || !page_table || !cos_table || !sin_table || !k_pages || !v_pages ||
+      !out)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(qkv) || !aligned16(k_pages) || !aligned16(v_pages) || !aligned16(workspace))
+    return fail(MQ_ERR_INVALID, "[%s] qkv, the pages and the workspace must be 16-byte aligned.",
+                op);
+  return hip_status(mq::launch_attention_step(qkv, positions, page_table, pages_per_seq,
+                                              page_size, num_pages, cos_table, sin_table, q_norm,
+                                              k_norm, norm_eps, k_pages, v_pages, batch, n_heads,
+                                              n_kv_heads, head_dim, scale,
+                                              static_cast<float*>(workspace), out, stream),
+                    op);
+}
+
 int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inter,
                 hipStream_t stream) {
   const char* op = "silu_mul";

@@ -181,44 +181,30 @@ constexpr int kMaxChunk = 512;
 constexpr int kTile = 4;
 constexpr float kNoScore = -1e30f;  // running max before the first position
 
+// Shared memory of one split block.
 template <int REP, int D>
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pages,
-    const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table,
-    int pages_per_seq, int page_size, int num_pages, const int64_t* __restrict__ pos,
-    float* __restrict__ part, int nkv, int chunk, float scale_log2) {
-  constexpr int LANES = D / 8;               // lanes per cached row
-  constexpr int GROUPS = kThreads / LANES;   // positions per pass of the block
+struct AttnShared {
+  __align__(16) uint16_t fresh[2][D];  // the new position's K and V rows (attn_step)
+  int32_t slot_of[kMaxChunk];
+  float mrg_m[kThreads / 64][REP], mrg_s[kThreads / 64][REP];
+  float mrg_a[kThreads / 64][REP][D];
+};
+
+// The split's partials from this lane's q fragments (qv: its 8 dims of each
+// query head, bf16 pairs) over positions l0 + [0, n) of the KV head rows kb /
+// vb (element pointers at this lane's 8 dims; row r at r * row_elems).
+// Position `fresh` of the split (or -1) takes its K / V row from sh.fresh
+// instead of the cache.  Writes pm[REP], ps[REP], pa[REP][D].
+template <int REP, int D>
+__device__ __forceinline__ void attn_block(const u32x4_t (&qv)[REP], AttnShared<REP, D>& sh, int n,
+                                           const uint16_t* kb, const uint16_t* vb,
+                                           int64_t row_elems, float scale_log2, int fresh,
+                                           float* pm, float* ps, float* pa) {
+  constexpr int LANES = D / 8;
+  constexpr int GROUPS = kThreads / LANES;
   constexpr int WAVES = kThreads / 64;
-  __shared__ int32_t slot_of[kMaxChunk];
-  __shared__ float mrg_m[WAVES][REP], mrg_s[WAVES][REP];
-  __shared__ float mrg_a[WAVES][REP][D];
-  const int split = blockIdx.x, kvh = blockIdx.y;
-  const int64_t b = blockIdx.z;
-  const int splits = gridDim.x;
-  const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
-  const int l0 = split * chunk;
-  const int n = min(L - l0, chunk);
-  if (n <= 0) return;  // past the sequence's end
-  float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
-  float* ps = pm + REP;
-  float* pa = ps + REP;
-  const int32_t* table = page_table + b * pages_per_seq;
-  for (int i = threadIdx.x; i < n; i += kThreads) {
-    const int l = l0 + i;
-    slot_of[i] = (int32_t)(clamp_index(table[l / page_size], num_pages) * page_size +
-                           l % page_size);
-  }
   const int sub = threadIdx.x % LANES, grp = threadIdx.x / LANES;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nh = nkv * REP;
-  // this lane's 8 dims of every query head, as bf16 pairs
-  u32x4_t qv[REP];
-#pragma unroll
-  for (int r = 0; r < REP; ++r)
-    qv[r] = reinterpret_cast<const u32x4_t*>(q + (b * nh + kvh * REP + r) * (int64_t)D)[sub];
-  __syncthreads();
-
   float m[REP], s[REP], acc[REP][8];
 #pragma unroll
   for (int r = 0; r < REP; ++r) {
@@ -227,17 +213,18 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
   }
-  const int64_t row_elems = (int64_t)nkv * D;
-  const uint16_t* kb = k_pages + kvh * D + sub * 8;
-  const uint16_t* vb = v_pages + kvh * D + sub * 8;
   for (int t0 = 0; t0 < n; t0 += GROUPS * kTile) {
     u32x4_t kr[kTile], vr[kTile];
 #pragma unroll
     for (int u = 0; u < kTile; ++u) {
       const int i = min(t0 + grp + GROUPS * u, n - 1);
-      const int64_t off = (int64_t)slot_of[i] * row_elems;
+      const int64_t off = (int64_t)sh.slot_of[i] * row_elems;
       kr[u] = *reinterpret_cast<const u32x4_t*>(kb + off);
       vr[u] = *reinterpret_cast<const u32x4_t*>(vb + off);
+      if (i == fresh) {
+        kr[u] = reinterpret_cast<const u32x4_t*>(sh.fresh[0])[sub];
+        vr[u] = reinterpret_cast<const u32x4_t*>(sh.fresh[1])[sub];
+      }
     }
     float x[kTile][REP];
 #pragma unroll
@@ -305,25 +292,25 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) mrg_a[wave][r][8 * sub + t] = acc[r][t];
+      for (int t = 0; t < 8; ++t) sh.mrg_a[wave][r][8 * sub + t] = acc[r][t];
       if (lane == 0) {
-        mrg_m[wave][r] = m[r];
-        mrg_s[wave][r] = s[r];
+        sh.mrg_m[wave][r] = m[r];
+        sh.mrg_s[wave][r] = s[r];
       }
     }
   }
   __syncthreads();
   for (int e = threadIdx.x; e < REP * D; e += kThreads) {
     const int r = e / D, dd = e % D;
-    float mx = mrg_m[0][r];
+    float mx = sh.mrg_m[0][r];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, mrg_m[w][r]);
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, sh.mrg_m[w][r]);
     float v = 0.f, sum = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
-      const float f = exp2f(mrg_m[w][r] - mx);
-      v = fmaf(mrg_a[w][r][dd], f, v);
-      sum = fmaf(mrg_s[w][r], f, sum);
+      const float f = exp2f(sh.mrg_m[w][r] - mx);
+      v = fmaf(sh.mrg_a[w][r][dd], f, v);
+      sum = fmaf(sh.mrg_s[w][r], f, sum);
     }
     pa[e] = v;
     if (dd == 0) {
@@ -333,32 +320,156 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
   }
 }
 
+// out[b, head kvh*REP + r, :] from the `used` splits' partials at base:
+// rescaled to their common max, over the rescaled sum.  Threads stride over
+// (r, dim) pairs starting at t.
+template <int REP, int D>
+__device__ __forceinline__ void attn_combine_heads(const float* base, int used, uint16_t* out,
+                                                   int t, int stride) {
+  constexpr int STRIDE = REP * (D + 2);
+  for (int e = t; e < REP * D; e += stride) {
+    const int r = e / D, dd = e % D;
+    float mx = -INFINITY;
+#pragma unroll 8
+    for (int sp = 0; sp < used; ++sp) mx = fmaxf(mx, base[sp * STRIDE + r]);
+    float num = 0.f, den = 0.f;
+#pragma unroll 8
+    for (int sp = 0; sp < used; ++sp) {
+      const float* p = base + sp * STRIDE;
+      const float f = exp2f(p[r] - mx);
+      den = fmaf(f, p[REP + r], den);
+      num = fmaf(f, p[2 * REP + r * D + dd], num);
+    }
+    out[e] = (uint16_t)f32_to_bf16_bits(num / den);
+  }
+}
+
+template <int REP, int D>
+__global__ __launch_bounds__(kThreads) void attn_split_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pages,
+    const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table,
+    int pages_per_seq, int page_size, int num_pages, const int64_t* __restrict__ pos,
+    float* __restrict__ part, int nkv, int chunk, float scale_log2) {
+  constexpr int LANES = D / 8;
+  __shared__ AttnShared<REP, D> sh;
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int splits = gridDim.x;
+  const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
+  const int l0 = split * chunk;
+  const int n = min(L - l0, chunk);
+  if (n <= 0) return;  // past the sequence's end
+  float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
+  const int32_t* table = page_table + b * pages_per_seq;
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const int l = l0 + i;
+    sh.slot_of[i] = (int32_t)(clamp_index(table[l / page_size], num_pages) * page_size +
+                              l % page_size);
+  }
+  const int sub = threadIdx.x % LANES;
+  const int nh = nkv * REP;
+  u32x4_t qv[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+    qv[r] = reinterpret_cast<const u32x4_t*>(q + (b * nh + kvh * REP + r) * (int64_t)D)[sub];
+  __syncthreads();
+  attn_block<REP, D>(qv, sh, n, k_pages + kvh * D + sub * 8, v_pages + kvh * D + sub * 8,
+                     (int64_t)nkv * D, scale_log2, -1, pm, pm + REP, pm + 2 * REP);
+}
+
+// The split kernel of one decode step of a layer's attention, straight from
+// the QKV projection: every split block ropes (and q-norms) the query heads of
+// its KV head from qkv; the split holding the new position also ropes k, and
+// writes k and v into the pages (using them from registers for that
+// position).  The partials go to `part` for attn_combine_kernel.  (Combining
+// in the last split to finish would save that launch, but publishing the
+// partials to a block on another XCD takes an agent-scope release -- an L2
+// write-back per block -- which costs far more than the launch.)
+template <int REP, int D>
+__global__ __launch_bounds__(kThreads) void attn_step_kernel(
+    const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
+    const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps,
+    uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages, float* __restrict__ part,
+    int nkv, int chunk, float scale_log2) {
+  constexpr int LANES = D / 8, HALF = D / 2, WAVES = kThreads / 64;
+  static_assert(HALF <= 64, "one rotated pair per lane");
+  __shared__ AttnShared<REP, D> sh;
+  __shared__ __align__(16) uint16_t qs[REP][D];  // the roped query heads
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int splits = gridDim.x;
+  const int p = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size);
+  const int L = p + 1;
+  const int l0 = split * chunk;
+  const int n = min(L - l0, chunk);
+  if (n <= 0) return;  // past the sequence's end
+  const bool owner = p < l0 + n;  // this split holds the new position
+  const int nh = nkv * REP;
+  const uint16_t* row = qkv + b * (int64_t)(nh + 2 * nkv) * D;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, sub = threadIdx.x % LANES;
+  for (int hh = wave; hh < REP + (owner ? 1 : 0); hh += WAVES) {
+    const bool is_k = hh == REP;
+    const int src = is_k ? nh + kvh : kvh * REP + hh;
+    const uint16_t* norm = is_k ? k_norm : q_norm;
+    float x1 = 0.f, x2 = 0.f;
+    if (lane < HALF) {
+      x1 = bf16_bits_to_f32(row[src * D + lane]);
+      x2 = bf16_bits_to_f32(row[src * D + lane + HALF]);
+    }
+    if (norm) {  // uniform per wave
+      const float inv = rsqrtf(wave_sum(fmaf(x1, x1, x2 * x2)) / (float)D + eps);
+      if (lane < HALF) {
+        x1 = bf16r(x1 * inv * bf16_bits_to_f32(norm[lane]));
+        x2 = bf16r(x2 * inv * bf16_bits_to_f32(norm[lane + HALF]));
+      }
+    }
+    if (lane < HALF) {
+      const float c = cos_t[(int64_t)p * HALF + lane], sn = sin_t[(int64_t)p * HALF + lane];
+      uint16_t* dst = is_k ? sh.fresh[0] : qs[hh];
+      dst[lane] = (uint16_t)f32_to_bf16_bits(x1 * c - x2 * sn);
+      dst[lane + HALF] = (uint16_t)f32_to_bf16_bits(x2 * c + x1 * sn);
+    }
+  }
+  if (owner && threadIdx.x < LANES)  // the new v row, as is
+    reinterpret_cast<u32x4_t*>(sh.fresh[1])[threadIdx.x] =
+        reinterpret_cast<const u32x4_t*>(row + (nh + nkv + kvh) * D)[threadIdx.x];
+  const int32_t* table = page_table + b * pages_per_seq;
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const int l = l0 + i;
+    sh.slot_of[i] = (int32_t)(clamp_index(table[l / page_size], num_pages) * page_size +
+                              l % page_size);
+  }
+  __syncthreads();
+  const int64_t row_elems = (int64_t)nkv * D;
+  if (owner && threadIdx.x < LANES) {  // append the new k and v rows to the pages
+    const int64_t at = (int64_t)sh.slot_of[p - l0] * row_elems + kvh * D + sub * 8;
+    *reinterpret_cast<u32x4_t*>(k_pages + at) = reinterpret_cast<const u32x4_t*>(sh.fresh[0])[sub];
+    *reinterpret_cast<u32x4_t*>(v_pages + at) = reinterpret_cast<const u32x4_t*>(sh.fresh[1])[sub];
+  }
+  u32x4_t qv[REP];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) qv[r] = reinterpret_cast<const u32x4_t*>(qs[r])[sub];
+  float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
+  attn_block<REP, D>(qv, sh, n, k_pages + kvh * D + sub * 8, v_pages + kvh * D + sub * 8,
+                     row_elems, scale_log2, owner ? p - l0 : -1, pm, pm + REP, pm + 2 * REP);
+}
+
 // Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over the sequence's
 // splits of the partials rescaled to their common max, over the rescaled sum.
 template <int REP, int D>
 __global__ __launch_bounds__(D) void attn_combine_kernel(
     const float* __restrict__ part, const int64_t* __restrict__ pos, int pages_per_seq,
     int page_size, uint16_t* __restrict__ out, int nkv, int splits, int chunk) {
-  constexpr int STRIDE = REP * (D + 2);
   const int hh = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int kvh = hh / REP, r = hh % REP;
-  const int dd = threadIdx.x;
   const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
   const int used = min(splits, (L + chunk - 1) / chunk);
-  const float* base = part + (b * nkv + kvh) * splits * (int64_t)STRIDE;
-  float mx = -INFINITY;
-#pragma unroll 8
-  for (int sp = 0; sp < used; ++sp) mx = fmaxf(mx, base[sp * STRIDE + r]);
-  float num = 0.f, den = 0.f;
-#pragma unroll 8
-  for (int sp = 0; sp < used; ++sp) {
-    const float* p = base + sp * STRIDE;
-    const float f = exp2f(p[r] - mx);
-    den = fmaf(f, p[REP + r], den);
-    num = fmaf(f, p[2 * REP + r * D + dd], num);
-  }
-  out[(b * nkv * REP + hh) * (int64_t)D + dd] = (uint16_t)f32_to_bf16_bits(num / den);
+  const float* base = part + (b * nkv + kvh) * splits * (int64_t)(REP * (D + 2));
+  attn_combine_heads<REP, D>(base, used, out + (b * nkv * REP + kvh * REP) * (int64_t)D,
+                             r * D + threadIdx.x, REP * D);
 }
 
 // ---------------------------------------------------------------- SiLU * up
@@ -383,10 +494,11 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   reinterpret_cast<u32x4_t*>(out + r * inter)[u] = o;
 }
 
-// Blocks of attn_split_kernel<REP, 128> one CU holds at once (4-wave blocks;
-// waves per SIMD as the register count allows).
+// Blocks of attn_split_kernel / attn_step_kernel<REP, D> one CU holds at
+// once (4-wave blocks; waves per SIMD as the register count allows, the lower
+// of the two kernels).
 int attn_blocks_per_cu(int rep) {
-  static const int occ[9] = {0, 8, 5, 4, 4, 4, 2, 3, 2};
+  static const int occ[9] = {0, 6, 5, 4, 4, 3, 2, 3, 2};
   return occ[rep < 1 ? 1 : rep > 8 ? 8 : rep];
 }
 
@@ -499,6 +611,65 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
     return launch_attention_d<128>(q, k_pages, v_pages, page_table, (int)pages_per_seq,
                                    (int)page_size, (int)num_pages, pos, B, nh, nkv, scale,
                                    workspace, out, chunk, splits, stream);
+  return hipErrorInvalidValue;
+}
+
+namespace {
+template <int D>
+hipError_t launch_step_d(const uint16_t* qkv, const int64_t* pos, const int32_t* page_table,
+                         int pages_per_seq, int page_size, int num_pages, const float* cos_t,
+                         const float* sin_t, const uint16_t* q_norm, const uint16_t* k_norm,
+                         float eps, uint16_t* k_pages, uint16_t* v_pages, int64_t B, int nh,
+                         int nkv, float scale, float* workspace, uint16_t* out, int chunk,
+                         int splits, hipStream_t stream) {
+  const float scale_log2 = scale * 1.4426950408889634f;
+  const dim3 grid((unsigned)splits, (unsigned)nkv, (unsigned)B);
+  const dim3 cgrid((unsigned)nh, (unsigned)B);
+#define MQ_STEP(REP)                                                                            \
+  case REP:                                                                                     \
+    hipLaunchKernelGGL((attn_step_kernel<REP, D>), grid, dim3(kThreads), 0, stream, qkv, pos,  \
+                       page_table, pages_per_seq, page_size, num_pages, cos_t, sin_t, q_norm,  \
+                       k_norm, eps, k_pages, v_pages, workspace, nkv, chunk, scale_log2);      \
+    hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,    \
+                       pos, pages_per_seq, page_size, out, nkv, splits, chunk);                 \
+    break;
+  switch (nh / nkv) {
+    MQ_STEP(1)
+    MQ_STEP(2)
+    MQ_STEP(3)
+    MQ_STEP(4)
+    MQ_STEP(5)
+    MQ_STEP(6)
+    MQ_STEP(7)
+    MQ_STEP(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef MQ_STEP
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attention_step(const uint16_t* qkv, const int64_t* pos,
+                                 const int32_t* page_table, int64_t pages_per_seq,
+                                 int64_t page_size, int64_t num_pages, const float* cos_t,
+                                 const float* sin_t, const uint16_t* q_norm,
+                                 const uint16_t* k_norm, float eps, uint16_t* k_pages,
+                                 uint16_t* v_pages, int64_t B, int nh, int nkv, int d,
+                                 float scale, float* workspace, uint16_t* out,
+                                 hipStream_t stream) {
+  if (B == 0) return hipSuccess;
+  const int64_t capacity = pages_per_seq * page_size;
+  const int chunk = attn_chunk(B, nkv, nh / nkv, d, capacity);
+  const int splits = (int)((capacity + chunk - 1) / chunk);
+  if (d == 64)
+    return launch_step_d<64>(qkv, pos, page_table, (int)pages_per_seq, (int)page_size,
+                             (int)num_pages, cos_t, sin_t, q_norm, k_norm, eps, k_pages, v_pages,
+                             B, nh, nkv, scale, workspace, out, chunk, splits, stream);
+  if (d == 128)
+    return launch_step_d<128>(qkv, pos, page_table, (int)pages_per_seq, (int)page_size,
+                              (int)num_pages, cos_t, sin_t, q_norm, k_norm, eps, k_pages,
+                              v_pages, B, nh, nkv, scale, workspace, out, chunk, splits, stream);
   return hipErrorInvalidValue;
 }
 

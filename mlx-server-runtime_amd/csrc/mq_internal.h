@@ -104,6 +104,15 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
                                    hipStream_t stream);
 hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter,
                            hipStream_t stream);
+// RoPE + append fused into the split attention kernel, then the combine.
+hipError_t launch_attention_step(const uint16_t* qkv, const int64_t* pos,
+                                 const int32_t* page_table, int64_t pages_per_seq,
+                                 int64_t page_size, int64_t num_pages, const float* cos_t,
+                                 const float* sin_t, const uint16_t* q_norm,
+                                 const uint16_t* k_norm, float eps, uint16_t* k_pages,
+                                 uint16_t* v_pages, int64_t B, int nh, int nkv, int d,
+                                 float scale, float* workspace, uint16_t* out,
+                                 hipStream_t stream);
 
 // Mixture-of-experts routing (mq_moe.hip).
 bool moe_route_supported(int E, int k);

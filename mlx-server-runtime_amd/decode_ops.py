@@ -13,6 +13,9 @@ calls these per layer and token:
     paged_decode_attention(q, cache, layer, positions, scale)
                                                    attention over the pages
                                                    (attention.py:206-298)
+    attention_step(qkv, positions, cache, layer, cos, sin, n_heads, scale, ...)
+                                                   the two above with RoPE + append
+                                                   inside the attention kernel
     silu_mul(gate_up)                              silu(gate) * up (qwen2.py:43-44)
 
 PagedKV holds the pages in the reference's layout (cache.py:686-695): per
@@ -181,6 +184,42 @@ def paged_decode_attention(q: torch.Tensor, cache: PagedKV, layer: int, position
     return out
 
 
+def attention_step(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, layer: int,
+                   cos: torch.Tensor, sin: torch.Tensor, n_heads: int, scale: float,
+                   q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,
+                   norm_eps: float = 1e-6) -> torch.Tensor:
+    """rope_kv_append + paged_decode_attention with the RoPE and append inside the
+    attention's split kernel (two launches instead of three, the same results):
+    qkv bf16 [B, (n_heads + 2 kv_heads) * head_dim] -> bf16 [B, n_heads * head_dim]."""
+    op = "decode_attention_step"
+    _require_gpu(op, qkv=qkv, positions=positions, cos=cos, sin=sin)
+    _check_bf16(op, "qkv", qkv)
+    B = qkv.shape[0]
+    d, nkv = cache.head_dim, cache.kv_heads
+    if qkv.shape != (B, (n_heads + 2 * nkv) * d):
+        raise ValueError(f"[{op}] qkv must be [B, {(n_heads + 2 * nkv) * d}], "
+                         f"got {tuple(qkv.shape)}")
+    if positions.dtype != torch.int64 or positions.shape != (B,) or cache.batch != B:
+        raise ValueError(f"[{op}] positions must be int64 [{B}] and match the page table")
+    if cos.dtype != torch.float32 or sin.shape != cos.shape or cos.shape[0] < cache.capacity \
+            or cos.shape[-1] != d // 2:
+        raise ValueError(f"[{op}] cos/sin must be float32 [>= {cache.capacity}, {d // 2}]")
+    for name, w in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if w is not None and (w.dtype != torch.bfloat16 or w.shape != (d,)):
+            raise ValueError(f"[{op}] {name} must be bfloat16 [{d}]")
+    L = _lib.lib()
+    ws_bytes = L.mq_paged_decode_attention_workspace(B, n_heads, nkv, d, cache.pages_per_seq,
+                                                     cache.page_size)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=qkv.device)
+    out = torch.empty(B, n_heads * d, dtype=torch.bfloat16, device=qkv.device)
+    _lib.check(L.mq_decode_attention_step(
+        _ptr(qkv.contiguous()), _ptr(positions), _ptr(cache.page_table), cache.pages_per_seq,
+        cache.page_size, cache.num_pages, _ptr(cos.contiguous()), _ptr(sin.contiguous()),
+        _ptr(q_norm), _ptr(k_norm), float(norm_eps), _ptr(cache.k[layer]), _ptr(cache.v[layer]),
+        B, n_heads, nkv, d, float(scale), _ptr(ws), ws_bytes, _ptr(out), _stream(qkv)), op)
+    return out
+
+
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     """gate_up bf16 [..., 2 * I] -> bf16 [..., I] = bf16(bf16(silu(gate)) * up)."""
     op = "silu_mul"
@@ -196,4 +235,5 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     return out
 
 
-__all__ = ["PagedKV", "rms_norm", "rope_kv_append", "paged_decode_attention", "silu_mul"]
+__all__ = ["PagedKV", "rms_norm", "rope_kv_append", "paged_decode_attention", "attention_step",
+           "silu_mul"]

@@ -22,9 +22,10 @@ same: q/k/v are concatenated into one quantized matrix (and gate/up into
 another) so each is one launch, which is exact because the output columns of
 a quantized matmul are independent.  Activations and the paged KV cache are
 bfloat16 (as in the reference, cache.py:659-695); RMSNorm, RoPE, the softmax
-and every accumulation are float32.  A decode step is ten launches per layer
-(QKV GEMV, RoPE + KV append, split attention + combine, o GEMV, residual add +
-RMSNorm, gate|up GEMV, SiLU * up, down GEMV, residual add + RMSNorm), captured
+and every accumulation are float32.  A decode step is nine launches per
+layer (QKV GEMV; split attention with RoPE and the KV append inside it; the
+splits' combine; o GEMV; residual add + RMSNorm; gate|up GEMV; SiLU * up;
+down GEMV; residual add + RMSNorm), captured
 once in a HIP graph and replayed per token (inputs live in static device
 buffers).  Prefill runs the same linears as GEMMs and float32 attention over
 the pages (the reference's dense-row gather, attention.py:264-298), so a
@@ -42,7 +43,7 @@ import torch
 import torch.nn.functional as F
 
 from . import core
-from .decode_ops import PagedKV, paged_decode_attention, rope_kv_append, silu_mul
+from .decode_ops import PagedKV, attention_step, silu_mul
 from .moe import MoEBlock, QExperts
 from .decode_ops import rms_norm as fused_rms_norm
 
@@ -319,9 +320,8 @@ class Qwen2Model:
         h = self._embed(tok)
         x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
-            q = rope_kv_append(layer.qkv(x), pos, cache, li, cos, sin, nh, layer.q_norm,
-                               layer.k_norm, c.rms_norm_eps)
-            a = paged_decode_attention(q, cache, li, pos, d ** -0.5)
+            a = attention_step(layer.qkv(x), pos, cache, li, cos, sin, nh, d ** -0.5,
+                               layer.q_norm, layer.k_norm, c.rms_norm_eps)
             x, h = self._ffn(li, h, layer.o(a))
         return self._head(x)
 

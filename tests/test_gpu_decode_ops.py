@@ -248,3 +248,50 @@ def test_errors(ops):
                      torch.ones(12, dtype=torch.bfloat16, device=DEV), 1e-6)
     with pytest.raises(ValueError):
         ops.silu_mul(torch.zeros(2, 7, dtype=torch.bfloat16, device=DEV))
+
+
+@pytest.mark.parametrize("B,nh,nkv,d,per,qk_norm", [
+    (1, 28, 4, 128, 40, False), (4, 28, 4, 128, 80, False), (8, 32, 4, 128, 36, True),
+    (3, 14, 2, 64, 5, True), (2, 8, 8, 128, 3, False), (32, 28, 4, 128, 80, False)])
+def test_attention_step_equals_rope_then_attention(ops, B, nh, nkv, d, per, qk_norm):
+    """The fused step (RoPE + append inside the split attention kernel) gives
+    the unfused path's results bit for bit and leaves the same pages, across
+    HIP-graph replays."""
+    ps = 16
+    c1 = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=B + per)
+    c2 = ops.PagedKV(1, c1.num_pages, ps, nkv, d, c1.page_table.cpu(), DEV)
+    g = _gen(B * 7 + nh)
+    fill = torch.randn(c1.k[0].shape, generator=g, device=DEV).to(torch.bfloat16)
+    for c in (c1, c2):
+        c.k[0].copy_(fill)
+        c.v[0].copy_(fill.flip(0))
+    cos, sin = _tables(d, c1.capacity)
+    qn = kn = None
+    if qk_norm:
+        qn = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(torch.bfloat16)
+        kn = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(torch.bfloat16)
+    qkv = torch.randn(B, (nh + 2 * nkv) * d, generator=g, device=DEV).to(torch.bfloat16)
+    pos = torch.randint(0, c1.capacity, (B,), generator=g, device=DEV)
+    pos[0] = c1.capacity - 1
+    scale = d ** -0.5
+    q = ops.rope_kv_append(qkv, pos, c1, 0, cos, sin, nh, qn, kn, 1e-6)
+    ref = ops.paged_decode_attention(q, c1, 0, pos, scale)
+    out = ops.attention_step(qkv, pos, c2, 0, cos, sin, nh, scale, qn, kn, 1e-6)
+    assert torch.equal(out, ref)
+    assert torch.equal(c1.k[0], c2.k[0]) and torch.equal(c1.v[0], c2.v[0])
+    # captured and replayed with advancing positions
+    step = lambda: ops.attention_step(qkv, pos, c2, 0, cos, sin, nh, scale, qn, kn, 1e-6)  # noqa
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    for _ in range(3):
+        pos.sub_(1).clamp_(min=0)
+        graph.replay()
+        torch.cuda.synchronize()
+        q = ops.rope_kv_append(qkv, pos, c1, 0, cos, sin, nh, qn, kn, 1e-6)
+        assert torch.equal(static, ops.paged_decode_attention(q, c1, 0, pos, scale))

@@ -32,7 +32,8 @@ def test_header_declares_the_abi():
         "mq_version", "mq_last_error", "mq_quantize", "mq_dequantize", "mq_embedding_lookup",
         "mq_quantized_matmul", "mq_quantized_matmul_workspace", "mq_quantized_matmul_ws",
         "mq_gather_qmm", "mq_rms_norm", "mq_rope_kv_append",
-        "mq_paged_decode_attention_workspace", "mq_paged_decode_attention", "mq_silu_mul",
+        "mq_paged_decode_attention_workspace", "mq_paged_decode_attention",
+        "mq_decode_attention_step", "mq_silu_mul",
         "mq_moe_route", "mq_moe_sort", "mq_moe_combine"])
 
 
