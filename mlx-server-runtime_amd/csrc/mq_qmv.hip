@@ -353,14 +353,16 @@ hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, cons
   return run_xu<BITS, TPR, R, S, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
 }
 
-constexpr int kTprs[] = {16, 32, 64, 128, 256};
+constexpr int kTprs[] = {8, 16, 32, 64, 128, 256};
 
 // Lanes per row: the narrowest whose lanes own at most 8 chunks each, widened
-// while the grid has fewer than 2 blocks per CU.
+// while the grid has fewer than 2 blocks per CU.  8 lanes only for short rows
+// (<= 24 chunks: 3 slots), where 16 lanes would leave a quarter of the slots
+// empty (an expert's down projection, K = 768).
 int pick_tpr(int64_t C, int64_t N, int64_t T) {
-  int pick = 0;
-  while (pick < 4 && (C + kTprs[pick] - 1) / kTprs[pick] > 8) ++pick;
-  while (pick < 4 && ((N * kTprs[pick]) / kBlock) * T < 512) ++pick;
+  int pick = C <= 24 ? 0 : 1;
+  while (pick < 5 && (C + kTprs[pick] - 1) / kTprs[pick] > 8) ++pick;
+  while (pick < 5 && ((N * kTprs[pick]) / kBlock) * T < 512) ++pick;
   return kTprs[pick];
 }
 
@@ -386,6 +388,8 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
   const int tpr = pick_tpr(C, N, g.T);
   const int slots = (int)((C + tpr - 1) / tpr);
   switch (tpr) {
+    case 8:
+      return run_mt<BITS, 8, 1, 3>(x, wq, s, b, bias, y, M, N, K, g, stream);
     // Chunk slots per lane S: the instantiated S >= NJ closest to it (slots
     // past NJ cost arithmetic on zeros, not memory traffic).  The S values
     // cover the model shapes exactly: K = 3584 / 18944 / 2048 / 768 at 4 and
