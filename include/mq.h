@@ -267,6 +267,31 @@ int mq_moe_sort(const int32_t* expert_ids, int64_t n, int top_k, int num_experts
 int mq_moe_combine(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scores, mq_bf16* out,
                    int64_t tokens, int top_k, int64_t hidden, hipStream_t stream);
 
+/*
+ * mq_moe_route then mq_moe_sort of the routed indices [tokens, top_k], with
+ * the same outputs bit for bit (the router of models/lfm2.py:365-373 and
+ * _gather_sort :613-618, which the reference runs back to back).  Up to 64
+ * tokens run as one block and one launch; more run as the two kernels.
+ */
+int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t tokens,
+                      int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
+                      mq_bf16* scores, int32_t* sorted_ids, int32_t* order, int32_t* inverse,
+                      int32_t* rows, hipStream_t stream);
+
+/*
+ * mq_moe_combine, then the residual add and the RMSNorm that follow the MoE
+ * block (models/lfm2.py:409 hidden + feed_forward(...), then the next layer's
+ * operator_norm :404 or the final embedding_norm :436), one kernel per token:
+ *   h = bf16(combine(y, inverse, scores) + residual)      -> residual_out
+ *   out = bf16(h * rsqrt(mean(h^2) + eps) * weight)
+ * Bit-identical to mq_moe_combine followed by mq_rms_norm(combined, residual,
+ * ...).  hidden % 8 == 0, <= 8192; residual_out may not alias residual.
+ */
+int mq_moe_combine_rms_norm(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scores,
+                            const mq_bf16* residual, mq_bf16* residual_out,
+                            const mq_bf16* weight, mq_bf16* out, int64_t tokens, int top_k,
+                            int64_t hidden, float eps, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,8 @@ EXPORTS = (
     "mq_moe_route",
     "mq_moe_sort",
     "mq_moe_combine",
+    "mq_moe_route_sort",
+    "mq_moe_combine_rms_norm",
 )
 
 _lock = threading.Lock()
@@ -79,6 +81,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_moe_route.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p]
     L.mq_moe_sort.argtypes = [_p, _i64, _int, _int, _p, _p, _p, _p, _p]
     L.mq_moe_combine.argtypes = [_p, _p, _p, _p, _i64, _int, _i64, _p]
+    L.mq_moe_route_sort.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p, _p, _p, _p, _p]
+    L.mq_moe_combine_rms_norm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _int, _i64,
+                                          ctypes.c_float, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
     L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t

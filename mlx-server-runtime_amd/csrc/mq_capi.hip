@@ -469,4 +469,48 @@ int mq_moe_combine(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scor
                     op);
 }
 
+int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t tokens,
+                      int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
+                      mq_bf16* scores, int32_t* sorted_ids, int32_t* order, int32_t* inverse,
+                      int32_t* rows, hipStream_t stream) {
+  const char* op = "moe_route_sort";
+  if (int rc = check_dim(op, "tokens", tokens)) return rc;
+  if (!mq::moe_route_supported(num_experts, top_k))
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] %d experts, top %d: 1 <= k <= min(E, 64), E <= 512.",
+                op, num_experts, top_k);
+  if (!mq::moe_sort_supported(tokens * top_k, num_experts))
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] %lld entries (< 2^30).", op,
+                (long long)(tokens * top_k));
+  if (tokens == 0) return ok();
+  if (!logits || !indices || !scores || !sorted_ids || !order || !inverse)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  return hip_status(mq::launch_moe_route_sort(logits, expert_bias, tokens, num_experts, top_k,
+                                              norm_topk_prob != 0, indices, scores, sorted_ids,
+                                              order, inverse, rows, stream),
+                    op);
+}
+
+int mq_moe_combine_rms_norm(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scores,
+                            const mq_bf16* residual, mq_bf16* residual_out,
+                            const mq_bf16* weight, mq_bf16* out, int64_t tokens, int top_k,
+                            int64_t hidden, float eps, hipStream_t stream) {
+  const char* op = "moe_combine_rms_norm";
+  if (int rc = check_dim(op, "tokens", tokens)) return rc;
+  if (top_k < 1 || (int64_t)top_k * tokens >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] top_k=%d is out of range.", op, top_k);
+  if (!mq::moe_combine_norm_supported(hidden))
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] hidden=%lld is not supported (a multiple of 8, <= 8192).",
+                op, (long long)hidden);
+  if (tokens == 0) return ok();
+  if (!y || !scores || !residual || !residual_out || !weight || !out)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(y) || !aligned16(residual) || !aligned16(residual_out) || !aligned16(weight) ||
+      !aligned16(out))
+    return fail(MQ_ERR_INVALID, "[%s] y, residual, residual_out, weight and out must be 16-byte "
+                "aligned.", op);
+  return hip_status(mq::launch_moe_combine_norm(y, inverse, scores, residual, residual_out, weight,
+                                                out, tokens, top_k, hidden, eps, stream),
+                    op);
+}
+
 }  // extern "C"

@@ -124,5 +124,14 @@ hipError_t launch_moe_sort(const int32_t* ids, int64_t n, int k, int E, int32_t*
                            int32_t* order, int32_t* inverse, int32_t* rows, hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t* y, const int32_t* inverse, const uint16_t* scores,
                               uint16_t* out, int64_t T, int k, int64_t H, hipStream_t stream);
+hipError_t launch_moe_route_sort(const uint16_t* logits, const float* expert_bias, int64_t T,
+                                 int E, int k, bool normalize, int32_t* indices, uint16_t* scores,
+                                 int32_t* sorted_ids, int32_t* order, int32_t* inverse,
+                                 int32_t* rows, hipStream_t stream);
+bool moe_combine_norm_supported(int64_t H);
+hipError_t launch_moe_combine_norm(const uint16_t* y, const int32_t* inverse,
+                                   const uint16_t* scores, const uint16_t* residual,
+                                   uint16_t* residual_out, const uint16_t* w, uint16_t* normed,
+                                   int64_t T, int k, int64_t H, float eps, hipStream_t stream);
 
 }  // namespace mq

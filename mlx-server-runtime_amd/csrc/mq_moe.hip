@@ -15,7 +15,11 @@
 //                        of x is never materialised);
 //  * moe_combine_kernel  _scatter_unsort plus the weighting of lfm2.py:375:
 //                        out[t] = sum_j bf16(y[inverse[t*k + j]] * score[t, j]),
-//                        float32 sum, one rounding.
+//                        float32 sum, one rounding;
+//  * moe_route_sort_kernel  both of the first two in one block, for a decode
+//                        step's few tokens;
+//  * moe_combine_norm_kernel  the combine, the residual add and the next
+//                        RMSNorm in one kernel per token.
 #include <algorithm>
 
 #include "mq_common.h"
@@ -29,13 +33,13 @@ namespace {
 constexpr int kMaxExperts = 512;
 constexpr int kRouteWaves = 4;
 
-__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
-    const uint16_t* __restrict__ logits, const float* __restrict__ expert_bias, int64_t T, int E,
-    int k, int normalize, int32_t* __restrict__ indices, uint16_t* __restrict__ scores) {
+// Token t's top-k by one whole wave.
+__device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
+                                            const float* __restrict__ expert_bias, int64_t t,
+                                            int E, int k, int normalize, int32_t* indices,
+                                            uint16_t* __restrict__ scores) {
   constexpr int PER = kMaxExperts / 64;
-  const int64_t t = (int64_t)blockIdx.x * kRouteWaves + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (t >= T) return;  // whole waves
   const uint16_t* row = logits + t * E;
   float v[PER];
   float mx = -INFINITY;
@@ -102,6 +106,14 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
   }
 }
 
+__global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
+    const uint16_t* __restrict__ logits, const float* __restrict__ expert_bias, int64_t T, int E,
+    int k, int normalize, int32_t* __restrict__ indices, uint16_t* __restrict__ scores) {
+  const int64_t t = (int64_t)blockIdx.x * kRouteWaves + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves
+  route_token(logits, expert_bias, t, E, k, normalize, indices, scores);
+}
+
 // ---------------------------------------------------------------- sort
 // One block.  Entries are processed in chunks of kSortThreads, in order; an
 // entry's place is its expert's offset, plus the entries of that expert in
@@ -112,9 +124,12 @@ constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kMaxBuckets = kMaxExperts + 1;
 
-__global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
-    const int32_t* __restrict__ ids, int n, int k, int E, int32_t* __restrict__ sorted_ids,
-    int32_t* __restrict__ order, int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
+// The whole sort, by one block of kSortThreads.
+__device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int E,
+                                           int32_t* __restrict__ sorted_ids,
+                                           int32_t* __restrict__ order,
+                                           int32_t* __restrict__ inverse,
+                                           int32_t* __restrict__ rows) {
   __shared__ int offset[kMaxBuckets];
   __shared__ int wave_count[kSortWaves][kMaxBuckets];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -177,6 +192,28 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
   }
 }
 
+__global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
+    const int32_t* __restrict__ ids, int n, int k, int E, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ order, int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
+  sort_block(ids, n, k, E, sorted_ids, order, inverse, rows);
+}
+
+// Route (one wave per token) and then sort, in one block: a decode step's
+// few tokens need no more, and a launch in between costs more than both.
+// The block's index stores are visible to its own loads after the barrier.
+constexpr int kRouteSortMaxTokens = 64;
+
+__global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
+    const uint16_t* __restrict__ logits, const float* __restrict__ expert_bias, int T, int E,
+    int k, int normalize, int32_t* indices, uint16_t* __restrict__ scores,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ order,
+    int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
+  for (int t = threadIdx.x >> 6; t < T; t += kSortWaves)
+    route_token(logits, expert_bias, t, E, k, normalize, indices, scores);
+  __syncthreads();
+  sort_block(indices, T * k, k, E, sorted_ids, order, inverse, rows);
+}
+
 // ---------------------------------------------------------------- combine
 // Grid (T, ceil(H / (8 * 256))), 256 threads, 8 elements per thread.
 __global__ __launch_bounds__(256) void moe_combine_kernel(
@@ -205,7 +242,114 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   reinterpret_cast<u32x4_t*>(out + t * H)[u] = o;
 }
 
+// moe_combine_kernel followed by the residual add and the RMSNorm that the
+// next layer applies, per token: h = bf16(out + residual) -> residual_out,
+// normed = bf16(h * rsqrt(mean(h^2) + eps) * w).  The element mapping and the
+// reduction order are the RMSNorm kernel's (256 threads, 8 elements per
+// thread and pass, four passes), so the outputs equal those of the combine
+// then the norm bit for bit.  Grid T; H / 8 <= 1024.
+constexpr int kNormThreads = 256;
+constexpr int kNormUnits = 4;
+
+__global__ __launch_bounds__(kNormThreads) void moe_combine_norm_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ inverse,
+    const uint16_t* __restrict__ scores, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ residual_out, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ normed, int k, int H, int64_t y_rows, float eps) {
+  __shared__ float red[kNormThreads / 64];
+  const int64_t t = blockIdx.x;
+  const int units = H / 8;
+  u32x4_t hv[kNormUnits];
+  float ss = 0.f;
+#pragma unroll
+  for (int pass = 0; pass < kNormUnits; ++pass) {
+    const int u = threadIdx.x + pass * kNormThreads;
+    if (u < units) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < k; ++j) {
+        int64_t r = t * k + j;
+        if (inverse) r = inverse[r];
+        r = r < 0 ? 0 : (r >= y_rows ? y_rows - 1 : r);
+        const float sc = bf16_bits_to_f32(scores[t * k + j]);
+        const u32x4_t v = reinterpret_cast<const u32x4_t*>(y + r * H)[u];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += bf16_bits_to_f32(f32_to_bf16_bits(lo_bf16(v[q]) * sc));
+          acc[2 * q + 1] += bf16_bits_to_f32(f32_to_bf16_bits(hi_bf16(v[q]) * sc));
+        }
+      }
+      const u32x4_t rv = reinterpret_cast<const u32x4_t*>(residual + t * H)[u];
+      u32x4_t h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t c = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+        h[q] = pack_bf16x2(lo_bf16(c) + lo_bf16(rv[q]), hi_bf16(c) + hi_bf16(rv[q]));
+      }
+      reinterpret_cast<u32x4_t*>(residual_out + t * H)[u] = h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = lo_bf16(h[q]), b = hi_bf16(h[q]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+      hv[pass] = h;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) ss += red[i];
+  const float inv = rsqrtf(ss / (float)H + eps);
+#pragma unroll
+  for (int pass = 0; pass < kNormUnits; ++pass) {
+    const int u = threadIdx.x + pass * kNormThreads;
+    if (u < units) {
+      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(w)[u];
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pack_bf16x2(lo_bf16(hv[pass][q]) * inv * lo_bf16(wv[q]),
+                           hi_bf16(hv[pass][q]) * inv * hi_bf16(wv[q]));
+      reinterpret_cast<u32x4_t*>(normed + t * H)[u] = o;
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_moe_route_sort(const uint16_t* logits, const float* expert_bias, int64_t T,
+                                 int E, int k, bool normalize, int32_t* indices, uint16_t* scores,
+                                 int32_t* sorted_ids, int32_t* order, int32_t* inverse,
+                                 int32_t* rows, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  if (T > kRouteSortMaxTokens) {
+    const hipError_t e =
+        launch_moe_route(logits, expert_bias, T, E, k, normalize, indices, scores, stream);
+    if (e != hipSuccess) return e;
+    return launch_moe_sort(indices, T * k, k, E, sorted_ids, order, inverse, rows, stream);
+  }
+  hipLaunchKernelGGL(moe_route_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, logits,
+                     expert_bias, (int)T, E, k, normalize ? 1 : 0, indices, scores, sorted_ids,
+                     order, inverse, rows);
+  return hipGetLastError();
+}
+
+bool moe_combine_norm_supported(int64_t H) {
+  return H > 0 && H % 8 == 0 && H / 8 <= (int64_t)kNormThreads * kNormUnits;
+}
+
+hipError_t launch_moe_combine_norm(const uint16_t* y, const int32_t* inverse,
+                                   const uint16_t* scores, const uint16_t* residual,
+                                   uint16_t* residual_out, const uint16_t* w, uint16_t* normed,
+                                   int64_t T, int k, int64_t H, float eps, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  hipLaunchKernelGGL(moe_combine_norm_kernel, dim3((unsigned)T), dim3(kNormThreads), 0, stream,
+                     y, inverse, scores, residual, residual_out, w, normed, k, (int)H, T * k, eps);
+  return hipGetLastError();
+}
 
 bool moe_route_supported(int E, int k) {
   return E >= 1 && E <= kMaxExperts && k >= 1 && k <= 64 && k <= E;

@@ -12,11 +12,17 @@ _gather_sort/_scatter_unsort :613-622):
         token whose x feeds sorted pair p (gather_qmm's lhs indices)
     combine(y, inverse, scores) -> out
         out[t] = sum_j bf16(y[inverse[t*k + j]] * scores[t, j])
+    route_sort(logits, ...) -> (indices, scores, sorted_ids, order, inverse, rows)
+        route then expert_sort, one launch for up to 64 tokens
+    combine_rms_norm(y, inverse, scores, residual, weight, eps) -> (out, h)
+        h = bf16(combine(...) + residual), out = RMSNorm(h) * weight, one launch
 
 MoEBlock runs them around two gather_qmm calls: the experts' gate and up
 projections concatenated per expert (one call, [E, 2I, H]), SiLU * up, and
 the down projection.  Rows are sorted by expert when tokens * top_k >= 64,
-as in the reference.  There is no CPU fallback.
+as in the reference.  MoEBlock.residual_norm also folds the residual add and
+the next RMSNorm into the combine.  Every fused form equals its unfused
+sequence bit for bit.  There is no CPU fallback.
 """
 
 from __future__ import annotations
@@ -65,6 +71,40 @@ def expert_sort(indices: torch.Tensor, num_experts: int):
 def combine(y: torch.Tensor, inverse: torch.Tensor | None, scores: torch.Tensor) -> torch.Tensor:
     """y bf16 [T*k, H] (expert order when inverse is given) -> bf16 [T, H]."""
     op = "moe_combine"
+    y2, T, k, H = _combine_args(op, y, inverse, scores)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=y.device)
+    L = _lib.lib()
+    _lib.check(L.mq_moe_combine(_ptr(y2), _ptr(inverse), _ptr(scores.contiguous()), _ptr(out), T,
+                                k, H, _stream(y)), op)
+    return out
+
+
+def route_sort(logits: torch.Tensor, top_k: int, num_experts: int,
+               norm_topk_prob: bool = True, expert_bias: torch.Tensor | None = None):
+    """route(...) then expert_sort(indices, num_experts), in one launch when
+    logits has at most 64 rows -> (indices, scores, sorted_ids, order, inverse,
+    rows)."""
+    op = "moe_route_sort"
+    _require_gpu(op, logits=logits, expert_bias=expert_bias)
+    _check_bf16(op, "logits", logits)
+    T, E = logits.reshape(-1, logits.shape[-1]).shape
+    if E != num_experts:
+        raise ValueError(f"[{op}] logits have {E} experts, expected {num_experts}")
+    if expert_bias is not None and (expert_bias.dtype != torch.float32
+                                    or expert_bias.shape != (E,)):
+        raise ValueError(f"[{op}] expert_bias must be float32 [{E}]")
+    dev = logits.device
+    idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    sc = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(T * top_k, dtype=torch.int32, device=dev) for _ in range(4)]
+    L = _lib.lib()
+    _lib.check(L.mq_moe_route_sort(_ptr(logits.contiguous()), _ptr(expert_bias), T, E, top_k,
+                                   int(bool(norm_topk_prob)), _ptr(idx), _ptr(sc),
+                                   *(_ptr(t) for t in outs), _stream(logits)), op)
+    return (idx, sc, *outs)
+
+
+def _combine_args(op, y, inverse, scores):
     _require_gpu(op, y=y, inverse=inverse, scores=scores)
     _check_bf16(op, "y", y)
     _check_bf16(op, "scores", scores)
@@ -75,11 +115,30 @@ def combine(y: torch.Tensor, inverse: torch.Tensor | None, scores: torch.Tensor)
         raise ValueError(f"[{op}] y has {y2.shape[0]} rows, expected {T * k}")
     if inverse is not None and (inverse.dtype != torch.int32 or inverse.numel() != T * k):
         raise ValueError(f"[{op}] inverse must be int32 [{T * k}]")
+    return y2, T, k, H
+
+
+def combine_rms_norm(y: torch.Tensor, inverse: torch.Tensor | None, scores: torch.Tensor,
+                     residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """h = bf16(combine(y, inverse, scores) + residual); returns
+    (bf16(h * rsqrt(mean(h^2) + eps) * weight), h), both bf16 [T, H]."""
+    op = "moe_combine_rms_norm"
+    y2, T, k, H = _combine_args(op, y, inverse, scores)
+    _require_gpu(op, residual=residual, weight=weight)
+    _check_bf16(op, "residual", residual)
+    _check_bf16(op, "weight", weight)
+    if residual.numel() != T * H:
+        raise ValueError(f"[{op}] residual has {residual.numel()} elements, expected {T * H}")
+    if weight.shape != (H,):
+        raise ValueError(f"[{op}] weight must have shape ({H},), got {tuple(weight.shape)}")
     out = torch.empty(T, H, dtype=torch.bfloat16, device=y.device)
+    h = torch.empty_like(out)
     L = _lib.lib()
-    _lib.check(L.mq_moe_combine(_ptr(y2), _ptr(inverse), _ptr(scores.contiguous()), _ptr(out), T,
-                                k, H, _stream(y)), op)
-    return out
+    _lib.check(L.mq_moe_combine_rms_norm(_ptr(y2), _ptr(inverse), _ptr(scores.contiguous()),
+                                         _ptr(residual.contiguous()), _ptr(h),
+                                         _ptr(weight.contiguous()), _ptr(out), T, k, H,
+                                         float(eps), _stream(y)), op)
+    return out, h
 
 
 class QExperts:
@@ -111,25 +170,40 @@ class MoEBlock:
     def num_experts(self) -> int:
         return self.gate_up.num_experts
 
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        """x bf16 [..., H] -> bf16 [..., H]."""
-        shape = x.shape
-        xt = x.reshape(-1, shape[-1])
-        T = xt.shape[0]
-        idx, sc = route(self.gate(xt), self.top_k, self.norm_topk_prob, self.expert_bias)
-        xb = xt.reshape(T, 1, shape[-1])
-        if idx.numel() >= 64:  # the reference sorts at >= 64 pairs (lfm2.py:204)
-            sorted_ids, _, inverse, rows = expert_sort(idx, self.num_experts)
+    def _experts(self, xt: torch.Tensor):
+        """xt bf16 [T, H] -> (y [T*k, H] in expert or token order, inverse, scores)."""
+        T, H = xt.shape
+        logits = self.gate(xt)
+        xb = xt.reshape(T, 1, H)
+        if T * self.top_k >= 64:  # the reference sorts at >= 64 pairs (lfm2.py:204)
+            _, sc, sorted_ids, _, inverse, rows = route_sort(
+                logits, self.top_k, self.num_experts, self.norm_topk_prob, self.expert_bias)
             gu = self.gate_up(xb, lhs=rows, rhs=sorted_ids, sorted_indices=True)
             y = self.down(silu_mul(gu), rhs=sorted_ids, sorted_indices=True)
         else:
+            idx, sc = route(logits, self.top_k, self.norm_topk_prob, self.expert_bias)
             inverse = None
-            rows = torch.arange(T, device=x.device, dtype=torch.int32).repeat_interleave(
+            rows = torch.arange(T, device=xt.device, dtype=torch.int32).repeat_interleave(
                 self.top_k)
             flat = idx.reshape(-1)
             gu = self.gate_up(xb, lhs=rows, rhs=flat)
             y = self.down(silu_mul(gu), rhs=flat)
-        return combine(y.reshape(T * self.top_k, -1), inverse, sc).reshape(shape)
+        return y.reshape(T * self.top_k, H), inverse, sc
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """x bf16 [..., H] -> bf16 [..., H]."""
+        y, inverse, sc = self._experts(x.reshape(-1, x.shape[-1]))
+        return combine(y, inverse, sc).reshape(x.shape)
+
+    def residual_norm(self, x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      eps: float):
+        """The block, the residual add after it and the next RMSNorm
+        (lfm2.py:409, then :404 or :436): h = bf16(self(x) + residual) ->
+        (bf16(RMSNorm(h) * weight), h), shaped like x."""
+        y, inverse, sc = self._experts(x.reshape(-1, x.shape[-1]))
+        out, h = combine_rms_norm(y, inverse, sc, residual, weight, eps)
+        return out.reshape(x.shape), h.reshape(x.shape)
 
 
-__all__ = ["route", "expert_sort", "combine", "QExperts", "MoEBlock"]
+__all__ = ["route", "expert_sort", "combine", "route_sort", "combine_rms_norm", "QExperts",
+           "MoEBlock"]

@@ -261,7 +261,9 @@ class Qwen2Model:
         (the final norm after the last layer)."""
         layer, eps = self.layers[li], self.cfg.rms_norm_eps
         x, h = fused_rms_norm(o, layer.post_norm, eps, residual=h)
-        m = layer.moe(x) if layer.moe is not None else layer.down(silu_mul(layer.gate_up(x)))
+        if layer.moe is not None:
+            return layer.moe.residual_norm(x, h, self._next_norm(li), eps)
+        m = layer.down(silu_mul(layer.gate_up(x)))
         return fused_rms_norm(m, self._next_norm(li), eps, residual=h)
 
     # ------------------------------------------------------------ prefill

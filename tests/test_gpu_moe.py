@@ -102,6 +102,57 @@ def test_combine(moe, T, k, H, sorted_rows):
     assert torch.equal(out, acc.to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("T,E,k", [(1, 128, 8), (8, 128, 8), (37, 60, 4), (64, 512, 16),
+                                   (65, 128, 8), (300, 17, 3)])
+def test_route_sort_equals_route_then_sort(moe, T, E, k):
+    """One launch up to 64 tokens (else the two kernels): bit-equal outputs."""
+    logits = (torch.randn(T, E, generator=_gen(3 * T + E), device=DEV) * 2).to(torch.bfloat16)
+    bias = torch.randn(E, generator=_gen(2), device=DEV) * 0.01
+    for b in (None, bias):
+        idx, sc = moe.route(logits, k, True, b)
+        ref = (idx, sc) + moe.expert_sort(idx, E)
+        got = moe.route_sort(logits, k, E, True, b)
+        for a, r in zip(got, ref):
+            assert torch.equal(a, r)
+
+
+@pytest.mark.parametrize("T,k,H", [(8, 8, 2048), (3, 2, 256), (130, 8, 2048), (2, 4, 8192),
+                                   (1, 1, 8)])
+@pytest.mark.parametrize("sorted_rows", [True, False])
+def test_combine_rms_norm_equals_combine_then_norm(moe, T, k, H, sorted_rows):
+    """combine -> residual add -> RMSNorm in one kernel: bit-equal to the
+    combine kernel followed by the RMSNorm kernel."""
+    dops = importlib.import_module("mlx-server-runtime_amd.decode_ops")
+    g = _gen(T * H + 7 * k)
+    y = torch.randn(T * k, H, generator=g, device=DEV).to(torch.bfloat16)
+    sc = torch.rand(T, k, generator=g, device=DEV).to(torch.bfloat16)
+    res = (torch.randn(T, H, generator=g, device=DEV) * 4).to(torch.bfloat16)
+    w = (torch.rand(H, generator=g, device=DEV) + 0.5).to(torch.bfloat16)
+    inverse = None
+    if sorted_rows:
+        inverse = torch.randperm(T * k, generator=torch.Generator().manual_seed(T)).to(
+            device=DEV, dtype=torch.int32)
+    out, h = moe.combine_rms_norm(y, inverse, sc, res, w, 1e-6)
+    ref_out, ref_h = dops.rms_norm(moe.combine(y, inverse, sc), w, 1e-6, residual=res)
+    assert torch.equal(h, ref_h) and torch.equal(out, ref_out)
+
+
+def test_fused_entry_errors(moe):
+    logits = torch.zeros(4, 16, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="experts"):
+        moe.route_sort(logits, 2, 8)
+    y = torch.zeros(8, 64, dtype=torch.bfloat16, device=DEV)
+    sc = torch.zeros(4, 2, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="residual"):
+        moe.combine_rms_norm(y, None, sc, torch.zeros(3, 64, dtype=torch.bfloat16, device=DEV),
+                             w, 1e-6)
+    with pytest.raises(NotImplementedError, match="not supported"):
+        moe.combine_rms_norm(torch.zeros(8, 8200, dtype=torch.bfloat16, device=DEV), None, sc,
+                             torch.zeros(4, 8200, dtype=torch.bfloat16, device=DEV),
+                             torch.ones(8200, dtype=torch.bfloat16, device=DEV), 1e-6)
+
+
 def _block(moe, mq, E, k, H, inter, seed=0):
     q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
     cfg = q2.Qwen2Config(H, 4 * H, 4, 2, 1, 100)
@@ -127,6 +178,20 @@ def test_moe_block_vs_float32(moe, mq, T):
     ref_idx = torch.topk(torch.softmax(_linear(mq, block.gate, x.float()), -1), k, -1).indices
     same = (torch.sort(idx.long(), -1).values == torch.sort(ref_idx, -1).values).all(-1)
     assert same.float().mean() >= 0.9
+
+
+@pytest.mark.parametrize("T", [2, 8, 100])
+def test_moe_block_residual_norm_equals_unfused(moe, mq, T):
+    """MoEBlock.residual_norm == rms_norm(block(x), residual), bit for bit."""
+    dops = importlib.import_module("mlx-server-runtime_amd.decode_ops")
+    block = _block(moe, mq, 16, 8, 256, 128, seed=9)
+    g = _gen(T + 11)
+    x = torch.randn(T, 256, generator=g, device=DEV).to(torch.bfloat16)
+    res = torch.randn(T, 256, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.rand(256, generator=g, device=DEV) + 0.5).to(torch.bfloat16)
+    out, h = block.residual_norm(x, res, w, 1e-6)
+    ref_out, ref_h = dops.rms_norm(block(x), w, 1e-6, residual=res)
+    assert torch.equal(h, ref_h) and torch.equal(out, ref_out)
 
 
 def test_moe_block_sorted_equals_unsorted(moe, mq):

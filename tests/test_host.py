@@ -34,7 +34,8 @@ def test_header_declares_the_abi():
         "mq_gather_qmm", "mq_rms_norm", "mq_rope_kv_append",
         "mq_paged_decode_attention_workspace", "mq_paged_decode_attention",
         "mq_decode_attention_step", "mq_silu_mul",
-        "mq_moe_route", "mq_moe_sort", "mq_moe_combine"])
+        "mq_moe_route", "mq_moe_sort", "mq_moe_combine", "mq_moe_route_sort",
+        "mq_moe_combine_rms_norm"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -120,6 +121,15 @@ def test_decoder_entry_validation(mq):
     assert L.mq_moe_sort(null, 0, 8, 128, null, null, null, null, null) == 0
     assert L.mq_moe_combine(null, null, null, null, 4, 8, 2044, null) == -2    # hidden % 8
     assert L.mq_moe_combine(null, null, null, null, 0, 8, 2048, null) == 0
+    rs = L.mq_moe_route_sort
+    assert rs(null, null, 4, 128, 8, 1, null, null, null, null, null, null, null) == -1
+    assert rs(null, null, 4, 600, 8, 1, null, null, null, null, null, null, null) == -2
+    assert rs(null, null, 0, 128, 8, 1, null, null, null, null, null, null, null) == 0
+    cn = L.mq_moe_combine_rms_norm
+    assert cn(null, null, null, null, null, null, null, 4, 8, 2048, 1e-6, null) == -1
+    assert cn(null, null, null, null, null, null, null, 4, 8, 8200, 1e-6, null) == -2  # > 8192
+    assert cn(null, null, null, null, null, null, null, 4, 0, 2048, 1e-6, null) == -1  # top_k
+    assert cn(null, null, null, null, null, null, null, 0, 8, 2048, 1e-6, null) == 0
 
 
 def test_capi_invalid_and_unsupported_codes(mq):
