@@ -1,0 +1,448 @@
+#pragma once
+// Decode-shaped quantized matmul (qmv) kernel and launch templates: y[m, n] = sum_k x[m, k] * (s*q + b)[n, k]
+// for a few activation rows (M <= 8).  This is mx.quantized_matmul(x, w, scales,
+// biases, transpose=True) as called by every QuantizedLinear at decode
+// (python/mlx_worker/native_mlx/models/qwen2.py:76-78,115,134,227), and, with a
+// per-batch expert index, mx.gather_qmm for unsorted / few-row MoE calls
+// (models/lfm2.py:176-187).
+//
+// HBM-bound: every weight byte is read once.  Design for gfx950:
+//  * a weight row is TPR lanes wide; lane l owns 16-byte chunks l, l+TPR, ...
+//    (32 4-bit or 16 8-bit codes per chunk), up to S chunks for each of its R
+//    rows.  Loads are issued in the order they are consumed -- x, this block's
+//    scales and biases, then the lane's weight chunks, D ahead of the one being
+//    contracted -- so waiting for x (vmcnt counts in issue order) never waits
+//    for weights, and the contraction of chunk j overlaps the arrival of
+//    chunks j+1..j+D.  Every block of a large GEMV is resident at once and
+//    the CU's memory queue is full for most of the kernel: issuing all chunks
+//    up front would leave each wave stalled in that queue with its first
+//    chunks landed, and all the arithmetic would follow the last load;
+//  * x is staged once per block in LDS as [m][slot][unit][lane] (16-byte
+//    units): consecutive lanes read consecutive addresses, and every slot/unit
+//    offset is a compile-time immediate.  Chunk sums of x and the block's
+//    scales and biases sit next to it.  Past the end of a row the LDS holds
+//    zeros, so padded lanes contribute 0 with no per-lane test;
+//  * 4-bit: ((word >> 4t) & 0x000F000F) | 0x43004300 (one v_and_or_b32 after
+//    the shift) is a pair of bfloat16 numbers 128+q, exact, contracted with an
+//    x pair by v_dot2_f32_bf16 (x stored pair-permuted: (x0,x4),(x1,x5),...);
+//    the chunk result d = sum x*(128+q) becomes s*d + (b - 128*s)*sum(x),
+//    equal to sum x*(s*q+b), right after the chunk's dot products;
+//  * 8-bit: bytes -> float (v_cvt_f32_ubyte) -> bfloat16 pairs (exact for
+//    q <= 255) -> v_dot2_f32_bf16 against natural x pairs; then s*d + b*sum(x);
+//  * per-row partial sums are reduced across the TPR lanes with DPP (LDS across
+//    waves when TPR > 64); float32 throughout, one bfloat16 rounding at the
+//    store, where QuantizedLinear's "+ bias" is fused.
+#include "mq_common.h"
+#include "mq_internal.h"
+
+namespace mq {
+namespace qmv {
+
+
+constexpr int kBlock = 256;
+constexpr int kQmvLdsBudget = 48 * 1024;
+// Two rows per lane group may use up to 52 KiB: still 3 blocks per CU.
+constexpr int kTwoRowLdsBudget = 52 * 1024;
+// Scale + bias DMA operations per wave: 2 arrays of ceil((RPB*G + GP) / 2)
+// words, at most 16 64-word operations each (RPB*G <= 2048 entries: a block
+// owns at most 256 * 8 chunks), over 4 waves.
+constexpr int kSbOpsPerWave = 8;
+// Weight chunks a lane keeps in flight ahead of the one it contracts, per
+// row count R (measured on the 4-bit K=3584 and K=18944 GEMVs: 2 for one
+// row per lane group, 3 for two).
+constexpr int lookahead(int rows) { return rows == 1 ? 2 : 3; }
+
+// Opaque register constants: the mask in an SGPR and the bfloat16 magic in a
+// VGPR let ((w >> s) & mask) | magic select v_and_or_b32 (gfx9 VOP3 encodings
+// take no literal and at most one scalar operand).
+struct Nibble {
+  uint32_t mask, magic;
+  __device__ __forceinline__ Nibble() {
+    __asm__ volatile("s_mov_b32 %0, 0xf000f" : "=s"(mask));
+    __asm__ volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+  }
+  __device__ __forceinline__ uint32_t pair(uint32_t w) const { return (w & mask) | magic; }
+};
+
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER>
+// The input pointers are deliberately not __restrict__: with it the compiler
+// may move their loads across the inline-asm barriers below (it proves the
+// asm cannot touch restrict memory), which breaks the issue order the waits
+// rely on.
+__global__ __launch_bounds__(kBlock) void qmv_kernel(
+    const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+    const uint16_t* bias, uint16_t* y, int M, int N, int K,
+    const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, int64_t E,
+    int64_t x_batches) {
+  constexpr int EPC = 128 / BITS;      // elements per 16-byte chunk
+  constexpr int UPC = EPC / 8;         // 8-element units per chunk (4 or 2)
+  constexpr int CPG = kGroup / EPC;    // chunks per group (2 or 4)
+  constexpr int SLOTS = kBlock / TPR;  // row slots per block
+  constexpr int RPB = SLOTS * R;       // rows per block
+  constexpr int WPR = TPR > 64 ? TPR / 64 : 1;  // waves per row (TPR > 64)
+  extern __shared__ u32x4_t smem[];
+  __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : 1];
+
+  const int C = K / EPC;                // chunks per row
+  const int G = K / kGroup;             // groups per row
+  const int NJ = (C + TPR - 1) / TPR;   // slots used (<= S)
+  const int CP = NJ * TPR;              // chunks per row, padded
+  const int GP = CP / CPG;              // groups per row, padded
+  const int64_t t = blockIdx.y;
+  int64_t xb = t, e = 0;
+  const int slot = threadIdx.x / TPR;
+  const int lane = threadIdx.x % TPR;
+  const int rb0 = blockIdx.x * RPB;
+  const int row0 = rb0 + slot * R;
+  // Without gather tables nothing here waits on memory before the first
+  // loads are issued: the index loads, their wait and the test would
+  // otherwise precede every address computation.
+  if constexpr (GATHER) {
+    if (lhs) xb = lhs[t];
+    if (rhs) e = rhs[t];
+    y += t * (int64_t)M * N;
+    if (xb < 0 || xb >= x_batches || e < 0 || e >= E) {  // index outside the tables: zeros
+      if (lane == 0)
+        for (int r = 0; r < R; ++r)
+          for (int m = 0; m < M; ++m)
+            if (row0 + r < N) y[(int64_t)m * N + row0 + r] = 0;
+      return;
+    }
+  }
+  // ---- 1. loads through buffer descriptors (out-of-range reads return 0):
+  // x, the block's scales/biases (contiguous: the block's rows are
+  // consecutive), then the first D weight chunks of this lane.  The rest are
+  // issued one per chunk contracted (step 3): a CU's memory queue fills long
+  // before every wave has issued all its loads, so a wave that issued them
+  // all up front would sit in the queue with its first chunks already
+  // landed, and the grid's arithmetic would pile up behind the last loads.
+  constexpr int D = S < lookahead(R) ? S : lookahead(R);
+  const int rows_here = min(RPB, N - rb0);
+  const rsrc_t xrs = make_rsrc(x + xb * (int64_t)M * K, (uint64_t)M * K * 2);
+  const rsrc_t wrs = make_rsrc(wq + (e * (int64_t)N + rb0) * (C * 4), (uint64_t)rows_here * C * 16);
+  const int64_t sb0 = e * (int64_t)N * G + (int64_t)rb0 * G;
+  const int n_sb = rows_here * G;  // <= RPB*G <= 1024 entries
+  const rsrc_t srs = make_rsrc(scales + sb0, (uint64_t)n_sb * 2);
+  const rsrc_t brs = make_rsrc(biases + sb0, (uint64_t)n_sb * 2);
+
+  const int x_units = MT * CP * UPC;  // padded 8-element units of x
+  u32x4_t xr[XU];
+#pragma unroll
+  for (int k = 0; k < XU; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    const int m = MT == 1 ? 0 : i / (CP * UPC);
+    const int u = i - m * (CP * UPC);  // unit within the row
+    const bool real = m < M && u < C * UPC;
+    xr[k] = buf_load16(xrs, real ? (uint32_t)(m * K + u * 8) * 2 : kOutOfRange);
+  }
+  // Scales and biases go straight to LDS (buffer_load ... lds, 4 bytes per
+  // lane).  Entries past the block's rows read as zeros.
+  u32x4_t* xl = smem;
+  float* xsum = reinterpret_cast<float*>(smem + MT * CP * UPC);
+  uint16_t* sl = reinterpret_cast<uint16_t*>(xsum + MT * CP);  // [RPB*G + GP] scales
+  const int sb_words = (RPB * G + GP + 1) / 2;                 // 32-bit words per array
+  uint16_t* bl = sl + 2 * ((sb_words + 63) / 64 * 64);          // biases, same layout
+  {
+    // A fixed number of operations per wave (the largest any shape needs;
+    // extra ones repeat the last), so that every wait below counts exactly.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
+    const int ops = (sb_words + 63) / 64;  // wave-wide 4-byte DMA operations per array
+#pragma unroll
+    for (int q = 0; q < kSbOpsPerWave; ++q) {
+      const int o = min(wave + q * (kBlock / 64), 2 * ops - 1);
+      const bool is_b = o >= ops;
+      const int oo = is_b ? o - ops : o;
+      uint16_t* dst = (is_b ? bl : sl) + oo * 128;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_b ? brs : srs,
+                                               (__attribute__((address_space(3))) void*)dst, 4,
+                                               (uint32_t)(oo * 64 + ln) * 4, 0, 0, 0);
+    }
+  }
+  // Weight chunk j of the lane's R rows; slots past NJ read nothing (out of
+  // range: zeros), so every chunk is one straight-line load per row and the
+  // waits below count exactly.  The empty asm statements pin the issue
+  // order: vmcnt retires in issue order.
+  u32x4_t wv[S][R];
+  auto issue = [&](int j) {
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      wv[j][r] = buf_load16<kBufNT>(
+          wrs, j < NJ ? (uint32_t)(((slot * R + r) * C + lane + j * TPR) * 16) : kOutOfRange);
+    __asm__ volatile("" ::: "memory");
+  };
+#pragma unroll
+  for (int j = 0; j < D; ++j) issue(j);
+  // x and this wave's scale/bias DMA have landed once at most the D*R weight
+  // loads are outstanding; the barrier below then publishes every wave's.
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(D * R) : "memory");
+
+  // ---- 2. LDS: x as [m][slot j][unit h][lane] (4-bit pair-permuted) and
+  // chunk sums [m][chunk]; zeros past the row.
+#pragma unroll
+  for (int k = 0; k < XU; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (k * kBlock >= x_units) break;  // uniform
+    const int m = MT == 1 ? 0 : i / (CP * UPC);
+    const int u = i - m * (CP * UPC);
+    const int c = u / UPC, h = u % UPC;
+    u32x4_t v = xr[k];
+    float s8 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s8 += lo_bf16(v[q]) + hi_bf16(v[q]);
+    if constexpr (BITS == 4) {
+      const u32x4_t p = {(v[0] & 0xffffu) | (v[2] << 16), (v[0] >> 16) | (v[2] & 0xffff0000u),
+                         (v[1] & 0xffffu) | (v[3] << 16), (v[1] >> 16) | (v[3] & 0xffff0000u)};
+      v = p;
+    }
+    s8 += dpp_f32<0xb1>(s8);  // the UPC (2 or 4) consecutive units of a chunk
+    if constexpr (UPC == 4) s8 += dpp_f32<0x4e>(s8);
+    if (i < x_units) {
+      xl[((m * NJ + c / TPR) * UPC + h) * TPR + c % TPR] = v;
+      if (h == 0) xsum[m * CP + c] = s8;
+    }
+  }
+  lds_barrier();
+
+  // ---- 3. contract: chunk j, then its scale/bias epilogue, after issuing
+  // chunk j + D.  Straight-line over all S chunks and MT rows so that the
+  // wait before chunk j covers chunks <= j only: rows m >= M are zeros in
+  // LDS; chunks past NJ (only when S > NJ) read a valid chunk and are masked
+  // out.
+  const Nibble nib;
+  float acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+
+  const u32x4_t* xlane = xl + lane;
+  const float* xslane = xsum + lane;
+  const uint16_t* slane = sl + slot * R * G + lane / CPG;
+  const uint16_t* blane = bl + slot * R * G + lane / CPG;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    if (j + D < S) issue(j + D);
+    const int jj = j < NJ ? j : NJ - 1;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      u32x4_t xv[UPC];
+#pragma unroll
+      for (int h = 0; h < UPC; ++h) xv[h] = xlane[((m * NJ + jj) * UPC + h) * TPR];
+      const float xs = xslane[m * CP + jj * TPR];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.f;
+        if constexpr (BITS == 4) {
+#pragma unroll
+          for (int wi = 0; wi < 4; ++wi) {
+            const uint32_t wd = wv[j][r][wi];
+            d = dot2_bf16(nib.pair(wd), xv[wi][0], d);
+            d = dot2_bf16(nib.pair(wd >> 4), xv[wi][1], d);
+            d = dot2_bf16(nib.pair(wd >> 8), xv[wi][2], d);
+            d = dot2_bf16(nib.pair(wd >> 12), xv[wi][3], d);
+          }
+        } else {
+#pragma unroll
+          for (int wi = 0; wi < 4; ++wi) {
+            const uint32_t wd = wv[j][r][wi];
+            d = dot2_bf16(pack_bf16x2(ubyte_f32<0>(wd), ubyte_f32<1>(wd)),
+                          xv[wi / 2][(wi % 2) * 2], d);
+            d = dot2_bf16(pack_bf16x2(ubyte_f32<2>(wd), ubyte_f32<3>(wd)),
+                          xv[wi / 2][(wi % 2) * 2 + 1], d);
+          }
+        }
+        const float sc = bf16_bits_to_f32(slane[r * G + jj * (TPR / CPG)]);
+        const float bi = bf16_bits_to_f32(blane[r * G + jj * (TPR / CPG)]);
+        if (j < NJ && m < M) {  // uniform
+          if constexpr (BITS == 4) {
+            acc[r][m] = fmaf(sc, d, acc[r][m]);
+            acc[r][m] = fmaf(fmaf(-128.f, sc, bi), xs, acc[r][m]);
+          } else {
+            acc[r][m] = fmaf(sc, d, acc[r][m]);
+            acc[r][m] = fmaf(bi, xs, acc[r][m]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- 4. reduce across the TPR lanes of each row, store ----
+  constexpr int W = TPR < 64 ? TPR : 64;
+  constexpr int SUM_LANE = dpp_sum_lane<W>();
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = dpp_group_sum<W>(acc[r][m]);
+
+  if constexpr (WPR == 1) {
+    if (lane % W == SUM_LANE) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row >= N) continue;
+        const float add = bias ? bf16_bits_to_f32(bias[row]) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          if (m < M) y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(acc[r][m] + add);
+      }
+    }
+  } else {
+    const int wave = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) red[(wave * R + r) * MT + m] = acc[r][m];
+    }
+    __syncthreads();
+    if (lane == 0) {
+      const int w0 = slot * WPR;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row >= N) continue;
+        const float add = bias ? bf16_bits_to_f32(bias[row]) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          float v = 0.f;
+#pragma unroll
+          for (int w = 0; w < WPR; ++w) v += red[((w0 + w) * R + r) * MT + m];
+          if (m < M) y[(int64_t)m * N + row] = (uint16_t)f32_to_bf16_bits(v + add);
+        }
+      }
+    }
+  }
+}
+
+// x units, chunk sums, then scales and biases: each array ceil((RPB*G + GP) / 2)
+// words rounded up to whole 64-lane DMA operations.
+inline int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R) {
+  const int epc = 128 / bits;
+  const int64_t C = K / epc;
+  const int64_t CP = (C + tpr - 1) / tpr * tpr;
+  const int64_t G = K / kGroup;
+  const int64_t GP = CP / (kGroup / epc);
+  const int64_t RPB = (kBlock / tpr) * R;
+  const int64_t sb_words = (RPB * G + GP + 1) / 2;
+  return MT * CP * 16 * (epc / 8) + MT * CP * 4 + 2 * ((sb_words + 63) / 64) * 256;
+}
+
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER>
+hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+               const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+               const GatherMap& g, hipStream_t stream) {
+  const int64_t rows_per_block = (kBlock / TPR) * R;
+  const size_t lds = (size_t)lds_bytes(BITS, TPR, MT, K, R);
+  const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)g.T);
+  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, GATHER>), grid, dim3(kBlock), lds, stream, x,
+                     wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E, g.x_batches);
+  return hipGetLastError();
+}
+
+template <int BITS, int TPR, int R, int S, int MT, bool GATHER>
+hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                  const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                  const GatherMap& g, hipStream_t stream) {
+  constexpr int EPC = 128 / BITS;
+  const int64_t CP = (K / EPC + TPR - 1) / TPR * TPR;
+  const int64_t units = (MT * CP * (EPC / 8) + kBlock - 1) / kBlock;  // x units per thread
+  if (units <= 2) return run<BITS, TPR, R, S, MT, 2, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 4) return run<BITS, TPR, R, S, MT, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 12) return run<BITS, TPR, R, S, MT, 12, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  return hipErrorInvalidValue;  // excluded by qmv_fits
+}
+
+template <int BITS, int TPR, int R, int S, bool GATHER>
+hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                  const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                  const GatherMap& g, hipStream_t stream) {
+  if (M <= 1) return run_xu<BITS, TPR, R, S, 1, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 2) return run_xu<BITS, TPR, R, S, 2, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 4) return run_xu<BITS, TPR, R, S, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  return run_xu<BITS, TPR, R, S, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+}
+
+inline constexpr int kTprs[] = {8, 16, 32, 64, 128, 256};
+
+// Lanes per row: the narrowest whose lanes own at most 8 chunks each, widened
+// while the grid has fewer than 2 blocks per CU.  8 lanes only for short rows
+// (<= 24 chunks: 3 slots), where 16 lanes would leave a quarter of the slots
+// empty (an expert's down projection, K = 768).
+inline int pick_tpr(int64_t C, int64_t N, int64_t T) {
+  int pick = C <= 24 ? 0 : 1;
+  while (pick < 5 && (C + kTprs[pick] - 1) / kTprs[pick] > 8) ++pick;
+  while (pick < 5 && ((N * kTprs[pick]) / kBlock) * T < 512) ++pick;
+  return kTprs[pick];
+}
+
+// R = 2 needs its scales to fit the block's LDS DMA budget (RPB * G + GP
+// entries per array, kSbOpsPerWave operations per wave) and the LDS budget.
+inline bool two_rows(int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t T) {
+  const int epc = 128 / bits;
+  const int64_t C = K / epc, G = K / kGroup;
+  const int64_t CP = (C + tpr - 1) / tpr * tpr, GP = CP / (kGroup / epc);
+  const int64_t rpb = (kBlock / tpr) * 2;
+  const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int64_t sb_words = (rpb * G + GP + 1) / 2;
+  return 2 * ((sb_words + 63) / 64) <= kSbOpsPerWave * (kBlock / 64) &&
+         lds_bytes(bits, tpr, mt, K, 2) <= kTwoRowLdsBudget && (N + rpb - 1) / rpb * T >= 512;
+}
+
+// Launches the GEMV for one code width; GATHER selects the kernels that
+// read per-batch x / expert indices.  Each (BITS, GATHER) pair is
+// instantiated in a translation unit of its own (mq_qmv*.hip), so that the
+// four compile in parallel.
+template <int BITS, bool GATHER>
+hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                    const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                    const GatherMap& g, hipStream_t stream) {
+  constexpr int EPC = 128 / BITS;
+  const int64_t C = K / EPC;
+  const int tpr = pick_tpr(C, N, g.T);
+  const int slots = (int)((C + tpr - 1) / tpr);
+  switch (tpr) {
+    case 8:
+      return run_mt<BITS, 8, 1, 3, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    // Chunk slots per lane S: the instantiated S >= NJ closest to it (slots
+    // past NJ cost arithmetic on zeros, not memory traffic).  The S values
+    // cover the model shapes exactly: K = 3584 / 18944 / 2048 / 768 at 4 and
+    // 8 bits.
+    case 16:
+      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 16, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    case 32:
+      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 32, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    case 64:
+      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 64, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    case 128:
+      // Two rows per lane group when that still leaves 512 blocks: a block
+      // stages all of x (long rows: up to 40 KB), so rows per block divide
+      // that L2 traffic (the down projection: 2.1x less x than weights).
+      if (slots <= 5 && two_rows(BITS, 128, M, N, K, g.T))
+        return run_mt<BITS, 128, 2, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 128, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    default:
+      if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return hipErrorInvalidValue;  // excluded by qmv_fits
+  }
+}
+
+}  // namespace qmv
+}  // namespace mq
+
+// Explicit instantiation (or, after `extern`, its declaration) of one
+// run_bits launch, inside namespace mq.
+#define MQ_QMV_INSTANCE(BITS, GATHER)                                                        \
+  template hipError_t qmv::run_bits<BITS, GATHER>(                                          \
+      const uint16_t*, const uint32_t*, const uint16_t*, const uint16_t*, const uint16_t*, \
+      uint16_t*, int64_t, int64_t, int64_t, const GatherMap&, hipStream_t)
