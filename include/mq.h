@@ -227,6 +227,23 @@ int mq_decode_attention_step(const mq_bf16* qkv, const int64_t* positions,
 int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inter,
                 hipStream_t stream);
 
+/*
+ * The MLP's gate|up projection and silu(gate) * up in one kernel
+ * (models/qwen2.py:132-133: down(silu(gate(x)) * up(x)) up to the down
+ * projection): wq [2N, K * bits / 32] with the gate rows first (as the fused
+ * gate|up matrix of mq_quantized_matmul), y bfloat16 [M, N] =
+ * mq_silu_mul(mq_quantized_matmul(x, wq, ...)), bit for bit.  Decode shapes
+ * of large matrices only (M <= 2, 2*N*K >= 2^25, K rows of at most 64 lanes:
+ * where mq_quantized_matmul runs its dot2 GEMV):
+ * mq_quantized_matmul_swiglu_supported says whether a shape is one; others
+ * return MQ_ERR_UNSUPPORTED.
+ */
+int mq_quantized_matmul_swiglu_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                         int bits);
+int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                               const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N, int64_t K,
+                               int group_size, int bits, hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * Mixture-of-experts routing around mq_gather_qmm (models/lfm2.py:348-375,
  * SwitchGLU lfm2.py:193-218 with _gather_sort/_scatter_unsort :613-622).

@@ -204,6 +204,35 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return y
 
 
+def swiglu_supported(M: int, N: int, K: int, group_size: int = 64, bits: int = 4) -> bool:
+    """Whether quantized_matmul_swiglu takes M rows of x against a [2N, K] gate|up matrix."""
+    return bool(_lib.lib().mq_quantized_matmul_swiglu_supported(M, N, K, group_size, bits))
+
+
+def quantized_matmul_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                            biases: torch.Tensor, group_size: int = 64,
+                            bits: int = 4) -> torch.Tensor:
+    """silu(x @ gate^T) * (x @ up^T) for a fused gate|up matrix w [2N, K] (gate
+    rows first), as silu_mul(quantized_matmul(x, w, ...)) computes it, bit for
+    bit, in one kernel (decode shapes: see swiglu_supported)."""
+    op = "quantized_matmul_swiglu"
+    _require_gpu(op, x=x, w=w, scales=scales, biases=biases)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    _check_bf16(op, "x", x)
+    if w.ndim != 2 or w.shape[0] % 2:
+        raise ValueError(f"[{op}] w must be [2N, K * bits / 32], got {tuple(w.shape)}")
+    if x.shape[-1] != K:
+        raise ValueError(f"[{op}] x has {x.shape[-1]} columns, expected {K}")
+    N = w.shape[0] // 2
+    xc = x.contiguous()
+    M = xc.numel() // K
+    y = torch.empty(tuple(x.shape[:-1]) + (N,), dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.lib().mq_quantized_matmul_swiglu(
+        _ptr(xc), _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()),
+        _ptr(y), M, N, K, group_size, bits, _stream(x)), op)
+    return y
+
+
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                lhs_indices: torch.Tensor | None = None, rhs_indices: torch.Tensor | None = None,
                transpose: bool = True, group_size: int = 64, bits: int = 4, mode: str = "affine",

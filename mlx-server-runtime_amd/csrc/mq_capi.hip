@@ -167,6 +167,35 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
   return 0;
 }
 
+int mq_quantized_matmul_swiglu_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                         int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
+  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
+  // Only where mq_quantized_matmul itself runs the dot2 GEMV on the 2N rows,
+  // so that the fused result is that of the two kernels, bit for bit.
+  if (use_matrix_core_gemv(M, 2 * N, K)) return 0;
+  return mq::qmv_swiglu_fits(M, N, K, bits) ? 1 : 0;
+}
+
+int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                               const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N, int64_t K,
+                               int group_size, int bits, hipStream_t stream) {
+  const char* op = "quantized_matmul_swiglu";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", 2 * N)) return rc;
+  if (M == 0 || N == 0) return ok();
+  if (!mq_quantized_matmul_swiglu_supported(M, N, K, group_size, bits))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] M=%lld, N=%lld, K=%lld is not a fused shape (M <= 2, 2*N*K >= 2^25, rows "
+                "of at most 64 lanes); use mq_quantized_matmul and mq_silu_mul.",
+                op, (long long)M, (long long)N, (long long)K);
+  if (!x || !wq || !scales || !biases || !y) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(wq))
+    return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
+  return hip_status(mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+}
+
 int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
                         const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
                         int64_t N, int64_t K, int group_size, int bits, int transpose,

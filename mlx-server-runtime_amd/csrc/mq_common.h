@@ -40,6 +40,14 @@ __device__ __forceinline__ float hi_bf16(uint32_t p) {
   return __builtin_bit_cast(float, p & 0xffff0000u);
 }
 
+// SwiGLU on bfloat16 values (models/qwen2.py:43-44, 132-133): silu(g) rounded
+// to bfloat16 as nn.silu stores it, times u, rounded -> bfloat16 bits.  One
+// definition for every kernel that computes it, so they agree bit for bit.
+__device__ __forceinline__ uint16_t silu_mul_bf16(float g, float u) {
+  const float s = bf16_bits_to_f32(f32_to_bf16_bits(g / (1.f + __expf(-g))));
+  return (uint16_t)f32_to_bf16_bits(s * u);
+}
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                          __builtin_bit_cast(bf16x2_t, b), c, false);

@@ -486,11 +486,9 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
   const u32x4_t up = reinterpret_cast<const u32x4_t*>(gu + r * 2 * inter + inter)[u];
   u32x4_t o;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float g0 = lo_bf16(g[q]), g1 = hi_bf16(g[q]);
-    const float s0 = bf16r(g0 / (1.f + __expf(-g0))), s1 = bf16r(g1 / (1.f + __expf(-g1)));
-    o[q] = pack_bf16x2(s0 * lo_bf16(up[q]), s1 * hi_bf16(up[q]));
-  }
+  for (int q = 0; q < 4; ++q)
+    o[q] = silu_mul_bf16(lo_bf16(g[q]), lo_bf16(up[q])) |
+           (uint32_t)silu_mul_bf16(hi_bf16(g[q]), hi_bf16(up[q])) << 16;
   reinterpret_cast<u32x4_t*>(out + r * inter)[u] = o;
 }
 

@@ -28,6 +28,10 @@ bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                       int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
+bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits);
+hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                             const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                             int bits, hipStream_t stream);
 
 // Same contract on the matrix cores for M <= 8 (4-bit) / 16 (8-bit); valid
 // when qmvm_fits(M, N, K, bits, T) (K a multiple of 256, at most 12 chunks

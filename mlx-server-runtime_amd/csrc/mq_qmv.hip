@@ -1,15 +1,17 @@
 // Decode-shaped quantized matmul (qmv): dispatch and the shape test.  The
 // kernel and its launch templates are in mq_qmv_kernel.h; this file
 // instantiates the plain 4-bit launches, mq_qmv_b8.hip / mq_qmv_g4.hip /
-// mq_qmv_g8.hip the others.
+// mq_qmv_g8.hip / mq_qmv_swiglu.hip the others.
 #include "mq_qmv_kernel.h"
 
 namespace mq {
 
-MQ_QMV_INSTANCE(4, false);
-extern MQ_QMV_INSTANCE(8, false);
-extern MQ_QMV_INSTANCE(4, true);
-extern MQ_QMV_INSTANCE(8, true);
+MQ_QMV_INSTANCE(4, false, 0);
+extern MQ_QMV_INSTANCE(8, false, 0);
+extern MQ_QMV_INSTANCE(4, true, 0);
+extern MQ_QMV_INSTANCE(8, true, 0);
+extern MQ_QMV_INSTANCE(4, false, 1);
+extern MQ_QMV_INSTANCE(8, false, 1);
 
 using qmv::kBlock;
 using qmv::kQmvLdsBudget;
@@ -27,6 +29,25 @@ bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T) {
   return qmv::lds_bytes(bits, tpr, mt, K, 1) <= kQmvLdsBudget && units <= 12 * kBlock;
 }
 
+// The SwiGLU GEMV: N outputs from a 2N-row matrix, M <= 2, at most one wave
+// per row (a block pairs RPB/2 gate rows with their up rows), and every byte
+// offset of the block's rows within one buffer descriptor.
+bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits) {
+  if (M < 1 || M > 2 || N < 1 || !qmv_fits(M, 2 * N, K, bits, 1)) return false;
+  const int64_t C = K / (128 / bits);
+  return qmv::pick_tpr(C, 2 * N, 1) <= 64 && 2 * N * C * 16 < (int64_t(1) << 32);
+}
+
+hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                             const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                             int bits, hipStream_t stream) {
+  if (N == 0 || M == 0) return hipSuccess;
+  const GatherMap g1{nullptr, nullptr, 1, 1, 1};
+  if (bits == 4)
+    return qmv::run_bits<4, false, 1>(x, wq, scales, biases, nullptr, y, M, N, K, g1, stream);
+  return qmv::run_bits<8, false, 1>(x, wq, scales, biases, nullptr, y, M, N, K, g1, stream);
+}
+
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                       int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream) {
@@ -34,10 +55,10 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
   // A plain matmul carries no tables: its kernels skip the index loads.
   const bool gather = g.lhs || g.rhs || g.T != 1;
   if (bits == 4)
-    return gather ? qmv::run_bits<4, true>(x, wq, scales, biases, bias, y, M, N, K, g, stream)
-                  : qmv::run_bits<4, false>(x, wq, scales, biases, bias, y, M, N, K, g, stream);
-  return gather ? qmv::run_bits<8, true>(x, wq, scales, biases, bias, y, M, N, K, g, stream)
-                : qmv::run_bits<8, false>(x, wq, scales, biases, bias, y, M, N, K, g, stream);
+    return gather ? qmv::run_bits<4, true, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream)
+                  : qmv::run_bits<4, false, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream);
+  return gather ? qmv::run_bits<8, true, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream)
+                : qmv::run_bits<8, false, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream);
 }
 
 }  // namespace mq

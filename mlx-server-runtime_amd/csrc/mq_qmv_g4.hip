@@ -2,5 +2,5 @@
 #include "mq_qmv_kernel.h"
 
 namespace mq {
-MQ_QMV_INSTANCE(4, true);
+MQ_QMV_INSTANCE(4, true, 0);
 }  // namespace mq

@@ -64,7 +64,11 @@ struct Nibble {
   __device__ __forceinline__ uint32_t pair(uint32_t w) const { return (w & mask) | magic; }
 };
 
-template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER>
+// EPI 0: y[m, n] = (x W^T)[m, n] (+ bias[n]).  EPI 1 (SwiGLU, the gate and up
+// projections of a Qwen2 MLP as one matrix of 2N rows, gate rows first):
+// y[m, n] = bf16(bf16(silu(g)) * u) with g, u the bfloat16 results of rows n
+// and N + n -- a block computes RPB/2 gate rows and the matching up rows.
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI>
 // The input pointers are deliberately not __restrict__: with it the compiler
 // may move their loads across the inline-asm barriers below (it proves the
 // asm cannot touch restrict memory), which breaks the issue order the waits
@@ -80,8 +84,10 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   constexpr int SLOTS = kBlock / TPR;  // row slots per block
   constexpr int RPB = SLOTS * R;       // rows per block
   constexpr int WPR = TPR > 64 ? TPR / 64 : 1;  // waves per row (TPR > 64)
+  constexpr int HALF = RPB / 2;        // SwiGLU: output rows per block
+  static_assert(EPI == 0 || (!GATHER && WPR == 1 && RPB % 2 == 0), "SwiGLU epilogue layout");
   extern __shared__ u32x4_t smem[];
-  __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : 1];
+  __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : EPI == 1 ? RPB * MT : 1];
 
   const int C = K / EPC;                // chunks per row
   const int G = K / kGroup;             // groups per row
@@ -92,7 +98,8 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   int64_t xb = t, e = 0;
   const int slot = threadIdx.x / TPR;
   const int lane = threadIdx.x % TPR;
-  const int rb0 = blockIdx.x * RPB;
+  // First weight row of the block (EPI 1: first gate row = first output row).
+  const int rb0 = blockIdx.x * (EPI == 1 ? HALF : RPB);
   const int row0 = rb0 + slot * R;
   // Without gather tables nothing here waits on memory before the first
   // loads are issued: the index loads, their wait and the test would
@@ -117,13 +124,17 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   // all up front would sit in the queue with its first chunks already
   // landed, and the grid's arithmetic would pile up behind the last loads.
   constexpr int D = S < lookahead(R) ? S : lookahead(R);
-  const int rows_here = min(RPB, N - rb0);
+  // Local row lr = slot*R + r lies rel(lr) rows past rb0: the block's rows
+  // are consecutive, or (EPI 1) HALF gate rows and, N rows further, their up
+  // rows.  Rows past the matrix read as zeros (out of the descriptor's range).
+  const int rows_here = min(EPI == 1 ? HALF : RPB, N - rb0);
+  const int span = EPI == 1 ? N + rows_here : rows_here;  // rows the descriptors cover
+  auto rel = [&](int lr) { return EPI == 1 && lr >= HALF ? N - HALF + lr : lr; };
   const rsrc_t xrs = make_rsrc(x + xb * (int64_t)M * K, (uint64_t)M * K * 2);
-  const rsrc_t wrs = make_rsrc(wq + (e * (int64_t)N + rb0) * (C * 4), (uint64_t)rows_here * C * 16);
+  const rsrc_t wrs = make_rsrc(wq + (e * (int64_t)N + rb0) * (C * 4), (uint64_t)span * C * 16);
   const int64_t sb0 = e * (int64_t)N * G + (int64_t)rb0 * G;
-  const int n_sb = rows_here * G;  // <= RPB*G <= 1024 entries
-  const rsrc_t srs = make_rsrc(scales + sb0, (uint64_t)n_sb * 2);
-  const rsrc_t brs = make_rsrc(biases + sb0, (uint64_t)n_sb * 2);
+  const rsrc_t srs = make_rsrc(scales + sb0, (uint64_t)span * G * 2);
+  const rsrc_t brs = make_rsrc(biases + sb0, (uint64_t)span * G * 2);
 
   const int x_units = MT * CP * UPC;  // padded 8-element units of x
   u32x4_t xr[XU];
@@ -143,19 +154,29 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   const int sb_words = (RPB * G + GP + 1) / 2;                 // 32-bit words per array
   uint16_t* bl = sl + 2 * ((sb_words + 63) / 64 * 64);          // biases, same layout
   {
-    // A fixed number of operations per wave (the largest any shape needs;
-    // extra ones repeat the last), so that every wait below counts exactly.
+    // A fixed number of operations per wave, so that every wait below counts
+    // exactly: the most this instance can need (a row has at most S*TPR
+    // chunks, so RPB*G + GP <= (RPB + 1) * S*TPR/CPG entries); extra ones
+    // repeat the last.  Each is a VMEM instruction in a congested queue.
+    constexpr int SB_WORDS_MAX = ((RPB + 1) * (S * TPR / CPG) + 1) / 2;
+    constexpr int OPS_PER_WAVE = (2 * ((SB_WORDS_MAX + 63) / 64) + kBlock / 64 - 1) / (kBlock / 64);
+    constexpr int NQ = OPS_PER_WAVE < kSbOpsPerWave ? OPS_PER_WAVE : kSbOpsPerWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
     const int ops = (sb_words + 63) / 64;  // wave-wide 4-byte DMA operations per array
 #pragma unroll
-    for (int q = 0; q < kSbOpsPerWave; ++q) {
+    for (int q = 0; q < NQ; ++q) {
       const int o = min(wave + q * (kBlock / 64), 2 * ops - 1);
       const bool is_b = o >= ops;
       const int oo = is_b ? o - ops : o;
       uint16_t* dst = (is_b ? bl : sl) + oo * 128;
+      // Word w holds entries 2w, 2w+1 of one local row (G is even); EPI 1
+      // moves the up half (w >= HALF*G/2, pad words included) N - HALF rows on.
+      const int w = oo * 64 + ln;
+      const uint32_t src = EPI == 1 && 2 * w >= HALF * G ? (uint32_t)(2 * w + (N - HALF) * G) * 2
+                                                          : (uint32_t)w * 4;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(is_b ? brs : srs,
                                                (__attribute__((address_space(3))) void*)dst, 4,
-                                               (uint32_t)(oo * 64 + ln) * 4, 0, 0, 0);
+                                               src, 0, 0, 0);
     }
   }
   // Weight chunk j of the lane's R rows; slots past NJ read nothing (out of
@@ -168,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r)
       wv[j][r] = buf_load16<kBufNT>(
-          wrs, j < NJ ? (uint32_t)(((slot * R + r) * C + lane + j * TPR) * 16) : kOutOfRange);
+          wrs, j < NJ ? (uint32_t)((rel(slot * R + r) * C + lane + j * TPR) * 16) : kOutOfRange);
     __asm__ volatile("" ::: "memory");
   };
 #pragma unroll
@@ -275,7 +296,21 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[r][m] = dpp_group_sum<W>(acc[r][m]);
 
-  if constexpr (WPR == 1) {
+  if constexpr (EPI == 1) {
+    // g and u rounded to bfloat16 as the GEMV would store them, then
+    // silu_mul's arithmetic on the pair.
+    if (lane % W == SUM_LANE) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          red[m * RPB + slot * R + r] = bf16_bits_to_f32(f32_to_bf16_bits(acc[r][m]));
+    }
+    __syncthreads();
+    const int o = threadIdx.x % HALF, m = threadIdx.x / HALF;
+    if (m < M && m < MT && o < rows_here)
+      y[(int64_t)m * N + rb0 + o] = silu_mul_bf16(red[m * RPB + o], red[m * RPB + HALF + o]);
+  } else if constexpr (WPR == 1) {
     if (lane % W == SUM_LANE) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -328,39 +363,43 @@ inline int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R) {
   return MT * CP * 16 * (epc / 8) + MT * CP * 4 + 2 * ((sb_words + 63) / 64) * 256;
 }
 
-template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER>
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                const GatherMap& g, hipStream_t stream) {
-  const int64_t rows_per_block = (kBlock / TPR) * R;
+  const int64_t rows_per_block = (kBlock / TPR) * R / (EPI == 1 ? 2 : 1);
   const size_t lds = (size_t)lds_bytes(BITS, TPR, MT, K, R);
   const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)g.T);
-  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, GATHER>), grid, dim3(kBlock), lds, stream, x,
+  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, GATHER, EPI>), grid, dim3(kBlock), lds, stream, x,
                      wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E, g.x_batches);
   return hipGetLastError();
 }
 
-template <int BITS, int TPR, int R, int S, int MT, bool GATHER>
+template <int BITS, int TPR, int R, int S, int MT, bool GATHER, int EPI>
 hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                   const GatherMap& g, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t CP = (K / EPC + TPR - 1) / TPR * TPR;
   const int64_t units = (MT * CP * (EPC / 8) + kBlock - 1) / kBlock;  // x units per thread
-  if (units <= 2) return run<BITS, TPR, R, S, MT, 2, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (units <= 4) return run<BITS, TPR, R, S, MT, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (units <= 12) return run<BITS, TPR, R, S, MT, 12, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 2) return run<BITS, TPR, R, S, MT, 2, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 4) return run<BITS, TPR, R, S, MT, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (units <= 12) return run<BITS, TPR, R, S, MT, 12, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
   return hipErrorInvalidValue;  // excluded by qmv_fits
 }
 
-template <int BITS, int TPR, int R, int S, bool GATHER>
+template <int BITS, int TPR, int R, int S, bool GATHER, int EPI>
 hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                   const GatherMap& g, hipStream_t stream) {
-  if (M <= 1) return run_xu<BITS, TPR, R, S, 1, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 2) return run_xu<BITS, TPR, R, S, 2, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 4) return run_xu<BITS, TPR, R, S, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  return run_xu<BITS, TPR, R, S, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 1) return run_xu<BITS, TPR, R, S, 1, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 2) return run_xu<BITS, TPR, R, S, 2, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if constexpr (EPI == 1) {
+    return hipErrorInvalidValue;  // SwiGLU: M <= 2 (excluded by qmv_swiglu_fits)
+  } else {
+    if (M <= 4) return run_xu<BITS, TPR, R, S, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    return run_xu<BITS, TPR, R, S, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  }
 }
 
 inline constexpr int kTprs[] = {8, 16, 32, 64, 128, 256};
@@ -390,50 +429,56 @@ inline bool two_rows(int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t
 }
 
 // Launches the GEMV for one code width; GATHER selects the kernels that
-// read per-batch x / expert indices.  Each (BITS, GATHER) pair is
-// instantiated in a translation unit of its own (mq_qmv*.hip), so that the
-// four compile in parallel.
-template <int BITS, bool GATHER>
+// read per-batch x / expert indices, EPI the SwiGLU epilogue (N output rows
+// of a 2N-row matrix).  Each (BITS, GATHER, EPI) triple is instantiated in a
+// translation unit of its own (mq_qmv*.hip), so that they compile in
+// parallel.
+template <int BITS, bool GATHER, int EPI>
 hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                     const GatherMap& g, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t C = K / EPC;
-  const int tpr = pick_tpr(C, N, g.T);
+  const int tpr = pick_tpr(C, EPI == 1 ? 2 * N : N, g.T);
   const int slots = (int)((C + tpr - 1) / tpr);
   switch (tpr) {
     case 8:
-      return run_mt<BITS, 8, 1, 3, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 8, 1, 3, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
     // Chunk slots per lane S: the instantiated S >= NJ closest to it (slots
     // past NJ cost arithmetic on zeros, not memory traffic).  The S values
     // cover the model shapes exactly: K = 3584 / 18944 / 2048 / 768 at 4 and
     // 8 bits.
     case 16:
-      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 16, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 16, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
     case 32:
-      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 32, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 32, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
     case 64:
-      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 64, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-    case 128:
-      // Two rows per lane group when that still leaves 512 blocks: a block
-      // stages all of x (long rows: up to 40 KB), so rows per block divide
-      // that L2 traffic (the down projection: 2.1x less x than weights).
-      if (slots <= 5 && two_rows(BITS, 128, M, N, K, g.T))
-        return run_mt<BITS, 128, 2, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 128, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 64, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
     default:
-      if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return hipErrorInvalidValue;  // excluded by qmv_fits
+      if constexpr (EPI == 1) {
+        return hipErrorInvalidValue;  // SwiGLU: one wave per row at most
+      } else {
+        if (tpr == 128) {
+          // Two rows per lane group when that still leaves 512 blocks: a block
+          // stages all of x (long rows: up to 40 KB), so rows per block divide
+          // that L2 traffic (the down projection: 2.1x less x than weights).
+          if (slots <= 5 && two_rows(BITS, 128, M, N, K, g.T))
+            return run_mt<BITS, 128, 2, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+          if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+          return run_mt<BITS, 128, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+        }
+        if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+        if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+        if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+        return hipErrorInvalidValue;  // excluded by qmv_fits
+      }
   }
 }
 
@@ -442,7 +487,7 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
 
 // Explicit instantiation (or, after `extern`, its declaration) of one
 // run_bits launch, inside namespace mq.
-#define MQ_QMV_INSTANCE(BITS, GATHER)                                                        \
-  template hipError_t qmv::run_bits<BITS, GATHER>(                                          \
+#define MQ_QMV_INSTANCE(BITS, GATHER, EPI)                                                   \
+  template hipError_t qmv::run_bits<BITS, GATHER, EPI>(                                     \
       const uint16_t*, const uint32_t*, const uint16_t*, const uint16_t*, const uint16_t*, \
       uint16_t*, int64_t, int64_t, int64_t, const GatherMap&, hipStream_t)

@@ -22,10 +22,10 @@ same: q/k/v are concatenated into one quantized matrix (and gate/up into
 another) so each is one launch, which is exact because the output columns of
 a quantized matmul are independent.  Activations and the paged KV cache are
 bfloat16 (as in the reference, cache.py:659-695); RMSNorm, RoPE, the softmax
-and every accumulation are float32.  A decode step is nine launches per
+and every accumulation are float32.  A decode step is eight launches per
 layer (QKV GEMV; split attention with RoPE and the KV append inside it; the
-splits' combine; o GEMV; residual add + RMSNorm; gate|up GEMV; SiLU * up;
-down GEMV; residual add + RMSNorm), captured
+splits' combine; o GEMV; residual add + RMSNorm; gate|up GEMV with SiLU * up
+in its epilogue; down GEMV; residual add + RMSNorm), captured
 once in a HIP graph and replayed per token (inputs live in static device
 buffers).  Prefill runs the same linears as GEMMs and float32 attention over
 the pages (the reference's dense-row gather, attention.py:264-298), so a
@@ -117,6 +117,17 @@ def _random_qlinear(gen, n_out, n_in, cfg, bias, device, std=0.02) -> QLinear:
     bv = ((torch.randn(n_out, generator=gen, device=device) * std).to(torch.bfloat16)
           if bias else None)
     return QLinear(wq, s, b, bv, cfg.group_size, cfg.bits)
+
+
+def _gate_up_silu(gate_up: QLinear, x: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up of the fused gate|up projection: one kernel at decode
+    shapes (the same bits as the two-kernel path), else the two kernels."""
+    K = x.shape[-1]
+    if gate_up.bias is None and core.swiglu_supported(x.numel() // K, gate_up.out_features // 2, K,
+                                                      gate_up.group_size, gate_up.bits):
+        return core.quantized_matmul_swiglu(x, gate_up.wq, gate_up.scales, gate_up.biases,
+                                            gate_up.group_size, gate_up.bits)
+    return silu_mul(gate_up(x))
 
 
 def _concat(parts: list[QLinear]) -> QLinear:
@@ -263,7 +274,7 @@ class Qwen2Model:
         x, h = fused_rms_norm(o, layer.post_norm, eps, residual=h)
         if layer.moe is not None:
             return layer.moe.residual_norm(x, h, self._next_norm(li), eps)
-        m = layer.down(silu_mul(layer.gate_up(x)))
+        m = layer.down(_gate_up_silu(layer.gate_up, x))
         return fused_rms_norm(m, self._next_norm(li), eps, residual=h)
 
     # ------------------------------------------------------------ prefill

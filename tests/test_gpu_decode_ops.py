@@ -67,6 +67,38 @@ def test_rms_norm_batched_shape(ops):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("M,N,K,bits", [(1, 18944, 3584, 4), (2, 18944, 3584, 8),
+                                        (1, 18948, 3584, 4), (1, 1025, 16384, 4),
+                                        (2, 2049, 8192, 8)])
+def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
+    """The gate|up GEMV with silu(gate) * up in its epilogue: bit-equal to the
+    GEMV followed by silu_mul.  N = 18948, 1025 and 2049 leave a partial last
+    block (8 and 2 output rows per block; 16 and 64 lanes per row)."""
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    assert core.swiglu_supported(M, N, K, 64, bits)
+    g = _gen(N + K + bits)
+    w = (torch.randn(2 * N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = core.quantize(w, 64, bits)
+    x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    out = core.quantized_matmul_swiglu(x, wq, sc, bi, 64, bits)
+    gu = core.quantized_matmul(x, wq, sc, bi, True, 64, bits)
+    pad = -N % 8  # silu_mul takes widths of whole 8-element units; it is elementwise
+    g, u = (F.pad(t, (0, pad)) for t in (gu[:, :N], gu[:, N:]))
+    ref = ops.silu_mul(torch.cat([g, u], -1))[:, :N]
+    assert out.shape == (M, N) and torch.equal(out, ref)
+
+
+def test_quantized_matmul_swiglu_refuses_other_shapes(ops):
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    w = torch.zeros(2 * 1792, 18944 // 8, dtype=torch.int32, device=DEV)
+    sc = torch.zeros(2 * 1792, 18944 // 64, dtype=torch.bfloat16, device=DEV)
+    assert not core.swiglu_supported(1, 1792, 18944, 64, 4)  # rows of 128 lanes
+    assert not core.swiglu_supported(1, 4864, 896, 64, 4)    # small: the matrix-core GEMV
+    with pytest.raises(NotImplementedError, match="not a fused shape"):
+        core.quantized_matmul_swiglu(torch.zeros(1, 18944, dtype=torch.bfloat16, device=DEV),
+                                     w, sc, sc, 64, 4)
+
+
 @pytest.mark.parametrize("rows,inter", [(1, 18944), (32, 18944), (5, 8), (3, 768)])
 def test_silu_mul(ops, rows, inter):
     gu = (torch.randn(rows, 2 * inter, generator=_gen(inter + rows), device=DEV) * 4

@@ -35,7 +35,8 @@ def test_header_declares_the_abi():
         "mq_paged_decode_attention_workspace", "mq_paged_decode_attention",
         "mq_decode_attention_step", "mq_silu_mul",
         "mq_moe_route", "mq_moe_sort", "mq_moe_combine", "mq_moe_route_sort",
-        "mq_moe_combine_rms_norm"])
+        "mq_moe_combine_rms_norm", "mq_quantized_matmul_swiglu_supported",
+        "mq_quantized_matmul_swiglu"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -125,6 +126,15 @@ def test_decoder_entry_validation(mq):
     assert rs(null, null, 4, 128, 8, 1, null, null, null, null, null, null, null) == -1
     assert rs(null, null, 4, 600, 8, 1, null, null, null, null, null, null, null) == -2
     assert rs(null, null, 0, 128, 8, 1, null, null, null, null, null, null, null) == 0
+    sup = L.mq_quantized_matmul_swiglu_supported
+    assert sup(1, 18944, 3584, 64, 4) == 1 and sup(2, 18944, 3584, 64, 8) == 1
+    assert sup(4, 18944, 3584, 64, 4) == 0                                      # M > 2
+    assert sup(1, 1792, 18944, 64, 4) == 0                                      # 128-lane rows
+    assert sup(1, 18944, 3584, 32, 4) == 0 and sup(1, 18944, 3584, 64, 3) == 0
+    sw = L.mq_quantized_matmul_swiglu
+    assert sw(null, null, null, null, null, 4, 18944, 3584, 64, 4, null) == -2   # not fused
+    assert sw(null, null, null, null, null, 1, 18944, 3584, 64, 4, null) == -1   # null pointers
+    assert sw(null, null, null, null, null, 0, 18944, 3584, 64, 4, null) == 0
     cn = L.mq_moe_combine_rms_norm
     assert cn(null, null, null, null, null, null, null, 4, 8, 2048, 1e-6, null) == -1
     assert cn(null, null, null, null, null, null, null, 4, 8, 8200, 1e-6, null) == -2  # > 8192
