@@ -244,6 +244,30 @@ int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf
                                const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N, int64_t K,
                                int group_size, int bits, hipStream_t stream);
 
+/*
+ * mq_rms_norm of one row followed by the quantized linear that reads it, in
+ * one kernel (the decoder's norm -> linear pairs, models/qwen2.py:157
+ * input_layernorm -> q/k/v, :162-163 hidden = x + attn_out,
+ * post_attention_layernorm -> gate|up, :199 final norm -> lm_head :227):
+ *   h = residual ? bf16(a + residual) : a          (h -> residual_out)
+ *   x = bf16(h * rsqrt(mean(h^2) + eps) * norm_weight)   as mq_rms_norm, bit for bit
+ *   y = x @ dequantize(wq)^T (+ bias)                   as the dot2 GEMV
+ *   or, with swiglu, y [1, N] = silu(gate) * up of a [2N, K] gate|up matrix
+ *   (as mq_quantized_matmul_swiglu).
+ * a, residual, residual_out, norm_weight bfloat16 [K]; M must be 1 and
+ * K <= 8192; residual_out may not overlap a or residual (every block reads
+ * them while the first writes it).  mq_rms_norm_quantized_matmul_supported
+ * says whether a shape is taken; others return MQ_ERR_UNSUPPORTED.
+ */
+int mq_rms_norm_quantized_matmul_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                           int bits, int swiglu);
+int mq_rms_norm_quantized_matmul(const mq_bf16* a, const mq_bf16* residual, mq_bf16* residual_out,
+                                 const mq_bf16* norm_weight, float eps, const uint32_t* wq,
+                                 const mq_bf16* scales, const mq_bf16* biases,
+                                 const mq_bf16* bias_vec, mq_bf16* y, int64_t M, int64_t N,
+                                 int64_t K, int group_size, int bits, int swiglu,
+                                 hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * Mixture-of-experts routing around mq_gather_qmm (models/lfm2.py:348-375,
  * SwitchGLU lfm2.py:193-218 with _gather_sort/_scatter_unsort :613-622).

@@ -42,6 +42,8 @@ EXPORTS = (
     "mq_moe_combine_rms_norm",
     "mq_quantized_matmul_swiglu_supported",
     "mq_quantized_matmul_swiglu",
+    "mq_rms_norm_quantized_matmul_supported",
+    "mq_rms_norm_quantized_matmul",
 )
 
 _lock = threading.Lock()
@@ -86,6 +88,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_moe_route_sort.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p, _p, _p, _p, _p]
     L.mq_quantized_matmul_swiglu_supported.argtypes = [_i64, _i64, _i64, _int, _int]
     L.mq_quantized_matmul_swiglu.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _p]
+    L.mq_rms_norm_quantized_matmul_supported.argtypes = [_i64, _i64, _i64, _int, _int, _int]
+    L.mq_rms_norm_quantized_matmul.argtypes = [_p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p,
+                                               _i64, _i64, _i64, _int, _int, _int, _p]
     L.mq_moe_combine_rms_norm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _int, _i64,
                                           ctypes.c_float, _p]
     for name in EXPORTS[2:]:

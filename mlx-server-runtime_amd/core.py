@@ -233,6 +233,52 @@ def quantized_matmul_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tens
     return y
 
 
+def rms_norm_qmm_supported(M: int, N: int, K: int, group_size: int = 64, bits: int = 4,
+                           swiglu: bool = False) -> bool:
+    """Whether rms_norm_quantized_matmul takes this shape (N outputs)."""
+    return bool(_lib.lib().mq_rms_norm_quantized_matmul_supported(M, N, K, group_size, bits,
+                                                                  int(swiglu)))
+
+
+def rms_norm_quantized_matmul(a: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                              w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                              bias: torch.Tensor | None = None,
+                              residual: torch.Tensor | None = None, group_size: int = 64,
+                              bits: int = 4, swiglu: bool = False):
+    """RMSNorm of one row then the quantized linear (or its SwiGLU form), one
+    kernel: h = bf16(a + residual) (a without residual), x = rms_norm(h) *
+    norm_weight as decode_ops.rms_norm computes it, y = quantized_matmul(x, w)
+    (+ bias), or silu(gate) * up of a [2N, K] gate|up w.  Returns (y, h)."""
+    op = "rms_norm_quantized_matmul"
+    _require_gpu(op, a=a, norm_weight=norm_weight, w=w, scales=scales, biases=biases, bias=bias,
+                 residual=residual)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    _check_bf16(op, "a", a)
+    _check_bf16(op, "norm_weight", norm_weight)
+    if a.shape[-1] != K or a.numel() != K:
+        raise ValueError(f"[{op}] a must be one row of {K}, got {tuple(a.shape)}")
+    if norm_weight.shape != (K,):
+        raise ValueError(f"[{op}] norm_weight must have shape ({K},)")
+    N = w.shape[0] // 2 if swiglu else w.shape[0]
+    ac = a.contiguous()
+    h = None
+    if residual is not None:
+        _check_bf16(op, "residual", residual)
+        if residual.shape != a.shape:
+            raise ValueError(f"[{op}] residual shape {tuple(residual.shape)} != {tuple(a.shape)}")
+        residual = residual.contiguous()
+        h = torch.empty_like(ac)
+    if bias is not None:
+        _check_bf16(op, "bias", bias)
+        bias = bias.contiguous()
+    y = torch.empty(tuple(a.shape[:-1]) + (N,), dtype=torch.bfloat16, device=a.device)
+    _lib.check(_lib.lib().mq_rms_norm_quantized_matmul(
+        _ptr(ac), _ptr(residual), _ptr(h), _ptr(norm_weight.contiguous()), float(eps),
+        _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(bias),
+        _ptr(y), 1, N, K, group_size, bits, int(swiglu), _stream(a)), op)
+    return y, (ac if h is None else h)
+
+
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                lhs_indices: torch.Tensor | None = None, rhs_indices: torch.Tensor | None = None,
                transpose: bool = True, group_size: int = 64, bits: int = 4, mode: str = "affine",

@@ -196,6 +196,54 @@ int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf
   return hip_status(mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream), op);
 }
 
+int mq_rms_norm_quantized_matmul_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                           int bits, int swiglu) {
+  if (M != 1 || N <= 0 || K <= 0 || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
+  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
+  return mq::qmv_norm_fits(N, K, bits, swiglu != 0) ? 1 : 0;
+}
+
+namespace {
+bool overlap(const void* a, const void* b, int64_t bytes) {
+  const char *pa = static_cast<const char*>(a), *pb = static_cast<const char*>(b);
+  return pa < pb + bytes && pb < pa + bytes;
+}
+}  // namespace
+
+int mq_rms_norm_quantized_matmul(const mq_bf16* a, const mq_bf16* residual, mq_bf16* residual_out,
+                                 const mq_bf16* norm_weight, float eps, const uint32_t* wq,
+                                 const mq_bf16* scales, const mq_bf16* biases,
+                                 const mq_bf16* bias_vec, mq_bf16* y, int64_t M, int64_t N,
+                                 int64_t K, int group_size, int bits, int swiglu,
+                                 hipStream_t stream) {
+  const char* op = "rms_norm_quantized_matmul";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", swiglu ? 2 * N : N)) return rc;
+  if (M == 0 || N == 0) return ok();
+  if (!mq_rms_norm_quantized_matmul_supported(M, N, K, group_size, bits, swiglu))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] M=%lld, N=%lld, K=%lld%s is not a fused shape (one row, K <= 8192); use "
+                "mq_rms_norm and mq_quantized_matmul.",
+                op, (long long)M, (long long)N, (long long)K, swiglu ? " (SwiGLU)" : "");
+  if (swiglu && bias_vec)
+    return fail(MQ_ERR_INVALID, "[%s] the SwiGLU form takes no bias.", op);
+  if (!residual != !residual_out)
+    return fail(MQ_ERR_INVALID, "[%s] residual and residual_out go together.", op);
+  if (!a || !norm_weight || !wq || !scales || !biases || !y)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(a) || !aligned16(norm_weight) || !aligned16(wq) ||
+      (residual && (!aligned16(residual) || !aligned16(residual_out))))
+    return fail(MQ_ERR_INVALID, "[%s] a, residual, residual_out, norm_weight and wq must be "
+                "16-byte aligned.", op);
+  // Every block reads a and residual while the first one writes residual_out.
+  if (residual_out && (overlap(residual_out, residual, K * 2) || overlap(residual_out, a, K * 2)))
+    return fail(MQ_ERR_INVALID, "[%s] residual_out may not overlap a or residual.", op);
+  return hip_status(mq::launch_qmv_norm(a, residual, residual_out, norm_weight, eps, wq, scales,
+                                        biases, bias_vec, y, N, K, bits, swiglu != 0, stream),
+                    op);
+}
+
 int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
                         const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
                         int64_t N, int64_t K, int group_size, int bits, int transpose,

@@ -29,6 +29,12 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                       int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
 bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits);
+bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu);
+hipError_t launch_qmv_norm(const uint16_t* a, const uint16_t* res, uint16_t* res_out,
+                           const uint16_t* norm_w, float eps, const uint32_t* wq,
+                           const uint16_t* scales, const uint16_t* biases, const uint16_t* bias,
+                           uint16_t* y, int64_t N, int64_t K, int bits, bool swiglu,
+                           hipStream_t stream);
 hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
                              int bits, hipStream_t stream);

@@ -1,17 +1,21 @@
 // Decode-shaped quantized matmul (qmv): dispatch and the shape test.  The
 // kernel and its launch templates are in mq_qmv_kernel.h; this file
 // instantiates the plain 4-bit launches, mq_qmv_b8.hip / mq_qmv_g4.hip /
-// mq_qmv_g8.hip / mq_qmv_swiglu.hip the others.
+// mq_qmv_g8.hip / mq_qmv_swiglu.hip / mq_qmv_norm*.hip the others.
 #include "mq_qmv_kernel.h"
 
 namespace mq {
 
-MQ_QMV_INSTANCE(4, false, 0);
-extern MQ_QMV_INSTANCE(8, false, 0);
-extern MQ_QMV_INSTANCE(4, true, 0);
-extern MQ_QMV_INSTANCE(8, true, 0);
-extern MQ_QMV_INSTANCE(4, false, 1);
-extern MQ_QMV_INSTANCE(8, false, 1);
+MQ_QMV_INSTANCE(4, false, 0, false);
+extern MQ_QMV_INSTANCE(8, false, 0, false);
+extern MQ_QMV_INSTANCE(4, true, 0, false);
+extern MQ_QMV_INSTANCE(8, true, 0, false);
+extern MQ_QMV_INSTANCE(4, false, 1, false);
+extern MQ_QMV_INSTANCE(8, false, 1, false);
+extern MQ_QMV_INSTANCE(4, false, 0, true);
+extern MQ_QMV_INSTANCE(8, false, 0, true);
+extern MQ_QMV_INSTANCE(4, false, 1, true);
+extern MQ_QMV_INSTANCE(8, false, 1, true);
 
 using qmv::kBlock;
 using qmv::kQmvLdsBudget;
@@ -43,9 +47,38 @@ hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16
                              int bits, hipStream_t stream) {
   if (N == 0 || M == 0) return hipSuccess;
   const GatherMap g1{nullptr, nullptr, 1, 1, 1};
+  const qmv::NormIn none{};
   if (bits == 4)
-    return qmv::run_bits<4, false, 1>(x, wq, scales, biases, nullptr, y, M, N, K, g1, stream);
-  return qmv::run_bits<8, false, 1>(x, wq, scales, biases, nullptr, y, M, N, K, g1, stream);
+    return qmv::run_bits<4, false, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g1, none,
+                                             stream);
+  return qmv::run_bits<8, false, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g1, none,
+                                           stream);
+}
+
+// RMSNorm of one row, then the GEMV (or the SwiGLU GEMV over a 2N-row
+// matrix): the row's 8-element units must fit the norm's four per thread.
+bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu) {
+  if (K > 8192) return false;
+  return swiglu ? qmv_swiglu_fits(1, N, K, bits) : qmv_fits(1, N, K, bits, 1);
+}
+
+hipError_t launch_qmv_norm(const uint16_t* a, const uint16_t* res, uint16_t* res_out,
+                           const uint16_t* norm_w, float eps, const uint32_t* wq,
+                           const uint16_t* scales, const uint16_t* biases, const uint16_t* bias,
+                           uint16_t* y, int64_t N, int64_t K, int bits, bool swiglu,
+                           hipStream_t stream) {
+  if (N == 0) return hipSuccess;
+  const GatherMap g1{nullptr, nullptr, 1, 1, 1};
+  const qmv::NormIn nrm{res, res_out, norm_w, eps};
+  if (swiglu)
+    return bits == 4 ? qmv::run_bits<4, false, 1, true>(a, wq, scales, biases, nullptr, y, 1, N,
+                                                        K, g1, nrm, stream)
+                     : qmv::run_bits<8, false, 1, true>(a, wq, scales, biases, nullptr, y, 1, N,
+                                                        K, g1, nrm, stream);
+  return bits == 4 ? qmv::run_bits<4, false, 0, true>(a, wq, scales, biases, bias, y, 1, N, K, g1,
+                                                      nrm, stream)
+                   : qmv::run_bits<8, false, 0, true>(a, wq, scales, biases, bias, y, 1, N, K, g1,
+                                                      nrm, stream);
 }
 
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
@@ -54,11 +87,16 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
   if (N == 0 || M == 0 || g.T == 0) return hipSuccess;
   // A plain matmul carries no tables: its kernels skip the index loads.
   const bool gather = g.lhs || g.rhs || g.T != 1;
+  const qmv::NormIn none{};
   if (bits == 4)
-    return gather ? qmv::run_bits<4, true, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream)
-                  : qmv::run_bits<4, false, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream);
-  return gather ? qmv::run_bits<8, true, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream)
-                : qmv::run_bits<8, false, 0>(x, wq, scales, biases, bias, y, M, N, K, g, stream);
+    return gather ? qmv::run_bits<4, true, 0, false>(x, wq, scales, biases, bias, y, M, N, K, g,
+                                                     none, stream)
+                  : qmv::run_bits<4, false, 0, false>(x, wq, scales, biases, bias, y, M, N, K, g,
+                                                      none, stream);
+  return gather ? qmv::run_bits<8, true, 0, false>(x, wq, scales, biases, bias, y, M, N, K, g,
+                                                   none, stream)
+                : qmv::run_bits<8, false, 0, false>(x, wq, scales, biases, bias, y, M, N, K, g,
+                                                    none, stream);
 }
 
 }  // namespace mq

@@ -2,5 +2,5 @@
 #include "mq_qmv_kernel.h"
 
 namespace mq {
-MQ_QMV_INSTANCE(8, true, 0);
+MQ_QMV_INSTANCE(8, true, 0, false);
 }  // namespace mq

@@ -64,11 +64,23 @@ struct Nibble {
   __device__ __forceinline__ uint32_t pair(uint32_t w) const { return (w & mask) | magic; }
 };
 
+// NORM: x is not the GEMV's input but a row a (M = 1) that the block first
+// turns into it, as the RMSNorm kernel (mq_rms_norm) does, bit for bit:
+// h = bf16(a + res) (h = a without res), x = bf16(h * rsqrt(mean(h^2) + eps)
+// * w), in that kernel's element mapping (thread t: 8-element units t, t+256,
+// ...) and reduction order.  Block 0 stores h to res_out.
+struct NormIn {
+  const uint16_t* res;
+  uint16_t* res_out;
+  const uint16_t* w;
+  float eps;
+};
+
 // EPI 0: y[m, n] = (x W^T)[m, n] (+ bias[n]).  EPI 1 (SwiGLU, the gate and up
 // projections of a Qwen2 MLP as one matrix of 2N rows, gate rows first):
 // y[m, n] = bf16(bf16(silu(g)) * u) with g, u the bfloat16 results of rows n
 // and N + n -- a block computes RPB/2 gate rows and the matching up rows.
-template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI>
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI, bool NORM>
 // The input pointers are deliberately not __restrict__: with it the compiler
 // may move their loads across the inline-asm barriers below (it proves the
 // asm cannot touch restrict memory), which breaks the issue order the waits
@@ -77,7 +89,7 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
     const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* bias, uint16_t* y, int M, int N, int K,
     const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, int64_t E,
-    int64_t x_batches) {
+    int64_t x_batches, NormIn nrm) {
   constexpr int EPC = 128 / BITS;      // elements per 16-byte chunk
   constexpr int UPC = EPC / 8;         // 8-element units per chunk (4 or 2)
   constexpr int CPG = kGroup / EPC;    // chunks per group (2 or 4)
@@ -86,6 +98,7 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   constexpr int WPR = TPR > 64 ? TPR / 64 : 1;  // waves per row (TPR > 64)
   constexpr int HALF = RPB / 2;        // SwiGLU: output rows per block
   static_assert(EPI == 0 || (!GATHER && WPR == 1 && RPB % 2 == 0), "SwiGLU epilogue layout");
+  static_assert(!NORM || (!GATHER && MT == 1 && XU <= 4), "RMSNorm input: one row of <= 8192");
   extern __shared__ u32x4_t smem[];
   __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : EPI == 1 ? RPB * MT : 1];
 
@@ -146,6 +159,21 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
     const bool real = m < M && u < C * UPC;
     xr[k] = buf_load16(xrs, real ? (uint32_t)(m * K + u * 8) * 2 : kOutOfRange);
   }
+  u32x4_t rr[NORM ? XU : 1], nw[NORM ? XU : 1];  // residual and norm weight units
+  if constexpr (NORM) {
+    const rsrc_t rrs = make_rsrc(nrm.res, nrm.res ? (uint64_t)K * 2 : 0);
+    const rsrc_t wns = make_rsrc(nrm.w, (uint64_t)K * 2);
+#pragma unroll
+    for (int k = 0; k < XU; ++k) {
+      const int u = threadIdx.x + k * kBlock;
+      rr[k] = buf_load16(rrs, u < C * UPC ? (uint32_t)u * 16 : kOutOfRange);
+    }
+#pragma unroll
+    for (int k = 0; k < XU; ++k) {
+      const int u = threadIdx.x + k * kBlock;
+      nw[k] = buf_load16(wns, u < C * UPC ? (uint32_t)u * 16 : kOutOfRange);
+    }
+  }
   // Scales and biases go straight to LDS (buffer_load ... lds, 4 bytes per
   // lane).  Entries past the block's rows read as zeros.
   u32x4_t* xl = smem;
@@ -197,6 +225,51 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   // x and this wave's scale/bias DMA have landed once at most the D*R weight
   // loads are outstanding; the barrier below then publishes every wave's.
   __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(D * R) : "memory");
+
+  if constexpr (NORM) {
+    // ---- 1b. x = RMSNorm(a (+ res)) * w, as rmsnorm_kernel computes it.
+    __shared__ float nred[kBlock / 64];
+    const bool has_res = nrm.res != nullptr;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < XU; ++k) {
+      const int u = threadIdx.x + k * kBlock;
+      if (u < C * UPC) {
+        u32x4_t v = xr[k];
+        if (has_res) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = pack_bf16x2(lo_bf16(v[q]) + lo_bf16(rr[k][q]), hi_bf16(v[q]) + hi_bf16(rr[k][q]));
+          if (blockIdx.x == 0) reinterpret_cast<u32x4_t*>(nrm.res_out)[u] = v;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float a = lo_bf16(v[q]), b = hi_bf16(v[q]);
+          ss = fmaf(a, a, ss);
+          ss = fmaf(b, b, ss);
+        }
+        xr[k] = v;
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kBlock / 64; ++i) ss += nred[i];
+    const float inv = rsqrtf(ss / (float)K + nrm.eps);
+#pragma unroll
+    for (int k = 0; k < XU; ++k) {
+      const int u = threadIdx.x + k * kBlock;
+      if (u < C * UPC) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          xr[k][q] = pack_bf16x2(lo_bf16(xr[k][q]) * inv * lo_bf16(nw[k][q]),
+                                 hi_bf16(xr[k][q]) * inv * hi_bf16(nw[k][q]));
+      }
+    }
+  }
 
   // ---- 2. LDS: x as [m][slot j][unit h][lane] (4-bit pair-permuted) and
   // chunk sums [m][chunk]; zeros past the row.
@@ -363,42 +436,64 @@ inline int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R) {
   return MT * CP * 16 * (epc / 8) + MT * CP * 4 + 2 * ((sb_words + 63) / 64) * 256;
 }
 
-template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI>
+template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI, bool NORM>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-               const GatherMap& g, hipStream_t stream) {
+               const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
   const int64_t rows_per_block = (kBlock / TPR) * R / (EPI == 1 ? 2 : 1);
   const size_t lds = (size_t)lds_bytes(BITS, TPR, MT, K, R);
   const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)g.T);
-  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, GATHER, EPI>), grid, dim3(kBlock), lds, stream, x,
-                     wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E, g.x_batches);
+  hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, GATHER, EPI, NORM>), grid, dim3(kBlock),
+                     lds, stream, x, wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E,
+                     g.x_batches, nrm);
   return hipGetLastError();
 }
 
-template <int BITS, int TPR, int R, int S, int MT, bool GATHER, int EPI>
+template <int BITS, int TPR, int R, int S, int MT, bool GATHER, int EPI, bool NORM>
 hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                  const GatherMap& g, hipStream_t stream) {
+                  const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t CP = (K / EPC + TPR - 1) / TPR * TPR;
   const int64_t units = (MT * CP * (EPC / 8) + kBlock - 1) / kBlock;  // x units per thread
-  if (units <= 2) return run<BITS, TPR, R, S, MT, 2, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (units <= 4) return run<BITS, TPR, R, S, MT, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (units <= 12) return run<BITS, TPR, R, S, MT, 12, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  return hipErrorInvalidValue;  // excluded by qmv_fits
+  if (units <= 2)
+    return run<BITS, TPR, R, S, MT, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                          stream);
+  if (units <= 4)
+    return run<BITS, TPR, R, S, MT, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                          stream);
+  if constexpr (NORM) {
+    return hipErrorInvalidValue;  // rows of <= 8192 (excluded by qmv_norm_fits)
+  } else {
+    if (units <= 12)
+      return run<BITS, TPR, R, S, MT, 12, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                             stream);
+    return hipErrorInvalidValue;  // excluded by qmv_fits
+  }
 }
 
-template <int BITS, int TPR, int R, int S, bool GATHER, int EPI>
+template <int BITS, int TPR, int R, int S, bool GATHER, int EPI, bool NORM>
 hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                  const GatherMap& g, hipStream_t stream) {
-  if (M <= 1) return run_xu<BITS, TPR, R, S, 1, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 2) return run_xu<BITS, TPR, R, S, 2, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if constexpr (EPI == 1) {
-    return hipErrorInvalidValue;  // SwiGLU: M <= 2 (excluded by qmv_swiglu_fits)
+                  const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
+  if (M <= 1)
+    return run_xu<BITS, TPR, R, S, 1, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                         stream);
+  if constexpr (NORM) {
+    return hipErrorInvalidValue;  // one row (excluded by qmv_norm_fits)
   } else {
-    if (M <= 4) return run_xu<BITS, TPR, R, S, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-    return run_xu<BITS, TPR, R, S, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+    if (M <= 2)
+      return run_xu<BITS, TPR, R, S, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                           stream);
+    if constexpr (EPI == 1) {
+      return hipErrorInvalidValue;  // SwiGLU: M <= 2 (excluded by qmv_swiglu_fits)
+    } else {
+      if (M <= 4)
+        return run_xu<BITS, TPR, R, S, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g,
+                                                             nrm, stream);
+      return run_xu<BITS, TPR, R, S, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                           stream);
+    }
   }
 }
 
@@ -430,37 +525,37 @@ inline bool two_rows(int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t
 
 // Launches the GEMV for one code width; GATHER selects the kernels that
 // read per-batch x / expert indices, EPI the SwiGLU epilogue (N output rows
-// of a 2N-row matrix).  Each (BITS, GATHER, EPI) triple is instantiated in a
-// translation unit of its own (mq_qmv*.hip), so that they compile in
-// parallel.
-template <int BITS, bool GATHER, int EPI>
+// of a 2N-row matrix), NORM the RMSNorm input (see NormIn).  Each
+// instantiation lives in a translation unit of its own (mq_qmv*.hip), so that
+// they compile in parallel.
+template <int BITS, bool GATHER, int EPI, bool NORM>
 hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                    const GatherMap& g, hipStream_t stream) {
+                    const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t C = K / EPC;
   const int tpr = pick_tpr(C, EPI == 1 ? 2 * N : N, g.T);
   const int slots = (int)((C + tpr - 1) / tpr);
   switch (tpr) {
     case 8:
-      return run_mt<BITS, 8, 1, 3, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      return run_mt<BITS, 8, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
     // Chunk slots per lane S: the instantiated S >= NJ closest to it (slots
     // past NJ cost arithmetic on zeros, not memory traffic).  The S values
     // cover the model shapes exactly: K = 3584 / 18944 / 2048 / 768 at 4 and
     // 8 bits.
     case 16:
-      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 16, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      return run_mt<BITS, 16, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
     case 32:
-      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 32, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      return run_mt<BITS, 32, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
     case 64:
-      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-      return run_mt<BITS, 64, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      return run_mt<BITS, 64, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
     default:
       if constexpr (EPI == 1) {
         return hipErrorInvalidValue;  // SwiGLU: one wave per row at most
@@ -470,13 +565,13 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
           // stages all of x (long rows: up to 40 KB), so rows per block divide
           // that L2 traffic (the down projection: 2.1x less x than weights).
           if (slots <= 5 && two_rows(BITS, 128, M, N, K, g.T))
-            return run_mt<BITS, 128, 2, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-          if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-          return run_mt<BITS, 128, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+            return run_mt<BITS, 128, 2, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+          if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+          return run_mt<BITS, 128, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
         }
-        if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-        if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
-        if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER, EPI>(x, wq, s, b, bias, y, M, N, K, g, stream);
+        if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+        if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+        if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
         return hipErrorInvalidValue;  // excluded by qmv_fits
       }
   }
@@ -487,7 +582,8 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
 
 // Explicit instantiation (or, after `extern`, its declaration) of one
 // run_bits launch, inside namespace mq.
-#define MQ_QMV_INSTANCE(BITS, GATHER, EPI)                                                   \
-  template hipError_t qmv::run_bits<BITS, GATHER, EPI>(                                     \
+#define MQ_QMV_INSTANCE(BITS, GATHER, EPI, NORM)                                             \
+  template hipError_t qmv::run_bits<BITS, GATHER, EPI, NORM>(                               \
       const uint16_t*, const uint32_t*, const uint16_t*, const uint16_t*, const uint16_t*, \
-      uint16_t*, int64_t, int64_t, int64_t, const GatherMap&, hipStream_t)
+      uint16_t*, int64_t, int64_t, int64_t, const GatherMap&, const qmv::NormIn&,          \
+      hipStream_t)

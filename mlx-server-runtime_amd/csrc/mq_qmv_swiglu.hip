@@ -3,6 +3,6 @@
 #include "mq_qmv_kernel.h"
 
 namespace mq {
-MQ_QMV_INSTANCE(4, false, 1);
-MQ_QMV_INSTANCE(8, false, 1);
+MQ_QMV_INSTANCE(4, false, 1, false);
+MQ_QMV_INSTANCE(8, false, 1, false);
 }  // namespace mq

@@ -22,10 +22,11 @@ same: q/k/v are concatenated into one quantized matrix (and gate/up into
 another) so each is one launch, which is exact because the output columns of
 a quantized matmul are independent.  Activations and the paged KV cache are
 bfloat16 (as in the reference, cache.py:659-695); RMSNorm, RoPE, the softmax
-and every accumulation are float32.  A decode step is eight launches per
-layer (QKV GEMV; split attention with RoPE and the KV append inside it; the
-splits' combine; o GEMV; residual add + RMSNorm; gate|up GEMV with SiLU * up
-in its epilogue; down GEMV; residual add + RMSNorm), captured
+and every accumulation are float32.  A decode step at batch 1 is six
+launches per dense layer (residual add + RMSNorm + QKV GEMV; split attention
+with RoPE and the KV append inside it; the splits' combine; o GEMV; residual
+add + RMSNorm + gate|up GEMV with SiLU * up in its epilogue; down GEMV; the
+norms run inside the GEMVs' input staging), captured
 once in a HIP graph and replayed per token (inputs live in static device
 buffers).  Prefill runs the same linears as GEMMs and float32 attention over
 the pages (the reference's dense-row gather, attention.py:264-298), so a
@@ -262,6 +263,32 @@ class Qwen2Model:
             return core.quantized_matmul(x, e.wq, e.scales, e.biases, True, e.group_size, e.bits)
         return self.lm_head(x)
 
+    def _head_linear(self) -> QLinear:
+        """The LM head as a quantized linear (untied, or the tied embedding's as_linear)."""
+        if self.lm_head is not None:
+            return self.lm_head
+        e = self.embed
+        return QLinear(e.wq, e.scales, e.biases, None, e.group_size, e.bits)
+
+    def _norm_linear(self, ql: QLinear, a: torch.Tensor, res: torch.Tensor | None,
+                     norm_w: torch.Tensor, swiglu: bool = False):
+        """ql on rms_norm(a (+ res)) * norm_w -- with silu(gate) * up when swiglu
+        -- -> (y, h), h the residual stream after the add (a without res).  One
+        kernel for a single row where the shape allows; the same bits either way
+        up to the GEMV kernel the unfused path picks."""
+        eps = self.cfg.rms_norm_eps
+        K = a.shape[-1]
+        n_out = ql.out_features // 2 if swiglu else ql.out_features
+        if (a.numel() == K and not (swiglu and ql.bias is not None)
+                and core.rms_norm_qmm_supported(1, n_out, K, ql.group_size, ql.bits, swiglu)):
+            return core.rms_norm_quantized_matmul(a, norm_w, eps, ql.wq, ql.scales, ql.biases,
+                                                  ql.bias, res, ql.group_size, ql.bits, swiglu)
+        if res is None:
+            x, h = fused_rms_norm(a, norm_w, eps), a
+        else:
+            x, h = fused_rms_norm(a, norm_w, eps, residual=res)
+        return (_gate_up_silu(ql, x) if swiglu else ql(x)), h
+
     def _next_norm(self, li: int) -> torch.Tensor:
         return (self.layers[li + 1].input_norm if li + 1 < len(self.layers)
                 else self.final_norm)
@@ -329,13 +356,28 @@ class Qwen2Model:
         """One token per sequence: tok [B] int, pos [B] int64 (its position, on the
         device) -> logits [B, vocab].  Static shapes only, so it can be captured."""
         c = self.cfg
-        d, nh = c.head_dim, c.num_attention_heads
+        d, nh, eps = c.head_dim, c.num_attention_heads, c.rms_norm_eps
         h = self._embed(tok)
-        x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
+        # The next linear's input: rms_norm(src[0] (+ src[1])) * that layer's
+        # norm weight, computed inside the linear's kernel; or x, when an MoE
+        # block has already normalised it.
+        src, x = (h, None), None
         for li, layer in enumerate(self.layers):
-            a = attention_step(layer.qkv(x), pos, cache, li, cos, sin, nh, d ** -0.5,
-                               layer.q_norm, layer.k_norm, c.rms_norm_eps)
-            x, h = self._ffn(li, h, layer.o(a))
+            if x is None:
+                qkv, h = self._norm_linear(layer.qkv, *src, layer.input_norm)
+            else:
+                qkv = layer.qkv(x)
+            a = attention_step(qkv, pos, cache, li, cos, sin, nh, d ** -0.5,
+                               layer.q_norm, layer.k_norm, eps)
+            o = layer.o(a)
+            if layer.moe is not None:
+                xm, h = fused_rms_norm(o, layer.post_norm, eps, residual=h)
+                x, h = layer.moe.residual_norm(xm, h, self._next_norm(li), eps)
+            else:
+                act, h = self._norm_linear(layer.gate_up, o, h, layer.post_norm, swiglu=True)
+                src, x = (layer.down(act), h), None
+        if x is None:
+            return self._norm_linear(self._head_linear(), *src, self.final_norm)[0]
         return self._head(x)
 
     def generate(self, prompt: torch.Tensor, n_new: int, max_len: int | None = None,

@@ -88,6 +88,57 @@ def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     assert out.shape == (M, N) and torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("N,K,bits,swiglu,with_res", [
+    (18944, 3584, 4, True, True), (18944, 3584, 8, True, False), (37888, 3584, 4, False, True),
+    (4096, 8192, 4, False, True), (4096, 8192, 8, False, False), (9475, 3584, 4, True, True)])
+def test_rms_norm_quantized_matmul_equals_two_kernels(ops, N, K, bits, swiglu, with_res):
+    """RMSNorm inside the GEMV's input staging: bit-equal to rms_norm followed by
+    the dot2 GEMV (these shapes are large enough that quantized_matmul runs it),
+    and the residual stream h bit-equal to rms_norm's."""
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    assert core.rms_norm_qmm_supported(1, N, K, 64, bits, swiglu)
+    g = _gen(N + K + bits + swiglu)
+    rows = 2 * N if swiglu else N
+    w = (torch.randn(rows, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = core.quantize(w, 64, bits)
+    a = (torch.randn(1, K, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    res = torch.randn(1, K, generator=g, device=DEV).to(torch.bfloat16) if with_res else None
+    nw = (torch.rand(K, generator=g, device=DEV) + 0.5).to(torch.bfloat16)
+    y, h = core.rms_norm_quantized_matmul(a, nw, 1e-6, wq, sc, bi, None, res, 64, bits, swiglu)
+    if with_res:
+        x, ref_h = ops.rms_norm(a, nw, 1e-6, residual=res)
+    else:
+        x, ref_h = ops.rms_norm(a, nw, 1e-6), a
+    if swiglu:
+        gu = core.quantized_matmul(x, wq, sc, bi, True, 64, bits)
+        pad = -N % 8
+        ref = ops.silu_mul(torch.cat([F.pad(gu[:, :N], (0, pad)), F.pad(gu[:, N:], (0, pad))],
+                                     -1))[:, :N]
+    else:
+        ref = core.quantized_matmul(x, wq, sc, bi, True, 64, bits)
+    assert torch.equal(h, ref_h) and torch.equal(y, ref)
+
+
+def test_rms_norm_quantized_matmul_small_matrix_with_bias(ops):
+    """The Qwen2-7B QKV shape (quantized_matmul picks the matrix-core GEMV for
+    it, so the rounding differs): within 1e-2 norm-wise of rms_norm + the
+    unfused linear with its bias; h exact."""
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    N, K = 4608, 3584
+    g = _gen(11)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = core.quantize(w, 64, 4)
+    bias = (torch.randn(N, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    a = torch.randn(1, K, generator=g, device=DEV).to(torch.bfloat16)
+    res = torch.randn(1, K, generator=g, device=DEV).to(torch.bfloat16)
+    nw = (torch.rand(K, generator=g, device=DEV) + 0.5).to(torch.bfloat16)
+    y, h = core.rms_norm_quantized_matmul(a, nw, 1e-6, wq, sc, bi, bias, res, 64, 4)
+    x, ref_h = ops.rms_norm(a, nw, 1e-6, residual=res)
+    ref = core.quantized_matmul(x, wq, sc, bi, True, 64, 4, bias=bias)
+    assert torch.equal(h, ref_h)
+    assert float((y.float() - ref.float()).abs().max() / ref.float().abs().max()) < 1e-2
+
+
 def test_quantized_matmul_swiglu_refuses_other_shapes(ops):
     core = importlib.import_module("mlx-server-runtime_amd.core")
     w = torch.zeros(2 * 1792, 18944 // 8, dtype=torch.int32, device=DEV)

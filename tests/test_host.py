@@ -36,7 +36,8 @@ def test_header_declares_the_abi():
         "mq_decode_attention_step", "mq_silu_mul",
         "mq_moe_route", "mq_moe_sort", "mq_moe_combine", "mq_moe_route_sort",
         "mq_moe_combine_rms_norm", "mq_quantized_matmul_swiglu_supported",
-        "mq_quantized_matmul_swiglu"])
+        "mq_quantized_matmul_swiglu", "mq_rms_norm_quantized_matmul_supported",
+        "mq_rms_norm_quantized_matmul"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -135,6 +136,20 @@ def test_decoder_entry_validation(mq):
     assert sw(null, null, null, null, null, 4, 18944, 3584, 64, 4, null) == -2   # not fused
     assert sw(null, null, null, null, null, 1, 18944, 3584, 64, 4, null) == -1   # null pointers
     assert sw(null, null, null, null, null, 0, 18944, 3584, 64, 4, null) == 0
+    ns = L.mq_rms_norm_quantized_matmul_supported
+    assert ns(1, 4608, 3584, 64, 4, 0) == 1 and ns(1, 18944, 3584, 64, 4, 1) == 1
+    assert ns(2, 4608, 3584, 64, 4, 0) == 0                                     # one row only
+    assert ns(1, 3584, 18944, 64, 4, 0) == 0                                    # K > 8192
+    nq = L.mq_rms_norm_quantized_matmul
+    assert nq(null, null, null, null, 1e-6, null, null, null, null, null, 1, 4608, 3584, 64, 4, 0,
+              null) == -1                                                        # null pointers
+    assert nq(null, null, null, null, 1e-6, null, null, null, null, null, 2, 4608, 3584, 64, 4, 0,
+              null) == -2                                                        # not fused
+    buf = ctypes.create_string_buffer(8192)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
+    assert nq(p, p, p, p, 1e-6, p, p, p, None, p, 1, 4608, 1024, 64, 4, 0,
+              null) == -1                                                        # out overlaps
+    assert b"overlap" in L.mq_last_error()
     cn = L.mq_moe_combine_rms_norm
     assert cn(null, null, null, null, null, null, null, 4, 8, 2048, 1e-6, null) == -1
     assert cn(null, null, null, null, null, null, null, 4, 8, 8200, 1e-6, null) == -2  # > 8192
