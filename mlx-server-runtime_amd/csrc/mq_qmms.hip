@@ -47,13 +47,12 @@ __device__ __forceinline__ void dma16(rsrc_t r, lds_t* dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, 0, 0, 0);
 }
 
-// End of a step: wait until at most N memory operations are outstanding, N
-// being the number of x DMA operations issued in this step and the one
-// before, then sync the block.  vmcnt retires in issue order and the DMAs
-// (LDS writes) never move across this asm, so every older DMA -- in
-// particular the next step's x tile -- has landed whatever the compiler did
-// with the register loads (it may move those across the asm: they read
-// __restrict__ memory).
+// End of a step: wait until at most N memory operations are outstanding, then
+// sync the block.  vmcnt retires in issue order.  Every memory operation of
+// the kernel stays where the program issues it (the streamed inputs are not
+// __restrict__, and the loads sit between empty asm statements with memory
+// clobbers), so N can count exactly the operations issued after the DMA that
+// must have landed: the next step's x tile.
 template <int N>
 __device__ __forceinline__ void step_barrier() {
   __asm__ volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
@@ -82,9 +81,11 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, 
 }
 
 template <int BITS, int MI, bool PARTIAL>
+// x, wq, scales and biases are deliberately not __restrict__: with it the
+// compiler may move their loads across the barriers' inline asm, and the
+// barriers' counts assume the issue order below.
 __global__ __launch_bounds__(kThreads) void qmms_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
     int M, int N, int K, int tiles_n, int tiles_m, int chunks_per_split) {
   constexpr int BM = 32 * MI;
@@ -135,9 +136,16 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
       dma16(xrs, (lds_t*)(lds + stage * kXStage + (i * 4 + wave) * 1024), xoff[i] + kt * (BK * 2));
   };
   auto load_codes = [&](u32x4_t (&cw)[NC], int kt) {
+    __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (int p = 0; p < NC; ++p) cw[p] = buf_load16(wrs, coff + kt * (BK * BITS / 8) + p * 16);
+    __asm__ volatile("" ::: "memory");
   };
+  // At the end of step kt the x DMA of step kt + 1 (issued in step kt - 2)
+  // must have landed; issued after it: the codes of step kt + 2, then per
+  // step kt - 1 and kt MI DMAs and NC code loads (and, at a chunk's first
+  // step, two scale/bias loads, which only add to the count).
+  constexpr int kInFlight = NC + 2 * (MI + NC);
 
   f32x16_t acc[MI];
 #pragma unroll
@@ -163,8 +171,10 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
     for (int u = 0; u < kChunk; ++u) {
       const int kt = c * kChunk + u;
       if (u == 0) {
+        __asm__ volatile("" ::: "memory");
         svn = buf_load16(srs, soff + (c + 1) * 16);
         bvn = buf_load16(brs, soff + (c + 1) * 16);
+        __asm__ volatile("" ::: "memory");
       }
       dma_x(kt + 3, (st + 3) & 3);
 
@@ -188,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
       }
       // refill the slot just consumed with the codes kPrefetch steps ahead
       load_codes(q, kt + kPrefetch);
-      step_barrier<2 * MI>();
+      step_barrier<kInFlight>();
       st = (st + 1) & 3;
     }
     sv = svn;
@@ -259,8 +269,8 @@ template <int BITS, int MI, bool PARTIAL>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
-  const int lds = kStages * 32 * MI * BK * 2;
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
+  const int lds = kStages * 32 * MI * BK * 2;
   hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL>), grid, dim3(kThreads), lds, stream, x, wq,
                      scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
                      p.tiles_m, p.chunks_per_split);
