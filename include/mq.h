@@ -228,21 +228,58 @@ int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inte
                 hipStream_t stream);
 
 /*
- * The MLP's gate|up projection and silu(gate) * up in one kernel
- * (models/qwen2.py:132-133: down(silu(gate(x)) * up(x)) up to the down
- * projection): wq [2N, K * bits / 32] with the gate rows first (as the fused
- * gate|up matrix of mq_quantized_matmul), y bfloat16 [M, N] =
- * mq_silu_mul(mq_quantized_matmul(x, wq, ...)), bit for bit.  Decode shapes
- * of large matrices only (M <= 2, 2*N*K >= 2^25, K rows of at most 64 lanes:
- * where mq_quantized_matmul runs its dot2 GEMV):
- * mq_quantized_matmul_swiglu_supported says whether a shape is one; others
- * return MQ_ERR_UNSUPPORTED.
+ * The MLP's gate|up projection and silu(gate) * up without the [M, 2N]
+ * intermediate (models/qwen2.py:132-133: down(silu(gate(x)) * up(x)) up to
+ * the down projection): wq [2N, K * bits / 32] with the gate rows first (as
+ * the fused gate|up matrix of mq_quantized_matmul), y bfloat16 [M, N] =
+ * mq_silu_mul(mq_quantized_matmul_ws(x, wq, ...)), bit for bit.  Taken for
+ * decode shapes: M <= 2 on large matrices (2*N*K >= 2^25, K rows of at most 64
+ * lanes: the dot2 GEMV with a SwiGLU epilogue, no workspace), and the skinny
+ * GEMM's split-K plans (e.g. M = 32: its fixed-order reduce applies the
+ * SwiGLU; needs mq_quantized_matmul_swiglu_workspace bytes, which is what
+ * mq_quantized_matmul_workspace gives the unfused product).
+ * mq_quantized_matmul_swiglu_supported says whether a shape is taken; others
+ * return MQ_ERR_UNSUPPORTED.  mq_quantized_matmul_swiglu is the _ws form
+ * without a workspace.
  */
 int mq_quantized_matmul_swiglu_supported(int64_t M, int64_t N, int64_t K, int group_size,
                                          int bits);
+size_t mq_quantized_matmul_swiglu_workspace(int64_t M, int64_t N, int64_t K, int group_size,
+                                            int bits);
+int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                                  const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N,
+                                  int64_t K, int group_size, int bits, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
 int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
                                const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N, int64_t K,
                                int group_size, int bits, hipStream_t stream);
+
+/*
+ * A quantized linear followed by the residual add and the RMSNorm that read
+ * its output (models/qwen2.py:162-163 hidden = x + attn_out ->
+ * post_attention_layernorm; :164 hidden + mlp_out -> the next layer's
+ * input_layernorm or the final norm :199):
+ *   y = x @ dequantize(wq)^T (+ bias)        bfloat16, as mq_quantized_matmul_ws
+ *   h = bf16(y + residual)                   -> residual_out
+ *   out = bf16(h * rsqrt(mean(h^2) + eps) * norm_weight)
+ * equal bit for bit to mq_quantized_matmul_ws (with its workspace) followed by
+ * mq_rms_norm(y, residual, ...).  Taken for the skinny GEMM's split-K plans
+ * with N <= 8192 (e.g. the o and down projections at decode batch 32: the
+ * split-K reduce does the add and the norm, one launch fewer);
+ * mq_quantized_matmul_add_rms_norm_supported says which.  x [M, K],
+ * residual, residual_out, out [M, N], norm_weight [N], all bfloat16.
+ */
+int mq_quantized_matmul_add_rms_norm_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                               int bits);
+size_t mq_quantized_matmul_add_rms_norm_workspace(int64_t M, int64_t N, int64_t K,
+                                                  int group_size, int bits);
+int mq_quantized_matmul_add_rms_norm(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                                     const mq_bf16* biases, const mq_bf16* bias_vec,
+                                     const mq_bf16* residual, mq_bf16* residual_out,
+                                     const mq_bf16* norm_weight, float eps, mq_bf16* out,
+                                     int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                     void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream);
 
 /*
  * mq_rms_norm of one row followed by the quantized linear that reads it, in

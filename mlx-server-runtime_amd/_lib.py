@@ -44,6 +44,11 @@ EXPORTS = (
     "mq_quantized_matmul_swiglu",
     "mq_rms_norm_quantized_matmul_supported",
     "mq_rms_norm_quantized_matmul",
+    "mq_quantized_matmul_swiglu_workspace",
+    "mq_quantized_matmul_swiglu_ws",
+    "mq_quantized_matmul_add_rms_norm_supported",
+    "mq_quantized_matmul_add_rms_norm_workspace",
+    "mq_quantized_matmul_add_rms_norm",
 )
 
 _lock = threading.Lock()
@@ -91,12 +96,22 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_rms_norm_quantized_matmul_supported.argtypes = [_i64, _i64, _i64, _int, _int, _int]
     L.mq_rms_norm_quantized_matmul.argtypes = [_p, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p, _p,
                                                _i64, _i64, _i64, _int, _int, _int, _p]
+    L.mq_quantized_matmul_swiglu_workspace.argtypes = [_i64, _i64, _i64, _int, _int]
+    L.mq_quantized_matmul_swiglu_ws.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int,
+                                                _p, ctypes.c_size_t, _p]
+    L.mq_quantized_matmul_add_rms_norm_supported.argtypes = [_i64, _i64, _i64, _int, _int]
+    L.mq_quantized_matmul_add_rms_norm_workspace.argtypes = [_i64, _i64, _i64, _int, _int]
+    L.mq_quantized_matmul_add_rms_norm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _p,
+                                                   ctypes.c_float, _p, _i64, _i64, _i64, _int,
+                                                   _int, _p, ctypes.c_size_t, _p]
     L.mq_moe_combine_rms_norm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _int, _i64,
                                           ctypes.c_float, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
     L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t
     L.mq_paged_decode_attention_workspace.restype = ctypes.c_size_t
+    L.mq_quantized_matmul_swiglu_workspace.restype = ctypes.c_size_t
+    L.mq_quantized_matmul_add_rms_norm_workspace.restype = ctypes.c_size_t
 
 
 def lib() -> ctypes.CDLL:

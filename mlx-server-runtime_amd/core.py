@@ -227,10 +227,59 @@ def quantized_matmul_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tens
     xc = x.contiguous()
     M = xc.numel() // K
     y = torch.empty(tuple(x.shape[:-1]) + (N,), dtype=torch.bfloat16, device=x.device)
-    _lib.check(_lib.lib().mq_quantized_matmul_swiglu(
+    L = _lib.lib()
+    ws_bytes = L.mq_quantized_matmul_swiglu_workspace(M, N, K, group_size, bits) if M else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.check(L.mq_quantized_matmul_swiglu_ws(
         _ptr(xc), _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()),
-        _ptr(y), M, N, K, group_size, bits, _stream(x)), op)
+        _ptr(y), M, N, K, group_size, bits, _ptr(ws), ws_bytes, _stream(x)), op)
     return y
+
+
+def add_norm_supported(M: int, N: int, K: int, group_size: int = 64, bits: int = 4) -> bool:
+    """Whether quantized_matmul_add_rms_norm takes this shape."""
+    return bool(_lib.lib().mq_quantized_matmul_add_rms_norm_supported(M, N, K, group_size, bits))
+
+
+def quantized_matmul_add_rms_norm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                                  biases: torch.Tensor, residual: torch.Tensor,
+                                  norm_weight: torch.Tensor, eps: float,
+                                  bias: torch.Tensor | None = None, group_size: int = 64,
+                                  bits: int = 4):
+    """y = quantized_matmul(x, w) (+ bias), h = bf16(y + residual), out =
+    rms_norm(h) * norm_weight, in the GEMM and its split-K reduce; equal bit for
+    bit to quantized_matmul then decode_ops.rms_norm(y, ..., residual).
+    Returns (out, h)."""
+    op = "quantized_matmul_add_rms_norm"
+    _require_gpu(op, x=x, w=w, scales=scales, biases=biases, residual=residual,
+                 norm_weight=norm_weight, bias=bias)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    _check_bf16(op, "x", x)
+    _check_bf16(op, "residual", residual)
+    _check_bf16(op, "norm_weight", norm_weight)
+    if x.shape[-1] != K:
+        raise ValueError(f"[{op}] x has {x.shape[-1]} columns, expected {K}")
+    N = w.shape[0]
+    xc = x.contiguous()
+    M = xc.numel() // K
+    out_shape = tuple(x.shape[:-1]) + (N,)
+    if tuple(residual.shape) != out_shape:
+        raise ValueError(f"[{op}] residual must have shape {out_shape}")
+    if norm_weight.shape != (N,):
+        raise ValueError(f"[{op}] norm_weight must have shape ({N},)")
+    if bias is not None:
+        _check_bf16(op, "bias", bias)
+        bias = bias.contiguous()
+    out = torch.empty(out_shape, dtype=torch.bfloat16, device=x.device)
+    h = torch.empty_like(out)
+    L = _lib.lib()
+    ws_bytes = L.mq_quantized_matmul_add_rms_norm_workspace(M, N, K, group_size, bits) if M else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.check(L.mq_quantized_matmul_add_rms_norm(
+        _ptr(xc), _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()),
+        _ptr(bias), _ptr(residual.contiguous()), _ptr(h), _ptr(norm_weight.contiguous()),
+        float(eps), _ptr(out), M, N, K, group_size, bits, _ptr(ws), ws_bytes, _stream(x)), op)
+    return out, h
 
 
 def rms_norm_qmm_supported(M: int, N: int, K: int, group_size: int = 64, bits: int = 4,

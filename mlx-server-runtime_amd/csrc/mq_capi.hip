@@ -167,33 +167,125 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
   return 0;
 }
 
-int mq_quantized_matmul_swiglu_supported(int64_t M, int64_t N, int64_t K, int group_size,
-                                         int bits) {
+}  // extern "C"
+
+namespace {
+// How mq_quantized_matmul_swiglu runs a shape: 1 the dot2 GEMV with the SwiGLU
+// epilogue (where mq_quantized_matmul itself runs that GEMV on the 2N rows),
+// 2 the skinny GEMM's K splits with a SwiGLU reduce (where mq_quantized_matmul
+// with its workspace splits K), 0 not fused.
+int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
-  // Only where mq_quantized_matmul itself runs the dot2 GEMV on the 2N rows,
-  // so that the fused result is that of the two kernels, bit for bit.
-  if (use_matrix_core_gemv(M, 2 * N, K)) return 0;
-  return mq::qmv_swiglu_fits(M, N, K, bits) ? 1 : 0;
+  if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
+  if (use_skinny(M, 2 * N, K, bits) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
+  return 0;
 }
 
-int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
-                               const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N, int64_t K,
-                               int group_size, int bits, hipStream_t stream) {
+// mq_quantized_matmul_add_rms_norm takes the skinny GEMM's split plans (the
+// reduce ends in the norm) for rows of at most 8192.
+bool add_norm_fusable(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return false;
+  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64 || N % 8 || N > 8192) return false;
+  return use_skinny(M, N, K, bits) && mq::qmms_split_fusable(M, N, K, bits);
+}
+}  // namespace
+
+extern "C" {
+
+int mq_quantized_matmul_swiglu_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                         int bits) {
+  return swiglu_route(M, N, K, group_size, bits) != 0 ? 1 : 0;
+}
+
+size_t mq_quantized_matmul_swiglu_workspace(int64_t M, int64_t N, int64_t K, int group_size,
+                                            int bits) {
+  if (swiglu_route(M, N, K, group_size, bits) != 2) return 0;
+  return mq::qmms_workspace_bytes(M, 2 * N, K, bits);
+}
+
+int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                                  const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N,
+                                  int64_t K, int group_size, int bits, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
   const char* op = "quantized_matmul_swiglu";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", 2 * N)) return rc;
   if (M == 0 || N == 0) return ok();
-  if (!mq_quantized_matmul_swiglu_supported(M, N, K, group_size, bits))
+  const int route = swiglu_route(M, N, K, group_size, bits);
+  if (!route)
     return fail(MQ_ERR_UNSUPPORTED,
-                "[%s] M=%lld, N=%lld, K=%lld is not a fused shape (M <= 2, 2*N*K >= 2^25, rows "
-                "of at most 64 lanes); use mq_quantized_matmul and mq_silu_mul.",
+                "[%s] M=%lld, N=%lld, K=%lld is not a fused shape; use mq_quantized_matmul and "
+                "mq_silu_mul.",
                 op, (long long)M, (long long)N, (long long)K);
   if (!x || !wq || !scales || !biases || !y) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
   if (!aligned16(x) || !aligned16(wq))
     return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
-  return hip_status(mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+  if (route == 1)
+    return hip_status(mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+  const size_t need = mq::qmms_workspace_bytes(M, 2 * N, K, bits);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(MQ_ERR_INVALID,
+                "[%s] this shape needs a 16-byte aligned workspace of %zu bytes "
+                "(mq_quantized_matmul_swiglu_workspace).",
+                op, need);
+  return hip_status(mq::launch_qmms_swiglu(x, wq, scales, biases, y, M, N, K, bits, workspace,
+                                           workspace_bytes, stream),
+                    op);
+}
+
+int mq_quantized_matmul_swiglu(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                               const mq_bf16* biases, mq_bf16* y, int64_t M, int64_t N, int64_t K,
+                               int group_size, int bits, hipStream_t stream) {
+  return mq_quantized_matmul_swiglu_ws(x, wq, scales, biases, y, M, N, K, group_size, bits,
+                                       nullptr, 0, stream);
+}
+
+int mq_quantized_matmul_add_rms_norm_supported(int64_t M, int64_t N, int64_t K, int group_size,
+                                               int bits) {
+  return add_norm_fusable(M, N, K, group_size, bits) ? 1 : 0;
+}
+
+size_t mq_quantized_matmul_add_rms_norm_workspace(int64_t M, int64_t N, int64_t K,
+                                                  int group_size, int bits) {
+  return add_norm_fusable(M, N, K, group_size, bits) ? mq::qmms_workspace_bytes(M, N, K, bits)
+                                                     : 0;
+}
+
+int mq_quantized_matmul_add_rms_norm(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                                     const mq_bf16* biases, const mq_bf16* bias_vec,
+                                     const mq_bf16* residual, mq_bf16* residual_out,
+                                     const mq_bf16* norm_weight, float eps, mq_bf16* out,
+                                     int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                     void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream) {
+  const char* op = "quantized_matmul_add_rms_norm";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", N)) return rc;
+  if (M == 0 || N == 0) return ok();
+  if (!add_norm_fusable(M, N, K, group_size, bits))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] M=%lld, N=%lld, K=%lld is not a fused shape (a split skinny GEMM, N <= "
+                "8192); use mq_quantized_matmul_ws and mq_rms_norm.",
+                op, (long long)M, (long long)N, (long long)K);
+  if (!x || !wq || !scales || !biases || !residual || !residual_out || !norm_weight || !out)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(wq) || !aligned16(residual) || !aligned16(residual_out) ||
+      !aligned16(norm_weight) || !aligned16(out))
+    return fail(MQ_ERR_INVALID, "[%s] x, wq, residual, residual_out, norm_weight and out must be "
+                "16-byte aligned.", op);
+  const size_t need = mq::qmms_workspace_bytes(M, N, K, bits);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(MQ_ERR_INVALID,
+                "[%s] this shape needs a 16-byte aligned workspace of %zu bytes "
+                "(mq_quantized_matmul_add_rms_norm_workspace).",
+                op, need);
+  return hip_status(mq::launch_qmms_add_norm(x, wq, scales, biases, bias_vec, residual,
+                                             residual_out, norm_weight, eps, out, M, N, K, bits,
+                                             workspace, workspace_bytes, stream),
+                    op);
 }
 
 int mq_rms_norm_quantized_matmul_supported(int64_t M, int64_t N, int64_t K, int group_size,

@@ -73,6 +73,19 @@ hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t
 // enough workspace it runs unsplit.
 bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits);
 size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits);
+// Split plans of the skinny GEMM whose reduce can take an epilogue: SwiGLU of
+// a [2 Nout, K] gate|up matrix, or + residual and RMSNorm (N <= 8192).
+bool qmms_split_fusable(int64_t M, int64_t N, int64_t K, int bits);
+hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t Nout,
+                              int64_t K, int bits, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream);
+hipError_t launch_qmms_add_norm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                                const uint16_t* biases, const uint16_t* bias,
+                                const uint16_t* residual, uint16_t* residual_out,
+                                const uint16_t* norm_w, float eps, uint16_t* out, int64_t M,
+                                int64_t N, int64_t K, int bits, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,

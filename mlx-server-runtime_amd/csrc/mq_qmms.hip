@@ -237,6 +237,99 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ p
   y[i] = (uint16_t)f32_to_bf16_bits(acc);
 }
 
+// splitk_reduce's sums (same order), then silu_mul on the bf16 results: y
+// [M, Nout] from partials of the [M, 2 Nout] gate|up product.
+__global__ __launch_bounds__(256) void splitk_reduce_swiglu(const float* __restrict__ partial,
+                                                            int S, uint16_t* __restrict__ y,
+                                                            int64_t M, int Nout) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * Nout) return;
+  const int64_t m = i / Nout;
+  const int n = (int)(i - m * Nout);
+  const int64_t N2 = 2 * (int64_t)Nout, MN2 = M * N2;
+  const float* p = partial + m * N2 + n;
+  float g = 0.f, u = 0.f;
+  for (int s = 0; s < S; ++s) {
+    g += p[s * MN2];
+    u += p[s * MN2 + Nout];
+  }
+  y[i] = silu_mul_bf16(bf16_bits_to_f32(f32_to_bf16_bits(g)), bf16_bits_to_f32(f32_to_bf16_bits(u)));
+}
+
+// splitk_reduce's sums (same order, + bias), rounded to bf16 as it stores
+// them, then the RMSNorm kernel's residual add and norm on the row: one block
+// (256 threads) per row m, 8-element units t, t + 256, ... (N <= 8192), the
+// same reduction order -- equal bit for bit to splitk_reduce + mq_rms_norm.
+__global__ __launch_bounds__(256) void splitk_reduce_add_norm(
+    const float* __restrict__ partial, int S, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ residual_out,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int64_t M, int N, float eps) {
+  constexpr int kUnits = 4;
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const int units = N / 8;
+  const int64_t MN = M * N;
+  u32x4_t hv[kUnits];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kUnits; ++k) {
+    const int u = threadIdx.x + k * 256;
+    if (u < units) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      const float* p = partial + m * N + u * 8;
+      for (int s = 0; s < S; ++s) {
+        const f32x4_t a = reinterpret_cast<const f32x4_t*>(p + s * MN)[0];
+        const f32x4_t b = reinterpret_cast<const f32x4_t*>(p + s * MN)[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += a[e];
+          acc[4 + e] += b[e];
+        }
+      }
+      if (bias) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += bf16_bits_to_f32(bias[u * 8 + e]);
+      }
+      const u32x4_t r = reinterpret_cast<const u32x4_t*>(residual + m * N)[u];
+      u32x4_t h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t yv = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+        h[q] = pack_bf16x2(lo_bf16(yv) + lo_bf16(r[q]), hi_bf16(yv) + hi_bf16(r[q]));
+      }
+      reinterpret_cast<u32x4_t*>(residual_out + m * N)[u] = h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = lo_bf16(h[q]), b = hi_bf16(h[q]);
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+      hv[k] = h;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss += red[i];
+  const float inv = rsqrtf(ss / (float)N + eps);
+#pragma unroll
+  for (int k = 0; k < kUnits; ++k) {
+    const int u = threadIdx.x + k * 256;
+    if (u < units) {
+      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(w)[u];
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pack_bf16x2(lo_bf16(hv[k][q]) * inv * lo_bf16(wv[q]),
+                           hi_bf16(hv[k][q]) * inv * hi_bf16(wv[q]));
+      reinterpret_cast<u32x4_t*>(out + m * N)[u] = o;
+    }
+  }
+}
+
 struct Plan {
   int mi, tiles_n, tiles_m, splits, chunks_per_split;
 };
@@ -307,6 +400,50 @@ bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits) {
 size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits) {
   const Plan p = plan(M, N, K, bits, true);
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+}
+
+// The fused reduces need the split plan (the kernels' partial sums).
+bool qmms_split_fusable(int64_t M, int64_t N, int64_t K, int bits) {
+  return qmms_fits(M, N, K, bits) && plan(M, N, K, bits, true).splits > 1;
+}
+
+hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t Nout,
+                              int64_t K, int bits, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream) {
+  if (M == 0 || Nout == 0) return hipSuccess;
+  const int64_t N = 2 * Nout;
+  const Plan p = plan(M, N, K, bits, true);
+  if (p.splits < 2 || !workspace || workspace_bytes < (size_t)p.splits * M * N * sizeof(float))
+    return hipErrorInvalidValue;  // excluded by the caller's checks
+  float* part = static_cast<float*>(workspace);
+  const hipError_t e =
+      bits == 4 ? run_mi<4, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream)
+                : run_mi<8, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(splitk_reduce_swiglu, dim3((unsigned)((M * Nout + 255) / 256)), dim3(256), 0,
+                     stream, part, p.splits, y, M, (int)Nout);
+  return hipGetLastError();
+}
+
+hipError_t launch_qmms_add_norm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                                const uint16_t* biases, const uint16_t* bias,
+                                const uint16_t* residual, uint16_t* residual_out,
+                                const uint16_t* norm_w, float eps, uint16_t* out, int64_t M,
+                                int64_t N, int64_t K, int bits, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+  if (M == 0 || N == 0) return hipSuccess;
+  const Plan p = plan(M, N, K, bits, true);
+  if (p.splits < 2 || !workspace || workspace_bytes < (size_t)p.splits * M * N * sizeof(float))
+    return hipErrorInvalidValue;  // excluded by the caller's checks
+  float* part = static_cast<float*>(workspace);
+  const hipError_t e =
+      bits == 4 ? run_mi<4, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream)
+                : run_mi<8, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(splitk_reduce_add_norm, dim3((unsigned)M), dim3(256), 0, stream, part,
+                     p.splits, bias, residual, residual_out, norm_w, out, M, (int)N, eps);
+  return hipGetLastError();
 }
 
 hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

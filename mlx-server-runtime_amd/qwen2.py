@@ -26,7 +26,8 @@ and every accumulation are float32.  A decode step at batch 1 is six
 launches per dense layer (residual add + RMSNorm + QKV GEMV; split attention
 with RoPE and the KV append inside it; the splits' combine; o GEMV; residual
 add + RMSNorm + gate|up GEMV with SiLU * up in its epilogue; down GEMV; the
-norms run inside the GEMVs' input staging), captured
+norms run inside the GEMVs' input staging); batched, the residual adds, the
+norms and SiLU * up run in the skinny GEMMs' split-K reduces instead; captured
 once in a HIP graph and replayed per token (inputs live in static device
 buffers).  Prefill runs the same linears as GEMMs and float32 attention over
 the pages (the reference's dense-row gather, attention.py:264-298), so a
@@ -289,6 +290,19 @@ class Qwen2Model:
             x, h = fused_rms_norm(a, norm_w, eps, residual=res)
         return (_gate_up_silu(ql, x) if swiglu else ql(x)), h
 
+    def _linear_add_norm(self, ql: QLinear, inp: torch.Tensor, h: torch.Tensor,
+                         norm_w: torch.Tensor):
+        """ql(inp), its residual add and the RMSNorm after it -> (x, h): x the next
+        linear's normed input, h the residual stream.  One GEMM plus its reduce
+        where the skinny GEMM splits K (batched decode), else the two ops; the
+        same bits either way."""
+        eps = self.cfg.rms_norm_eps
+        K = inp.shape[-1]
+        if core.add_norm_supported(inp.numel() // K, ql.out_features, K, ql.group_size, ql.bits):
+            return core.quantized_matmul_add_rms_norm(inp, ql.wq, ql.scales, ql.biases, h, norm_w,
+                                                      eps, ql.bias, ql.group_size, ql.bits)
+        return fused_rms_norm(ql(inp), norm_w, eps, residual=h)
+
     def _next_norm(self, li: int) -> torch.Tensor:
         return (self.layers[li + 1].input_norm if li + 1 < len(self.layers)
                 else self.final_norm)
@@ -301,8 +315,8 @@ class Qwen2Model:
         x, h = fused_rms_norm(o, layer.post_norm, eps, residual=h)
         if layer.moe is not None:
             return layer.moe.residual_norm(x, h, self._next_norm(li), eps)
-        m = layer.down(_gate_up_silu(layer.gate_up, x))
-        return fused_rms_norm(m, self._next_norm(li), eps, residual=h)
+        return self._linear_add_norm(layer.down, _gate_up_silu(layer.gate_up, x), h,
+                                     self._next_norm(li))
 
     # ------------------------------------------------------------ prefill
     def prefill(self, ids: torch.Tensor, cache: PagedKV, start: int = 0,
@@ -358,9 +372,21 @@ class Qwen2Model:
         c = self.cfg
         d, nh, eps = c.head_dim, c.num_attention_heads, c.rms_norm_eps
         h = self._embed(tok)
-        # The next linear's input: rms_norm(src[0] (+ src[1])) * that layer's
-        # norm weight, computed inside the linear's kernel; or x, when an MoE
-        # block has already normalised it.
+        if tok.numel() > 1:  # batched: the norms ride on the GEMMs' split-K reduces
+            x = fused_rms_norm(h, self.layers[0].input_norm, eps)
+            for li, layer in enumerate(self.layers):
+                a = attention_step(layer.qkv(x), pos, cache, li, cos, sin, nh, d ** -0.5,
+                                   layer.q_norm, layer.k_norm, eps)
+                x, h = self._linear_add_norm(layer.o, a, h, layer.post_norm)
+                if layer.moe is not None:
+                    x, h = layer.moe.residual_norm(x, h, self._next_norm(li), eps)
+                else:
+                    x, h = self._linear_add_norm(layer.down, _gate_up_silu(layer.gate_up, x), h,
+                                                 self._next_norm(li))
+            return self._head(x)
+        # One row: the next linear's input is rms_norm(src[0] (+ src[1])) *
+        # that layer's norm weight, computed inside the linear's kernel; or x,
+        # when an MoE block has already normalised it.
         src, x = (h, None), None
         for li, layer in enumerate(self.layers):
             if x is None:

@@ -69,7 +69,8 @@ def test_rms_norm_batched_shape(ops):
 
 @pytest.mark.parametrize("M,N,K,bits", [(1, 18944, 3584, 4), (2, 18944, 3584, 8),
                                         (1, 18948, 3584, 4), (1, 1025, 16384, 4),
-                                        (2, 2049, 8192, 8)])
+                                        (2, 2049, 8192, 8), (32, 18944, 3584, 4),
+                                        (32, 18944, 3584, 8), (16, 9475, 3584, 4)])
 def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     """The gate|up GEMV with silu(gate) * up in its epilogue: bit-equal to the
     GEMV followed by silu_mul.  N = 18948, 1025 and 2049 leave a partial last
@@ -137,6 +138,29 @@ def test_rms_norm_quantized_matmul_small_matrix_with_bias(ops):
     ref = core.quantized_matmul(x, wq, sc, bi, True, 64, 4, bias=bias)
     assert torch.equal(h, ref_h)
     assert float((y.float() - ref.float()).abs().max() / ref.float().abs().max()) < 1e-2
+
+
+@pytest.mark.parametrize("M,N,K,bits,with_bias", [
+    (32, 3584, 18944, 4, False), (32, 3584, 3584, 4, True), (32, 4096, 4096, 8, False),
+    (27, 3584, 18944, 4, True)])
+def test_quantized_matmul_add_rms_norm_equals_two_kernels(ops, M, N, K, bits, with_bias):
+    """The skinny GEMM whose split-K reduce adds the residual and applies the
+    RMSNorm: bit-equal to quantized_matmul (its workspace, the same split plan)
+    followed by rms_norm, the residual stream included; 27 rows leave a
+    partial row tile."""
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    assert core.add_norm_supported(M, N, K, 64, bits)
+    g = _gen(M + N + K + bits)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = core.quantize(w, 64, bits)
+    x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    res = torch.randn(M, N, generator=g, device=DEV).to(torch.bfloat16)
+    nw = (torch.rand(N, generator=g, device=DEV) + 0.5).to(torch.bfloat16)
+    bias = (torch.randn(N, generator=g, device=DEV) * 0.1).to(torch.bfloat16) if with_bias else None
+    out, h = core.quantized_matmul_add_rms_norm(x, wq, sc, bi, res, nw, 1e-6, bias, 64, bits)
+    y = core.quantized_matmul(x, wq, sc, bi, True, 64, bits, bias=bias)
+    ref_out, ref_h = ops.rms_norm(y, nw, 1e-6, residual=res)
+    assert torch.equal(h, ref_h) and torch.equal(out, ref_out)
 
 
 def test_quantized_matmul_swiglu_refuses_other_shapes(ops):

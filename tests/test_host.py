@@ -37,7 +37,9 @@ def test_header_declares_the_abi():
         "mq_moe_route", "mq_moe_sort", "mq_moe_combine", "mq_moe_route_sort",
         "mq_moe_combine_rms_norm", "mq_quantized_matmul_swiglu_supported",
         "mq_quantized_matmul_swiglu", "mq_rms_norm_quantized_matmul_supported",
-        "mq_rms_norm_quantized_matmul"])
+        "mq_rms_norm_quantized_matmul", "mq_quantized_matmul_swiglu_workspace",
+        "mq_quantized_matmul_swiglu_ws", "mq_quantized_matmul_add_rms_norm_supported",
+        "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -136,6 +138,22 @@ def test_decoder_entry_validation(mq):
     assert sw(null, null, null, null, null, 4, 18944, 3584, 64, 4, null) == -2   # not fused
     assert sw(null, null, null, null, null, 1, 18944, 3584, 64, 4, null) == -1   # null pointers
     assert sw(null, null, null, null, null, 0, 18944, 3584, 64, 4, null) == 0
+    # batch-32 decode shapes: the skinny GEMM's split-K plans take the fused reduces
+    assert sup(32, 18944, 3584, 64, 4) == 1
+    assert L.mq_quantized_matmul_swiglu_workspace(32, 18944, 3584, 64, 4) == \
+        L.mq_quantized_matmul_workspace(32, 2 * 18944, 3584, 64, 4) > 0
+    assert L.mq_quantized_matmul_swiglu_workspace(1, 18944, 3584, 64, 4) == 0  # the GEMV path
+    assert sw(null, null, null, null, null, 32, 18944, 3584, 64, 4, null) == -1  # null pointers
+    an = L.mq_quantized_matmul_add_rms_norm_supported
+    assert an(32, 3584, 18944, 64, 4) == 1 and an(32, 3584, 3584, 64, 4) == 1
+    assert an(1, 3584, 18944, 64, 4) == 0                                       # a GEMV
+    assert L.mq_quantized_matmul_add_rms_norm_workspace(32, 3584, 18944, 64, 4) == \
+        L.mq_quantized_matmul_workspace(32, 3584, 18944, 64, 4) > 0
+    buf = ctypes.create_string_buffer(64)
+    p16 = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
+    assert L.mq_quantized_matmul_add_rms_norm(p16, p16, p16, p16, None, p16, p16, p16, 1e-6, p16,
+                                              32, 3584, 18944, 64, 4, None, 0, null) == -1
+    assert b"workspace" in L.mq_last_error()
     ns = L.mq_rms_norm_quantized_matmul_supported
     assert ns(1, 4608, 3584, 64, 4, 0) == 1 and ns(1, 18944, 3584, 64, 4, 1) == 1
     assert ns(2, 4608, 3584, 64, 4, 0) == 0                                     # one row only
