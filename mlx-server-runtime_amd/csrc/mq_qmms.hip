@@ -346,11 +346,13 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   // taller tiles, which carry more work per step.
   const int64_t want = 1024 / p.mi;
   if (can_split && base < want) {
-    // The partial sums (written once, read once) stay under half the weight
-    // bytes.
+    // The partial sums (written once, read once) stay under an eighth of the
+    // weight bytes, or 4 MiB, which stays in the Infinity Cache: small
+    // matrices (a layer's q/k/v or o at M = 32) then get short blocks, whose
+    // serial step latency otherwise sets the kernel time.
     const int64_t weight_bytes = N * K * bits / 8;
-    splits = std::min<int64_t>({(want + base - 1) / base, chunks,
-                                weight_bytes / (16 * M * N)});
+    const int64_t cap = std::max<int64_t>(weight_bytes / (16 * M * N), (4 << 20) / (4 * M * N));
+    splits = std::min<int64_t>({(want + base - 1) / base, chunks, cap});
   }
   if (splits < 1) splits = 1;
   p.chunks_per_split = (int)((chunks + splits - 1) / splits);
