@@ -167,18 +167,31 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
 }
 
 // ---------------------------------------------------------------- attention
-// Grid (splits, nkv, B), 256 threads.  A cached row of one KV head (D bf16,
-// 2D bytes) is read by LANES = D/8 lanes, 16 bytes each.  The block's lane
-// groups take the split's positions round robin, kTile positions per group at
-// a time with the K and V rows of all of them loaded together.  Each group
-// keeps its own running max, sum and weighted values (online softmax), and the
-// groups are merged at the end.  Scores are kept in log2 units
-// (q.k * scale * log2 e), so every exponential is exp2.
+// Grid (splits, nkv, B), 256 threads (4 waves).  A split block takes its
+// positions in passes of 64; wave w takes positions t0 + 16w + [0, 16) of the
+// pass t0:
+//  * scores S = Q K^T by v_mfma_f32_16x16x32_bf16: A = the KV head's REP
+//    query heads (rows >= REP zero), B = the wave's 16 K rows; lane l holds
+//    dims 32s + 8(l/16) .. +7 of position l % 16 for k-step s, 16 contiguous
+//    bytes of the cached row.  D row 4(l/16) + i, column l % 16 = score of
+//    head 4(l/16) + i at position l % 16;
+//  * an online softmax per wave over its positions: the head's max and sum
+//    over the wave's 16 positions by DPP within the 16 lanes of a D row;
+//  * P V on the vector ALU: lane l accumulates dims DPL*l .. DPL*l + DPL - 1
+//    (DPL = D / 64) of every head over the wave's 16 positions, P passing
+//    through a wave-private LDS tile (no block barrier inside the loop);
+//  * the four waves' (max, sum, weighted values) merged through LDS at the
+//    end.
+// Scores are kept in log2 units (q.k * scale * log2 e), so every exponential
+// is exp2.
 //
 // Partials per (b, kv head, split), float32: m[REP], s[REP], acc[REP][D];
 // splits past the sequence's end are neither written nor read.
 constexpr int kMaxChunk = 512;
-constexpr int kTile = 4;
+constexpr int kPass = 64;  // positions per pass: 16 per wave
+// Waves per SIMD (= blocks per CU: a 4-wave block puts one wave on each SIMD)
+// the split kernels are held to, by query heads per KV head.
+constexpr int kAttnWaves[9] = {0, 4, 4, 4, 3, 4, 4, 4, 3};
 constexpr float kNoScore = -1e30f;  // running max before the first position
 
 // Shared memory of one split block.
@@ -186,119 +199,155 @@ template <int REP, int D>
 struct AttnShared {
   __align__(16) uint16_t fresh[2][D];  // the new position's K and V rows (attn_step)
   int32_t slot_of[kMaxChunk];
+  __align__(16) float p_tile[kThreads / 64][16][16];  // per wave: P[position][head]
+  __align__(16) float f_tile[kThreads / 64][16];      // per wave: the pass's rescale per head
   float mrg_m[kThreads / 64][REP], mrg_s[kThreads / 64][REP];
   float mrg_a[kThreads / 64][REP][D];
 };
 
-// The split's partials from this lane's q fragments (qv: its 8 dims of each
-// query head, bf16 pairs) over positions l0 + [0, n) of the KV head rows kb /
-// vb (element pointers at this lane's 8 dims; row r at r * row_elems).
-// Position `fresh` of the split (or -1) takes its K / V row from sh.fresh
-// instead of the cache.  Writes pm[REP], ps[REP], pa[REP][D].
-template <int REP, int D>
-__device__ __forceinline__ void attn_block(const u32x4_t (&qv)[REP], AttnShared<REP, D>& sh, int n,
-                                           const uint16_t* kb, const uint16_t* vb,
-                                           int64_t row_elems, float scale_log2, int fresh,
-                                           float* pm, float* ps, float* pa) {
-  constexpr int LANES = D / 8;
-  constexpr int GROUPS = kThreads / LANES;
-  constexpr int WAVES = kThreads / 64;
-  const int sub = threadIdx.x % LANES, grp = threadIdx.x / LANES;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float m[REP], s[REP], acc[REP][8];
+template <int WIDTH>
+__device__ __forceinline__ float dpp_group_max(float v) {
+  static_assert(WIDTH == 16, "rows of 16 lanes");
+  v = fmaxf(v, dpp_f32<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  return v;
+}
+
+// One pass's rows of a wave, as this lane holds them: the MFMA B operand
+// (its slice of the K row of position l % 16) and its dims of the wave's 16
+// V rows (D = 128: a bf16 pair; D = 64: one bf16 in the low half).
+template <int D>
+struct AttnPass {
+  u32x4_t k[D / 32];
+  uint32_t v[16];
+};
+
+// Loads a pass's rows: `slot` is the cache slot of this lane's position
+// (l % 16 of the wave's 16); kb / vb point at the KV head's dim 0 of slot 0.
+template <int D>
+__device__ __forceinline__ void attn_load_pass(AttnPass<D>& ps, const uint16_t* kb,
+                                               const uint16_t* vb, int64_t row_elems, int slot) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const uint16_t* kr = kb + slot * row_elems + 8 * g;
 #pragma unroll
-  for (int r = 0; r < REP; ++r) {
-    m[r] = kNoScore;
-    s[r] = 0.f;
+  for (int s = 0; s < D / 32; ++s) ps.k[s] = *reinterpret_cast<const u32x4_t*>(kr + 32 * s);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[r][t] = 0.f;
+  for (int j = 0; j < 16; ++j) {
+    const uint16_t* vr = vb + __builtin_amdgcn_readlane(slot, j) * row_elems;  // lane j: position j
+    if constexpr (D == 128)
+      ps.v[j] = reinterpret_cast<const uint32_t*>(vr)[lane];
+    else
+      ps.v[j] = vr[lane];
   }
-  for (int t0 = 0; t0 < n; t0 += GROUPS * kTile) {
-    u32x4_t kr[kTile], vr[kTile];
+}
+
+// The split's partials over positions l0 + [0, n) of the KV head whose rows
+// start at kb / vb (row r at r * row_elems).  qa: this lane's A operand (query
+// head l % 16, dims 32s + 8(l/16) .. +7).  Position `fresh` of the split (or
+// -1) takes its K / V row from sh.fresh instead of the cache.  `first` holds
+// the first pass's rows, loaded before n was known; sh.slot_of the slots of
+// positions [0, n) (read from the second pass on).  Writes pm[REP], ps[REP],
+// pa[REP][D].
+template <int REP, int D>
+__device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShared<REP, D>& sh,
+                                           int n, const uint16_t* kb, const uint16_t* vb,
+                                           int64_t row_elems, float scale_log2, int fresh,
+                                           const AttnPass<D>& first, float* pm, float* ps,
+                                           float* pa) {
+  constexpr int DPL = D / 64, NS = D / 32, WAVES = kThreads / 64;
+  static_assert(REP <= 16 && (D == 64 || D == 128), "one MFMA row per query head");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+  float m4[4], s4[4];  // running max / sum of heads 4g + i over the wave's positions
+  float acc[REP][DPL];
 #pragma unroll
-    for (int u = 0; u < kTile; ++u) {
-      const int i = min(t0 + grp + GROUPS * u, n - 1);
-      const int64_t off = (int64_t)sh.slot_of[i] * row_elems;
-      kr[u] = *reinterpret_cast<const u32x4_t*>(kb + off);
-      vr[u] = *reinterpret_cast<const u32x4_t*>(vb + off);
-      if (i == fresh) {
-        kr[u] = reinterpret_cast<const u32x4_t*>(sh.fresh[0])[sub];
-        vr[u] = reinterpret_cast<const u32x4_t*>(sh.fresh[1])[sub];
+  for (int i = 0; i < 4; ++i) {
+    m4[i] = kNoScore;
+    s4[i] = 0.f;
+  }
+#pragma unroll
+  for (int h = 0; h < REP; ++h)
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) acc[h][t] = 0.f;
+  float* pw = &sh.p_tile[wave][0][0];
+  float* fw = sh.f_tile[wave];
+  AttnPass<D> cur = first;
+  for (int t0 = 0; t0 < n; t0 += kPass) {
+    const int base = t0 + 16 * wave;  // the wave's first position of the pass
+    if (t0 > 0) attn_load_pass<D>(cur, kb, vb, row_elems, sh.slot_of[min(base + c, n - 1)]);
+    if (fresh >= base && fresh < base + 16) {  // uniform
+      if (c == fresh - base) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          cur.k[s] = *reinterpret_cast<const u32x4_t*>(sh.fresh[0] + 32 * s + 8 * g);
+      }
+      const uint32_t fv = D == 128 ? reinterpret_cast<const uint32_t*>(sh.fresh[1])[lane]
+                                   : (uint32_t)sh.fresh[1][lane];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (base + j == fresh) cur.v[j] = fv;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)  // rows past the end may hold anything: no V from them
+      if (base + j >= n) cur.v[j] = 0u;
+
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[s]),
+                                                  __builtin_bit_cast(bf16x8_t, cur.k[s]), d, 0,
+                                                  0, 0);
+    const bool valid = base + c < n;
+    float pv[4], fv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = valid ? d[i] * scale_log2 : -INFINITY;
+      const float mn = fmaxf(m4[i], dpp_group_max<16>(x));
+      fv[i] = exp2f(m4[i] - mn);
+      pv[i] = exp2f(x - mn);
+      s4[i] = fmaf(s4[i], fv[i], dpp_group_sum<16>(pv[i]));
+      m4[i] = mn;
+    }
+    *reinterpret_cast<f32x4_t*>(pw + c * 16 + 4 * g) = f32x4_t{pv[0], pv[1], pv[2], pv[3]};
+    if (c == 0) *reinterpret_cast<f32x4_t*>(fw + 4 * g) = f32x4_t{fv[0], fv[1], fv[2], fv[3]};
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's tiles are written
+
+    float fh[REP];
+#pragma unroll
+    for (int h = 0; h < REP; ++h) fh[h] = fw[h];
+#pragma unroll
+    for (int h = 0; h < REP; ++h)
+#pragma unroll
+      for (int t = 0; t < DPL; ++t) acc[h][t] *= fh[h];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float vf[DPL];
+      vf[0] = lo_bf16(cur.v[j]);
+      if constexpr (DPL == 2) vf[1] = hi_bf16(cur.v[j]);
+#pragma unroll
+      for (int h = 0; h < REP; ++h) {
+        const float pj = pw[j * 16 + h];
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[h][t] = fmaf(pj, vf[t], acc[h][t]);
       }
     }
-    float x[kTile][REP];
-#pragma unroll
-    for (int u = 0; u < kTile; ++u) {
-      const bool valid = t0 + grp + GROUPS * u < n;
-#pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        float d = 0.f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) d = dot2_bf16(qv[r][t], kr[u][t], d);
-        d = dpp_group_sum<LANES>(d);
-        x[u][r] = valid ? d * scale_log2 : -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      float mt = x[0][r];
-#pragma unroll
-      for (int u = 1; u < kTile; ++u) mt = fmaxf(mt, x[u][r]);
-      const float mn = fmaxf(m[r], mt);
-      const float f = exp2f(m[r] - mn);
-      float psum = 0.f;
-#pragma unroll
-      for (int u = 0; u < kTile; ++u) {
-        x[u][r] = exp2f(x[u][r] - mn);  // now the weight p of position u
-        psum += x[u][r];
-      }
-      s[r] = fmaf(s[r], f, psum);
-      m[r] = mn;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[r][t] *= f;
-    }
-#pragma unroll
-    for (int u = 0; u < kTile; ++u) {
-      float vf[8];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        vf[2 * t] = lo_bf16(vr[u][t]);
-        vf[2 * t + 1] = hi_bf16(vr[u][t]);
-      }
-#pragma unroll
-      for (int r = 0; r < REP; ++r)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[r][t] = fmaf(x[u][r], vf[t], acc[r][t]);
-    }
+    __asm__ volatile("" ::: "memory");  // this pass's tile reads stay ahead of the next writes
   }
 
-  // merge the lane groups of each wave (butterfly: every group ends with the
-  // wave's totals), then the waves through LDS
+  // merge the waves through LDS
+  if (c == 0) {
 #pragma unroll
-  for (int off = LANES; off < 64; off <<= 1) {
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      const float mo = __shfl_xor(m[r], off, 64);
-      const float so = __shfl_xor(s[r], off, 64);
-      const float mn = fmaxf(m[r], mo);
-      const float f1 = exp2f(m[r] - mn), f2 = exp2f(mo - mn);
-      s[r] = s[r] * f1 + so * f2;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[r][t] = acc[r][t] * f1 + __shfl_xor(acc[r][t], off, 64) * f2;
-      m[r] = mn;
-    }
-  }
-  if (lane < LANES) {
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) sh.mrg_a[wave][r][8 * sub + t] = acc[r][t];
-      if (lane == 0) {
-        sh.mrg_m[wave][r] = m[r];
-        sh.mrg_s[wave][r] = s[r];
+    for (int i = 0; i < 4; ++i)
+      if (4 * g + i < REP) {
+        sh.mrg_m[wave][4 * g + i] = m4[i];
+        sh.mrg_s[wave][4 * g + i] = s4[i];
       }
-    }
   }
+#pragma unroll
+  for (int h = 0; h < REP; ++h)
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) sh.mrg_a[wave][h][DPL * lane + t] = acc[h][t];
   __syncthreads();
   for (int e = threadIdx.x; e < REP * D; e += kThreads) {
     const int r = e / D, dd = e % D;
@@ -318,6 +367,59 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qv)[REP], AttnShared<
       ps[r] = sum;
     }
   }
+}
+
+// Cache slot (page * page_size + offset) of position l of a sequence whose
+// page table is `table`; positions past the table's end map into its last
+// page, so that a speculative lookup stays in bounds.
+__device__ __forceinline__ int attn_slot(const int32_t* table, int pages_per_seq, int page_size,
+                                         int num_pages, int l) {
+  return (int)(clamp_index(table[min(l / page_size, pages_per_seq - 1)], num_pages) * page_size +
+               l % page_size);
+}
+
+// The loads a split block issues before it knows the sequence's length, so
+// that none of them waits for the position: the slots of the split's
+// positions l0 + threadIdx.x + kThreads * k (for sh.slot_of), and the first
+// pass's rows.  Positions past the sequence's end are looked up too and
+// masked later.
+template <int D>
+struct AttnPrefetch {
+  static constexpr int kSlots = kMaxChunk / kThreads;
+  int slot[kSlots];
+  AttnPass<D> first;
+
+  __device__ __forceinline__ void issue(const int32_t* table, int pages_per_seq, int page_size,
+                                        int num_pages, int l0, int chunk, const uint16_t* kb,
+                                        const uint16_t* vb, int64_t row_elems) {
+    const int wave = threadIdx.x >> 6, c = threadIdx.x & 15;
+    attn_load_pass<D>(first, kb, vb, row_elems,
+                      attn_slot(table, pages_per_seq, page_size, num_pages,
+                                l0 + min(16 * wave + c, chunk - 1)));
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k)
+      slot[k] = attn_slot(table, pages_per_seq, page_size, num_pages,
+                          l0 + min((int)threadIdx.x + kThreads * k, chunk - 1));
+  }
+
+  // sh.slot_of[i] for the split's first n positions
+  __device__ __forceinline__ void store_slots(int32_t* slot_of, int n) const {
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k)
+      if ((int)threadIdx.x + kThreads * k < n) slot_of[threadIdx.x + kThreads * k] = slot[k];
+  }
+};
+
+// This lane's A operand from the KV head's REP query heads (q: head 0, dim 0,
+// heads `head_stride` elements apart): head l % 16, dims 32s + 8(l/16) .. +7.
+template <int REP, int D>
+__device__ __forceinline__ void attn_load_q(u32x4_t (&qa)[D / 32], const uint16_t* q,
+                                            int64_t head_stride) {
+  const int c = threadIdx.x & 15, g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s)
+    qa[s] = c < REP ? *reinterpret_cast<const u32x4_t*>(q + c * head_stride + 32 * s + 8 * g)
+                    : u32x4_t{0u, 0u, 0u, 0u};
 }
 
 // out[b, head kvh*REP + r, :] from the `used` splits' partials at base:
@@ -344,37 +446,36 @@ __device__ __forceinline__ void attn_combine_heads(const float* base, int used, 
   }
 }
 
+// (The pointers the speculative loads read are not __restrict__: with it the
+// compiler may sink those loads below the asm barrier that orders them ahead
+// of the first wait.)
 template <int REP, int D>
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pages,
-    const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table,
-    int pages_per_seq, int page_size, int num_pages, const int64_t* __restrict__ pos,
+__global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_split_kernel(
+    const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages, const int32_t* page_table,
+    int pages_per_seq, int page_size, int num_pages, const int64_t* pos,
     float* __restrict__ part, int nkv, int chunk, float scale_log2) {
-  constexpr int LANES = D / 8;
   __shared__ AttnShared<REP, D> sh;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int splits = gridDim.x;
-  const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
   const int l0 = split * chunk;
+  const int nh = nkv * REP;
+  const int64_t pos_b = pos[b];
+  asm volatile("" ::: "memory");  // the position's load goes out first
+  u32x4_t qa[D / 32];
+  attn_load_q<REP, D>(qa, q + (b * nh + kvh * REP) * (int64_t)D, D);
+  AttnPrefetch<D> pf;
+  pf.issue(page_table + b * pages_per_seq, pages_per_seq, page_size, num_pages, l0, chunk,
+           k_pages + kvh * D, v_pages + kvh * D, (int64_t)nkv * D);
+  asm volatile("" ::: "memory");  // every load above is issued before the first wait
+  const int L = (int)clamp_index(pos_b, (int64_t)pages_per_seq * page_size) + 1;
   const int n = min(L - l0, chunk);
   if (n <= 0) return;  // past the sequence's end
   float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
-  const int32_t* table = page_table + b * pages_per_seq;
-  for (int i = threadIdx.x; i < n; i += kThreads) {
-    const int l = l0 + i;
-    sh.slot_of[i] = (int32_t)(clamp_index(table[l / page_size], num_pages) * page_size +
-                              l % page_size);
-  }
-  const int sub = threadIdx.x % LANES;
-  const int nh = nkv * REP;
-  u32x4_t qv[REP];
-#pragma unroll
-  for (int r = 0; r < REP; ++r)
-    qv[r] = reinterpret_cast<const u32x4_t*>(q + (b * nh + kvh * REP + r) * (int64_t)D)[sub];
+  pf.store_slots(sh.slot_of, n);
   __syncthreads();
-  attn_block<REP, D>(qv, sh, n, k_pages + kvh * D + sub * 8, v_pages + kvh * D + sub * 8,
-                     (int64_t)nkv * D, scale_log2, -1, pm, pm + REP, pm + 2 * REP);
+  attn_block<REP, D>(qa, sh, n, k_pages + kvh * D, v_pages + kvh * D, (int64_t)nkv * D,
+                     scale_log2, -1, pf.first, pm, pm + REP, pm + 2 * REP);
 }
 
 // The split kernel of one decode step of a layer's attention, straight from
@@ -386,13 +487,12 @@ __global__ __launch_bounds__(kThreads) void attn_split_kernel(
 // partials to a block on another XCD takes an agent-scope release -- an L2
 // write-back per block -- which costs far more than the launch.)
 template <int REP, int D>
-__global__ __launch_bounds__(kThreads) void attn_step_kernel(
-    const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
-    const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps,
-    uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages, float* __restrict__ part,
-    int nkv, int chunk, float scale_log2) {
+__global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_step_kernel(
+    const uint16_t* __restrict__ qkv, const int64_t* pos, const int32_t* page_table,
+    int pages_per_seq, int page_size, int num_pages, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ k_norm, float eps, uint16_t* k_pages, uint16_t* v_pages,
+    float* __restrict__ part, int nkv, int chunk, float scale_log2) {
   constexpr int LANES = D / 8, HALF = D / 2, WAVES = kThreads / 64;
   static_assert(HALF <= 64, "one rotated pair per lane");
   __shared__ AttnShared<REP, D> sh;
@@ -400,9 +500,15 @@ __global__ __launch_bounds__(kThreads) void attn_step_kernel(
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int splits = gridDim.x;
-  const int p = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size);
-  const int L = p + 1;
   const int l0 = split * chunk;
+  const int64_t pos_b = pos[b];
+  asm volatile("" ::: "memory");  // the position's load goes out first
+  AttnPrefetch<D> pf;
+  pf.issue(page_table + b * pages_per_seq, pages_per_seq, page_size, num_pages, l0, chunk,
+           k_pages + kvh * D, v_pages + kvh * D, (int64_t)nkv * D);
+  asm volatile("" ::: "memory");  // every load above is issued before the first wait
+  const int p = (int)clamp_index(pos_b, (int64_t)pages_per_seq * page_size);
+  const int L = p + 1;
   const int n = min(L - l0, chunk);
   if (n <= 0) return;  // past the sequence's end
   const bool owner = p < l0 + n;  // this split holds the new position
@@ -435,12 +541,7 @@ __global__ __launch_bounds__(kThreads) void attn_step_kernel(
   if (owner && threadIdx.x < LANES)  // the new v row, as is
     reinterpret_cast<u32x4_t*>(sh.fresh[1])[threadIdx.x] =
         reinterpret_cast<const u32x4_t*>(row + (nh + nkv + kvh) * D)[threadIdx.x];
-  const int32_t* table = page_table + b * pages_per_seq;
-  for (int i = threadIdx.x; i < n; i += kThreads) {
-    const int l = l0 + i;
-    sh.slot_of[i] = (int32_t)(clamp_index(table[l / page_size], num_pages) * page_size +
-                              l % page_size);
-  }
+  pf.store_slots(sh.slot_of, n);
   __syncthreads();
   const int64_t row_elems = (int64_t)nkv * D;
   if (owner && threadIdx.x < LANES) {  // append the new k and v rows to the pages
@@ -448,12 +549,11 @@ __global__ __launch_bounds__(kThreads) void attn_step_kernel(
     *reinterpret_cast<u32x4_t*>(k_pages + at) = reinterpret_cast<const u32x4_t*>(sh.fresh[0])[sub];
     *reinterpret_cast<u32x4_t*>(v_pages + at) = reinterpret_cast<const u32x4_t*>(sh.fresh[1])[sub];
   }
-  u32x4_t qv[REP];
-#pragma unroll
-  for (int r = 0; r < REP; ++r) qv[r] = reinterpret_cast<const u32x4_t*>(qs[r])[sub];
+  u32x4_t qa[D / 32];
+  attn_load_q<REP, D>(qa, &qs[0][0], D);
   float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
-  attn_block<REP, D>(qv, sh, n, k_pages + kvh * D + sub * 8, v_pages + kvh * D + sub * 8,
-                     row_elems, scale_log2, owner ? p - l0 : -1, pm, pm + REP, pm + 2 * REP);
+  attn_block<REP, D>(qa, sh, n, k_pages + kvh * D, v_pages + kvh * D, row_elems, scale_log2,
+                     owner ? p - l0 : -1, pf.first, pm, pm + REP, pm + 2 * REP);
 }
 
 // Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over the sequence's
@@ -493,18 +593,13 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
 }
 
 // Blocks of attn_split_kernel / attn_step_kernel<REP, D> one CU holds at
-// once (4-wave blocks; waves per SIMD as the register count allows, the lower
-// of the two kernels).
-int attn_blocks_per_cu(int rep) {
-  static const int occ[9] = {0, 6, 5, 4, 4, 3, 2, 3, 2};
-  return occ[rep < 1 ? 1 : rep > 8 ? 8 : rep];
-}
+// once.
+int attn_blocks_per_cu(int rep) { return kAttnWaves[rep < 1 ? 1 : rep > 8 ? 8 : rep]; }
 
-// Positions per split: whole tile passes (64 positions at head_dim 128), at
-// most kMaxChunk, and as many splits as keep every CU busy in one round of
+// Positions per split: whole passes (kPass positions), at most kMaxChunk, and as many splits as keep every CU busy in one round of
 // blocks (a split is latency-bound, so a second round costs a full split).
 int attn_chunk(int64_t B, int nkv, int rep, int d, int64_t capacity) {
-  const int64_t pass = (int64_t)(kThreads / (d / 8)) * kTile;
+  const int64_t pass = kPass;
   const int64_t blocks = B * nkv;
   const int64_t target = 256 * (int64_t)attn_blocks_per_cu(rep);
   int64_t splits = std::max<int64_t>(1, target / blocks);
