@@ -191,7 +191,7 @@ constexpr int kMaxChunk = 512;
 constexpr int kPass = 64;  // positions per pass: 16 per wave
 // Waves per SIMD (= blocks per CU: a 4-wave block puts one wave on each SIMD)
 // the split kernels are held to, by query heads per KV head.
-constexpr int kAttnWaves[9] = {0, 4, 4, 4, 3, 4, 4, 4, 3};
+constexpr int kAttnWaves[9] = {0, 4, 4, 4, 4, 4, 3, 3, 3};
 constexpr float kNoScore = -1e30f;  // running max before the first position
 
 // Shared memory of one split block.
@@ -304,8 +304,8 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
     for (int i = 0; i < 4; ++i) {
       const float x = valid ? d[i] * scale_log2 : -INFINITY;
       const float mn = fmaxf(m4[i], dpp_group_max<16>(x));
-      fv[i] = exp2f(m4[i] - mn);
-      pv[i] = exp2f(x - mn);
+      fv[i] = __builtin_amdgcn_exp2f(m4[i] - mn);  // arguments <= 0: no range fix-up needed
+      pv[i] = __builtin_amdgcn_exp2f(x - mn);
       s4[i] = fmaf(s4[i], fv[i], dpp_group_sum<16>(pv[i]));
       m4[i] = mn;
     }
@@ -313,6 +313,14 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
     if (c == 0) *reinterpret_cast<f32x4_t*>(fw + 4 * g) = f32x4_t{fv[0], fv[1], fv[2], fv[3]};
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's tiles are written
 
+    // P rows are read kAhead positions before their use (a ring of kAhead
+    // rows in registers), so the LDS latency is paid once, not per position.
+    constexpr int kAhead = 4;
+    float pr[kAhead][REP];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j)
+#pragma unroll
+      for (int h = 0; h < REP; ++h) pr[j][h] = pw[j * 16 + h];
     float fh[REP];
 #pragma unroll
     for (int h = 0; h < REP; ++h) fh[h] = fw[h];
@@ -325,12 +333,17 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
       float vf[DPL];
       vf[0] = lo_bf16(cur.v[j]);
       if constexpr (DPL == 2) vf[1] = hi_bf16(cur.v[j]);
+      float pj[REP];
 #pragma unroll
-      for (int h = 0; h < REP; ++h) {
-        const float pj = pw[j * 16 + h];
+      for (int h = 0; h < REP; ++h) pj[h] = pr[j % kAhead][h];
+      if (j + kAhead < 16) {
 #pragma unroll
-        for (int t = 0; t < DPL; ++t) acc[h][t] = fmaf(pj, vf[t], acc[h][t]);
+        for (int h = 0; h < REP; ++h) pr[j % kAhead][h] = pw[(j + kAhead) * 16 + h];
       }
+#pragma unroll
+      for (int h = 0; h < REP; ++h)
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[h][t] = fmaf(pj[h], vf[t], acc[h][t]);
     }
     __asm__ volatile("" ::: "memory");  // this pass's tile reads stay ahead of the next writes
   }
@@ -420,30 +433,6 @@ __device__ __forceinline__ void attn_load_q(u32x4_t (&qa)[D / 32], const uint16_
   for (int s = 0; s < D / 32; ++s)
     qa[s] = c < REP ? *reinterpret_cast<const u32x4_t*>(q + c * head_stride + 32 * s + 8 * g)
                     : u32x4_t{0u, 0u, 0u, 0u};
-}
-
-// out[b, head kvh*REP + r, :] from the `used` splits' partials at base:
-// rescaled to their common max, over the rescaled sum.  Threads stride over
-// (r, dim) pairs starting at t.
-template <int REP, int D>
-__device__ __forceinline__ void attn_combine_heads(const float* base, int used, uint16_t* out,
-                                                   int t, int stride) {
-  constexpr int STRIDE = REP * (D + 2);
-  for (int e = t; e < REP * D; e += stride) {
-    const int r = e / D, dd = e % D;
-    float mx = -INFINITY;
-#pragma unroll 8
-    for (int sp = 0; sp < used; ++sp) mx = fmaxf(mx, base[sp * STRIDE + r]);
-    float num = 0.f, den = 0.f;
-#pragma unroll 8
-    for (int sp = 0; sp < used; ++sp) {
-      const float* p = base + sp * STRIDE;
-      const float f = exp2f(p[r] - mx);
-      den = fmaf(f, p[REP + r], den);
-      num = fmaf(f, p[2 * REP + r * D + dd], num);
-    }
-    out[e] = (uint16_t)f32_to_bf16_bits(num / den);
-  }
 }
 
 // (The pointers the speculative loads read are not __restrict__: with it the
@@ -558,18 +547,56 @@ __global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_step_kernel(
 
 // Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over the sequence's
 // splits of the partials rescaled to their common max, over the rescaled sum.
+// The partials of the first kCombineAhead splits are loaded before the
+// position (which says how many splits the sequence used) arrives; the pointers
+// are not __restrict__ so that the asm barriers keep those loads ahead of the
+// wait.
+constexpr int kCombineAhead = 16;
+
 template <int REP, int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(
-    const float* __restrict__ part, const int64_t* __restrict__ pos, int pages_per_seq,
-    int page_size, uint16_t* __restrict__ out, int nkv, int splits, int chunk) {
+__global__ __launch_bounds__(D) void attn_combine_kernel(const float* part, const int64_t* pos,
+                                                         int pages_per_seq, int page_size,
+                                                         uint16_t* __restrict__ out, int nkv,
+                                                         int splits, int chunk) {
+  constexpr int STRIDE = REP * (D + 2);
   const int hh = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int kvh = hh / REP, r = hh % REP;
-  const int L = (int)clamp_index(pos[b], (int64_t)pages_per_seq * page_size) + 1;
+  const int64_t pos_b = pos[b];
+  asm volatile("" ::: "memory");  // the position's load goes out first
+  const float* base = part + (b * nkv + kvh) * splits * (int64_t)STRIDE;
+  float pm[kCombineAhead], ps[kCombineAhead], pa[kCombineAhead];
+#pragma unroll
+  for (int sp = 0; sp < kCombineAhead; ++sp)
+    if (sp < splits) {  // uniform; splits past the used ones are loaded and ignored
+      const float* p = base + sp * STRIDE;
+      pm[sp] = p[r];
+      ps[sp] = p[REP + r];
+      pa[sp] = p[2 * REP + r * D + threadIdx.x];
+    }
+  asm volatile("" ::: "memory");  // every load above is issued before the first wait
+  const int L = (int)clamp_index(pos_b, (int64_t)pages_per_seq * page_size) + 1;
   const int used = min(splits, (L + chunk - 1) / chunk);
-  const float* base = part + (b * nkv + kvh) * splits * (int64_t)(REP * (D + 2));
-  attn_combine_heads<REP, D>(base, used, out + (b * nkv * REP + kvh * REP) * (int64_t)D,
-                             r * D + threadIdx.x, REP * D);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < kCombineAhead; ++sp)
+    if (sp < used) mx = fmaxf(mx, pm[sp]);
+  for (int sp = kCombineAhead; sp < used; ++sp) mx = fmaxf(mx, base[sp * STRIDE + r]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < kCombineAhead; ++sp)
+    if (sp < used) {
+      const float f = exp2f(pm[sp] - mx);
+      den = fmaf(f, ps[sp], den);
+      num = fmaf(f, pa[sp], num);
+    }
+  for (int sp = kCombineAhead; sp < used; ++sp) {
+    const float* p = base + sp * STRIDE;
+    const float f = exp2f(p[r] - mx);
+    den = fmaf(f, p[REP + r], den);
+    num = fmaf(f, p[2 * REP + r * D + threadIdx.x], num);
+  }
+  out[(b * nkv * REP + hh) * (int64_t)D + threadIdx.x] = (uint16_t)f32_to_bf16_bits(num / den);
 }
 
 // ---------------------------------------------------------------- SiLU * up
