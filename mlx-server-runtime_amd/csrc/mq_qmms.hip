@@ -226,15 +226,38 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
 }
 
 // y[m, n] = bf16(sum over splits of partial[s, m, n] (in split order) + bias[n])
+// acc[e] += the S split-K partials p[s * stride + off[e]] (e < W), added in
+// split order.  The loads of B splits go out before the first add, so S
+// splits cost ceil(S / B) memory round trips instead of S.
+template <int W, int B>
+__device__ __forceinline__ void add_splits(const float* p, int S, int64_t stride,
+                                           const int (&off)[W], float (&acc)[W]) {
+  for (int s0 = 0; s0 < S; s0 += B) {
+    float v[B][W];
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+      if (s0 + i < S) {  // uniform
+#pragma unroll
+        for (int e = 0; e < W; ++e) v[i][e] = p[(s0 + i) * stride + off[e]];
+      }
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+      if (s0 + i < S) {
+#pragma unroll
+        for (int e = 0; e < W; ++e) acc[e] += v[i][e];
+      }
+  }
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ partial, int S,
                                                      const uint16_t* __restrict__ bias,
                                                      uint16_t* __restrict__ y, int64_t MN, int N) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= MN) return;
-  float acc = 0.f;
-  for (int s = 0; s < S; ++s) acc += partial[s * MN + i];
-  if (bias) acc += bf16_bits_to_f32(bias[i % N]);
-  y[i] = (uint16_t)f32_to_bf16_bits(acc);
+  float acc[1] = {0.f};
+  add_splits<1, 16>(partial + i, S, MN, {0}, acc);
+  if (bias) acc[0] += bf16_bits_to_f32(bias[i % N]);
+  y[i] = (uint16_t)f32_to_bf16_bits(acc[0]);
 }
 
 // splitk_reduce's sums (same order), then silu_mul on the bf16 results: y
@@ -249,7 +272,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_swiglu(const float* __restr
   const int64_t N2 = 2 * (int64_t)Nout, MN2 = M * N2;
   const float* p = partial + m * N2 + n;
   float g = 0.f, u = 0.f;
-  for (int s = 0; s < S; ++s) {
+  for (int s = 0; s < S; ++s) {  // few splits here (the gate|up product is wide)
     g += p[s * MN2];
     u += p[s * MN2 + Nout];
   }
@@ -269,28 +292,41 @@ __global__ __launch_bounds__(256) void splitk_reduce_add_norm(
   const int64_t m = blockIdx.x;
   const int units = N / 8;
   const int64_t MN = M * N;
-  u32x4_t hv[kUnits];
+  u32x4_t hv[kUnits], rv[kUnits], wv[kUnits], bv[kUnits];
+  // the row's residual, norm weight and bias first: none of them waits for the
+  // partial sums
+#pragma unroll
+  for (int k = 0; k < kUnits; ++k) {
+    const int u = threadIdx.x + k * 256;
+    if (u < units) {
+      rv[k] = reinterpret_cast<const u32x4_t*>(residual + m * N)[u];
+      wv[k] = reinterpret_cast<const u32x4_t*>(w)[u];
+      if (bias) {
+        if ((reinterpret_cast<uintptr_t>(bias) & 15) == 0) {  // uniform
+          bv[k] = reinterpret_cast<const u32x4_t*>(bias)[u];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bv[k][q] = (uint32_t)bias[u * 8 + 2 * q] | (uint32_t)bias[u * 8 + 2 * q + 1] << 16;
+        }
+      }
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < kUnits; ++k) {
     const int u = threadIdx.x + k * 256;
     if (u < units) {
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      const float* p = partial + m * N + u * 8;
-      for (int s = 0; s < S; ++s) {
-        const f32x4_t a = reinterpret_cast<const f32x4_t*>(p + s * MN)[0];
-        const f32x4_t b = reinterpret_cast<const f32x4_t*>(p + s * MN)[1];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] += a[e];
-          acc[4 + e] += b[e];
-        }
-      }
+      add_splits<8, 16>(partial + m * N + u * 8, S, MN, {0, 1, 2, 3, 4, 5, 6, 7}, acc);
       if (bias) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += bf16_bits_to_f32(bias[u * 8 + e]);
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += lo_bf16(bv[k][q]);
+          acc[2 * q + 1] += hi_bf16(bv[k][q]);
+        }
       }
-      const u32x4_t r = reinterpret_cast<const u32x4_t*>(residual + m * N)[u];
+      const u32x4_t r = rv[k];
       u32x4_t h;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -319,12 +355,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_add_norm(
   for (int k = 0; k < kUnits; ++k) {
     const int u = threadIdx.x + k * 256;
     if (u < units) {
-      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(w)[u];
       u32x4_t o;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        o[q] = pack_bf16x2(lo_bf16(hv[k][q]) * inv * lo_bf16(wv[q]),
-                           hi_bf16(hv[k][q]) * inv * hi_bf16(wv[q]));
+        o[q] = pack_bf16x2(lo_bf16(hv[k][q]) * inv * lo_bf16(wv[k][q]),
+                           hi_bf16(hv[k][q]) * inv * hi_bf16(wv[k][q]));
       reinterpret_cast<u32x4_t*>(out + m * N)[u] = o;
     }
   }
