@@ -170,16 +170,18 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
 // Grid (splits, nkv, B), 256 threads (4 waves).  A split block takes its
 // positions in passes of 64; wave w takes positions t0 + 16w + [0, 16) of the
 // pass t0:
-//  * scores S = Q K^T by v_mfma_f32_16x16x32_bf16: A = the KV head's REP
-//    query heads (rows >= REP zero), B = the wave's 16 K rows; lane l holds
-//    dims 32s + 8(l/16) .. +7 of position l % 16 for k-step s, 16 contiguous
-//    bytes of the cached row.  D row 4(l/16) + i, column l % 16 = score of
-//    head 4(l/16) + i at position l % 16;
-//  * an online softmax per wave over its positions: the head's max and sum
-//    over the wave's 16 positions by DPP within the 16 lanes of a D row;
-//  * P V on the vector ALU: lane l accumulates dims DPL*l .. DPL*l + DPL - 1
-//    (DPL = D / 64) of every head over the wave's 16 positions, P passing
-//    through a wave-private LDS tile (no block barrier inside the loop);
+//  * scores S^T = K Q^T by v_mfma_f32_16x16x32_bf16: A = the wave's 16 K
+//    rows (lane l holds dims 32s + 8(l/16) .. +7 of position l % 16 for
+//    k-step s, 16 contiguous bytes of the cached row), B = the KV head's REP
+//    query heads (columns >= REP zero).  Lane l gets the scores of head l % 16
+//    at positions 4(l/16) .. +3;
+//  * an online softmax per wave over its positions: a head's max and sum
+//    over the wave's 16 positions from the lane's 4 and two lane shuffles;
+//  * P V by v_mfma_f32_16x16x16_bf16: A = P in bfloat16, exactly as the
+//    scores sit in the lanes; B = V, whose rows the wave stages through a
+//    private LDS tile so that a lane can read 4 positions of one dim; the
+//    output tile t holds heads 4(l/16) .. +3 at dim 16t + l % 16 (no block
+//    barrier inside the loop);
 //  * the four waves' (max, sum, weighted values) merged through LDS at the
 //    end.
 // Scores are kept in log2 units (q.k * scale * log2 e), so every exponential
@@ -191,7 +193,7 @@ constexpr int kMaxChunk = 512;
 constexpr int kPass = 64;  // positions per pass: 16 per wave
 // Waves per SIMD (= blocks per CU: a 4-wave block puts one wave on each SIMD)
 // the split kernels are held to, by query heads per KV head.
-constexpr int kAttnWaves[9] = {0, 4, 4, 4, 4, 4, 3, 3, 3};
+constexpr int kAttnWaves[9] = {0, 4, 4, 4, 4, 4, 4, 4, 4};
 constexpr float kNoScore = -1e30f;  // running max before the first position
 
 // Shared memory of one split block.
@@ -199,8 +201,10 @@ template <int REP, int D>
 struct AttnShared {
   __align__(16) uint16_t fresh[2][D];  // the new position's K and V rows (attn_step)
   int32_t slot_of[kMaxChunk];
-  __align__(16) float p_tile[kThreads / 64][16][16];  // per wave: P[position][head]
-  __align__(16) float f_tile[kThreads / 64][16];      // per wave: the pass's rescale per head
+  // per wave: its 16 V rows of the pass, rows padded to D + 4 elements so that
+  // a column read by the 4 lane groups spreads over distinct banks
+  __align__(16) uint16_t v_tile[kThreads / 64][16][D + 4];
+  __align__(16) float f_tile[kThreads / 64][16];  // per wave: the pass's rescale per head
   float mrg_m[kThreads / 64][REP], mrg_s[kThreads / 64][REP];
   float mrg_a[kThreads / 64][REP][D];
 };
@@ -244,8 +248,8 @@ __device__ __forceinline__ void attn_load_pass(AttnPass<D>& ps, const uint16_t* 
 }
 
 // The split's partials over positions l0 + [0, n) of the KV head whose rows
-// start at kb / vb (row r at r * row_elems).  qa: this lane's A operand (query
-// head l % 16, dims 32s + 8(l/16) .. +7).  Position `fresh` of the split (or
+// start at kb / vb (row r at r * row_elems).  qa: this lane's query operand
+// (head l % 16, dims 32s + 8(l/16) .. +7).  Position `fresh` of the split (or
 // -1) takes its K / V row from sh.fresh instead of the cache.  `first` holds
 // the first pass's rows, loaded before n was known; sh.slot_of the slots of
 // positions [0, n) (read from the second pass on).  Writes pm[REP], ps[REP],
@@ -256,21 +260,15 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
                                            int64_t row_elems, float scale_log2, int fresh,
                                            const AttnPass<D>& first, float* pm, float* ps,
                                            float* pa) {
-  constexpr int DPL = D / 64, NS = D / 32, WAVES = kThreads / 64;
-  static_assert(REP <= 16 && (D == 64 || D == 128), "one MFMA row per query head");
+  constexpr int NS = D / 32, NT = D / 16, VS = D + 4, WAVES = kThreads / 64;
+  static_assert(REP <= 16 && (D == 64 || D == 128), "one MFMA column per query head");
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-  float m4[4], s4[4];  // running max / sum of heads 4g + i over the wave's positions
-  float acc[REP][DPL];
+  float m = kNoScore, s = 0.f;  // running max / sum of head c over the wave's positions
+  f32x4_t acc[NT];              // tile t: heads 4g + r at dim 16t + c
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m4[i] = kNoScore;
-    s4[i] = 0.f;
-  }
-#pragma unroll
-  for (int h = 0; h < REP; ++h)
-#pragma unroll
-    for (int t = 0; t < DPL; ++t) acc[h][t] = 0.f;
-  float* pw = &sh.p_tile[wave][0][0];
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint16_t* vt = &sh.v_tile[wave][0][0];
   float* fw = sh.f_tile[wave];
   AttnPass<D> cur = first;
   for (int t0 = 0; t0 < n; t0 += kPass) {
@@ -279,8 +277,8 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
     if (fresh >= base && fresh < base + 16) {  // uniform
       if (c == fresh - base) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
-          cur.k[s] = *reinterpret_cast<const u32x4_t*>(sh.fresh[0] + 32 * s + 8 * g);
+        for (int k = 0; k < NS; ++k)
+          cur.k[k] = *reinterpret_cast<const u32x4_t*>(sh.fresh[0] + 32 * k + 8 * g);
       }
       const uint32_t fv = D == 128 ? reinterpret_cast<const uint32_t*>(sh.fresh[1])[lane]
                                    : (uint32_t)sh.fresh[1][lane];
@@ -288,79 +286,65 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
       for (int j = 0; j < 16; ++j)
         if (base + j == fresh) cur.v[j] = fv;
     }
+    // the V rows to the wave's tile; rows past the end may hold anything: zeros
 #pragma unroll
-    for (int j = 0; j < 16; ++j)  // rows past the end may hold anything: no V from them
-      if (base + j >= n) cur.v[j] = 0u;
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t v = base + j < n ? cur.v[j] : 0u;
+      if constexpr (D == 128)
+        *reinterpret_cast<uint32_t*>(vt + j * VS + 2 * lane) = v;
+      else
+        vt[j * VS + lane] = (uint16_t)v;
+    }
 
     f32x4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[s]),
-                                                  __builtin_bit_cast(bf16x8_t, cur.k[s]), d, 0,
-                                                  0, 0);
-    const bool valid = base + c < n;
-    float pv[4], fv[4];
+    for (int k = 0; k < NS; ++k)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[k]),
+                                                  __builtin_bit_cast(bf16x8_t, qa[k]), d, 0, 0,
+                                                  0);
+    // d[r]: head c at position base + 4g + r
+    float x[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = valid ? d[i] * scale_log2 : -INFINITY;
-      const float mn = fmaxf(m4[i], dpp_group_max<16>(x));
-      fv[i] = __builtin_amdgcn_exp2f(m4[i] - mn);  // arguments <= 0: no range fix-up needed
-      pv[i] = __builtin_amdgcn_exp2f(x - mn);
-      s4[i] = fmaf(s4[i], fv[i], dpp_group_sum<16>(pv[i]));
-      m4[i] = mn;
-    }
-    *reinterpret_cast<f32x4_t*>(pw + c * 16 + 4 * g) = f32x4_t{pv[0], pv[1], pv[2], pv[3]};
-    if (c == 0) *reinterpret_cast<f32x4_t*>(fw + 4 * g) = f32x4_t{fv[0], fv[1], fv[2], fv[3]};
+    for (int r = 0; r < 4; ++r) x[r] = base + 4 * g + r < n ? d[r] * scale_log2 : -INFINITY;
+    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float f = __builtin_amdgcn_exp2f(m - mn);  // arguments <= 0: no range fix-up needed
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(x[r] - mn);
+    float psum = (p[0] + p[1]) + (p[2] + p[3]);
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    s = fmaf(s, f, psum);
+    m = mn;
+    if (g == 0) fw[c] = f;
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's tiles are written
 
-    // P rows are read kAhead positions before their use (a ring of kAhead
-    // rows in registers), so the LDS latency is paid once, not per position.
-    constexpr int kAhead = 4;
-    float pr[kAhead][REP];
+    const f32x4_t fr = *reinterpret_cast<const f32x4_t*>(fw + 4 * g);  // heads 4g + r
+    const u32x2_t pp = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    const s16x4_t pa16 = __builtin_bit_cast(s16x4_t, pp);
 #pragma unroll
-    for (int j = 0; j < kAhead; ++j)
-#pragma unroll
-      for (int h = 0; h < REP; ++h) pr[j][h] = pw[j * 16 + h];
-    float fh[REP];
-#pragma unroll
-    for (int h = 0; h < REP; ++h) fh[h] = fw[h];
-#pragma unroll
-    for (int h = 0; h < REP; ++h)
-#pragma unroll
-      for (int t = 0; t < DPL; ++t) acc[h][t] *= fh[h];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float vf[DPL];
-      vf[0] = lo_bf16(cur.v[j]);
-      if constexpr (DPL == 2) vf[1] = hi_bf16(cur.v[j]);
-      float pj[REP];
-#pragma unroll
-      for (int h = 0; h < REP; ++h) pj[h] = pr[j % kAhead][h];
-      if (j + kAhead < 16) {
-#pragma unroll
-        for (int h = 0; h < REP; ++h) pr[j % kAhead][h] = pw[(j + kAhead) * 16 + h];
-      }
-#pragma unroll
-      for (int h = 0; h < REP; ++h)
-#pragma unroll
-        for (int t = 0; t < DPL; ++t) acc[h][t] = fmaf(pj[h], vf[t], acc[h][t]);
+    for (int t = 0; t < NT; ++t) {
+      const uint16_t* col = vt + 4 * g * VS + 16 * t + c;
+      const s16x4_t vb16 = {(short)col[0], (short)col[VS], (short)col[2 * VS],
+                            (short)col[3 * VS]};
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa16, vb16, acc[t] * fr, 0, 0, 0);
     }
     __asm__ volatile("" ::: "memory");  // this pass's tile reads stay ahead of the next writes
   }
 
   // merge the waves through LDS
-  if (c == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (4 * g + i < REP) {
-        sh.mrg_m[wave][4 * g + i] = m4[i];
-        sh.mrg_s[wave][4 * g + i] = s4[i];
-      }
+  if (g == 0 && c < REP) {
+    sh.mrg_m[wave][c] = m;
+    sh.mrg_s[wave][c] = s;
   }
 #pragma unroll
-  for (int h = 0; h < REP; ++h)
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int t = 0; t < DPL; ++t) sh.mrg_a[wave][h][DPL * lane + t] = acc[h][t];
+    for (int r = 0; r < 4; ++r)
+      if (4 * g + r < REP) sh.mrg_a[wave][4 * g + r][16 * t + c] = acc[t][r];
   __syncthreads();
   for (int e = threadIdx.x; e < REP * D; e += kThreads) {
     const int r = e / D, dd = e % D;
@@ -370,9 +354,9 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
     float v = 0.f, sum = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
-      const float f = exp2f(sh.mrg_m[w][r] - mx);
-      v = fmaf(sh.mrg_a[w][r][dd], f, v);
-      sum = fmaf(sh.mrg_s[w][r], f, sum);
+      const float fw2 = exp2f(sh.mrg_m[w][r] - mx);
+      v = fmaf(sh.mrg_a[w][r][dd], fw2, v);
+      sum = fmaf(sh.mrg_s[w][r], fw2, sum);
     }
     pa[e] = v;
     if (dd == 0) {
