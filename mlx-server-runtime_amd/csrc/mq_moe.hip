@@ -33,12 +33,38 @@ namespace {
 constexpr int kMaxExperts = 512;
 constexpr int kRouteWaves = 4;
 
-// Token t's top-k by one whole wave.
+constexpr int kMaxTopK = 64;  // one output lane per pick
+
+// A routing wave's LDS: the token's gate keys, then its picks in rank order.
+struct RouteScratch {
+  uint64_t key[kMaxExperts];
+  float pick_gate[kMaxTopK];
+  int pick_id[kMaxTopK];
+};
+
+// A 64-bit key ordered as the routing order: larger gate first, then the
+// smaller expert id.  The high word is the gate's bits made monotonic as
+// unsigned (negative floats flipped, the sign bit set on the rest; -0 taken
+// as +0, which float comparison treats as equal), the low word ~id.
+__device__ __forceinline__ uint64_t route_key(float gate, int id) {
+  const uint32_t u = __float_as_uint(gate + 0.f);
+  const uint32_t m = (u >> 31) ? ~u : (u | 0x80000000u);
+  return (uint64_t)m << 32 | (uint32_t)~(uint32_t)id;
+}
+
+// Token t's top-k by one whole wave.  The picks are the experts of rank < k,
+// rank = the number of experts with a larger gate, or an equal gate and a
+// smaller id (a larger route_key): the arg-max order taken k times
+// (descending gates, ties to the lower id), found without k dependent rounds
+// of lane shuffles.  PER =
+// experts per lane (E <= 64 * PER).
+template <int PER>
 __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
                                             const float* __restrict__ expert_bias, int64_t t,
                                             int E, int k, int normalize, int32_t* indices,
-                                            uint16_t* __restrict__ scores) {
-  constexpr int PER = kMaxExperts / 64;
+                                            uint16_t* __restrict__ scores, RouteScratch& rs,
+                                            int* flat) {
+  static_assert(64 * PER <= kMaxExperts, "the LDS holds kMaxExperts gates");
   const int lane = threadIdx.x & 63;
   const uint16_t* row = logits + t * E;
   float v[PER];
@@ -65,53 +91,68 @@ __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
     const int e = lane + 64 * j;
     v[j] = e < E ? v[j] * inv + (expert_bias ? expert_bias[e] : 0.f) : -INFINITY;
   }
-  // k rounds of a wave arg-max (larger gate, then smaller id)
-  float picked = 0.f, total = 0.f;
-  int picked_id = 0;
-  for (int r = 0; r < k; ++r) {
-    float best = -INFINITY;
-    int best_id = 0x7fffffff;
+  // ranks against every gate of the token, staged in the wave's LDS as keys
+  const int EP = (E + 1) & ~1;
+  uint64_t key[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = lane + 64 * j;
-      if (v[j] > best || (v[j] == best && e < best_id)) {
-        best = v[j];
-        best_id = e;
-      }
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float ob = __shfl_xor(best, off, 64);
-      const int oi = __shfl_xor(best_id, off, 64);
-      if (ob > best || (ob == best && oi < best_id)) {
-        best = ob;
-        best_id = oi;
-      }
-    }
-    // every lane now holds the round's winner; its owner removes it
-#pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (lane + 64 * j == best_id) v[j] = -INFINITY;
-    if (lane == r) {
-      picked = best;
-      picked_id = best_id;
-    }
-    total += best;
+  for (int j = 0; j < PER; ++j) {
+    key[j] = lane + 64 * j < E ? route_key(v[j], lane + 64 * j) : 0ull;  // 0: below all
+    if (lane + 64 * j < EP) rs.key[lane + 64 * j] = key[j];
   }
+  if (lane < kMaxTopK) {
+    rs.pick_gate[lane] = -INFINITY;
+    rs.pick_id[lane] = 0x7fffffff;
+  }
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's stores are visible
+  int rank[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) rank[j] = 0;
+  for (int e0 = 0; e0 < EP; e0 += 2) {
+    const uint64_t w0 = rs.key[e0], w1 = rs.key[e0 + 1];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) rank[j] += (int)(w0 > key[j]) + (int)(w1 > key[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (lane + 64 * j < E && rank[j] < k) {
+      rs.pick_gate[rank[j]] = v[j];
+      rs.pick_id[rank[j]] = lane + 64 * j;
+    }
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   if (lane < k) {
-    float sc = picked;
+    float total = 0.f;  // in rank order, as k arg-max rounds add them
+    for (int r = 0; r < k; ++r) total += rs.pick_gate[r];
+    float sc = rs.pick_gate[lane];
     if (normalize) sc = sc / (total + 1e-20f);
-    indices[t * k + lane] = picked_id;
+    indices[t * k + lane] = rs.pick_id[lane];
+    if (flat) flat[t * k + lane] = rs.pick_id[lane];
     scores[t * k + lane] = (uint16_t)f32_to_bf16_bits(sc);
   }
+  __asm__ volatile("" ::: "memory");  // the reads above stay ahead of the next token's stores
+}
+
+__device__ __forceinline__ void route_token_any(const uint16_t* __restrict__ logits,
+                                                const float* __restrict__ expert_bias, int64_t t,
+                                                int E, int k, int normalize, int32_t* indices,
+                                                uint16_t* __restrict__ scores, RouteScratch& rs,
+                                                int* flat = nullptr) {
+  if (E <= 64)
+    route_token<1>(logits, expert_bias, t, E, k, normalize, indices, scores, rs, flat);
+  else if (E <= 128)
+    route_token<2>(logits, expert_bias, t, E, k, normalize, indices, scores, rs, flat);
+  else if (E <= 256)
+    route_token<4>(logits, expert_bias, t, E, k, normalize, indices, scores, rs, flat);
+  else
+    route_token<8>(logits, expert_bias, t, E, k, normalize, indices, scores, rs, flat);
 }
 
 __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
     const uint16_t* __restrict__ logits, const float* __restrict__ expert_bias, int64_t T, int E,
     int k, int normalize, int32_t* __restrict__ indices, uint16_t* __restrict__ scores) {
+  __shared__ RouteScratch rs[kRouteWaves];
   const int64_t t = (int64_t)blockIdx.x * kRouteWaves + (threadIdx.x >> 6);
   if (t >= T) return;  // whole waves
-  route_token(logits, expert_bias, t, E, k, normalize, indices, scores);
+  route_token_any(logits, expert_bias, t, E, k, normalize, indices, scores, rs[threadIdx.x >> 6]);
 }
 
 // ---------------------------------------------------------------- sort
@@ -143,12 +184,27 @@ __device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int
     atomicAdd(&offset[(id >= 0 && id < E) ? id : E], 1);
   }
   __syncthreads();
-  if (tid == 0) {  // exclusive scan over at most 513 buckets
-    int run = 0;
-    for (int e = 0; e < buckets; ++e) {
-      const int c = offset[e];
-      offset[e] = run;
-      run += c;
+  if (tid < 64) {  // exclusive scan over at most 513 buckets: one wave, PB per lane
+    constexpr int PB = (kMaxBuckets + 63) / 64;
+    int cnt[PB], local = 0;
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int e = tid * PB + q;
+      cnt[q] = e < buckets ? offset[e] : 0;
+      local += cnt[q];
+    }
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (tid >= off) incl += o;
+    }
+    int run = incl - local;
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int e = tid * PB + q;
+      if (e < buckets) offset[e] = run;
+      run += cnt[q];
     }
   }
   __syncthreads();
@@ -208,10 +264,36 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
     int k, int normalize, int32_t* indices, uint16_t* __restrict__ scores,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ order,
     int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
+  __shared__ RouteScratch rs[kSortWaves];
+  __shared__ int flat[64];  // the picks, for the one-wave sort
+  const int n = T * k;
   for (int t = threadIdx.x >> 6; t < T; t += kSortWaves)
-    route_token(logits, expert_bias, t, E, k, normalize, indices, scores);
+    route_token_any(logits, expert_bias, t, E, k, normalize, indices, scores,
+                    rs[threadIdx.x >> 6], n <= 64 ? flat : nullptr);
   __syncthreads();
-  sort_block(indices, T * k, k, E, sorted_ids, order, inverse, rows);
+  if (n > 64) {
+    sort_block(indices, n, k, E, sorted_ids, order, inverse, rows);
+    return;
+  }
+  // At most 64 pairs: one wave places each at its rank among the keys
+  // (bucket, index) -- the counting sort's stable order, with no histogram,
+  // scan or further barrier.
+  if (threadIdx.x < 64) {
+    const int i = threadIdx.x;
+    int id = 0, key = 0x7fffffff;
+    if (i < n) {
+      id = flat[i];
+      key = ((id >= 0 && id < E) ? id : E) << 6 | i;
+    }
+    int pos = 0;
+    for (int j = 0; j < n; ++j) pos += (int)(__builtin_amdgcn_readlane(key, j) < key);
+    if (i < n) {
+      sorted_ids[pos] = id;
+      order[pos] = i;
+      inverse[i] = pos;
+      if (rows) rows[pos] = i / k;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- combine
