@@ -132,6 +132,27 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
                   int group_size, int bits, int transpose, int sorted_indices,
                   hipStream_t stream);
 
+/*
+ * SwitchGLU's gate and up projections and silu(gate) * up for gathered
+ * (token, expert) pairs without the [T, M, 2N] intermediate
+ * (models/lfm2.py:208-214: up_proj and gate_proj, then nn.silu(gate) * up
+ * into down_proj; the two projections run as one gate|up bank): every expert's
+ * matrix is 2N rows, gate rows first (wq [E, 2N, K * bits / 32], scales and
+ * biases [E, 2N, K / group_size]); y bfloat16 [T, M, N] =
+ * mq_silu_mul(mq_gather_qmm(x, ..., N = 2N, sorted_indices = 0)), bit for bit.
+ * Arguments as mq_gather_qmm's (transpose = True).  Taken for a decode
+ * step's pairs (T * M <= 64, M <= 2, rows of at most 64 lanes: where
+ * mq_gather_qmm runs its per-pair GEMV); mq_gather_qmm_swiglu_supported says
+ * which shapes, others return MQ_ERR_UNSUPPORTED.
+ */
+int mq_gather_qmm_swiglu_supported(int64_t T, int64_t M, int64_t N, int64_t K, int group_size,
+                                   int bits);
+int mq_gather_qmm_swiglu(const mq_bf16* x, const int32_t* lhs_indices,
+                         const int32_t* rhs_indices, const uint32_t* wq, const mq_bf16* scales,
+                         const mq_bf16* biases, mq_bf16* y, int64_t T, int64_t M, int64_t N,
+                         int64_t K, int64_t E, int64_t x_batches, int group_size, int bits,
+                         hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * Decoder step around the quantized linears (models/qwen2.py:47-163).
  * KV pages are the reference's layout (cache.py:686-695): per layer,

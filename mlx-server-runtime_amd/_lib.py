@@ -49,6 +49,8 @@ EXPORTS = (
     "mq_quantized_matmul_add_rms_norm_supported",
     "mq_quantized_matmul_add_rms_norm_workspace",
     "mq_quantized_matmul_add_rms_norm",
+    "mq_gather_qmm_swiglu_supported",
+    "mq_gather_qmm_swiglu",
 )
 
 _lock = threading.Lock()
@@ -106,6 +108,9 @@ def _declare(L: ctypes.CDLL) -> None:
                                                    _int, _p, ctypes.c_size_t, _p]
     L.mq_moe_combine_rms_norm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _int, _i64,
                                           ctypes.c_float, _p]
+    L.mq_gather_qmm_swiglu_supported.argtypes = [_i64, _i64, _i64, _i64, _int, _int]
+    L.mq_gather_qmm_swiglu.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                       _i64, _int, _int, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
     L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t

@@ -379,3 +379,44 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
                                N, K, E, n_xb, group_size, bits, 1, int(bool(sorted_indices)),
                                _stream(x)), op)
     return y
+
+
+def gather_swiglu_supported(T: int, M: int, N: int, K: int, group_size: int = 64,
+                            bits: int = 4) -> bool:
+    """Whether gather_qmm_swiglu takes T (batch, expert) pairs of M rows, N outputs."""
+    return bool(_lib.lib().mq_gather_qmm_swiglu_supported(T, M, N, K, group_size, bits))
+
+
+def gather_qmm_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                      biases: torch.Tensor, lhs_indices: torch.Tensor | None,
+                      rhs_indices: torch.Tensor, group_size: int = 64,
+                      bits: int = 4) -> torch.Tensor:
+    """SwitchGLU's gate/up projections and silu(gate) * up (models/lfm2.py:208-214) for
+    gathered pairs: w [E, 2N, K*bits/32] holds every expert's gate rows, then its up
+    rows; x [n_x, M, K]; rhs_indices [T] (expert per pair), lhs_indices [T] (x batch
+    per pair, or None: pair t reads batch t).  Returns bf16 [T, M, N] =
+    silu_mul(gather_qmm(x, w, ...)), bit for bit, for the shapes
+    gather_swiglu_supported takes."""
+    op = "gather_qmm_swiglu"
+    _require_gpu(op, x=x, w=w, scales=scales, biases=biases, lhs_indices=lhs_indices,
+                 rhs_indices=rhs_indices)
+    K = _check_quantized(op, w, scales, biases, group_size, bits)
+    _check_bf16(op, "x", x)
+    if x.ndim < 2 or x.shape[-1] != K:
+        raise ValueError(f"[{op}] x must be [..., M, {K}], got {tuple(x.shape)}")
+    if w.ndim != 3 or w.shape[1] % 2:
+        raise ValueError(f"[{op}] w must be [E, 2N, K*bits/32], got {tuple(w.shape)}")
+    M, N, E = x.shape[-2], w.shape[1] // 2, w.shape[0]
+    n_xb = math.prod(x.shape[:-2])
+    rhs = rhs_indices.reshape(-1).to(torch.int32).contiguous()
+    T = rhs.numel()
+    lhs = None if lhs_indices is None else lhs_indices.reshape(-1).to(torch.int32).contiguous()
+    if lhs is not None and lhs.numel() != T:
+        raise ValueError(f"[{op}] lhs_indices and rhs_indices differ in length")
+    y = torch.empty(T, M, N, dtype=torch.bfloat16, device=x.device)
+    L = _lib.lib()
+    _lib.check(L.mq_gather_qmm_swiglu(_ptr(x.contiguous()), _ptr(lhs), _ptr(rhs),
+                                      _ptr(w.contiguous()), _ptr(scales.contiguous()),
+                                      _ptr(biases.contiguous()), _ptr(y), T, M, N, K, E, n_xb,
+                                      group_size, bits, _stream(x)), op)
+    return y

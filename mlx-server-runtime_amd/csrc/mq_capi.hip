@@ -437,6 +437,46 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
   return hip_status(e, op);
 }
 
+int mq_gather_qmm_swiglu_supported(int64_t T, int64_t M, int64_t N, int64_t K, int group_size,
+                                   int bits) {
+  if ((bits != 4 && bits != 8) || group_size != 64 || K < 1 || K % 64) return 0;
+  // Only where mq_gather_qmm itself runs the per-pair GEMV (at most 64 rows in
+  // all): more pairs go to the sorted gather GEMM, which reads each expert once.
+  if (T * M > 64) return 0;
+  return mq::gather_qmv_swiglu_fits(M, N, K, bits, T) ? 1 : 0;
+}
+
+int mq_gather_qmm_swiglu(const mq_bf16* x, const int32_t* lhs_indices,
+                         const int32_t* rhs_indices, const uint32_t* wq, const mq_bf16* scales,
+                         const mq_bf16* biases, mq_bf16* y, int64_t T, int64_t M, int64_t N,
+                         int64_t K, int64_t E, int64_t x_batches, int group_size, int bits,
+                         hipStream_t stream) {
+  const char* op = "gather_qmm_swiglu";
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "T", T)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", N)) return rc;
+  if (int rc = check_dim(op, "E", E)) return rc;
+  if (int rc = check_dim(op, "x_batches", x_batches)) return rc;
+  if (!lhs_indices && x_batches != T)
+    return fail(MQ_ERR_INVALID, "[%s] without lhs_indices x must have T=%lld batches, got %lld.",
+                op, (long long)T, (long long)x_batches);
+  if (T == 0 || M == 0 || N == 0) return ok();
+  if (!mq_gather_qmm_swiglu_supported(T, M, N, K, group_size, bits))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] T=%lld M=%lld N=%lld K=%lld is not a shape the fused kernel takes "
+                "(mq_gather_qmm_swiglu_supported).",
+                op, (long long)T, (long long)M, (long long)N, (long long)K);
+  if (E == 0) return fail(MQ_ERR_INVALID, "[%s] the expert table is empty.", op);
+  if (!x || !rhs_indices || !wq || !scales || !biases || !y)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(wq))
+    return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
+  const mq::GatherMap g{lhs_indices, rhs_indices, T, E, x_batches};
+  return hip_status(
+      mq::launch_gather_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, g, stream), op);
+}
+
 int mq_rms_norm(const mq_bf16* x, const mq_bf16* residual, mq_bf16* residual_out,
                 const mq_bf16* weight, mq_bf16* out, int64_t rows, int64_t dim, float eps,
                 hipStream_t stream) {

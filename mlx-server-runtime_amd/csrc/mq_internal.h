@@ -28,6 +28,13 @@ bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                       int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
+// Gathered SwiGLU GEMV: y [T, M, N] per (batch, expert) pair of g; every
+// expert's matrix is 2N rows (gate rows, then up rows).
+bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
+hipError_t launch_gather_qmv_swiglu(const uint16_t* x, const uint32_t* wq,
+                                    const uint16_t* scales, const uint16_t* biases, uint16_t* y,
+                                    int64_t M, int64_t N, int64_t K, int bits, const GatherMap& g,
+                                    hipStream_t stream);
 bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits);
 bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu);
 hipError_t launch_qmv_norm(const uint16_t* a, const uint16_t* res, uint16_t* res_out,

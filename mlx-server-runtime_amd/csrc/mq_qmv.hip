@@ -16,6 +16,8 @@ extern MQ_QMV_INSTANCE(4, false, 0, true);
 extern MQ_QMV_INSTANCE(8, false, 0, true);
 extern MQ_QMV_INSTANCE(4, false, 1, true);
 extern MQ_QMV_INSTANCE(8, false, 1, true);
+extern MQ_QMV_INSTANCE(4, true, 1, false);
+extern MQ_QMV_INSTANCE(8, true, 1, false);
 
 using qmv::kBlock;
 using qmv::kQmvLdsBudget;
@@ -53,6 +55,29 @@ hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16
                                              stream);
   return qmv::run_bits<8, false, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g1, none,
                                            stream);
+}
+
+// The SwiGLU GEMV per gathered (batch, expert) pair: every expert's matrix is
+// 2N rows (gate rows, then up rows).  The lanes split each row exactly as the
+// plain gathered GEMV of the 2N-row matrix does, so the results are those of
+// that GEMV followed by silu_mul, bit for bit.
+bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T) {
+  if (M < 1 || M > 2 || N < 1 || T < 1 || !qmv_fits(M, 2 * N, K, bits, T)) return false;
+  const int64_t C = K / (128 / bits);
+  return qmv::pick_tpr(C, 2 * N, T) <= 64 && 2 * N * C * 16 < (int64_t(1) << 32);
+}
+
+hipError_t launch_gather_qmv_swiglu(const uint16_t* x, const uint32_t* wq,
+                                    const uint16_t* scales, const uint16_t* biases, uint16_t* y,
+                                    int64_t M, int64_t N, int64_t K, int bits, const GatherMap& g,
+                                    hipStream_t stream) {
+  if (N == 0 || M == 0 || g.T == 0) return hipSuccess;
+  const qmv::NormIn none{};
+  if (bits == 4)
+    return qmv::run_bits<4, true, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g, none,
+                                            stream);
+  return qmv::run_bits<8, true, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g, none,
+                                          stream);
 }
 
 // RMSNorm of one row, then the GEMV (or the SwiGLU GEMV over a 2N-row

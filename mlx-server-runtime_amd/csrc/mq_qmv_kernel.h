@@ -77,7 +77,8 @@ struct NormIn {
 };
 
 // EPI 0: y[m, n] = (x W^T)[m, n] (+ bias[n]).  EPI 1 (SwiGLU, the gate and up
-// projections of a Qwen2 MLP as one matrix of 2N rows, gate rows first):
+// projections of a Qwen2 MLP as one matrix of 2N rows, gate rows first;
+// with GATHER, every expert's matrix is 2N rows):
 // y[m, n] = bf16(bf16(silu(g)) * u) with g, u the bfloat16 results of rows n
 // and N + n -- a block computes RPB/2 gate rows and the matching up rows.
 template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI, bool NORM>
@@ -97,7 +98,7 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   constexpr int RPB = SLOTS * R;       // rows per block
   constexpr int WPR = TPR > 64 ? TPR / 64 : 1;  // waves per row (TPR > 64)
   constexpr int HALF = RPB / 2;        // SwiGLU: output rows per block
-  static_assert(EPI == 0 || (!GATHER && WPR == 1 && RPB % 2 == 0), "SwiGLU epilogue layout");
+  static_assert(EPI == 0 || (WPR == 1 && RPB % 2 == 0), "SwiGLU epilogue layout");
   static_assert(!NORM || (!GATHER && MT == 1 && XU <= 4), "RMSNorm input: one row of <= 8192");
   extern __shared__ u32x4_t smem[];
   __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : EPI == 1 ? RPB * MT : 1];
@@ -122,10 +123,14 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
     if (rhs) e = rhs[t];
     y += t * (int64_t)M * N;
     if (xb < 0 || xb >= x_batches || e < 0 || e >= E) {  // index outside the tables: zeros
-      if (lane == 0)
+      if constexpr (EPI == 1) {
+        const int o = threadIdx.x % HALF, m = threadIdx.x / HALF;
+        if (m < M && rb0 + o < N) y[(int64_t)m * N + rb0 + o] = 0;
+      } else if (lane == 0) {
         for (int r = 0; r < R; ++r)
           for (int m = 0; m < M; ++m)
             if (row0 + r < N) y[(int64_t)m * N + row0 + r] = 0;
+      }
       return;
     }
   }
@@ -144,8 +149,9 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   const int span = EPI == 1 ? N + rows_here : rows_here;  // rows the descriptors cover
   auto rel = [&](int lr) { return EPI == 1 && lr >= HALF ? N - HALF + lr : lr; };
   const rsrc_t xrs = make_rsrc(x + xb * (int64_t)M * K, (uint64_t)M * K * 2);
-  const rsrc_t wrs = make_rsrc(wq + (e * (int64_t)N + rb0) * (C * 4), (uint64_t)span * C * 16);
-  const int64_t sb0 = e * (int64_t)N * G + (int64_t)rb0 * G;
+  const int64_t erows = EPI == 1 ? 2 * (int64_t)N : N;  // rows of one expert's matrix
+  const rsrc_t wrs = make_rsrc(wq + (e * erows + rb0) * (C * 4), (uint64_t)span * C * 16);
+  const int64_t sb0 = e * erows * G + (int64_t)rb0 * G;
   const rsrc_t srs = make_rsrc(scales + sb0, (uint64_t)span * G * 2);
   const rsrc_t brs = make_rsrc(biases + sb0, (uint64_t)span * G * 2);
 

@@ -157,6 +157,17 @@ class QExperts:
                                rhs_indices=rhs, transpose=True, group_size=self.group_size,
                                bits=self.bits, sorted_indices=sorted_indices)
 
+    def swiglu(self, x, lhs, rhs, sorted_indices=False):
+        """silu(gate) * up of a gate|up bank (every expert: gate rows, then up rows)
+        for the pairs (lhs, rhs): the fused kernel where it takes the shape, else
+        gather_qmm then silu_mul -- the same bits either way."""
+        T, M, K = rhs.numel(), x.shape[-2], x.shape[-1]
+        N = self.wq.shape[1] // 2
+        if core.gather_swiglu_supported(T, M, N, K, self.group_size, self.bits):
+            return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
+                                          self.group_size, self.bits)
+        return silu_mul(self(x, lhs=lhs, rhs=rhs, sorted_indices=sorted_indices))
+
 
 class MoEBlock:
     """Top-k routed SwiGLU experts (Lfm2MoE.__call__, models/lfm2.py:365-375)."""
@@ -178,16 +189,16 @@ class MoEBlock:
         if T * self.top_k >= 64:  # the reference sorts at >= 64 pairs (lfm2.py:204)
             _, sc, sorted_ids, _, inverse, rows = route_sort(
                 logits, self.top_k, self.num_experts, self.norm_topk_prob, self.expert_bias)
-            gu = self.gate_up(xb, lhs=rows, rhs=sorted_ids, sorted_indices=True)
-            y = self.down(silu_mul(gu), rhs=sorted_ids, sorted_indices=True)
+            act = self.gate_up.swiglu(xb, rows, sorted_ids, sorted_indices=True)
+            y = self.down(act, rhs=sorted_ids, sorted_indices=True)
         else:
             idx, sc = route(logits, self.top_k, self.norm_topk_prob, self.expert_bias)
             inverse = None
             rows = torch.arange(T, device=xt.device, dtype=torch.int32).repeat_interleave(
                 self.top_k)
             flat = idx.reshape(-1)
-            gu = self.gate_up(xb, lhs=rows, rhs=flat)
-            y = self.down(silu_mul(gu), rhs=flat)
+            act = self.gate_up.swiglu(xb, rows, flat)
+            y = self.down(act, rhs=flat)
         return y.reshape(T * self.top_k, H), inverse, sc
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:

@@ -153,6 +153,35 @@ def test_fused_entry_errors(moe):
                              torch.ones(8200, dtype=torch.bfloat16, device=DEV), 1e-6)
 
 
+@pytest.mark.parametrize("T,E,inter,K,bits,lhs", [(64, 128, 768, 2048, 4, True),
+                                                   (64, 128, 768, 2048, 8, True),
+                                                   (24, 16, 128, 256, 4, True),
+                                                   (5, 8, 256, 512, 4, False)])
+def test_gather_qmm_swiglu_equals_gather_then_silu_mul(moe, mq, T, E, inter, K, bits, lhs):
+    """The gathered SwiGLU GEMV (every expert: gate rows, then up rows) is bit for
+    bit gather_qmm of the 2N-row bank followed by silu_mul; out-of-range expert
+    ids give zero rows in both."""
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    dops = importlib.import_module("mlx-server-runtime_amd.decode_ops")
+    g = _gen(T * 7 + bits)
+    w = (torch.randn(E, 2 * inter, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, s, b = mq.quantize(w, 64, bits)
+    n_x = 8 if lhs else T
+    x = torch.randn(n_x, 1, K, generator=g, device=DEV).to(torch.bfloat16)
+    rhs = torch.randint(0, E, (T,), generator=g, device=DEV, dtype=torch.int32)
+    rhs[T // 2] = E + 3  # out of the table
+    rows = (torch.randint(0, n_x, (T,), generator=g, device=DEV, dtype=torch.int32)
+            if lhs else None)
+    assert core.gather_swiglu_supported(T, 1, inter, K, 64, bits)
+    out = core.gather_qmm_swiglu(x, wq, s, b, rows, rhs, 64, bits)
+    gu = core.gather_qmm(x, wq, s, b, lhs_indices=rows, rhs_indices=rhs, group_size=64,
+                         bits=bits)
+    ref = dops.silu_mul(gu.reshape(T, 2 * inter)).reshape(T, 1, inter)
+    assert out.shape == (T, 1, inter)
+    assert torch.equal(out, ref)
+    assert not out[T // 2].any()
+
+
 def _block(moe, mq, E, k, H, inter, seed=0):
     q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
     cfg = q2.Qwen2Config(H, 4 * H, 4, 2, 1, 100)

@@ -39,7 +39,8 @@ def test_header_declares_the_abi():
         "mq_quantized_matmul_swiglu", "mq_rms_norm_quantized_matmul_supported",
         "mq_rms_norm_quantized_matmul", "mq_quantized_matmul_swiglu_workspace",
         "mq_quantized_matmul_swiglu_ws", "mq_quantized_matmul_add_rms_norm_supported",
-        "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm"])
+        "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm",
+        "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -240,3 +241,25 @@ def test_python_layer_error_mapping(mq):
     with pytest.raises(RuntimeError):
         mq._lib.check(-3, "x")
     mq._lib.check(0, "x")
+
+
+def test_gather_swiglu_queries_and_validation(mq):
+    """Which gathered SwiGLU shapes the fused kernel takes, and its argument errors
+    (no GPU work: every call here returns before a launch)."""
+    L = _L(mq)
+    sup = L.mq_gather_qmm_swiglu_supported
+    assert sup(64, 1, 768, 2048, 64, 4) == 1 and sup(64, 1, 768, 2048, 64, 8) == 1
+    assert sup(64, 4, 768, 2048, 64, 4) == 0       # more than 2 rows per pair
+    assert sup(4096, 1, 768, 2048, 64, 4) == 0     # prefill: the sorted gather GEMM
+    assert sup(64, 1, 768, 2048, 32, 4) == 0       # group size
+    assert sup(64, 1, 768, 2000, 64, 4) == 0       # K not a multiple of the group
+    null = None
+    f = L.mq_gather_qmm_swiglu
+    assert f(null, null, null, null, null, null, null, 0, 1, 768, 2048, 128, 0, 64, 4, null) == 0
+    assert f(null, null, null, null, null, null, null, 64, 1, 768, 2048, 128, 64, 64, 4,
+             null) == -1                           # null pointers
+    assert b"null" in L.mq_last_error()
+    assert f(null, null, null, null, null, null, null, 64, 1, 768, 2048, 128, 8, 64, 4,
+             null) == -1                           # no lhs: x must have T batches
+    assert f(null, null, null, null, null, null, null, 64, 4, 768, 2048, 128, 64, 64, 4,
+             null) == -2                           # a shape the kernel does not take
