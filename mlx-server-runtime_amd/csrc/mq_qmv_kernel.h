@@ -44,9 +44,9 @@ constexpr int kQmvLdsBudget = 48 * 1024;
 // Two rows per lane group may use up to 52 KiB: still 3 blocks per CU.
 constexpr int kTwoRowLdsBudget = 52 * 1024;
 // Scale + bias DMA operations per wave: 2 arrays of ceil((RPB*G + GP) / 2)
-// words, at most 16 64-word operations each (RPB*G <= 2048 entries: a block
-// owns at most 256 * 8 chunks), over 4 waves.
-constexpr int kSbOpsPerWave = 8;
+// words in 64-word operations, over 4 waves (an instance issues the most it
+// can need, capped here; four rows per lane group at K = 18944 need 11).
+constexpr int kSbOpsPerWave = 12;
 // Weight chunks a lane keeps in flight ahead of the one it contracts, per
 // row count R (measured on the 4-bit K=3584 and K=18944 GEMVs: 2 for one
 // row per lane group, 3 for two).
@@ -516,17 +516,20 @@ inline int pick_tpr(int64_t C, int64_t N, int64_t T) {
   return kTprs[pick];
 }
 
-// R = 2 needs its scales to fit the block's LDS DMA budget (RPB * G + GP
-// entries per array, kSbOpsPerWave operations per wave) and the LDS budget.
-inline bool two_rows(int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t T) {
+// R rows per lane group needs the scales to fit the block's LDS DMA budget
+// (RPB * G + GP entries per array, kSbOpsPerWave operations per wave), the
+// LDS budget, and at least min_blocks blocks.
+inline bool rows_fit(int R, int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t T,
+                     int64_t min_blocks) {
   const int epc = 128 / bits;
   const int64_t C = K / epc, G = K / kGroup;
   const int64_t CP = (C + tpr - 1) / tpr * tpr, GP = CP / (kGroup / epc);
-  const int64_t rpb = (kBlock / tpr) * 2;
+  const int64_t rpb = (kBlock / tpr) * R;
   const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const int64_t sb_words = (rpb * G + GP + 1) / 2;
   return 2 * ((sb_words + 63) / 64) <= kSbOpsPerWave * (kBlock / 64) &&
-         lds_bytes(bits, tpr, mt, K, 2) <= kTwoRowLdsBudget && (N + rpb - 1) / rpb * T >= 512;
+         lds_bytes(bits, tpr, mt, K, R) <= kTwoRowLdsBudget &&
+         (N + rpb - 1) / rpb * T >= min_blocks;
 }
 
 // Launches the GEMV for one code width; GATHER selects the kernels that
@@ -567,10 +570,13 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
         return hipErrorInvalidValue;  // SwiGLU: one wave per row at most
       } else {
         if (tpr == 128) {
-          // Two rows per lane group when that still leaves 512 blocks: a block
-          // stages all of x (long rows: up to 40 KB), so rows per block divide
-          // that L2 traffic (the down projection: 2.1x less x than weights).
-          if (slots <= 5 && two_rows(BITS, 128, M, N, K, g.T))
+          // More rows per lane group while the blocks still fill the GPU: a
+          // block stages all of x (long rows: up to 40 KB), so rows per block
+          // divide that L2 traffic, and fewer blocks fit one round of
+          // residency (3 per CU at this LDS size).
+          if (slots <= 5 && M == 1 && rows_fit(4, BITS, 128, M, N, K, g.T, 256))
+            return run_mt<BITS, 128, 4, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+          if (slots <= 5 && rows_fit(2, BITS, 128, M, N, K, g.T, 512))
             return run_mt<BITS, 128, 2, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
           if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
           return run_mt<BITS, 128, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
