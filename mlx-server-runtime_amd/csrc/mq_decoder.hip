@@ -188,7 +188,8 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
 // is exp2.
 //
 // Partials per (b, kv head, split), float32: m[REP], s[REP], acc[REP][D];
-// splits past the sequence's end are neither written nor read.
+// splits past the sequence's end are neither written nor read.  A grid of
+// one split per sequence writes the normalised output itself (no combine).
 constexpr int kMaxChunk = 512;
 constexpr int kPass = 64;  // positions per pass: 16 per wave
 // Waves per SIMD (= blocks per CU: a 4-wave block puts one wave on each SIMD)
@@ -253,13 +254,14 @@ __device__ __forceinline__ void attn_load_pass(AttnPass<D>& ps, const uint16_t* 
 // -1) takes its K / V row from sh.fresh instead of the cache.  `first` holds
 // the first pass's rows, loaded before n was known; sh.slot_of the slots of
 // positions [0, n) (read from the second pass on).  Writes pm[REP], ps[REP],
-// pa[REP][D].
+// pa[REP][D] -- or, with `direct` (the sequence's only split), its REP heads'
+// output rows bf16(pa / ps), which is what the combine makes of one split.
 template <int REP, int D>
 __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShared<REP, D>& sh,
                                            int n, const uint16_t* kb, const uint16_t* vb,
                                            int64_t row_elems, float scale_log2, int fresh,
                                            const AttnPass<D>& first, float* pm, float* ps,
-                                           float* pa) {
+                                           float* pa, uint16_t* direct) {
   constexpr int NS = D / 32, NT = D / 16, VS = D + 4, WAVES = kThreads / 64;
   static_assert(REP <= 16 && (D == 64 || D == 128), "one MFMA column per query head");
   typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -358,10 +360,14 @@ __device__ __forceinline__ void attn_block(const u32x4_t (&qa)[D / 32], AttnShar
       v = fmaf(sh.mrg_a[w][r][dd], fw2, v);
       sum = fmaf(sh.mrg_s[w][r], fw2, sum);
     }
-    pa[e] = v;
-    if (dd == 0) {
-      pm[r] = mx;
-      ps[r] = sum;
+    if (direct) {  // uniform
+      direct[e] = (uint16_t)f32_to_bf16_bits(v / sum);
+    } else {
+      pa[e] = v;
+      if (dd == 0) {
+        pm[r] = mx;
+        ps[r] = sum;
+      }
     }
   }
 }
@@ -426,7 +432,8 @@ template <int REP, int D>
 __global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_split_kernel(
     const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages, const int32_t* page_table,
     int pages_per_seq, int page_size, int num_pages, const int64_t* pos,
-    float* __restrict__ part, int nkv, int chunk, float scale_log2) {
+    float* __restrict__ part, uint16_t* __restrict__ out, int nkv, int chunk,
+    float scale_log2) {
   __shared__ AttnShared<REP, D> sh;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int64_t b = blockIdx.z;
@@ -448,7 +455,8 @@ __global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_split_kernel(
   pf.store_slots(sh.slot_of, n);
   __syncthreads();
   attn_block<REP, D>(qa, sh, n, k_pages + kvh * D, v_pages + kvh * D, (int64_t)nkv * D,
-                     scale_log2, -1, pf.first, pm, pm + REP, pm + 2 * REP);
+                     scale_log2, -1, pf.first, pm, pm + REP, pm + 2 * REP,
+                     splits == 1 ? out + (b * nh + kvh * REP) * (int64_t)D : nullptr);
 }
 
 // The split kernel of one decode step of a layer's attention, straight from
@@ -465,7 +473,7 @@ __global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_step_kernel(
     int pages_per_seq, int page_size, int num_pages, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, float eps, uint16_t* k_pages, uint16_t* v_pages,
-    float* __restrict__ part, int nkv, int chunk, float scale_log2) {
+    float* __restrict__ part, uint16_t* __restrict__ out, int nkv, int chunk, float scale_log2) {
   constexpr int LANES = D / 8, HALF = D / 2, WAVES = kThreads / 64;
   static_assert(HALF <= 64, "one rotated pair per lane");
   __shared__ AttnShared<REP, D> sh;
@@ -526,7 +534,8 @@ __global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_step_kernel(
   attn_load_q<REP, D>(qa, &qs[0][0], D);
   float* pm = part + ((b * nkv + kvh) * splits + split) * (int64_t)(REP * (D + 2));
   attn_block<REP, D>(qa, sh, n, k_pages + kvh * D, v_pages + kvh * D, row_elems, scale_log2,
-                     owner ? p - l0 : -1, pf.first, pm, pm + REP, pm + 2 * REP);
+                     owner ? p - l0 : -1, pf.first, pm, pm + REP, pm + 2 * REP,
+                     splits == 1 ? out + (b * nh + kvh * REP) * (int64_t)D : nullptr);
 }
 
 // Grid (nh, B), D threads: out bf16 [B, nh * D] = sum over the sequence's
@@ -676,9 +685,10 @@ hipError_t launch_attention_d(const uint16_t* q, const uint16_t* k_pages, const 
   case REP:                                                                                     \
     hipLaunchKernelGGL((attn_split_kernel<REP, D>), grid, dim3(kThreads), 0, stream, q,        \
                        k_pages, v_pages, page_table, pages_per_seq, page_size, num_pages, pos,  \
-                       workspace, nkv, chunk, scale_log2);                                      \
-    hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,    \
-                       pos, pages_per_seq, page_size, out, nkv, splits, chunk);                 \
+                       workspace, out, nkv, chunk, scale_log2);                                 \
+    if (splits > 1) /* one split writes the output itself */                                   \
+      hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,  \
+                         pos, pages_per_seq, page_size, out, nkv, splits, chunk);               \
     break;
   switch (nh / nkv) {
     MQ_ATTN(1)
@@ -733,9 +743,10 @@ hipError_t launch_step_d(const uint16_t* qkv, const int64_t* pos, const int32_t*
   case REP:                                                                                     \
     hipLaunchKernelGGL((attn_step_kernel<REP, D>), grid, dim3(kThreads), 0, stream, qkv, pos,  \
                        page_table, pages_per_seq, page_size, num_pages, cos_t, sin_t, q_norm,  \
-                       k_norm, eps, k_pages, v_pages, workspace, nkv, chunk, scale_log2);      \
-    hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,    \
-                       pos, pages_per_seq, page_size, out, nkv, splits, chunk);                 \
+                       k_norm, eps, k_pages, v_pages, workspace, out, nkv, chunk, scale_log2); \
+    if (splits > 1) /* one split writes the output itself */                                   \
+      hipLaunchKernelGGL((attn_combine_kernel<REP, D>), cgrid, dim3(D), 0, stream, workspace,  \
+                         pos, pages_per_seq, page_size, out, nkv, splits, chunk);               \
     break;
   switch (nh / nkv) {
     MQ_STEP(1)

@@ -261,6 +261,7 @@ def _attention_ref(q, cache, layer, pos, scale):
     (2, 32, 4, 7, [100, 111]),                 # 8 query heads per KV head
     (2, 12, 4, 3, [47, 16]),                   # 3 per KV head
     (32, 28, 4, 80, None),                     # batch 32 decode at ~1.2K context
+    (20, 16, 4, 3, [47, 0, 30] * 6 + [1, 2]),  # many pairs, short rows: one 4-wave split
 ])
 def test_paged_decode_attention(ops, B, nh, nkv, per, positions, d):
     ps = 16
