@@ -616,8 +616,9 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* __re
 // once.
 int attn_blocks_per_cu(int rep) { return kAttnWaves[rep < 1 ? 1 : rep > 8 ? 8 : rep]; }
 
-// Positions per split: whole passes (kPass positions), at most kMaxChunk, and as many splits as keep every CU busy in one round of
-// blocks (a split is latency-bound, so a second round costs a full split).
+// Positions per split: whole passes (kPass positions), at most kMaxChunk,
+// and as many splits as keep every CU busy in one round of blocks (a split is
+// latency-bound, so a second round costs a full split).
 int attn_chunk(int64_t B, int nkv, int rep, int d, int64_t capacity) {
   const int64_t pass = kPass;
   const int64_t blocks = B * nkv;
