@@ -179,6 +179,7 @@ int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
   if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
   if (use_skinny(M, 2 * N, K, bits) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
+  if (use_skinny(M, 2 * N, K, bits) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
   return 0;
 }
 
@@ -224,6 +225,9 @@ int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq
     return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
   if (route == 1)
     return hip_status(mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+  if (route == 3)
+    return hip_status(
+        mq::launch_qmms_swiglu_direct(x, wq, scales, biases, y, M, N, K, bits, stream), op);
   const size_t need = mq::qmms_workspace_bytes(M, 2 * N, K, bits);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return fail(MQ_ERR_INVALID,

@@ -83,6 +83,13 @@ size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits);
 // Split plans of the skinny GEMM whose reduce can take an epilogue: SwiGLU of
 // a [2 Nout, K] gate|up matrix, or + residual and RMSNorm (N <= 8192).
 bool qmms_split_fusable(int64_t M, int64_t N, int64_t K, int bits);
+// The skinny GEMM's unsplit one-tile plan for a 2*Nout-row gate|up matrix,
+// with silu(gate) * up in its epilogue.
+bool qmms_swiglu_direct(int64_t M, int64_t Nout, int64_t K, int bits);
+hipError_t launch_qmms_swiglu_direct(const uint16_t* x, const uint32_t* wq,
+                                     const uint16_t* scales, const uint16_t* biases, uint16_t* y,
+                                     int64_t M, int64_t Nout, int64_t K, int bits,
+                                     hipStream_t stream);
 hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t M, int64_t Nout,
                               int64_t K, int bits, void* workspace, size_t workspace_bytes,

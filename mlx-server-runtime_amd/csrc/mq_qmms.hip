@@ -80,10 +80,15 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, 
   return __builtin_bit_cast(bf16x8_t, o);
 }
 
-template <int BITS, int MI, bool PARTIAL>
+// EPI 1 (SwiGLU; one 32-row tile, no split): the matrix is N = 2*Nout rows,
+// gate rows first; a block takes gate columns n0 .. n0+63 (waves 0, 1) and
+// the matching up columns Nout + n0 .. (waves 2, 3), and stores
+// y[m, n] = bf16(bf16(silu(g)) * u) with g, u rounded to bfloat16 as the
+// plain kernel stores them -- silu_mul of its output, bit for bit.
 // x, wq, scales and biases are deliberately not __restrict__: with it the
 // compiler may move their loads across the barriers' inline asm, and the
 // barriers' counts assume the issue order below.
+template <int BITS, int MI, bool PARTIAL, int EPI = 0>
 __global__ __launch_bounds__(kThreads) void qmms_kernel(
     const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
@@ -92,6 +97,7 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
   constexpr int kXStage = BM * BK * 2;
   constexpr int CB = BITS * 4;           // code bytes per lane per step
   constexpr int NC = BITS == 4 ? 1 : 2;  // 16-byte code loads per lane per step
+  static_assert(EPI == 0 || (MI == 1 && !PARTIAL), "SwiGLU epilogue: one tile, no split");
   extern __shared__ u32x4_t smem[];
   char* const lds = reinterpret_cast<char*>(smem);
   const int l = threadIdx.x & 63;
@@ -103,7 +109,8 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
   blk /= tiles_n;
   const int tm = blk % tiles_m;
   const int split = blk / tiles_m;
-  const int n0 = tn * BN, m0 = tm * BM;
+  const int Nout = N / 2;  // EPI 1: output columns
+  const int n0 = tn * (EPI == 1 ? BN / 2 : BN), m0 = tm * BM;
   const int KT = K / BK;
   const int G = K / kGroup;
   const int c_begin = split * chunks_per_split;
@@ -124,7 +131,8 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
     xoff[i] = (uint32_t)((m0 + row) * K + (((l & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
   }
   // This lane's column; columns past N lie beyond the descriptors (zeros).
-  const int n = n0 + wave * 32 + (l & 31);
+  const int n = EPI == 1 ? (wave < 2 ? 0 : Nout) + n0 + (wave & 1) * 32 + (l & 31)
+                         : n0 + wave * 32 + (l & 31);
   const uint32_t coff = (uint32_t)n * (uint32_t)(K * BITS / 8) + h * CB;
   const uint32_t soff = (uint32_t)n * (uint32_t)G * 2;
   // A fragment: row 32i + l % 32, logical chunk 4h + ks at (4h + ks) ^ f(row).
@@ -208,6 +216,30 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: D[m][n], lane holds column l % 32, rows 8(v/4) + 4(l/32) + v%4 ----
+  if constexpr (EPI == 1) {
+    // up waves hand their bf16-rounded values to the gate waves through the
+    // (now idle) x stages: [32 rows][64 columns] floats
+    float* up = reinterpret_cast<float*>(lds);
+    __syncthreads();  // every wave is done with the x stages
+    const int cl = (wave & 1) * 32 + (l & 31);
+    if (wave >= 2) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        up[(8 * (v >> 2) + 4 * (l >> 5) + (v & 3)) * 64 + cl] =
+            bf16_bits_to_f32(f32_to_bf16_bits(acc[0][v]));
+    }
+    __syncthreads();
+    if (wave < 2 && n0 + cl < Nout) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
+        if (m0 + r < M)
+          y[(int64_t)(m0 + r) * Nout + n0 + cl] = silu_mul_bf16(
+              bf16_bits_to_f32(f32_to_bf16_bits(acc[0][v])), up[r * 64 + cl]);
+      }
+    }
+    return;
+  }
   if (n >= N) return;
   const float add = (!PARTIAL && bias) ? bf16_bits_to_f32(bias[n]) : 0.f;
 #pragma unroll
@@ -380,7 +412,10 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   // Blocks wanted: 4 per CU (256 CUs) for one 32-row M tile, fewer for
   // taller tiles, which carry more work per step.
   const int64_t want = 1024 / p.mi;
-  if (can_split && base < want) {
+  // 32-row tiles that already give a block per CU run unsplit: measured at
+  // M = 32 on the 37888-row gate|up matrix (296 tiles), one pass over K
+  // beats three splits plus their reduce.
+  if (can_split && base < want && !(p.mi == 1 && base >= 256)) {
     // The partial sums (written once, read once) stay under an eighth of the
     // weight bytes, or 4 MiB, which stays in the Infinity Cache: small
     // matrices (a layer's q/k/v or o at M = 32) then get short blocks, whose
@@ -395,13 +430,14 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   return p;
 }
 
-template <int BITS, int MI, bool PARTIAL>
+template <int BITS, int MI, bool PARTIAL, int EPI = 0>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
   const int lds = kStages * 32 * MI * BK * 2;
-  hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL>), grid, dim3(kThreads), lds, stream, x, wq,
+  hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL, EPI>), grid, dim3(kThreads), lds, stream, x,
+                     wq,
                      scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
                      p.tiles_m, p.chunks_per_split);
   return hipGetLastError();
@@ -442,6 +478,29 @@ size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits) {
 // The fused reduces need the split plan (the kernels' partial sums).
 bool qmms_split_fusable(int64_t M, int64_t N, int64_t K, int bits) {
   return qmms_fits(M, N, K, bits) && plan(M, N, K, bits, true).splits > 1;
+}
+
+// The unsplit one-tile plan of the 2*Nout-row matrix: the SwiGLU in the
+// GEMM's own epilogue (no workspace, no reduce).
+bool qmms_swiglu_direct(int64_t M, int64_t Nout, int64_t K, int bits) {
+  if (!qmms_fits(M, 2 * Nout, K, bits)) return false;
+  const Plan p = plan(M, 2 * Nout, K, bits, true);
+  return p.splits == 1 && p.mi == 1 && p.tiles_m == 1;
+}
+
+hipError_t launch_qmms_swiglu_direct(const uint16_t* x, const uint32_t* wq,
+                                     const uint16_t* scales, const uint16_t* biases, uint16_t* y,
+                                     int64_t M, int64_t Nout, int64_t K, int bits,
+                                     hipStream_t stream) {
+  if (M == 0 || Nout == 0) return hipSuccess;
+  Plan p = plan(M, 2 * Nout, K, bits, true);
+  if (p.splits != 1 || p.mi != 1 || p.tiles_m != 1) return hipErrorInvalidValue;
+  p.tiles_n = (int)((Nout + BN / 2 - 1) / (BN / 2));  // 64 gate + 64 up columns per block
+  return bits == 4
+             ? run<4, 1, false, 1>(x, wq, scales, biases, nullptr, y, nullptr, M, 2 * Nout, K, p,
+                                   stream)
+             : run<8, 1, false, 1>(x, wq, scales, biases, nullptr, y, nullptr, M, 2 * Nout, K, p,
+                                   stream);
 }
 
 hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

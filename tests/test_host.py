@@ -139,10 +139,14 @@ def test_decoder_entry_validation(mq):
     assert sw(null, null, null, null, null, 4, 18944, 3584, 64, 4, null) == -2   # not fused
     assert sw(null, null, null, null, null, 1, 18944, 3584, 64, 4, null) == -1   # null pointers
     assert sw(null, null, null, null, null, 0, 18944, 3584, 64, 4, null) == 0
-    # batch-32 decode shapes: the skinny GEMM's split-K plans take the fused reduces
+    # batch-32 gate|up: the skinny GEMM runs unsplit with SiLU * up in its epilogue
     assert sup(32, 18944, 3584, 64, 4) == 1
-    assert L.mq_quantized_matmul_swiglu_workspace(32, 18944, 3584, 64, 4) == \
-        L.mq_quantized_matmul_workspace(32, 2 * 18944, 3584, 64, 4) > 0
+    assert L.mq_quantized_matmul_swiglu_workspace(32, 18944, 3584, 64, 4) == 0
+    assert L.mq_quantized_matmul_workspace(32, 2 * 18944, 3584, 64, 4) == 0
+    # batch 16, fewer columns: the split-K plan with the fused reduce
+    assert sup(16, 9475, 3584, 64, 4) == 1
+    assert L.mq_quantized_matmul_swiglu_workspace(16, 9475, 3584, 64, 4) == \
+        L.mq_quantized_matmul_workspace(16, 2 * 9475, 3584, 64, 4) > 0
     assert L.mq_quantized_matmul_swiglu_workspace(1, 18944, 3584, 64, 4) == 0  # the GEMV path
     assert sw(null, null, null, null, null, 32, 18944, 3584, 64, 4, null) == -1  # null pointers
     an = L.mq_quantized_matmul_add_rms_norm_supported
