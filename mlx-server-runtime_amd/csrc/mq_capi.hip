@@ -173,7 +173,8 @@ namespace {
 // How mq_quantized_matmul_swiglu runs a shape: 1 the dot2 GEMV with the SwiGLU
 // epilogue (where mq_quantized_matmul itself runs that GEMV on the 2N rows),
 // 2 the skinny GEMM's K splits with a SwiGLU reduce (where mq_quantized_matmul
-// with its workspace splits K), 0 not fused.
+// with its workspace splits K), 3 the unsplit one-tile skinny GEMM with the
+// SwiGLU in its epilogue, 0 not fused.
 int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;

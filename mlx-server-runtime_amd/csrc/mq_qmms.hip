@@ -409,20 +409,22 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   const int chunks = (int)(K / (BK * kChunk));
   const int64_t base = (int64_t)p.tiles_n * p.tiles_m;
   int64_t splits = 1;
-  // Blocks wanted: 4 per CU (256 CUs) for one 32-row M tile, fewer for
-  // taller tiles, which carry more work per step.
-  const int64_t want = 1024 / p.mi;
-  // 32-row tiles that already give a block per CU run unsplit: measured at
-  // M = 32 on the 37888-row gate|up matrix (296 tiles), one pass over K
-  // beats three splits plus their reduce.
-  if (can_split && base < want && !(p.mi == 1 && base >= 256)) {
+  // Blocks wanted: for 32-row tiles at most one per CU (256 CUs), the
+  // splits rounded down; for taller tiles, which carry more work per step,
+  // 512 / 256 blocks, rounded up. Measured at M = 16..32: the down
+  // projection 3584 x 18944 at 8 splits (224 blocks) takes 20 us where 13
+  // splits (364 blocks, two on some CUs) take 23 us, and 28672 x 4096 runs
+  // unsplit (224 tiles) in 24 us against 34 us in 5 splits.
+  const int64_t want = p.mi == 1 ? 256 : 1024 / p.mi;
+  if (can_split && base < want) {
     // The partial sums (written once, read once) stay under an eighth of the
     // weight bytes, or 4 MiB, which stays in the Infinity Cache: small
     // matrices (a layer's q/k/v or o at M = 32) then get short blocks, whose
     // serial step latency otherwise sets the kernel time.
     const int64_t weight_bytes = N * K * bits / 8;
     const int64_t cap = std::max<int64_t>(weight_bytes / (16 * M * N), (4 << 20) / (4 * M * N));
-    splits = std::min<int64_t>({(want + base - 1) / base, chunks, cap});
+    const int64_t per_tile = p.mi == 1 ? want / base : (want + base - 1) / base;
+    splits = std::min<int64_t>({per_tile, chunks, cap});
   }
   if (splits < 1) splits = 1;
   p.chunks_per_split = (int)((chunks + splits - 1) / splits);

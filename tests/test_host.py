@@ -143,10 +143,14 @@ def test_decoder_entry_validation(mq):
     assert sup(32, 18944, 3584, 64, 4) == 1
     assert L.mq_quantized_matmul_swiglu_workspace(32, 18944, 3584, 64, 4) == 0
     assert L.mq_quantized_matmul_workspace(32, 2 * 18944, 3584, 64, 4) == 0
-    # batch 16, fewer columns: the split-K plan with the fused reduce
+    # 2 * 9475 rows are 149 column tiles, under one block per CU, yet no
+    # second split fits: unsplit, with the epilogue
     assert sup(16, 9475, 3584, 64, 4) == 1
-    assert L.mq_quantized_matmul_swiglu_workspace(16, 9475, 3584, 64, 4) == \
-        L.mq_quantized_matmul_workspace(16, 2 * 9475, 3584, 64, 4) > 0
+    assert L.mq_quantized_matmul_swiglu_workspace(16, 9475, 3584, 64, 4) == 0
+    # batch 16, 2 * 4739 rows (75 tiles): three K splits with the fused reduce
+    assert sup(16, 4739, 3584, 64, 4) == 1
+    assert L.mq_quantized_matmul_swiglu_workspace(16, 4739, 3584, 64, 4) == \
+        L.mq_quantized_matmul_workspace(16, 2 * 4739, 3584, 64, 4) == 3 * 16 * 2 * 4739 * 4
     assert L.mq_quantized_matmul_swiglu_workspace(1, 18944, 3584, 64, 4) == 0  # the GEMV path
     assert sw(null, null, null, null, null, 32, 18944, 3584, 64, 4, null) == -1  # null pointers
     an = L.mq_quantized_matmul_add_rms_norm_supported
