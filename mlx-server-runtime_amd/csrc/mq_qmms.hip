@@ -7,9 +7,9 @@
 //
 // Every weight is read from HBM and dequantized exactly once per M tile, so
 // for M <= 128 the kernel streams the codes like a GEMV while the matrix
-// cores do the arithmetic.  A 256-thread block owns 128 columns (32 per
-// wave) and an M tile of 32*MI rows (MI = 1, 2, 4), and walks K in steps of
-// one quantization group:
+// cores do the arithmetic.  A block of 4 waves owns 128 columns (32 per
+// wave; unsplit 32-row plans may take 5, 6 or 8 waves) and an M tile of
+// 32*MI rows (MI = 1, 2, 4), and walks K in steps of one quantization group:
 // * x tiles (32*MI rows x 64) are copied HBM -> LDS by buffer_load_dwordx4
 //   ... lds three steps ahead into four stages, rows of 128 bytes with the
 //   16-byte chunk index XOR-ed with (row >> 1) & 7.
@@ -34,8 +34,7 @@
 namespace mq {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int BN = 128;
+constexpr int BN = 128;  // columns of a 4-wave block
 constexpr int BK = 64;
 constexpr int kChunk = 8;     // groups per scale/bias load
 constexpr int kPrefetch = 4;  // steps of codes in flight per lane (divides kChunk)
@@ -80,16 +79,20 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, 
   return __builtin_bit_cast(bf16x8_t, o);
 }
 
+// W waves per block (4, or 5, 6, 8 for unsplit 32-row tiles: the block count
+// then stays within one per CU); waves 0-3 copy the x tiles.
 // EPI 1 (SwiGLU; one 32-row tile, no split): the matrix is N = 2*Nout rows,
-// gate rows first; a block takes gate columns n0 .. n0+63 (waves 0, 1) and
-// the matching up columns Nout + n0 .. (waves 2, 3), and stores
-// y[m, n] = bf16(bf16(silu(g)) * u) with g, u rounded to bfloat16 as the
-// plain kernel stores them -- silu_mul of its output, bit for bit.
+// gate rows first; wave w of a block takes gate columns n0 + 16w .. +15 in
+// lanes l % 32 < 16 and the matching up columns Nout + n0 + 16w .. in lanes
+// l % 32 >= 16, and its gate lanes store y[m, n] = bf16(bf16(silu(g)) * u)
+// with g, u rounded to bfloat16 as the plain kernel stores them -- silu_mul
+// of its output, bit for bit (each column's MFMA sums do not depend on the
+// lane that holds it).
 // x, wq, scales and biases are deliberately not __restrict__: with it the
 // compiler may move their loads across the barriers' inline asm, and the
 // barriers' counts assume the issue order below.
-template <int BITS, int MI, bool PARTIAL, int EPI = 0>
-__global__ __launch_bounds__(kThreads) void qmms_kernel(
+template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4>
+__global__ __launch_bounds__(64 * W) void qmms_kernel(
     const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
     int M, int N, int K, int tiles_n, int tiles_m, int chunks_per_split) {
@@ -98,6 +101,7 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
   constexpr int CB = BITS * 4;           // code bytes per lane per step
   constexpr int NC = BITS == 4 ? 1 : 2;  // 16-byte code loads per lane per step
   static_assert(EPI == 0 || (MI == 1 && !PARTIAL), "SwiGLU epilogue: one tile, no split");
+  static_assert(W == 4 || (MI == 1 && !PARTIAL), "wider blocks: one tile, no split");
   extern __shared__ u32x4_t smem[];
   char* const lds = reinterpret_cast<char*>(smem);
   const int l = threadIdx.x & 63;
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
   const int tm = blk % tiles_m;
   const int split = blk / tiles_m;
   const int Nout = N / 2;  // EPI 1: output columns
-  const int n0 = tn * (EPI == 1 ? BN / 2 : BN), m0 = tm * BM;
+  const int n0 = tn * (EPI == 1 ? 16 * W : 32 * W), m0 = tm * BM;
   const int KT = K / BK;
   const int G = K / kGroup;
   const int c_begin = split * chunks_per_split;
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
     xoff[i] = (uint32_t)((m0 + row) * K + (((l & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
   }
   // This lane's column; columns past N lie beyond the descriptors (zeros).
-  const int n = EPI == 1 ? (wave < 2 ? 0 : Nout) + n0 + (wave & 1) * 32 + (l & 31)
+  const int n = EPI == 1 ? ((l & 16) ? Nout : 0) + n0 + wave * 16 + (l & 15)
                          : n0 + wave * 32 + (l & 31);
   const uint32_t coff = (uint32_t)n * (uint32_t)(K * BITS / 8) + h * CB;
   const uint32_t soff = (uint32_t)n * (uint32_t)G * 2;
@@ -139,6 +143,7 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
   const uint32_t aoff = (uint32_t)((l & 31) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
 
   auto dma_x = [&](int kt, int stage) {
+    if (W > 4 && wave >= 4) return;  // uniform
 #pragma unroll
     for (int i = 0; i < MI; ++i)
       dma16(xrs, (lds_t*)(lds + stage * kXStage + (i * 4 + wave) * 1024), xoff[i] + kt * (BK * 2));
@@ -217,26 +222,15 @@ __global__ __launch_bounds__(kThreads) void qmms_kernel(
 
   // ---- epilogue: D[m][n], lane holds column l % 32, rows 8(v/4) + 4(l/32) + v%4 ----
   if constexpr (EPI == 1) {
-    // up waves hand their bf16-rounded values to the gate waves through the
-    // (now idle) x stages: [32 rows][64 columns] floats
-    float* up = reinterpret_cast<float*>(lds);
-    __syncthreads();  // every wave is done with the x stages
-    const int cl = (wave & 1) * 32 + (l & 31);
-    if (wave >= 2) {
+    // lane l ^ 16 holds the up column of gate lane l (same rows)
+    const int cl = n0 + wave * 16 + (l & 15);
 #pragma unroll
-      for (int v = 0; v < 16; ++v)
-        up[(8 * (v >> 2) + 4 * (l >> 5) + (v & 3)) * 64 + cl] =
-            bf16_bits_to_f32(f32_to_bf16_bits(acc[0][v]));
-    }
-    __syncthreads();
-    if (wave < 2 && n0 + cl < Nout) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
-        if (m0 + r < M)
-          y[(int64_t)(m0 + r) * Nout + n0 + cl] = silu_mul_bf16(
-              bf16_bits_to_f32(f32_to_bf16_bits(acc[0][v])), up[r * 64 + cl]);
-      }
+    for (int v = 0; v < 16; ++v) {
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][v]));
+      const float u = __shfl_xor(g, 16, 64);
+      const int r = 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
+      if (!(l & 16) && cl < Nout && m0 + r < M)
+        y[(int64_t)(m0 + r) * Nout + cl] = silu_mul_bf16(g, u);
     }
     return;
   }
@@ -398,7 +392,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_add_norm(
 }
 
 struct Plan {
-  int mi, tiles_n, tiles_m, splits, chunks_per_split;
+  int mi, waves, tiles_n, tiles_m, splits, chunks_per_split;
 };
 
 Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
@@ -429,26 +423,56 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   if (splits < 1) splits = 1;
   p.chunks_per_split = (int)((chunks + splits - 1) / splits);
   p.splits = (chunks + p.chunks_per_split - 1) / p.chunks_per_split;
+  // Unsplit 32-row plans with more tiles than CUs take wider blocks (5, 6 or
+  // 8 waves of 32 columns) where that brings them within one per CU: at
+  // M = 32 the 37888-row gate|up matrix in 296 blocks of 128 columns takes
+  // 36.9 us, as 40 CUs run two blocks, where 32768 rows in 256 blocks take
+  // 22.2 us.
+  p.waves = 4;
+  if (p.mi == 1 && p.splits == 1 && base > 256) {
+    for (const int w : {5, 6, 8}) {
+      const int t = (int)((N + 32 * w - 1) / (32 * w));
+      if (t <= 256) {
+        p.waves = w;
+        p.tiles_n = t;
+        break;
+      }
+    }
+  }
   return p;
 }
 
-template <int BITS, int MI, bool PARTIAL, int EPI = 0>
+template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
   const int lds = kStages * 32 * MI * BK * 2;
-  hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL, EPI>), grid, dim3(kThreads), lds, stream, x,
-                     wq,
-                     scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
+  hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL, EPI, W>), grid, dim3(64 * W), lds, stream,
+                     x, wq, scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
                      p.tiles_m, p.chunks_per_split);
   return hipGetLastError();
+}
+
+// one unsplit 32-row tile: the plan's block width
+template <int BITS, int EPI>
+hipError_t run_wide(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                    const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
+                    int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
+  switch (p.waves) {
+    case 5: return run<BITS, 1, false, EPI, 5>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    case 6: return run<BITS, 1, false, EPI, 6>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    case 8: return run<BITS, 1, false, EPI, 8>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    default: return run<BITS, 1, false, EPI, 4>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+  }
 }
 
 template <int BITS, bool PARTIAL>
 hipError_t run_mi(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                   const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                   int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
+  if constexpr (!PARTIAL)
+    if (p.mi == 1) return run_wide<BITS, 0>(x, wq, scales, biases, bias, y, M, N, K, p, stream);
   switch (p.mi) {
     case 1: return run<BITS, 1, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
     case 2: return run<BITS, 2, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
@@ -468,8 +492,9 @@ hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t
 bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits) {
   const int64_t lim = (int64_t)1 << 31;
   // whole 8-group chunks; 32-bit offsets with room for the tiles' overhang
+  // (up to 256 columns for the widest blocks)
   return K % (BK * kChunk) == 0 && M >= 1 && (M + 128) * K * 2 < lim &&
-         (N + BN) * K * bits / 8 < lim && (N + BN) * (K / kGroup) * 2 < lim;
+         (N + 256) * K * bits / 8 < lim && (N + 256) * (K / kGroup) * 2 < lim;
 }
 
 size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits) {
@@ -497,12 +522,10 @@ hipError_t launch_qmms_swiglu_direct(const uint16_t* x, const uint32_t* wq,
   if (M == 0 || Nout == 0) return hipSuccess;
   Plan p = plan(M, 2 * Nout, K, bits, true);
   if (p.splits != 1 || p.mi != 1 || p.tiles_m != 1) return hipErrorInvalidValue;
-  p.tiles_n = (int)((Nout + BN / 2 - 1) / (BN / 2));  // 64 gate + 64 up columns per block
-  return bits == 4
-             ? run<4, 1, false, 1>(x, wq, scales, biases, nullptr, y, nullptr, M, 2 * Nout, K, p,
-                                   stream)
-             : run<8, 1, false, 1>(x, wq, scales, biases, nullptr, y, nullptr, M, 2 * Nout, K, p,
-                                   stream);
+  // 16 gate + 16 up columns per wave
+  p.tiles_n = (int)((Nout + 16 * p.waves - 1) / (16 * p.waves));
+  return bits == 4 ? run_wide<4, 1>(x, wq, scales, biases, nullptr, y, M, 2 * Nout, K, p, stream)
+                   : run_wide<8, 1>(x, wq, scales, biases, nullptr, y, M, 2 * Nout, K, p, stream);
 }
 
 hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

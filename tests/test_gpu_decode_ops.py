@@ -71,13 +71,15 @@ def test_rms_norm_batched_shape(ops):
                                         (1, 18948, 3584, 4), (1, 1025, 16384, 4),
                                         (2, 2049, 8192, 8), (32, 18944, 3584, 4),
                                         (32, 18944, 3584, 8), (16, 9475, 3584, 4),
-                                        (16, 4739, 3584, 4), (32, 14336, 4096, 4)])
+                                        (16, 4739, 3584, 4), (32, 14336, 4096, 4),
+                                        (16, 24000, 512, 4), (32, 20000, 1024, 8)])
 def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     """The gate|up GEMV with silu(gate) * up in its epilogue: bit-equal to the
     GEMV followed by silu_mul.  N = 18948, 1025 and 2049 leave a partial last
     block (8 and 2 output rows per block; 16 and 64 lanes per row).  At 16 and
     32 rows the skinny GEMM: K split with the SwiGLU in the reduce (4739) or
-    unsplit with it in the GEMM's epilogue (9475 ends in a 3-column tile)."""
+    unsplit with it in the GEMM's epilogue (9475 ends in a 3-column tile;
+    24000 and 20000 take blocks of 6 and 5 waves)."""
     core = importlib.import_module("mlx-server-runtime_amd.core")
     assert core.swiglu_supported(M, N, K, 64, bits)
     g = _gen(N + K + bits)

@@ -223,6 +223,26 @@ def test_skinny_split_k(mq, orc, bits, MNK):
     assert_close(y1, orc.qmm(x, wq, s, b, 64, bits, bias=bias))
 
 
+@pytest.mark.parametrize("MNKbits", [(24, 33000, 512, 4), (32, 45000, 512, 8),
+                                     (17, 60000, 512, 4), (32, 70000, 512, 4)])
+def test_skinny_wide_blocks(mq, orc, MNKbits):
+    """Unsplit 32-row tiles with more 128-column tiles than CUs: blocks of 5
+    (33000 columns, a 40-column last block), 6 (45000) or 8 (60000) waves keep
+    the block count within 256; 70000 columns fit no width and keep 4-wave
+    blocks.  Checked against the oracle and run to run."""
+    M, N, K, bits = MNKbits
+    assert mq._lib.lib().mq_quantized_matmul_workspace(M, N, K, 64, bits) == 0  # unsplit
+    rng = np.random.default_rng(N + bits)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    args = (bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
+    y = mq.quantized_matmul(*args, bias=bf16_dev(bias))
+    assert_close(y, orc.qmm(x, wq, s, b, 64, bits, bias=bias))
+    assert torch.equal(mq.quantized_matmul(*args, bias=bf16_dev(bias)).view(torch.int16),
+                       y.view(torch.int16))
+
+
 @pytest.mark.parametrize("MNK", [(2048, 3584, 18944), (512, 4096, 8192), (1100, 3584, 4096)])
 def test_large_tiles_split_k(mq, orc, MNK):
     """Few 256x256 tiles and a long K (the down projection of a 2048-row
