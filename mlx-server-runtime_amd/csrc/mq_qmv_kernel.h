@@ -43,6 +43,10 @@ constexpr int kBlock = 256;
 constexpr int kQmvLdsBudget = 48 * 1024;
 // Two rows per lane group may use up to 52 KiB: still 3 blocks per CU.
 constexpr int kTwoRowLdsBudget = 52 * 1024;
+// Four rows per lane group (half the blocks) may use up to 56 KiB, 2 blocks
+// per CU: the 4-bit K = 18944 GEMV (53 KiB) takes 11.5 us in 448 blocks of
+// 8 rows against 12.1 us in 896 blocks of 4.
+constexpr int kFourRowLdsBudget = 56 * 1024;
 // Scale + bias DMA operations per wave: 2 arrays of ceil((RPB*G + GP) / 2)
 // words in 64-word operations, over 4 waves (an instance issues the most it
 // can need, capped here; four rows per lane group at K = 18944 need 11).
@@ -528,7 +532,7 @@ inline bool rows_fit(int R, int bits, int tpr, int64_t M, int64_t N, int64_t K, 
   const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const int64_t sb_words = (rpb * G + GP + 1) / 2;
   return 2 * ((sb_words + 63) / 64) <= kSbOpsPerWave * (kBlock / 64) &&
-         lds_bytes(bits, tpr, mt, K, R) <= kTwoRowLdsBudget &&
+         lds_bytes(bits, tpr, mt, K, R) <= (R >= 4 ? kFourRowLdsBudget : kTwoRowLdsBudget) &&
          (N + rpb - 1) / rpb * T >= min_blocks;
 }
 
@@ -573,7 +577,7 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
           // More rows per lane group while the blocks still fill the GPU: a
           // block stages all of x (long rows: up to 40 KB), so rows per block
           // divide that L2 traffic, and fewer blocks fit one round of
-          // residency (3 per CU at this LDS size).
+          // residency (2 or 3 per CU at these LDS sizes).
           if (slots <= 5 && M == 1 && rows_fit(4, BITS, 128, M, N, K, g.T, 256))
             return run_mt<BITS, 128, 4, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
           if (slots <= 5 && rows_fit(2, BITS, 128, M, N, K, g.T, 512))
