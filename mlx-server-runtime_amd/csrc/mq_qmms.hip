@@ -397,28 +397,42 @@ struct Plan {
 
 Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   Plan p;
-  p.mi = M <= 32 ? 1 : M <= 64 ? 2 : 4;
-  p.tiles_n = (int)((N + BN - 1) / BN);
-  p.tiles_m = (int)((M + 32 * p.mi - 1) / (32 * p.mi));
   const int chunks = (int)(K / (BK * kChunk));
+  p.tiles_n = (int)((N + BN - 1) / BN);
+  // Above 32 rows: 128-row tiles where they alone give >= 128 tiles or K is
+  // long enough (>= 16 chunks) to split finely, else 64-row tiles. Measured
+  // at M = 128: 18944 x 3584 in 148 unsplit 128-row tiles 33.6 us (64-row:
+  // 35.7), 4608 x 3584 in 72 64-row tiles x 3 splits 16.6 us (128-row tiles
+  // x 7 splits: 19.2); at M = 256, 4608 x 3584 in 144 unsplit 64-row tiles
+  // 20.0 us (128-row x 3 splits: 23.4).
+  p.mi = 1;
+  if (M > 32) {
+    const int64_t tiles4 = (int64_t)p.tiles_n * ((M + 127) / 128);
+    p.mi = M > 64 && (tiles4 >= 128 || chunks >= 16) ? 4 : 2;
+  }
+  p.tiles_m = (int)((M + 32 * p.mi - 1) / (32 * p.mi));
   const int64_t base = (int64_t)p.tiles_n * p.tiles_m;
   int64_t splits = 1;
-  // Blocks wanted: for 32-row tiles at most one per CU (256 CUs), the
-  // splits rounded down; for taller tiles, which carry more work per step,
-  // 512 / 256 blocks, rounded up. Measured at M = 16..32: the down
-  // projection 3584 x 18944 at 8 splits (224 blocks) takes 20 us where 13
-  // splits (364 blocks, two on some CUs) take 23 us, and 28672 x 4096 runs
-  // unsplit (224 tiles) in 24 us against 34 us in 5 splits.
-  const int64_t want = p.mi == 1 ? 256 : 1024 / p.mi;
-  if (can_split && base < want) {
-    // The partial sums (written once, read once) stay under an eighth of the
-    // weight bytes, or 4 MiB, which stays in the Infinity Cache: small
-    // matrices (a layer's q/k/v or o at M = 32) then get short blocks, whose
-    // serial step latency otherwise sets the kernel time.
-    const int64_t weight_bytes = N * K * bits / 8;
-    const int64_t cap = std::max<int64_t>(weight_bytes / (16 * M * N), (4 << 20) / (4 * M * N));
-    const int64_t per_tile = p.mi == 1 ? want / base : (want + base - 1) / base;
-    splits = std::min<int64_t>({per_tile, chunks, cap});
+  // Blocks wanted: at most one per CU (256 CUs), the splits rounded down.
+  // Measured at M = 16..32: the down projection 3584 x 18944 at 8 splits
+  // (224 blocks) takes 20 us where 13 splits (364 blocks, two on some CUs)
+  // take 23 us, and 28672 x 4096 runs unsplit (224 tiles) in 24 us against
+  // 34 us in 5 splits. At M = 64..256 the same holds: the 128-row down
+  // projection in 28 tiles x 8 splits takes 32.0 us (4 splits: 47.7), and
+  // 148 tiles of 18944 x 3584 run unsplit in 33.6 us (2 splits: 42.7).
+  if (can_split && base < 256) {
+    int64_t cap = chunks;
+    if (p.mi == 1) {
+      // The partial sums (written once, read once) stay under an eighth of
+      // the weight bytes, or 4 MiB, which stays in the Infinity Cache: small
+      // matrices (a layer's q/k/v or o at M = 32) then get short blocks,
+      // whose serial step latency otherwise sets the kernel time. Taller
+      // tiles carry enough work per step that their partials (at most
+      // 256 blocks x 128 x 128 floats, 16 MiB) cost less than idle CUs.
+      const int64_t weight_bytes = N * K * bits / 8;
+      cap = std::max<int64_t>(weight_bytes / (16 * M * N), (4 << 20) / (4 * M * N));
+    }
+    splits = std::min<int64_t>({256 / base, chunks, cap});
   }
   if (splits < 1) splits = 1;
   p.chunks_per_split = (int)((chunks + splits - 1) / splits);

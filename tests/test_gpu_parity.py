@@ -192,7 +192,7 @@ def test_quantized_matmul_deterministic(mq, orc):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("MNK", [(9, 512, 8192), (32, 300, 4096), (100, 640, 8192),
-                                 (160, 600, 16384)])
+                                 (160, 600, 16384), (128, 640, 4096), (250, 300, 3584)])
 def test_skinny_split_k(mq, orc, bits, MNK):
     """Few columns and a long K: the skinny kernel splits K over blocks into a
     float32 workspace.  Checked against the oracle, run to run, and against the
