@@ -18,10 +18,13 @@ q/k norms; models/lfm2.py:569-591 for per-path quantization overrides):
   `mlp.experts.{e}.*`, stacked on load).
 
 Tensors are read with safetensors (no pickle), straight to the target device.
-Modules stored unquantized are quantized on load with the config's (or the
-caller's) group size and bits, as nn.quantize would.  Scales and biases must
-be bfloat16 (the kernels' type); a float16 checkpoint raises
-NotImplementedError rather than silently rounding its scales.
+Modules stored without `{path}.scales` (and every module of a checkpoint
+with no `quantization` entry) stay unquantized bfloat16 linears, as the
+reference's class_predicate leaves them; expert banks must be quantized.
+Scales and biases must be bfloat16 (the kernels' type); a float16 checkpoint
+raises NotImplementedError rather than silently rounding its scales, and so
+do configs this backend cannot run as the reference would (a float16 KV
+cache, rope_traditional).
 
 `save` writes a model back in the same layout (used to round-trip the
 loader in the tests).
@@ -38,7 +41,7 @@ import torch
 
 from . import core
 from .moe import MoEBlock, QExperts
-from .qwen2 import Layer, QLinear, Qwen2Config, Qwen2Model, _concat
+from .qwen2 import DenseLinear, Layer, QLinear, Qwen2Config, Qwen2Model, _concat
 
 
 class WeightArtifactValidationError(ValueError):
@@ -63,6 +66,19 @@ def parse_config(payload: dict[str, Any]) -> tuple[Qwen2Config, dict | None]:
     head_dim = int(payload.get("head_dim") or hidden // heads)
     if heads % kv_heads or (mt == "qwen2" and hidden % heads):
         raise ValueError("invalid head dimensions")
+    # The reference's paged KV cache takes the checkpoint's dtype (float16 when
+    # the config names none, qwen2.py:261-263, qwen3.py:253-255); the
+    # kernels here keep a bfloat16 cache, so only bfloat16 loads.
+    kv_dtype = str(payload.get("torch_dtype", "float16")).lower()
+    if kv_dtype not in ("float16", "bfloat16"):
+        raise ValueError("native paged KV requires float16 or bfloat16 torch_dtype")
+    if kv_dtype != "bfloat16":
+        raise NotImplementedError(
+            f"torch_dtype {kv_dtype}: this backend keeps a bfloat16 paged KV cache")
+    if payload.get("rope_traditional", False):  # qwen2.py:64,276
+        raise NotImplementedError("rope_traditional=True: this backend implements the "
+                                  "non-traditional (rotate-half) RoPE only")
+    rope_scale = _rope_scale(payload.get("rope_scaling")) if mt != "qwen2" else 1.0
     quant = payload.get("quantization") or payload.get("quantization_config")
     group_size = int(quant["group_size"]) if quant else 64
     bits = int(quant["bits"]) if quant else 4
@@ -72,7 +88,7 @@ def parse_config(payload: dict[str, Any]) -> tuple[Qwen2Config, dict | None]:
         num_attention_heads=heads, num_key_value_heads=kv_heads,
         num_hidden_layers=int(payload["num_hidden_layers"]),
         vocab_size=int(payload["vocab_size"]), rms_norm_eps=float(payload["rms_norm_eps"]),
-        rope_theta=float(payload.get("rope_theta", 1_000_000.0)),
+        rope_theta=float(payload.get("rope_theta", 1_000_000.0)), rope_scale=rope_scale,
         tie_word_embeddings=bool(payload.get("tie_word_embeddings", True)),
         group_size=group_size, bits=bits,
         head_dim_=head_dim if head_dim != hidden // heads else 0,
@@ -83,6 +99,24 @@ def parse_config(payload: dict[str, Any]) -> tuple[Qwen2Config, dict | None]:
         moe_intermediate_size=int(payload.get("moe_intermediate_size", 0)) if moe else 0,
         norm_topk_prob=bool(payload.get("norm_topk_prob", True)))
     return cfg, quant
+
+
+def _rope_scale(rope_scaling: dict[str, Any] | None) -> float:
+    """Position scale of Qwen3's RoPE (models/qwen3.py:356-367): 1/factor for
+    "linear" scaling, 1 for none or "default", anything else rejected.  The
+    reference's Qwen2 reads rope_scaling but never applies it
+    (models/qwen2.py:62-66)."""
+    if not rope_scaling:
+        return 1.0
+    rope_type = rope_scaling.get("type") or rope_scaling.get("rope_type")
+    if rope_type == "linear":
+        factor = float(rope_scaling.get("factor", 1.0))
+        if factor <= 0:
+            raise ValueError("Qwen3 rope scaling factor must be positive")
+        return 1.0 / factor
+    if rope_type in (None, "default"):
+        return 1.0
+    raise ValueError(f"unsupported Qwen3 RoPE scaling type: {rope_type}")
 
 
 # ---------------------------------------------------------------- index
@@ -167,34 +201,51 @@ class _Builder:
     def norm(self, path: str) -> torch.Tensor:
         return self.take(f"{path}.weight").to(torch.bfloat16).contiguous()
 
-    def linear(self, path: str) -> QLinear:
-        gs, bits = self.params(path)
+    def linear(self, path: str) -> QLinear | DenseLinear:
+        """{path}.* -> QLinear when the checkpoint holds {path}.scales (with the
+        config's or the path's own group size and bits, lfm2.py:579-589), else
+        an unquantized DenseLinear, as the reference's class_predicate leaves
+        such a module (qwen2.py:316-324)."""
         bias = self.take(f"{path}.bias").to(torch.bfloat16) if self.has(f"{path}.bias") else None
-        if self.has(f"{path}.scales"):
-            wq = self.take(f"{path}.weight")
-            s = self._bf16(f"{path}.scales", self.take(f"{path}.scales"))
-            b = self._bf16(f"{path}.biases", self.take(f"{path}.biases"))
-            K = s.shape[-1] * gs
-            if wq.shape[-1] * 32 != K * bits:
+        if not self.quant or not self.has(f"{path}.scales"):
+            w = self.take(f"{path}.weight")
+            if not w.is_floating_point():
                 raise WeightArtifactValidationError(
-                    f"{path}: weight {tuple(wq.shape)} does not hold {K} {bits}-bit codes per row")
-            wq = wq.view(torch.int32) if wq.dtype == torch.uint32 else wq
-        else:  # unquantized in the checkpoint: quantize as nn.quantize would
-            w = self.take(f"{path}.weight").to(torch.bfloat16)
-            wq, s, b = core.quantize(w, gs, bits)
+                    f"{path}: integer weight {tuple(w.shape)} without {path}.scales")
+            return DenseLinear(w.to(torch.bfloat16), bias)
+        gs, bits = self.params(path)
+        wq = self.take(f"{path}.weight")
+        s = self._bf16(f"{path}.scales", self.take(f"{path}.scales"))
+        b = self._bf16(f"{path}.biases", self.take(f"{path}.biases"))
+        K = s.shape[-1] * gs
+        if wq.shape[-1] * 32 != K * bits:
+            raise WeightArtifactValidationError(
+                f"{path}: weight {tuple(wq.shape)} does not hold {K} {bits}-bit codes per row")
+        wq = wq.view(torch.int32) if wq.dtype == torch.uint32 else wq
         return QLinear(wq.contiguous(), s, b, bias, gs, bits)
 
     def experts(self, path: str, proj: str) -> QExperts:
         stacked = f"{path}.switch_mlp.{proj}"
-        if self.has(f"{stacked}.weight"):
+        is_stacked = self.has(f"{stacked}.weight")
+        if is_stacked:
             ql = self.linear(stacked)
+            parts = [ql]
         else:
             E = self.cfg.num_experts
             parts = [self.linear(f"{path}.experts.{e}.{proj}") for e in range(E)]
+        if not all(isinstance(p, QLinear) for p in parts):
+            raise NotImplementedError(f"{path}.{proj}: unquantized experts (this backend runs "
+                                      "the experts through gather_qmm only)")
+        if not is_stacked:
             ql = QLinear(torch.stack([p.wq for p in parts]), torch.stack([p.scales for p in parts]),
                          torch.stack([p.biases for p in parts]), None, parts[0].group_size,
                          parts[0].bits)
         return QExperts(ql.wq, ql.scales, ql.biases, ql.group_size, ql.bits)
+
+
+def _qparams(ql) -> tuple[int, int] | None:
+    """(group_size, bits) of a quantized linear, None for an unquantized one."""
+    return (ql.group_size, ql.bits) if isinstance(ql, QLinear) else None
 
 
 def _fuse_experts(a: QExperts, b: QExperts) -> QExperts:
@@ -213,7 +264,7 @@ def build_model(cfg: Qwen2Config, tensors: dict[str, torch.Tensor], quant: dict 
     for i in range(cfg.num_hidden_layers):
         p = f"model.layers.{i}"
         parts = [bld.linear(f"{p}.self_attn.{n}_proj") for n in ("q", "k", "v")]
-        if len({(q.group_size, q.bits) for q in parts}) != 1:
+        if len({_qparams(q) for q in parts}) != 1:
             raise NotImplementedError(f"{p}: q/k/v quantized differently cannot be fused")
         layer = Layer(bld.norm(f"{p}.input_layernorm"), bld.norm(f"{p}.post_attention_layernorm"),
                       _concat(parts), bld.linear(f"{p}.self_attn.o_proj"))
@@ -228,7 +279,7 @@ def build_model(cfg: Qwen2Config, tensors: dict[str, torch.Tensor], quant: dict 
                                  cfg.norm_topk_prob)
         else:
             gate, up = bld.linear(f"{p}.mlp.gate_proj"), bld.linear(f"{p}.mlp.up_proj")
-            if (gate.group_size, gate.bits) != (up.group_size, up.bits):
+            if _qparams(gate) != _qparams(up):
                 raise NotImplementedError(f"{p}: gate/up quantized differently cannot be fused")
             layer.gate_up = _concat([gate, up])
             layer.down = bld.linear(f"{p}.mlp.down_proj")
@@ -256,9 +307,14 @@ def load(model_path: str | os.PathLike, device="cuda:0", strict: bool = True) ->
 
 
 # ---------------------------------------------------------------- save
-def _split_rows(ql: QLinear, sizes: list[int]) -> list[QLinear]:
+def _split_rows(ql, sizes: list[int]) -> list:
     out, r = [], 0
     for n in sizes:
+        if isinstance(ql, DenseLinear):
+            out.append(DenseLinear(ql.weight[r:r + n],
+                                   None if ql.bias is None else ql.bias[r:r + n]))
+            r += n
+            continue
         out.append(QLinear(ql.wq[r:r + n], ql.scales[r:r + n], ql.biases[r:r + n],
                            None if ql.bias is None else ql.bias[r:r + n], ql.group_size, ql.bits))
         r += n
@@ -275,6 +331,11 @@ def _export(model: Qwen2Model) -> tuple[dict[str, torch.Tensor], dict[str, dict]
     overrides: dict[str, dict] = {}
 
     def put(path, ql, gs=None, bits=None):
+        if isinstance(ql, DenseLinear):  # stored unquantized: no scales, no override
+            sd[f"{path}.weight"] = ql.weight
+            if ql.bias is not None:
+                sd[f"{path}.bias"] = ql.bias
+            return
         gs = gs or getattr(ql, "group_size", c.group_size)
         bits = bits or getattr(ql, "bits", c.bits)
         if (gs, bits) != (c.group_size, c.bits):
@@ -340,6 +401,8 @@ def config_payload(cfg: Qwen2Config, overrides: dict[str, dict] | None = None) -
            "attention_bias": cfg.attention_bias, "max_position_embeddings": 32768,
            "torch_dtype": "bfloat16",
            "quantization": {"group_size": cfg.group_size, "bits": cfg.bits, **(overrides or {})}}
+    if cfg.rope_scale != 1.0:
+        out["rope_scaling"] = {"type": "linear", "factor": 1.0 / cfg.rope_scale}
     if cfg.num_experts:
         out.update(num_experts=cfg.num_experts, num_experts_per_tok=cfg.num_experts_per_tok,
                    moe_intermediate_size=cfg.moe_intermediate_size,

@@ -60,6 +60,7 @@ class Qwen2Config:
     vocab_size: int
     rms_norm_eps: float = 1e-6
     rope_theta: float = 1e6
+    rope_scale: float = 1.0   # positions are multiplied by it (Qwen3 linear scaling)
     tie_word_embeddings: bool = False
     group_size: int = 64
     bits: int = 4
@@ -112,6 +113,28 @@ class QLinear:
         return self.wq.shape[0]
 
 
+class DenseLinear:
+    """A linear layer a checkpoint stores unquantized (no `{path}.scales`):
+    the reference keeps such a module an nn.Linear / nn.Embedding
+    (models/qwen2.py:316-324 quantizes only paths whose scales are present), so
+    it stays bfloat16 here, y = x @ weight^T (+ bias) through torch's GEMM.
+    weight bfloat16 [N, K]; as the embedding, its rows are looked up."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None):
+        if weight.dtype != torch.bfloat16 or weight.dim() != 2:
+            raise ValueError("DenseLinear takes a bfloat16 [N, K] weight")
+        self.weight, self.bias = weight.contiguous(), bias
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        K = x.shape[-1]
+        y = F.linear(x.reshape(-1, K), self.weight, self.bias)
+        return y.reshape(*x.shape[:-1], self.weight.shape[0])
+
+    @property
+    def out_features(self) -> int:
+        return self.weight.shape[0]
+
+
 def _random_qlinear(gen, n_out, n_in, cfg, bias, device, std=0.02) -> QLinear:
     w = (torch.randn(n_out, n_in, generator=gen, device=device) * std).to(torch.bfloat16)
     wq, s, b = core.quantize(w, cfg.group_size, cfg.bits)
@@ -121,22 +144,27 @@ def _random_qlinear(gen, n_out, n_in, cfg, bias, device, std=0.02) -> QLinear:
     return QLinear(wq, s, b, bv, cfg.group_size, cfg.bits)
 
 
-def _gate_up_silu(gate_up: QLinear, x: torch.Tensor) -> torch.Tensor:
+def _gate_up_silu(gate_up, x: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up of the fused gate|up projection: one kernel at decode
     shapes (the same bits as the two-kernel path), else the two kernels."""
     K = x.shape[-1]
-    if gate_up.bias is None and core.swiglu_supported(x.numel() // K, gate_up.out_features // 2, K,
-                                                      gate_up.group_size, gate_up.bits):
+    if (isinstance(gate_up, QLinear) and gate_up.bias is None
+            and core.swiglu_supported(x.numel() // K, gate_up.out_features // 2, K,
+                                      gate_up.group_size, gate_up.bits)):
         return core.quantized_matmul_swiglu(x, gate_up.wq, gate_up.scales, gate_up.biases,
                                             gate_up.group_size, gate_up.bits)
     return silu_mul(gate_up(x))
 
 
-def _concat(parts: list[QLinear]) -> QLinear:
+def _concat(parts: list):
     """Row-wise concatenation: one launch computes every part's columns."""
     bias = None
     if parts[0].bias is not None:
         bias = torch.cat([p.bias for p in parts])
+    if all(isinstance(p, DenseLinear) for p in parts):
+        return DenseLinear(torch.cat([p.weight for p in parts]), bias)
+    if not all(isinstance(p, QLinear) for p in parts):
+        raise NotImplementedError("a quantized and an unquantized projection cannot be fused")
     return QLinear(torch.cat([p.wq for p in parts]), torch.cat([p.scales for p in parts]),
                    torch.cat([p.biases for p in parts]), bias, parts[0].group_size,
                    parts[0].bits)
@@ -165,10 +193,12 @@ def _random_experts(gen, E, n_out, n_in, cfg, device, std=0.02) -> QExperts:
 
 
 def rope_tables(cfg: Qwen2Config, max_len: int, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """cos/sin [max_len, head_dim/2] of mx.fast.rope (traditional=False, base=theta)."""
+    """cos/sin [max_len, head_dim/2] of mx.fast.rope (traditional=False, base=theta,
+    scale): row p, column i holds cos/sin(p * scale * theta^(-2i/head_dim))."""
     half = cfg.head_dim // 2
     inv = cfg.rope_theta ** (-torch.arange(0, half, dtype=torch.float64, device=device) / half)
-    ang = torch.arange(max_len, dtype=torch.float64, device=device)[:, None] * inv[None, :]
+    pos = torch.arange(max_len, dtype=torch.float64, device=device) * cfg.rope_scale
+    ang = pos[:, None] * inv[None, :]
     return torch.cos(ang).float(), torch.sin(ang).float()
 
 
@@ -254,21 +284,23 @@ class Qwen2Model:
 
     def _embed(self, ids: torch.Tensor) -> torch.Tensor:
         e = self.embed
+        if isinstance(e, DenseLinear):  # an unquantized nn.Embedding
+            return e.weight.index_select(0, ids.reshape(-1).long()).reshape(
+                *ids.shape, e.weight.shape[1])
         return core.embedding_lookup(ids.to(torch.int32), e.wq, e.scales, e.biases,
                                      e.group_size, e.bits)
 
     def _head(self, x: torch.Tensor) -> torch.Tensor:
         """LM head on final-normed activations (untied, or the tied embedding's as_linear)."""
-        if self.lm_head is None:
-            e = self.embed
-            return core.quantized_matmul(x, e.wq, e.scales, e.biases, True, e.group_size, e.bits)
-        return self.lm_head(x)
+        return self._head_linear()(x)
 
-    def _head_linear(self) -> QLinear:
-        """The LM head as a quantized linear (untied, or the tied embedding's as_linear)."""
+    def _head_linear(self):
+        """The LM head as a linear (untied, or the tied embedding's as_linear)."""
         if self.lm_head is not None:
             return self.lm_head
         e = self.embed
+        if isinstance(e, DenseLinear):
+            return DenseLinear(e.weight)
         return QLinear(e.wq, e.scales, e.biases, None, e.group_size, e.bits)
 
     def _norm_linear(self, ql: QLinear, a: torch.Tensor, res: torch.Tensor | None,
@@ -280,7 +312,7 @@ class Qwen2Model:
         eps = self.cfg.rms_norm_eps
         K = a.shape[-1]
         n_out = ql.out_features // 2 if swiglu else ql.out_features
-        if (a.numel() == K and not (swiglu and ql.bias is not None)
+        if (isinstance(ql, QLinear) and a.numel() == K and not (swiglu and ql.bias is not None)
                 and core.rms_norm_qmm_supported(1, n_out, K, ql.group_size, ql.bits, swiglu)):
             return core.rms_norm_quantized_matmul(a, norm_w, eps, ql.wq, ql.scales, ql.biases,
                                                   ql.bias, res, ql.group_size, ql.bits, swiglu)
@@ -298,7 +330,8 @@ class Qwen2Model:
         same bits either way."""
         eps = self.cfg.rms_norm_eps
         K = inp.shape[-1]
-        if core.add_norm_supported(inp.numel() // K, ql.out_features, K, ql.group_size, ql.bits):
+        if isinstance(ql, QLinear) and core.add_norm_supported(inp.numel() // K, ql.out_features,
+                                                               K, ql.group_size, ql.bits):
             return core.quantized_matmul_add_rms_norm(inp, ql.wq, ql.scales, ql.biases, h, norm_w,
                                                       eps, ql.bias, ql.group_size, ql.bits)
         return fused_rms_norm(ql(inp), norm_w, eps, residual=h)
@@ -459,4 +492,4 @@ class Qwen2Model:
         return g, static_logits
 
 
-__all__ = ["Qwen2Config", "Qwen2Model", "QLinear", "rope_tables", "apply_rope"]
+__all__ = ["Qwen2Config", "Qwen2Model", "QLinear", "DenseLinear", "rope_tables", "apply_rope"]

@@ -11,12 +11,32 @@ by test_gpu_parity.py) one layer at a time.
 
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn.functional as F
 
 
 def _deq(mq, ql) -> torch.Tensor:
+    if not hasattr(ql, "wq"):  # an unquantized (bfloat16) linear
+        return ql.weight.float()
     return mq.dequantize(ql.wq, ql.scales, ql.biases, ql.group_size, ql.bits).float()
+
+
+def _rope(x: torch.Tensor, positions: torch.Tensor, theta: float, scale: float) -> torch.Tensor:
+    """Non-traditional RoPE (mx.fast.rope, traditional=False) written
+    independently of the decoder's tables: element i of the first half and
+    element i of the second half form the complex number x_i + j x_(i+d/2),
+    multiplied by exp(j * position * scale * theta^(-2i/d)).
+    x [..., S, d] float32, positions [S]."""
+    d = x.shape[-1]
+    half = d // 2
+    freq = torch.tensor([math.pow(theta, -2.0 * i / d) for i in range(half)],
+                        dtype=torch.float64, device=x.device)
+    ang = (positions.double() * scale)[:, None] * freq[None, :]
+    rot = torch.polar(torch.ones_like(ang), ang)                      # [S, half] complex128
+    z = torch.complex(x[..., :half].double(), x[..., half:].double()) * rot
+    return torch.cat([z.real, z.imag], -1).to(x.dtype)
 
 
 def _linear(mq, ql, x):
@@ -40,11 +60,14 @@ def _deq_experts(mq, qe) -> torch.Tensor:
 def moe_reference(mq, block, x, r=lambda t: t, indices=None):
     """Float32 restatement of the routed expert MLP (models/lfm2.py:365-375,
     SwitchGLU :193-218): softmax router, top-k, renormalised gates, per
-    expert down(silu(gate(x)) * up(x)), gate-weighted sum.  With indices
-    (int [T, k]) the routing choice is taken from there (the gates are still
-    recomputed here), which isolates the expert arithmetic from near-ties."""
+    expert down(silu(gate(x)) * up(x)), gate-weighted sum over the k choices
+    in order.  With indices (int [T, k]) the routing choice is taken from there
+    (the gates are still recomputed here), which isolates the expert arithmetic
+    from near-ties.  Each expert's rows are computed together (one matmul per
+    expert), so the weights are never gathered per pair."""
     shape = x.shape
     xt = x.reshape(-1, shape[-1]).float()
+    T, H = xt.shape
     gates = torch.softmax(_linear(mq, block.gate, xt), -1)
     if block.expert_bias is not None:
         gates = gates + block.expert_bias.float()
@@ -57,37 +80,53 @@ def moe_reference(mq, block, x, r=lambda t: t, indices=None):
     sc = r(sc)
     wgu, wd = _deq_experts(mq, block.gate_up), _deq_experts(mq, block.down)
     inter = wd.shape[-1]
+    flat = indices.reshape(-1)                       # pair p = (token p // k, choice p % k)
+    contrib = torch.zeros(T * block.top_k, H, device=xt.device)
+    for e in torch.unique(flat).tolist():
+        pairs = (flat == e).nonzero().squeeze(-1)
+        xe = xt[pairs // block.top_k]
+        gu = r(xe @ wgu[e].t())                                        # [n, 2I]
+        act = r(r(F.silu(gu[:, :inter])) * gu[:, inter:])
+        y = r(act @ wd[e].t())                                         # [n, H]
+        contrib[pairs] = r(y * sc.reshape(-1)[pairs, None])
+    contrib = contrib.reshape(T, block.top_k, H)
     out = torch.zeros_like(xt)
     for j in range(block.top_k):
-        e = indices[:, j]
-        gu = r(torch.bmm(wgu[e], xt.unsqueeze(-1)).squeeze(-1))        # [T, 2I]
-        act = r(r(F.silu(gu[:, :inter])) * gu[:, inter:])
-        y = r(torch.bmm(wd[e], act.unsqueeze(-1)).squeeze(-1))         # [T, H]
-        out = out + r(y * sc[:, j:j + 1])
+        out = out + contrib[:, j]
     return out.reshape(shape)
 
 
-def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = False
-                     ) -> torch.Tensor:
-    """tokens [B, S] (positions 0..S-1) -> float32 logits [B, S, vocab], causal.
+def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = False,
+                     head_from: int = 0) -> torch.Tensor:
+    """tokens [B, S] (positions 0..S-1) -> float32 logits [B, S - head_from, vocab]
+    of positions head_from..S-1, causal (the LM head on reference_hidden)."""
+    h = reference_hidden(mq, model, tokens, bf16_activations, head_from)
+    head = model.lm_head if model.lm_head is not None else model.embed
+    return h @ _deq(mq, head).t()
+
+
+def reference_hidden(mq, model, tokens: torch.Tensor, bf16_activations: bool = False,
+                     head_from: int = 0) -> torch.Tensor:
+    """tokens [B, S] -> float32 final-normed hidden states [B, S - head_from, hidden]
+    of positions head_from..S-1 (the LM head's input), causal.
 
     With bf16_activations, values are rounded to bfloat16 wherever the model
     under test -- and the reference's MLX graph -- stores bfloat16 (norm
     outputs, linear outputs, q and k after RoPE, the KV cache, the residual
     stream, the SiLU product), isolating the kernels' own arithmetic."""
-    from importlib import import_module
-
     r = (lambda t: t.to(torch.bfloat16).float()) if bf16_activations else (lambda t: t)
 
-    q2 = import_module("mlx-server-runtime_amd.qwen2")
     c = model.cfg
     B, S = tokens.shape
     d, nh, nkv = c.head_dim, c.num_attention_heads, c.num_key_value_heads
-    cos, sin = q2.rope_tables(c, S, tokens.device)
+    pos = torch.arange(S, device=tokens.device)
     causal = torch.full((S, S), float("-inf"), device=tokens.device).triu(1)
     e = model.embed
-    h = mq.embedding_lookup(tokens.reshape(-1).to(torch.int32), e.wq, e.scales, e.biases,
-                            e.group_size, e.bits).float().reshape(B, S, c.hidden_size)
+    if hasattr(e, "wq"):
+        h = mq.embedding_lookup(tokens.reshape(-1).to(torch.int32), e.wq, e.scales, e.biases,
+                                e.group_size, e.bits).float().reshape(B, S, c.hidden_size)
+    else:
+        h = e.weight.float()[tokens.reshape(-1).long()].reshape(B, S, c.hidden_size)
     for layer in model.layers:
         x = r(_rms(h, layer.input_norm, c.rms_norm_eps))
         qkv = r(_linear(mq, layer.qkv, x))
@@ -96,8 +135,8 @@ def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
         if layer.q_norm is not None:  # Qwen3 per-head RMSNorm (models/qwen3.py:84-85)
             q = r(_rms(q, layer.q_norm, c.rms_norm_eps))
             k = r(_rms(k, layer.k_norm, c.rms_norm_eps))
-        q = r(q2.apply_rope(q.transpose(1, 2), cos, sin))
-        k = r(q2.apply_rope(k.transpose(1, 2), cos, sin))
+        q = r(_rope(q.transpose(1, 2), pos, c.rope_theta, c.rope_scale))
+        k = r(_rope(k.transpose(1, 2), pos, c.rope_theta, c.rope_scale))
         v = v.reshape(B, S, nkv, d).transpose(1, 2)
         rep = nh // nkv
         k, v = k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1)
@@ -111,9 +150,7 @@ def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
         gu = r(_linear(mq, layer.gate_up, x))
         act = r(r(F.silu(gu[..., :c.intermediate_size])) * gu[..., c.intermediate_size:])
         h = r(h + r(_linear(mq, layer.down, act)))
-    h = r(_rms(h, model.final_norm, c.rms_norm_eps))
-    head = model.lm_head if model.lm_head is not None else model.embed
-    return h @ _deq(mq, head).t()
+    return r(_rms(h[:, head_from:], model.final_norm, c.rms_norm_eps))
 
 
 def greedy_agreement(ref_logits: torch.Tensor, prompt_len: int, tokens: torch.Tensor):

@@ -18,7 +18,7 @@ QWEN2 = {"model_type": "qwen2", "architectures": ["Qwen2ForCausalLM"], "hidden_s
          "intermediate_size": 256, "num_attention_heads": 4, "num_key_value_heads": 2,
          "num_hidden_layers": 2, "vocab_size": 64, "rms_norm_eps": 1e-6, "rope_theta": 1e6,
          "tie_word_embeddings": False, "max_position_embeddings": 4096,
-         "quantization": {"group_size": 64, "bits": 4}}
+         "torch_dtype": "bfloat16", "quantization": {"group_size": 64, "bits": 4}}
 
 
 def _q(gen, n, k, bits=4, lead=()):
@@ -194,3 +194,86 @@ def test_loader_rejects(tmp_path):
     wide["model.layers.0.mlp.down_proj.weight"] = torch.zeros(128, 3, dtype=torch.uint32)
     with pytest.raises(ck.WeightArtifactValidationError, match="codes per row"):
         ck.load(_write(tmp_path / "wide", QWEN2, wide), device="cpu")
+
+
+def test_parse_config_reference_options():
+    """torch_dtype and the RoPE options as the reference reads them
+    (models/qwen2.py:261-263,276-277; models/qwen3.py:253-255,356-367)."""
+    # no torch_dtype: the reference's KV cache is float16, which this backend does not keep
+    with pytest.raises(NotImplementedError, match="float16"):
+        ck.parse_config({k: v for k, v in QWEN2.items() if k != "torch_dtype"})
+    with pytest.raises(NotImplementedError, match="float16"):
+        ck.parse_config(dict(QWEN2, torch_dtype="float16"))
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        ck.parse_config(dict(QWEN2, torch_dtype="float32"))
+    assert ck.parse_config(dict(QWEN2, torch_dtype="BFloat16"))[0].hidden_size == 128
+    with pytest.raises(NotImplementedError, match="rope_traditional"):
+        ck.parse_config(dict(QWEN2, rope_traditional=True))
+    assert ck.parse_config(dict(QWEN2, rope_traditional=False))[0].rope_scale == 1.0
+    # Qwen3 applies linear RoPE scaling (positions * 1/factor); Qwen2 reads and ignores it
+    q3 = dict(QWEN2, model_type="qwen3", head_dim=64)
+    lin = {"type": "linear", "factor": 4.0}
+    assert ck.parse_config(dict(q3, rope_scaling=lin))[0].rope_scale == 0.25
+    assert ck.parse_config(dict(q3, rope_scaling={"rope_type": "default"}))[0].rope_scale == 1.0
+    assert ck.parse_config(dict(QWEN2, rope_scaling=lin))[0].rope_scale == 1.0
+    with pytest.raises(ValueError, match="unsupported Qwen3 RoPE scaling type"):
+        ck.parse_config(dict(q3, rope_scaling={"type": "yarn", "factor": 4.0}))
+    with pytest.raises(ValueError, match="positive"):
+        ck.parse_config(dict(q3, rope_scaling={"type": "linear", "factor": 0}))
+    # the scale reaches the tables: row p is position p * scale
+    c = ck.parse_config(dict(q3, rope_scaling=lin))[0]
+    cos4, _ = q2.rope_tables(c, 8, "cpu")
+    cos1, _ = q2.rope_tables(ck.parse_config(q3)[0], 8, "cpu")
+    assert torch.equal(cos4[4], cos1[1])
+
+
+def _dense(sd, path, gen):
+    """Replace a quantized module by an unquantized bfloat16 weight [N, K]."""
+    s = sd.pop(f"{path}.scales")
+    sd.pop(f"{path}.biases")
+    n, k = s.shape[0], s.shape[1] * 64
+    sd[f"{path}.weight"] = torch.randn(n, k, generator=gen).to(torch.bfloat16)
+
+
+def test_unquantized_modules_stay_dense(tmp_path):
+    """A module quantized iff its scales are stored (models/qwen2.py:316-324,
+    lfm2.py:579-589): lm_head and one o_proj stored in bfloat16 (lm_head also
+    marked false per path) load as unquantized linears, unchanged, and save
+    back the same; the rest stay quantized."""
+    gen = torch.Generator().manual_seed(5)
+    payload = dict(QWEN2, quantization={"group_size": 64, "bits": 4, "lm_head": False})
+    sd = _state(payload)
+    _dense(sd, "lm_head", gen)
+    _dense(sd, "model.layers.1.self_attn.o_proj", gen)
+    m = ck.load(_write(tmp_path / "a", payload, sd), device="cpu")
+    assert isinstance(m.lm_head, q2.DenseLinear)
+    assert torch.equal(m.lm_head.weight, sd["lm_head.weight"])
+    assert isinstance(m.layers[1].o, q2.DenseLinear) and isinstance(m.layers[0].o, q2.QLinear)
+    assert isinstance(m.layers[1].qkv, q2.QLinear)
+    ck.save(m, tmp_path / "b")
+    again = ck.state_dict(ck.load(tmp_path / "b", device="cpu"))
+    assert set(again) == set(sd)
+    assert torch.equal(again["lm_head.weight"], sd["lm_head.weight"])
+    assert torch.equal(again["model.layers.1.self_attn.o_proj.weight"],
+                       sd["model.layers.1.self_attn.o_proj.weight"])
+    # no quantization entry at all: every module is an unquantized linear
+    plain = {k: v for k, v in payload.items() if k != "quantization"}
+    sd2 = _state(QWEN2)
+    for name in [n[:-len(".scales")] for n in sd2 if n.endswith(".scales")]:
+        _dense(sd2, name, gen)
+    m2 = ck.load(_write(tmp_path / "c", plain, sd2), device="cpu")
+    assert isinstance(m2.embed, q2.DenseLinear) and isinstance(m2.layers[0].gate_up, q2.DenseLinear)
+    assert torch.equal(m2.layers[0].gate_up.weight,
+                       torch.cat([sd2["model.layers.0.mlp.gate_proj.weight"],
+                                  sd2["model.layers.0.mlp.up_proj.weight"]]))
+    # q quantized but k stored dense cannot share one fused q|k|v launch
+    sd3 = _state(QWEN2)
+    _dense(sd3, "model.layers.0.self_attn.k_proj", gen)
+    with pytest.raises(NotImplementedError, match="fused"):
+        ck.load(_write(tmp_path / "d", QWEN2, sd3), device="cpu")
+    # integer codes without scales are malformed
+    sd4 = _state(QWEN2)
+    sd4.pop("lm_head.scales")
+    sd4.pop("lm_head.biases")
+    with pytest.raises(ck.WeightArtifactValidationError, match="without lm_head.scales"):
+        ck.load(_write(tmp_path / "e", QWEN2, sd4), device="cpu")

@@ -8,6 +8,8 @@ import importlib
 import pytest
 import torch
 
+from qwen2_reference import reference_logits
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
@@ -32,3 +34,32 @@ def test_save_load_round_trip_same_logits(tmp_path, kind):
     b = m2.prefill(ids, m2.new_cache(2, 20), all_positions=True)
     assert torch.equal(a, b)
     assert torch.equal(m.generate(ids, 8), m2.generate(ids, 8))
+
+
+def test_unquantized_modules_decode(tmp_path):
+    """A checkpoint whose lm_head and one o_proj are stored unquantized (no
+    scales, as models/qwen2.py:316-324 leaves them): the loaded model keeps
+    them bfloat16, decodes the same in graph and eager mode, and its logits
+    match the float32 restatement on the same weights."""
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    ck = importlib.import_module("mlx-server-runtime_amd.checkpoint")
+    cfg = q2.Qwen2Config(256, 512, 4, 2, 2, 1000)
+    m = q2.Qwen2Model.random(cfg, seed=4, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    m.lm_head = q2.DenseLinear((torch.randn(1000, 256, generator=gen, device=DEV) * 0.02)
+                               .to(torch.bfloat16))
+    m.layers[1].o = q2.DenseLinear((torch.randn(256, 256, generator=gen, device=DEV) * 0.01)
+                                   .to(torch.bfloat16))
+    ck.save(m, tmp_path)
+    m2 = ck.load(tmp_path, device=DEV)
+    assert isinstance(m2.lm_head, q2.DenseLinear) and isinstance(m2.layers[1].o, q2.DenseLinear)
+    ids = torch.randint(0, 1000, (2, 24), generator=gen, device=DEV)
+    steps = []
+    toks = m2.generate(ids, 8, use_graph=False, logits_out=steps)
+    assert torch.equal(toks, m2.generate(ids, 8))
+    full = torch.cat([ids, toks], 1)[:, :-1]
+    ref = reference_logits(mq, m2, full)
+    ours = m2.prefill(full, m2.new_cache(2, full.shape[1]), all_positions=True)
+    err = float((ours.float() - ref).abs().max() / ref.abs().max())
+    assert err <= 3e-2, err
