@@ -3,8 +3,6 @@
 // include/mq.h.
 #include <cstdarg>
 #include <cstdio>
-#include <cstdlib>
-#include <cstring>
 
 #include "../../include/mq.h"
 #include "mq_internal.h"
@@ -31,6 +29,15 @@ int hip_status(hipError_t e, const char* what) {
   return ok();
 }
 
+}  // namespace
+
+int mq::set_last_error(int code, const char* msg) {
+  snprintf(g_err, sizeof(g_err), "%s", msg);
+  return code;
+}
+
+namespace {
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
@@ -38,19 +45,8 @@ constexpr int64_t kMaxDim = (int64_t)1 << 31;
 // GEMV kernel for decode-sized M.  Measured on MI355X: the dot2 kernel streams
 // large matrices faster at M <= 2 (its 256-byte row segments per load beat the
 // matrix-core kernel's 64-byte ones), the matrix-core kernel wins everywhere
-// else (its VALU cost does not grow with M).  MQ_GEMV=dot2|mfma forces one.
-int gemv_forced() {
-  static const int forced = [] {
-    const char* v = getenv("MQ_GEMV");
-    if (v && strcmp(v, "dot2") == 0) return 1;
-    if (v && strcmp(v, "mfma") == 0) return 2;
-    return 0;
-  }();
-  return forced;
-}
-
+// else (its VALU cost does not grow with M).
 bool use_matrix_core_gemv(int64_t M, int64_t N, int64_t K) {
-  if (const int forced = gemv_forced()) return forced == 2;
   return !(M <= 2 && N * K >= ((int64_t)1 << 25));
 }
 
@@ -87,33 +83,18 @@ int check_dim(const char* op, const char* name, int64_t v) {
   return MQ_OK;
 }
 
-// GEMM kernel for M above the GEMV range: the register-dequant 256x256 kernel
-// where it fits, else the LDS-dequant 256x256 kernel, else the 128x128 one.
-// MQ_QMM=tile128|lds256 forces one of the latter two (A/B runs).
-int gemm_override() {
-  static const int v = [] {
-    const char* e = getenv("MQ_QMM");
-    if (e && strcmp(e, "tile128") == 0) return 1;
-    if (e && strcmp(e, "lds256") == 0) return 2;
-    return 0;
-  }();
-  return v;
-}
-
 // The matrix-core GEMV for a dense matmul. It takes 8-bit rows up to 16,
 // but at 9..16 rows the skinny GEMM's one 32-row tile streams the codes
 // faster (M = 16, K = 3584: N = 18944 29.4 us against 34.6, N = 4608
 // 11.4 us against 14.1), so there it only serves shapes the skinny GEMM
 // does not fit.
 bool dense_gemv(int64_t M, int64_t N, int64_t K, int bits) {
-  return mq::qmvm_fits(M, N, K, bits, 1) &&
-         (M <= 8 || gemm_override() == 1 || !mq::qmms_fits(M, N, K, bits));
+  return mq::qmvm_fits(M, N, K, bits, 1) && (M <= 8 || !mq::qmms_fits(M, N, K, bits));
 }
 
 // Skinny MFMA kernel for M above the GEMV range and up to two 128-row tiles.
-// MQ_QMM=tile128 turns it off (A/B runs).
 bool use_skinny(int64_t M, int64_t N, int64_t K, int bits) {
-  return M <= 256 && gemm_override() != 1 && !dense_gemv(M, N, K, bits) &&
+  return M <= 256 && !dense_gemv(M, N, K, bits) &&
          !mq::qmv_fits(M, N, K, bits, 1) && mq::qmms_fits(M, N, K, bits);
 }
 
@@ -172,8 +153,7 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
   if (use_skinny(M, N, K, bits)) return mq::qmms_workspace_bytes(M, N, K, bits);
   if (dense_gemv(M, N, K, bits) || mq::qmv_fits(M, N, K, bits, 1)) return 0;
-  if (mq::qmm3_fits(M, N, K, bits) && gemm_override() == 0)
-    return mq::qmm3_workspace_bytes(M, N, K);
+  if (mq::qmm3_fits(M, N, K, bits)) return mq::qmm3_workspace_bytes(M, N, K);
   return 0;
 }
 
@@ -389,12 +369,12 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
     e = mq::launch_qmms(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
-  } else if (mq::qmm3_fits(M, N, K, bits) && gemm_override() == 0) {
+  } else if (mq::qmm3_fits(M, N, K, bits)) {
     if (workspace && !aligned16(workspace))
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
     e = mq::launch_qmm3(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
-  } else if (mq::qmm2_fits(M, N, K, bits) && gemm_override() != 1) {
+  } else if (mq::qmm2_fits(M, N, K, bits)) {
     e = mq::launch_qmm2(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
   } else {
     e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
@@ -438,8 +418,8 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
   // Single-row batches (a decode step's (token, expert) pairs) are many small
   // GEMVs: the dot2 kernel streams them faster than the matrix-core one
   // (measured on the 128-expert, 2048 x 768 banks at 64 pairs: 25 % faster
-  // decode).  MQ_GEMV forces one as for quantized_matmul.
-  const bool dot2_rows = M <= 2 && T > 1 && gemv_forced() != 2;
+  // decode).
+  const bool dot2_rows = M <= 2 && T > 1;
   if (few && mq::qmvm_fits(M, N, K, bits, T) &&
       ((use_matrix_core_gemv(M, N, K) && !dot2_rows) || !mq::qmv_fits(M, N, K, bits, T))) {
     e = mq::launch_qmvm(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);

@@ -8,6 +8,10 @@
 
 namespace mq {
 
+// Sets the calling thread's mq_last_error() message; returns code.  For
+// entry points defined outside mq_capi.hip.
+int set_last_error(int code, const char* msg);
+
 struct GatherMap {
   const int32_t* lhs;   // x batch per output batch (nullptr: identity)
   const int32_t* rhs;   // expert per output batch (nullptr: single matrix)

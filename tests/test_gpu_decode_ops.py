@@ -72,14 +72,17 @@ def test_rms_norm_batched_shape(ops):
                                         (2, 2049, 8192, 8), (32, 18944, 3584, 4),
                                         (32, 18944, 3584, 8), (16, 9475, 3584, 4),
                                         (16, 4739, 3584, 4), (32, 14336, 4096, 4),
-                                        (16, 24000, 512, 4), (32, 20000, 1024, 8)])
+                                        (16, 24000, 512, 4), (32, 20000, 1024, 8),
+                                        (16, 4739, 3584, 8), (16, 18944, 3584, 8),
+                                        (12, 9475, 3584, 8)])
 def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     """The gate|up GEMV with silu(gate) * up in its epilogue: bit-equal to the
     GEMV followed by silu_mul.  N = 18948, 1025 and 2049 leave a partial last
     block (8 and 2 output rows per block; 16 and 64 lanes per row).  At 16 and
     32 rows the skinny GEMM: K split with the SwiGLU in the reduce (4739) or
     unsplit with it in the GEMM's epilogue (9475 ends in a 3-column tile;
-    24000 and 20000 take blocks of 6 and 5 waves)."""
+    24000 and 20000 take blocks of 6 and 5 waves).  8-bit batches of 9-16 rows
+    take the skinny GEMM's 32-row tile too."""
     core = importlib.import_module("mlx-server-runtime_amd.core")
     assert core.swiglu_supported(M, N, K, 64, bits)
     g = _gen(N + K + bits)
@@ -147,12 +150,14 @@ def test_rms_norm_quantized_matmul_small_matrix_with_bias(ops):
 
 @pytest.mark.parametrize("M,N,K,bits,with_bias", [
     (32, 3584, 18944, 4, False), (32, 3584, 3584, 4, True), (32, 4096, 4096, 8, False),
-    (27, 3584, 18944, 4, True)])
+    (27, 3584, 18944, 4, True), (16, 3584, 18944, 8, False), (16, 3584, 3584, 8, True),
+    (128, 3584, 18944, 4, False), (128, 3584, 18944, 8, True)])
 def test_quantized_matmul_add_rms_norm_equals_two_kernels(ops, M, N, K, bits, with_bias):
     """The skinny GEMM whose split-K reduce adds the residual and applies the
     RMSNorm: bit-equal to quantized_matmul (its workspace, the same split plan)
     followed by rms_norm, the residual stream included; 27 rows leave a
-    partial row tile."""
+    partial row tile; 8-bit at 16 rows and 128-row plans (uneven last split)
+    too."""
     core = importlib.import_module("mlx-server-runtime_amd.core")
     assert core.add_norm_supported(M, N, K, 64, bits)
     g = _gen(M + N + K + bits)

@@ -14,6 +14,7 @@ their own row of x).
 
 from __future__ import annotations
 
+import functools
 import os
 
 import numpy as np
@@ -307,17 +308,46 @@ def test_decode_shapes_full_size(mq, orc, bits, KN):
     assert_close(y, orc.qmm(x, wq, s, b, 64, bits))
 
 
+@functools.lru_cache(maxsize=6)
+def _sweep_weights(orc, K, N, bits):
+    """Quantized N(0, 0.02) weights of one sweep shape, shared by its M cases."""
+    rng = np.random.default_rng(5151 + K + N + bits)
+    return quantized(orc, rng, N, K, bits)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("M", [16, 2048, 8192])
-def test_prefill_shape_sampled_rows(mq, orc, bits, M):
-    """K=3584, N=18944 at large M: sampled output rows against the oracle."""
-    K, N = 3584, 18944
-    rng = np.random.default_rng(5151 + M + bits)
-    wq, s, b = quantized(orc, rng, N, K, bits)
+@pytest.mark.parametrize("KN", [(3584, 18944), (18944, 3584), (3584, 4608)])
+@pytest.mark.parametrize("M", [16, 128, 2048, 8192])
+def test_sweep_shape_sampled_rows(mq, orc, bits, KN, M):
+    """Every point of the GEMM sweep above M = 1 (M in 16, 128, 2048, 8192 x
+    the three 7B shapes x both widths), each through the kernel and split plan
+    it runs at that size: sampled output rows (the first, the last, and rows of
+    the first and last row tiles) against the oracle."""
+    K, N = KN
+    wq, s, b = _sweep_weights(orc, K, N, bits)
+    rng = np.random.default_rng(7 + M + K + bits)
     x = rand_bf16(orc, rng, (M, K), 1.0)
     y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
-    rows = np.unique(np.r_[0, M - 1, rng.integers(0, M, 6)])
+    rows = np.unique(np.r_[0, 1, min(M, 255) - 1, M - 1, rng.integers(0, M, 5)])
     assert_close(y[torch.from_numpy(rows).to(DEV)], orc.qmm(x[rows], wq, s, b, 64, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [512, 4096])
+def test_group_tail_k_sampled_rows(mq, orc, bits, M):
+    """K = 11008 (a down projection whose K is not a multiple of 512): the
+    LDS-dequantizing GEMMs, 128 x 128 tiles at M = 512 (16 tiles of 256) and
+    256 x 256 tiles at M = 4096 (128 tiles)."""
+    K, N = 11008, 2048
+    rng = np.random.default_rng(99 + M + bits)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits,
+                            bias=bf16_dev(bias))
+    rows = np.unique(np.r_[0, 255, 256, M - 1, rng.integers(0, M, 5)])
+    assert_close(y[torch.from_numpy(rows).to(DEV)],
+                 orc.qmm(x[rows], wq, s, b, 64, bits, bias=bias))
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -462,3 +492,52 @@ def test_quantized_linear_module(mq, orc):
     e = seq[1](torch.tensor([1, 2], device=DEV))
     assert e.shape == (2, 128)
     assert seq[1].as_linear(e).shape == (2, 10)
+
+
+def test_nn_quantize_class_predicate(mq, orc):
+    """nn.quantize with the reference's class_predicate forms (models/qwen2.py:318-324,
+    models/lfm2.py:579-591): False leaves a module dense, a dict overrides
+    group_size/bits per path, True takes the defaults.  Each quantized layer's
+    codes equal the oracle's quantization of its bfloat16 weight, and its output
+    the oracle's matmul on them; the skipped layer is the original module."""
+    torch.manual_seed(1)
+    model = torch.nn.ModuleDict({
+        "q_proj": torch.nn.Linear(256, 128, bias=True),
+        "gate": torch.nn.Linear(256, 16, bias=False),
+        "lm_head": torch.nn.Linear(256, 96, bias=False),
+        "embed": torch.nn.Embedding(32, 256),
+    }).to(DEV).to(torch.bfloat16)
+    dense_gate = model["gate"]
+    before = {n: model[n].weight.detach().clone() for n in ("q_proj", "lm_head", "embed")}
+    seen = []
+
+    def predicate(path, module):
+        seen.append(path)
+        if path == "gate":
+            return False
+        if path == "lm_head":
+            return {"group_size": 64, "bits": 8}
+        return True
+
+    mq.nn.quantize(model, group_size=64, bits=4, class_predicate=predicate)
+    assert sorted(seen) == ["embed", "gate", "lm_head", "q_proj"]
+    assert model["gate"] is dense_gate
+    assert isinstance(model["q_proj"], mq.nn.QuantizedLinear) and model["q_proj"].bits == 4
+    assert isinstance(model["lm_head"], mq.nn.QuantizedLinear) and model["lm_head"].bits == 8
+    assert isinstance(model["embed"], mq.nn.QuantizedEmbedding) and model["embed"].bits == 4
+    x = torch.randn(5, 256, device=DEV).to(torch.bfloat16)
+    for name, bits in (("q_proj", 4), ("lm_head", 8), ("embed", 4)):
+        ql = model[name]
+        wq, s, b = u32_host(ql.weight), bits_host(ql.scales), bits_host(ql.biases)
+        ref_q = orc.quantize(bits_host(before[name]), 64, bits)
+        assert all(np.array_equal(a, r) for a, r in zip((wq, s, b), ref_q)), name
+    for name, bits in (("q_proj", 4), ("lm_head", 8)):
+        ql = model[name]
+        wq, s, b = u32_host(ql.weight), bits_host(ql.scales), bits_host(ql.biases)
+        bias = bits_host(ql.bias) if ql.bias is not None else None
+        assert_close(ql(x), orc.qmm(bits_host(x), wq, s, b, 64, bits, bias=bias))
+    emb = model["embed"]
+    ids = torch.tensor([0, 31, 7], device=DEV)
+    wq, s, b = u32_host(emb.weight), bits_host(emb.scales), bits_host(emb.biases)
+    assert np.array_equal(bits_host(emb(ids)),
+                          orc.dequantize(wq, s, b, 64, 4)[[0, 31, 7]])

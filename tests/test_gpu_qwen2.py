@@ -116,3 +116,53 @@ def test_small_decoder_shared_prefix_pages():
     full = torch.cat([prompt, toks], 1)[:, :-1]
     match, total, worst = greedy_agreement(reference_logits(mq, m, full), T, toks)
     assert match >= 0.9 * total and worst <= 0.05, (match, total, worst)
+
+
+def _per_position(a, b):
+    """Norm-wise relative error of every (row, position) logit vector."""
+    d = (a.float() - b.float()).abs().amax(-1)
+    return (d / b.float().abs().amax(-1)).flatten()
+
+
+def test_continuous_batching_7b_widths_shared_prefix():
+    """The continuous-batching workload at its own widths and batch, 2 layers
+    deep: Qwen2.5-7B widths (hidden 3584, MLP 18944, 28/4 heads, vocab 152064),
+    32 sequences with 1024-token prompts whose first 256 tokens are shared and
+    held once in shared pages (the reference's prefix-cache hit,
+    prefix_cache.py:364; slots as cache.py:459-471), page size 16, then 8
+    greedy decode steps: the skinny GEMMs at M = 32 with their fused reduces
+    and paged decode attention over ~1030 positions.
+
+    Checked: graph replay equals eager decode; the first token's logits with
+    the shared prefix equal a private prefill's; every decode step's logits
+    against the float32 restatement, within twice the distance between the
+    float32 restatement and one that rounds to bfloat16 wherever the model
+    stores bfloat16 (the error the bfloat16 graph itself carries) plus 1 %;
+    teacher-forced greedy tokens."""
+    import dataclasses
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = dataclasses.replace(q2.Qwen2Config.qwen25_7b(), num_hidden_layers=2)
+    m = q2.Qwen2Model.random(cfg, seed=0, device=DEV)
+    B, T, P, n = 32, 1024, 256, 8
+    prompt = torch.randint(0, cfg.vocab_size, (B, T),
+                           generator=torch.Generator(device=DEV).manual_seed(2), device=DEV)
+    prompt[:, :P] = prompt[0, :P]
+    steps = []
+    toks = m.generate(prompt, n, prefix_len=P, use_graph=False, logits_out=steps)
+    assert torch.equal(toks, m.generate(prompt, n, prefix_len=P))
+    private = []
+    m.generate(prompt, 1, logits_out=private)
+    assert _nrel(steps[0], private[0]) <= 2e-2
+    full = torch.cat([prompt, toks], 1)[:, :-1]
+    ref = reference_logits(mq, m, full, head_from=T - 1)
+    ref16 = reference_logits(mq, m, full, bf16_activations=True, head_from=T - 1)
+    dec = torch.stack(steps, 1)
+    e = _per_position(dec, ref)
+    e16 = _per_position(ref16, ref)
+    match, total, worst = greedy_agreement(ref, 1, toks)
+    print(f"config-4 shape (2 layers): decode logits err max {e.max():.4f} median "
+          f"{e.median():.4f}; bf16-storage restatement err max {e16.max():.4f}; greedy "
+          f"{match}/{total}, worst margin {worst:.3f} std")
+    assert e.max() <= 2 * e16.max() + 1e-2, (float(e.max()), float(e16.max()))
+    assert match >= 0.9 * total and worst <= 0.1, (match, total, worst)
