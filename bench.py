@@ -3,21 +3,22 @@
 Headline (the JSON line's `value`): mx.quantized_matmul as a decode GEMV,
 4-bit, group 64, x bf16 [1, 3584] against W [18944, 3584] -- the
 K=3584, N=18944 point of the quantized GEMM sweep, in HBM GB/s of algorithmic
-traffic (packed codes + scales + biases + x + y).  One step is one launch.
-16 weight replicas (611 MB, more than the 256 MB Infinity Cache) are used in
-rotation so every launch streams its weights from HBM.  The timed steps are
-replayed from a HIP graph so the GPU runs them back to back; HIP events on the
-launch stream bracket the timed region.
+traffic (packed codes + scales + biases + x + y).  16 weight replicas (611 MB,
+more than the 256 MB Infinity Cache) are used in rotation so every launch
+streams its weights from HBM; one step is one pass over them (16 launches,
+each on a different replica), so even a short run times hundreds of launches.
+The timed steps are replayed from a HIP graph so the GPU runs them back to
+back; HIP events on the launch stream bracket the timed region.
 
 Also reported: the full sweep M in {1,16,128,2048,8192} x (K,N) in
 {(3584,18944), (18944,3584), (3584,4608)} x bits {4,8} (GB/s, TFLOP/s and the
 fraction of the bounding roofline; for 4-bit M >= 128 also a dense bf16 GEMM
 of the same shape through torch.matmul, for scale), greedy decode of the
 Qwen2.5-7B-shaped 4-bit model (random init) at batch 1 and 32 in tokens/s,
-and the CPU baseline: the
-oracle's float32
-restatement of MLX's CPU quantized_matmul loop on the host cores, on a bounded
-sample of the headline workload.
+the read-only HBM floor (one launch reading the same bytes), and the CPU
+baseline: a vectorised float32 restatement of MLX's CPU quantized_matmul loop
+(not MLX, which is not installed) on every host thread the box allots, on a
+bounded sample of the headline workload.
 
     python bench.py [--steps 256] [--warmup 32] [--no-sweep] [--no-cpu] [--no-decode]
     python bench.py --profile   # eager launches + a copy kernel, for rocprofv3
@@ -52,8 +53,9 @@ def alg_bytes(M: int, N: int, K: int, bits: int) -> int:
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=64,
+                    help="timed steps; a step is one pass over the weight replicas")
+    ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--replicas", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -130,33 +132,75 @@ def read_traffic():
     return None
 
 
+def _host_cpu():
+    """Model name of the host CPU, from /proc/cpuinfo (what lscpu prints)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(args, orc, wq, s, b, x, N, K, bits):
-    threads = max(1, min(16, os.cpu_count() or 1))
-    orc.qmm_f32(x, wq, s, b, 64, bits, threads=threads)  # warm
+    """The float32 CPU loop on a bounded sample: as many calls of the headline
+    GEMV as fit in --cpu-seconds, on every thread this process may use
+    (its CPU affinity, capped by OMP_NUM_THREADS, which the GPU boxes set to
+    their per-GPU CPU share)."""
+    affinity = len(os.sched_getaffinity(0))
+    threads = affinity
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
+    orc.qmm_f32_lanes(x, wq, s, b, 64, bits, threads=threads)  # warm
     calls, t0 = 0, time.perf_counter()
     while True:
-        orc.qmm_f32(x, wq, s, b, 64, bits, threads=threads)
+        orc.qmm_f32_lanes(x, wq, s, b, 64, bits, threads=threads)
         calls += 1
         el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or calls >= 20000:
+        if el >= args.cpu_seconds or calls >= 200000:
             break
     gbs = alg_bytes(1, N, K, bits) * calls / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{calls} calls ({el:.1f} s) of the 4-bit K={K} N={N} M=1 qmv: the oracle's "
-                      "float32 restatement of MLX's CPU quantized_matmul loop, OpenMP over rows"}
+            "label": "restatement, not MLX",
+            "host": {"cpu": _host_cpu(), "nproc": os.cpu_count(), "affinity": affinity,
+                     "omp_num_threads": os.environ.get("OMP_NUM_THREADS")},
+            "sample": f"{calls} calls ({el:.1f} s) of the 4-bit K={K} N={N} M=1 qmv: a float32 "
+                      "restatement of MLX's CPU quantized_matmul loop (w = s*q + b, x*w summed "
+                      "in 16 float32 lanes per output), gcc -O3 AVX2/FMA, OpenMP over rows"}
 
 
-def hbm_floor(torch, nbytes: int, count: int = 16):
-    """Device-to-device copies moving `nbytes` in total (half read, half written),
-    `count` rotating sources so every copy reads from HBM: what one launch of a
-    plain streaming kernel of the GEMV's size achieves."""
+def hbm_floor(mq, torch, nbytes: int, count: int = 16):
+    """What one launch of a plain streaming kernel of the GEMV's size achieves:
+    `read`, a read-only kernel (mq_hbm_read) over `nbytes`, and `copy`, a device
+    copy moving `nbytes` in total (half read, half written); `count` rotating
+    buffers so every launch reads from HBM."""
+    import ctypes
+
+    L = mq._lib.lib()
+    nbytes -= nbytes % 16
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda:0").fill_(i) for i in range(count)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+
+    def read(i):
+        mq._lib.check(L.mq_hbm_read(ctypes.c_void_p(bufs[i % count].data_ptr()),
+                                    ctypes.c_size_t(nbytes), ctypes.c_void_p(sink.data_ptr()),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                      "hbm_read")
+
+    rms, _ = time_graph(torch, read, 256, warmup=8)
+    del bufs
     half = nbytes // 4  # bf16 elements per direction
     srcs = [torch.empty(half, dtype=torch.bfloat16, device="cuda:0").fill_(i) for i in range(count)]
     dst = torch.empty(half, dtype=torch.bfloat16, device="cuda:0")
-    ms, _ = time_graph(torch, lambda i: dst.copy_(srcs[i % count]), 256, warmup=8)
+    cms, _ = time_graph(torch, lambda i: dst.copy_(srcs[i % count]), 256, warmup=8)
     del srcs, dst
-    return {"kind": "device copy (torch copy_), one launch per step", "bytes": 4 * half,
-            "us": round(ms * 1e3, 3), "GBps": round(4 * half / (ms * 1e-3) / 1e9, 1)}
+    return {"read": {"kind": "read-only kernel (mq_hbm_read), one launch per buffer",
+                     "bytes": nbytes, "us": round(rms * 1e3, 3),
+                     "GBps": round(nbytes / (rms * 1e-3) / 1e9, 1)},
+            "copy": {"kind": "device copy (torch copy_), one launch per step", "bytes": 4 * half,
+                     "us": round(cms * 1e3, 3), "GBps": round(4 * half / (cms * 1e-3) / 1e9, 1)}}
 
 
 def _weight_bytes(model, batch: int) -> int:
@@ -341,7 +385,8 @@ def main():
                           "copy_bytes_each_way": src.numel() * 2}))
         return
 
-    ms, wall_ms = time_graph(torch, launch, args.steps, args.warmup)
+    R = len(replicas)  # launches per step: one pass over the replicas
+    ms, wall_ms = time_graph(torch, launch, args.steps * R, args.warmup * R)
     by = alg_bytes(M, N, K, bits)
     gbs = by / (ms * 1e-3) / 1e9
     traffic = read_traffic()
@@ -353,8 +398,11 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "settle_s": SETTLE_S,
-        "ms_per_step": round(ms, 6),
-        "ms_per_step_wall": round(wall_ms, 6),
+        "ms_per_step": round(ms * R, 6),
+        "ms_per_step_wall": round(wall_ms * R, 6),
+        "launches_per_step": R,
+        "launches_timed": args.steps * R,
+        "us_per_launch": round(ms * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -362,14 +410,15 @@ def main():
         "data": "synthetic: W ~ N(0,0.02) (seeds 0..15) cast to bf16 and quantized on the GPU; "
                 "x ~ N(0,1) bf16 (seed 1)",
         "config": {"workload": "quantized_matmul decode GEMV (qmv): 4-bit affine, group 64, "
-                               "x bf16 [1,3584] @ W[18944,3584]^T, 16 rotating weight replicas",
+                               f"x bf16 [1,3584] @ W[18944,3584]^T; a step is {R} launches, "
+                               f"one per rotating weight replica",
                    "M": M, "K": K, "N": N, "bits": bits, "group_size": 64,
-                   "bytes_per_step": by},
+                   "bytes_per_launch": by, "bytes_per_step": by * R},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
     }
-    line["hbm_floor"] = hbm_floor(torch, by)
+    line["hbm_floor"] = hbm_floor(mq, torch, by)
     if not args.no_decode:
         # Qwen2.5-7B shape, 4-bit: batch 1 (512-token prompt, 128 tokens) and
         # batch 32 (1024-token prompts, 256 tokens).

@@ -1,0 +1,32 @@
+/*
+ * mq_measure.h -- measurement helper of libmi355q (no counterpart in the
+ * reference: it exists so that a benchmark can time the hardware floor the
+ * quantized GEMV is compared with).
+ */
+#ifndef MQ_MEASURE_H
+#define MQ_MEASURE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Read `bytes` bytes at device address src once, in the decode GEMV's load
+ * pattern (16-byte non-temporal buffer loads, 64 consecutive chunks per wave
+ * instruction), and write nothing unless the XOR of every word is 0x9e3779b9
+ * (then that value to sink[0]): one launch whose time is the read-only HBM
+ * floor for a kernel streaming the same bytes.  src 16-byte aligned, bytes a
+ * multiple of 16 and below 2^32.  Returns MQ_OK (0), MQ_ERR_INVALID (-1) or
+ * MQ_ERR_HIP (-3); the message is mq_last_error()'s.
+ */
+int mq_hbm_read(const void* src, size_t bytes, uint32_t* sink, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MQ_MEASURE_H */

@@ -1,4 +1,4 @@
-"""ctypes binding of libmi355q.so (declarations in include/mq.h).
+"""ctypes binding of libmi355q.so (declarations in include/mq.h, include/mq_measure.h).
 
 The library is loaded from this package directory.  There is no fallback: if
 it is missing or cannot be loaded, every op raises.
@@ -18,7 +18,7 @@ MQ_ERR_INVALID = -1
 MQ_ERR_UNSUPPORTED = -2
 MQ_ERR_HIP = -3
 
-# Every symbol include/mq.h declares (checked by the CPU test suite).
+# Every symbol include/*.h declares (checked by the CPU test suite).
 EXPORTS = (
     "mq_version",
     "mq_last_error",
@@ -51,6 +51,7 @@ EXPORTS = (
     "mq_quantized_matmul_add_rms_norm",
     "mq_gather_qmm_swiglu_supported",
     "mq_gather_qmm_swiglu",
+    "mq_hbm_read",          # include/mq_measure.h
 )
 
 _lock = threading.Lock()
@@ -111,6 +112,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_gather_qmm_swiglu_supported.argtypes = [_i64, _i64, _i64, _i64, _int, _int]
     L.mq_gather_qmm_swiglu.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _int, _int, _p]
+    L.mq_hbm_read.argtypes = [_p, ctypes.c_size_t, _p, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
     L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t

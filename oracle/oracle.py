@@ -17,7 +17,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_FAST_PATH = os.path.join(_HERE, "libcpu_baseline.so")
 _lib = None
+_fast = None
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
@@ -29,9 +31,23 @@ _int = ctypes.c_int
 
 
 def build() -> str:
-    """Compile oracle/liboracle.so with its Makefile."""
+    """Compile oracle/liboracle.so (and the CPU-baseline loop) with its Makefile."""
     subprocess.run(["make", "-s", "-C", _HERE], check=True)
     return _LIB_PATH
+
+
+def fast_lib():
+    """oracle/libcpu_baseline.so: the vectorised float32 loop bench.py times."""
+    global _fast
+    if _fast is None:
+        if not os.path.exists(_FAST_PATH):
+            build()
+        L = ctypes.CDLL(_FAST_PATH)
+        L.cpu_qmm_f32_lanes.argtypes = [_u16p, _u32p, _u16p, _u16p, _i64, _i64, _i64, _int, _int,
+                                        _u16p, _int]
+        L.cpu_qmm_f32_lanes.restype = _int
+        _fast = L
+    return _fast
 
 
 def lib():
@@ -152,6 +168,22 @@ def qmm_f32(x_bf16, wq, scales, biases, group_size=64, bits=4, threads=1) -> np.
                              _p(np.ascontiguousarray(scales, np.uint16), _u16p),
                              _p(np.ascontiguousarray(biases, np.uint16), _u16p),
                              M, N, K, group_size, bits, _p(y, _u16p), threads), "qmm_f32")
+    return y
+
+
+def qmm_f32_lanes(x_bf16, wq, scales, biases, group_size=64, bits=4, threads=1) -> np.ndarray:
+    """qmm_f32's arithmetic with 16 partial sums per output (vectorised, -O3):
+    the CPU baseline's timed loop -> bfloat16 bits [M, N]."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    K = x.shape[-1]
+    M = int(np.prod(x.shape[:-1])) if x.ndim > 1 else 1
+    N = wq.shape[0]
+    y = np.empty(x.shape[:-1] + (N,), np.uint16)
+    _check(fast_lib().cpu_qmm_f32_lanes(
+        _p(x, _u16p), _p(np.ascontiguousarray(wq, np.uint32), _u32p),
+        _p(np.ascontiguousarray(scales, np.uint16), _u16p),
+        _p(np.ascontiguousarray(biases, np.uint16), _u16p),
+        M, N, K, group_size, bits, _p(y, _u16p), threads), "qmm_f32_lanes")
     return y
 
 

@@ -1,6 +1,6 @@
 """Host-side checks that need no GPU.
 
-* libmi355q.so loads and exports every function include/mq.h declares;
+* libmi355q.so loads and exports every function include/*.h declares;
 * the C ABI rejects what MLX rejects (MQ_ERR_INVALID), flags what this backend
   does not implement (MQ_ERR_UNSUPPORTED), and returns before any launch, so
   these calls run without a device (null pointers are never dereferenced);
@@ -11,6 +11,7 @@
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 
@@ -19,12 +20,15 @@ import torch
 
 from conftest import ROOT
 
-HEADER = os.path.join(ROOT, "include", "mq.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mq_\w+)\s*\(", text, re.M)))
+    names = set()
+    for path in HEADERS:
+        text = open(path).read()
+        names |= set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mq_\w+)\s*\(", text, re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_abi():
@@ -40,7 +44,7 @@ def test_header_declares_the_abi():
         "mq_rms_norm_quantized_matmul", "mq_quantized_matmul_swiglu_workspace",
         "mq_quantized_matmul_swiglu_ws", "mq_quantized_matmul_add_rms_norm_supported",
         "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm",
-        "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu"])
+        "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu", "mq_hbm_read"])
 
 
 def test_library_exports_every_declared_symbol(mq):

@@ -218,6 +218,11 @@ def test_qmm_f32_variant_close_to_double(orc, bits):
     assert normwise_rel_err(y, ref) < 5e-3  # bfloat16 output rounding dominates
     y1 = orc.qmm_f32(x, wq, s, b, 64, bits, threads=1)
     assert np.array_equal(orc.bf16_to_f32(y1), y)
+    # the vectorised loop the CPU baseline times: same products, 16 partial sums
+    yl = orc.bf16_to_f32(orc.qmm_f32_lanes(x, wq, s, b, 64, bits, threads=2))
+    assert normwise_rel_err(yl, ref) < 5e-3
+    assert np.array_equal(orc.qmm_f32_lanes(x, wq, s, b, 64, bits, threads=1),
+                          orc.f32_to_bf16(yl))
 
 
 # ---------------------------------------------------------------- gather_qmm
