@@ -23,7 +23,8 @@
  *   - Return value: MQ_OK, or a negative code with a message available from
  *     mq_last_error() on the calling thread.  Validation happens before any
  *     launch, so a failed call enqueues nothing.
- *   - Reentrant: no mutable global state besides the thread-local message.
+ *   - Reentrant: no mutable global state besides the thread-local message
+ *     (and mq_quantized_matmul_noalloc's per-GPU array, see there).
  */
 #ifndef MQ_H
 #define MQ_H
@@ -114,6 +115,27 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
                            const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
                            int64_t N, int64_t K, int group_size, int bits, int transpose,
                            void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * mq_quantized_matmul_ws without a workspace argument and without any
+ * allocation: the split-K partial sums live in a device array of this library
+ * (MQ_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; resolved
+ * once per device on its first call there).  No counterpart in the reference:
+ * it is for callers that cannot allocate (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  Same arguments, kernels, split plan
+ * and results bit for bit as mq_quantized_matmul_ws with
+ * mq_quantized_matmul_workspace() bytes.  Shapes whose plan needs more than
+ * MQ_NOALLOC_SCRATCH_BYTES (mq_quantized_matmul_workspace) return
+ * MQ_ERR_INVALID before any launch.  Every call on one GPU shares its array:
+ * calls that overlap on one GPU (unordered streams) race; order them on one
+ * stream.  The array is used on the device of `stream` (the current device
+ * for the NULL stream).
+ */
+#define MQ_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int mq_quantized_matmul_noalloc(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
+                                const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y,
+                                int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                int transpose, hipStream_t stream);
 
 /*
  * mx.gather_qmm(x, wq, scales, biases, lhs_indices, rhs_indices,

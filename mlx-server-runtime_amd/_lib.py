@@ -51,6 +51,7 @@ EXPORTS = (
     "mq_quantized_matmul_add_rms_norm",
     "mq_gather_qmm_swiglu_supported",
     "mq_gather_qmm_swiglu",
+    "mq_quantized_matmul_noalloc",
     "mq_hbm_read",          # include/mq_measure.h
 )
 
@@ -112,6 +113,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_gather_qmm_swiglu_supported.argtypes = [_i64, _i64, _i64, _i64, _int, _int]
     L.mq_gather_qmm_swiglu.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                        _i64, _int, _int, _p]
+    L.mq_quantized_matmul_noalloc.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int,
+                                              _int, _int, _p]
     L.mq_hbm_read.argtypes = [_p, ctypes.c_size_t, _p, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int

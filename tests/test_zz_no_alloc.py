@@ -1,0 +1,73 @@
+"""mq_quantized_matmul_noalloc (split-K partial sums in the library's own
+per-GPU device array) against mq_quantized_matmul_ws (a caller workspace),
+through the C ABI: bit-identical outputs -- the same kernels, split plan and
+fixed-order reduce -- on two calls in a row, the second smaller; shapes
+whose plan needs more than the array are refused before any launch."""
+
+from __future__ import annotations
+
+import ctypes
+import importlib
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+SCRATCH_BYTES = 16 << 20
+
+
+def _lib():
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    return mq, mq._lib.lib()
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _case(mq, L, M, N, K, bits, seed, bias):
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = core.quantize(w, 64, bits)
+    x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    bv = (torch.randn(N, generator=g, device=DEV) * 0.1).to(torch.bfloat16) if bias else None
+    need = L.mq_quantized_matmul_workspace(M, N, K, 64, bits)
+    assert need <= SCRATCH_BYTES, need
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV) if need else None
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    mq._lib.check(L.mq_quantized_matmul_ws(_ptr(x), _ptr(wq), _ptr(sc), _ptr(bi), _ptr(bv),
+                                           _ptr(ref), M, N, K, 64, bits, 1, _ptr(ws),
+                                           ctypes.c_size_t(need), stream), "ws")
+    mq._lib.check(L.mq_quantized_matmul_noalloc(_ptr(x), _ptr(wq), _ptr(sc), _ptr(bi), _ptr(bv),
+                                                _ptr(out), M, N, K, 64, bits, 1, stream),
+                  "noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), (M, N, K, bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_noalloc_equals_workspace_entry(bits):
+    """The down projection at 128 rows (14 MiB of partial sums), then the same
+    matrix at 32 rows (a smaller plan reusing the array), the fused QKV at 16
+    rows, each bit-equal to the workspace entry; a GEMV that needs no scratch
+    (M = 1) passes through unchanged."""
+    mq, L = _lib()
+    print(f"noalloc bits={bits}: M=128 then M=32, N=3584, K=18944", flush=True)
+    _case(mq, L, 128, 3584, 18944, bits, seed=1, bias=False)
+    _case(mq, L, 32, 3584, 18944, bits, seed=2, bias=True)
+    _case(mq, L, 16, 4608, 3584, bits, seed=3, bias=True)
+    assert L.mq_quantized_matmul_workspace(1, 18944, 3584, 64, bits) == 0
+    _case(mq, L, 1, 18944, 3584, bits, seed=4, bias=False)
+
+
+def test_noalloc_refuses_beyond_the_array():
+    mq, L = _lib()
+    M, N, K = 2048, 3584, 18944
+    assert L.mq_quantized_matmul_workspace(M, N, K, 64, 4) > SCRATCH_BYTES
+    rc = L.mq_quantized_matmul_noalloc(None, None, None, None, None, None, M, N, K, 64, 4, 1, None)
+    assert rc == mq._lib.MQ_ERR_INVALID
+    assert b"use mq_quantized_matmul_ws" in L.mq_last_error()
