@@ -74,25 +74,100 @@ def test_decoder_7b_widths_4_layers():
 
 
 def test_decoder_qwen25_7b_shape_64_tokens():
-    """Full Qwen2.5-7B shape, 512-token prompt, 64 greedy tokens.  Greedy
-    agreement is reported against both restatements: float32 throughout, and
-    bfloat16 at the storage points the model (and MLX) round at.  Random
-    weights leave many near-ties among 152064 logits, so the bound that
-    matters is on the margins of the disagreements."""
+    """Full Qwen2.5-7B shape (N(0, 0.02) random weights), 512-token prompt, 64
+    greedy tokens, teacher-forced against two restatements of the graph:
+    float32 throughout (ref32), and one that rounds to bfloat16 wherever the
+    model -- and MLX -- store bfloat16 (ref16).
+
+    On random weights ref16 itself picks a different token than ref32 at about
+    a sixth of these positions: rounding to bfloat16 moves every logit by up to
+    eps16 = max|ref16 - ref32| (~0.25, the logit std being ~1.2), and the top
+    two of 152064 random logits are often closer than that.  So no bfloat16
+    implementation, MLX included, can match ref32 64/64 here; the bound that
+    is derived instead, per position p:
+    * the kernels' logit error eps_p = max|ours - ref32| is at most 3 eps16_p
+      (the bfloat16 storage error; measured at most 2.5x);
+    * where our token differs from ref32's argmax, ref32's top-2 margin is at
+      most eps16_p: the bfloat16 rounding alone could flip it.
+    Zero disagreements are allowed at positions whose margin exceeds that.
+    The 64/64 identity is asserted on a model with confident predictions
+    (test_qwen25_7b_confident_continuation_64_tokens)."""
     mq = importlib.import_module("mlx-server-runtime_amd")
     q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
     cfg = q2.Qwen2Config.qwen25_7b()
-    toks, toks_graph, e_pre, e_dec, (match, total, worst) = _run(cfg, 1, 512, 64)
-    m, full = _run.last
-    ref16 = reference_logits(mq, m, full, bf16_activations=True)
-    match16, _, worst16 = greedy_agreement(ref16, 512, toks)
-    print(f"7B greedy: {match}/{total} tokens equal the float32 restatement's argmax "
-          f"(largest margin among the others {worst:.3f} std), {match16}/{total} the "
-          f"bfloat16-storage restatement's ({worst16:.3f} std); logits rel err {e_pre:.3f}")
-    assert torch.equal(toks, toks_graph)
-    assert e_pre <= 0.25 and e_dec <= 0.15, (e_pre, e_dec)
-    assert worst <= 0.5 and worst16 <= 0.5, (worst, worst16)
-    assert match >= 0.6 * total and match16 >= 0.6 * total, (match, match16, total)
+    T, n = 512, 64
+    m = q2.Qwen2Model.random(cfg, seed=0, device=DEV)
+    prompt = torch.randint(0, cfg.vocab_size, (1, T),
+                           generator=torch.Generator(device=DEV).manual_seed(2), device=DEV)
+    steps = []
+    toks = m.generate(prompt, n, use_graph=False, logits_out=steps)
+    assert torch.equal(toks, m.generate(prompt, n))
+    dec = torch.stack(steps, 1)[0].float()
+    full = torch.cat([prompt, toks], 1)[:, :-1]
+    r32 = reference_logits(mq, m, full, head_from=T - 1)[0]
+    r16 = reference_logits(mq, m, full, bf16_activations=True, head_from=T - 1)[0]
+    eps = (dec - r32).abs().amax(-1)
+    eps16 = (r16 - r32).abs().amax(-1)
+    top2 = r32.topk(2, -1).values
+    margin = top2[:, 0] - top2[:, 1]
+    differ = r32.argmax(-1) != toks[0]
+    match16 = int((r16.argmax(-1) == toks[0]).sum())
+    print(f"7B greedy: {n - int(differ.sum())}/{n} tokens equal ref32's argmax, {match16}/{n} "
+          f"ref16's; ref16 itself differs from ref32 at "
+          f"{int((r16.argmax(-1) != r32.argmax(-1)).sum())}; eps/eps16 max "
+          f"{float((eps / eps16).max()):.2f}; margin/eps16 at our differences "
+          f"{[round(float(v), 2) for v in (margin / eps16)[differ]]}")
+    assert bool((eps <= 3 * eps16).all()), (eps / eps16).max()
+    assert bool((margin[differ] <= eps16[differ]).all()), (margin / eps16)[differ]
+
+
+def test_qwen25_7b_confident_continuation_64_tokens():
+    """64/64 greedy-token identity at the full Qwen2.5-7B shape, on a model whose
+    predictions are confident, as a trained model's are: the random model of
+    the test above with an LM head that has learned a 64-token continuation.
+    For a target sequence of 64 distinct tokens, the float32 restatement's
+    final hidden states h_p at the 64 predicting positions (teacher-forced on
+    prompt + target) give dual directions d_p (the pseudo-inverse: d_p . h_q =
+    [p == q]); the head row of target token p gains 20 d_p (then the head is
+    re-quantized), which lifts that token's logit by ~20 at position p only.
+
+    Free-running greedy decode through the kernels must reproduce the target
+    64/64, and both restatements' argmax must equal it at every position
+    (teacher-forced, so their own greedy decode yields it too, by induction);
+    every position's top-1 margin is at least 4x the kernels' logit error."""
+    from qwen2_reference import reference_hidden
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    cfg = q2.Qwen2Config.qwen25_7b()
+    T, n, gain = 512, 64, 20.0
+    m = q2.Qwen2Model.random(cfg, seed=0, device=DEV)
+    prompt = torch.randint(0, cfg.vocab_size, (1, T),
+                           generator=torch.Generator(device=DEV).manual_seed(2), device=DEV)
+    target = torch.randperm(cfg.vocab_size, generator=torch.Generator(device=DEV).manual_seed(3),
+                            device=DEV)[:n]
+    seq = torch.cat([prompt[0], target[:-1]])[None]
+    H = reference_hidden(mq, m, seq, head_from=T - 1)[0]                # [n, hidden]
+    D = torch.linalg.pinv(H.double().t()).float()                       # D @ H^T = I
+    head = m.lm_head
+    W = mq.dequantize(head.wq, head.scales, head.biases, 64, 4).float()
+    W[target] += gain * D
+    wq, sc, bi = core.quantize(W.to(torch.bfloat16), 64, 4)
+    del W
+    m.lm_head = q2.QLinear(wq, sc, bi, None, 64, 4)
+    steps = []
+    toks = m.generate(prompt, n, logits_out=steps)
+    dec = torch.stack(steps, 1)[0].float()
+    assert torch.equal(toks[0], target), int((toks[0] == target).sum())
+    full = torch.cat([prompt, toks], 1)[:, :-1]
+    for bf16 in (False, True):
+        ref = reference_logits(mq, m, full, bf16_activations=bf16, head_from=T - 1)[0]
+        assert torch.equal(ref.argmax(-1), target), bf16
+        top2 = ref.topk(2, -1).values
+        ratio = (top2[:, 0] - top2[:, 1]) / (dec - ref).abs().amax(-1)
+        print(f"confident 7B: 64/64 tokens; {'ref16' if bf16 else 'ref32'} margin / logit "
+              f"error min {float(ratio.min()):.1f}")
+        assert float(ratio.min()) >= 4.0
 
 
 def test_small_decoder_shared_prefix_pages():
