@@ -153,7 +153,7 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
   if (use_skinny(M, N, K, bits)) return mq::qmms_workspace_bytes(M, N, K, bits);
   if (dense_gemv(M, N, K, bits) || mq::qmv_fits(M, N, K, bits, 1)) return 0;
-  if (mq::qmm3_fits(M, N, K, bits)) return mq::qmm3_workspace_bytes(M, N, K);
+  if (mq::qmm4_fits(M, N, K, bits)) return mq::qmm4_workspace_bytes(M, N, K);
   return 0;
 }
 
@@ -369,10 +369,10 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
     e = mq::launch_qmms(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
-  } else if (mq::qmm3_fits(M, N, K, bits)) {
+  } else if (mq::qmm4_fits(M, N, K, bits)) {
     if (workspace && !aligned16(workspace))
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
-    e = mq::launch_qmm3(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
+    e = mq::launch_qmm4(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
   } else if (mq::qmm2_fits(M, N, K, bits)) {
     e = mq::launch_qmm2(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);

@@ -64,13 +64,14 @@ hipError_t launch_qmm2(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, hipStream_t stream);
 
-// 256x256-tile MFMA path with weights dequantized in registers (qmm3_fits:
-// K a multiple of 512, >= 128 tiles, 32-bit offsets).
-// Few tiles and a long K: K is split over blocks through a float32 workspace
-// of qmm3_workspace_bytes (without it the launch runs unsplit).
-bool qmm3_fits(int64_t M, int64_t N, int64_t K, int bits);
-size_t qmm3_workspace_bytes(int64_t M, int64_t N, int64_t K);
-hipError_t launch_qmm3(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+// 256x256-tile MFMA path with weights dequantized in registers (qmm4_fits:
+// K a multiple of 512, >= 128 tiles, 32-bit offsets), one wave per SIMD, each
+// owning the block's 256 rows for 64 columns (every code dequantized once per
+// block).  Few tiles and a long K: K is split over blocks through a float32
+// workspace of qmm4_workspace_bytes (without it the launch runs unsplit).
+bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits);
+size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K);
+hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
