@@ -10,7 +10,9 @@ each on a different replica), so even a short run times hundreds of launches.
 The timed steps are replayed from a HIP graph so the GPU runs them back to
 back; HIP events on the launch stream bracket the timed region.
 
-Also reported: the full sweep M in {1,16,128,2048,8192} x (K,N) in
+Also reported: the expert GEMMs of an MoE layer's prefill (gather_qmm over
+32768 expert-sorted (token, expert) pairs at the Qwen3-30B-A3B shape), the
+full sweep M in {1,16,128,2048,8192} x (K,N) in
 {(3584,18944), (18944,3584), (3584,4608)} x bits {4,8} (GB/s, TFLOP/s and the
 fraction of the bounding roofline; for 4-bit M >= 128 also a dense bf16 GEMM
 of the same shape through torch.matmul, for scale), greedy decode of the
@@ -325,6 +327,50 @@ def sweep(mq, torch):
     return rows
 
 
+def gather_sweep(mq, torch):
+    """The expert GEMMs of one MoE layer's prefill at the Qwen3-30B-A3B shape:
+    8 x 512 tokens routed to 8 of 128 experts (uniform random), the 32768
+    (token, expert) pairs sorted by expert (models/lfm2.py:204,613-618), then
+    gather_qmm over the sorted rows (models/lfm2.py:176-187) -- the experts'
+    gate|up projection (2 x 768 rows, K = 2048, x rows gathered by token) and
+    the down projection (2048 rows, K = 768, rows already in pair order).  `us`
+    is given the sort's segment offsets (as the MoE block passes them);
+    `us_segments_derived` is the drop-in call that derives them from the ids."""
+    E, k, H, inter, T = 128, 8, 2048, 768, 4096
+    gen = torch.Generator(device="cuda:0").manual_seed(3)
+    ids = torch.rand(T, E, generator=gen, device="cuda:0").topk(k, -1).indices.reshape(-1)
+    order = torch.sort(ids, stable=True).indices
+    rhs = ids[order].to(torch.int32).contiguous()
+    lhs = (order // k).to(torch.int32).contiguous()
+    offs = torch.searchsorted(rhs, torch.arange(E + 1, device="cuda:0", dtype=torch.int32)
+                              ).to(torch.int32)
+    x = torch.randn(T, 1, H, generator=gen, device="cuda:0").to(torch.bfloat16)
+    act = torch.randn(T * k, 1, inter, generator=gen, device="cuda:0").to(torch.bfloat16)
+    rows = []
+    for name, N, K, xin, lhs_i in (("gate|up", 2 * inter, H, x, lhs), ("down", H, inter, act, None)):
+        w = (torch.randn(E * N, K, generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16)
+        wq, sc, bi = (t.reshape(E, N, -1) for t in mq.quantize(w, 64, 4))
+        del w
+
+        def launch(i, xin=xin, wq=wq, sc=sc, bi=bi, lhs_i=lhs_i, seg=offs):
+            mq.gather_qmm(xin, wq, sc, bi, lhs_indices=lhs_i, rhs_indices=rhs, group_size=64,
+                          bits=4, sorted_indices=True, expert_offsets=seg)
+
+        ms, _ = time_graph(torch, launch, 8, warmup=2, reps=4)
+        ms_derive, _ = time_graph(torch, lambda i: launch(i, seg=None), 8, warmup=2, reps=4)
+        flops = 2.0 * T * k * N * K
+        wbytes = E * (N * K // 2 + N * (K // 64) * 4)
+        tfl = flops / (ms * 1e-3) / 1e12
+        rows.append({"gemm": name, "pairs": T * k, "experts": E, "N": N, "K": K, "bits": 4,
+                     "us": round(ms * 1e3, 2), "TFLOPs": round(tfl, 2),
+                     "us_segments_derived": round(ms_derive * 1e3, 2),
+                     "GBps": round((wbytes + 2 * T * k * (N + K)) / (ms * 1e-3) / 1e9, 1),
+                     "bound": "mfma", "frac": round(tfl / BF16_PEAK_TFLOPS, 4)})
+        del wq, sc, bi
+    torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -427,6 +473,7 @@ def main():
                           decode_bench(torch, 8, 512, 128, model_name="qwen3_30b_a3b")]
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
+        line["gather_sweep"] = gather_sweep(mq, torch)
     if not args.no_cpu:
         wq, s, b = replicas[0]
         line["cpu_baseline"] = cpu_baseline(

@@ -145,14 +145,40 @@ int mq_quantized_matmul_noalloc(const mq_bf16* x, const uint32_t* wq, const mq_b
  * [E, N, K/group_size]; lhs int32 [T] or NULL (identity, needs x_batches == T);
  * rhs int32 [T]; y bfloat16 [T, M, N].  sorted_indices is the caller's promise
  * that rhs is non-decreasing (models/lfm2.py:202-218 sorts when it has >= 64
- * rows); results do not depend on it.  A t whose lhs/rhs is out of range gets
- * zeros.  Replaces QuantizedSwitchLinear.__call__ (models/lfm2.py:176-187).
+ * rows), as MLX's sorted path assumes: with it and more than 64 rows, tiles are
+ * cut along the experts' segments of rhs, and an rhs that is not
+ * non-decreasing gives wrong rows.  Without it the result is the same for any
+ * order.  A t whose lhs/rhs is out of range gets zeros.  Replaces
+ * QuantizedSwitchLinear.__call__ (models/lfm2.py:176-187).
  */
 int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* rhs_indices,
                   const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases, mq_bf16* y,
                   int64_t T, int64_t M, int64_t N, int64_t K, int64_t E, int64_t x_batches,
                   int group_size, int bits, int transpose, int sorted_indices,
                   hipStream_t stream);
+
+/*
+ * mq_gather_qmm with sorted_indices = 1 for rows sorted by mq_moe_sort or
+ * mq_moe_route_sort, given the segment offsets the sort wrote: expert e's
+ * batches are t in [expert_offsets[e], expert_offsets[e + 1]) (int32 [E + 1],
+ * device memory), batches from expert_offsets[E] on hold ids >= E (zeros).
+ * The same arguments and results as mq_gather_qmm otherwise.  The sorted GEMM
+ * cuts its tiles along these segments; without the offsets (mq_gather_qmm) it
+ * first derives them from rhs.  With swiglu, every expert's matrix is 2N rows
+ * (gate rows, then up rows: wq [E, 2N, K * bits / 32]) and y [T, M, N] =
+ * mq_silu_mul of the 2N-column product, bit for bit (SwitchGLU's gate and up
+ * projections and nn.silu(gate) * up, models/lfm2.py:208-214), with no
+ * [T, M, 2N] intermediate; shapes it does not take return
+ * MQ_ERR_UNSUPPORTED.  No counterpart in the reference: the call SwitchGLU
+ * makes after _gather_sort (models/lfm2.py:176-187,204,613-618), where MLX
+ * derives the segments itself.
+ */
+int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
+                           const int32_t* rhs_indices, const int32_t* expert_offsets,
+                           const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases,
+                           mq_bf16* y, int64_t T, int64_t M, int64_t N, int64_t K, int64_t E,
+                           int64_t x_batches, int group_size, int bits, int swiglu,
+                           hipStream_t stream);
 
 /*
  * SwitchGLU's gate and up projections and silu(gate) * up for gathered
@@ -280,7 +306,9 @@ int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inte
  * lanes: the dot2 GEMV with a SwiGLU epilogue, no workspace), and the skinny
  * GEMM's split-K plans (e.g. M = 32: its fixed-order reduce applies the
  * SwiGLU; needs mq_quantized_matmul_swiglu_workspace bytes, which is what
- * mq_quantized_matmul_workspace gives the unfused product).
+ * mq_quantized_matmul_workspace gives the unfused product); and for prefill
+ * shapes the large-M GEMM runs unsplit (SiLU * up in its epilogue, no
+ * workspace).
  * mq_quantized_matmul_swiglu_supported says whether a shape is taken; others
  * return MQ_ERR_UNSUPPORTED.  mq_quantized_matmul_swiglu is the _ws form
  * without a workspace.
@@ -371,11 +399,14 @@ int mq_moe_route(const mq_bf16* logits, const float* expert_bias, int64_t tokens
  * expert ids [n] (n = tokens * top_k): sorted_ids[p] = ids[order[p]],
  * inverse[order[p]] = p, and rows[p] = order[p] / top_k (the x row that
  * mq_gather_qmm takes as lhs index; rows may be NULL).  Ids outside
- * [0, num_experts) sort last, unchanged.  int32 throughout; one block.
+ * [0, num_experts) sort last, unchanged.  expert_offsets (int32
+ * [num_experts + 1], or NULL) receives where each expert's run of sorted_ids
+ * starts (the last entry counts the ids inside [0, num_experts)), for
+ * mq_gather_qmm_segments.  int32 throughout; one block.
  */
 int mq_moe_sort(const int32_t* expert_ids, int64_t n, int top_k, int num_experts,
                 int32_t* sorted_ids, int32_t* order, int32_t* inverse, int32_t* rows,
-                hipStream_t stream);
+                int32_t* expert_offsets, hipStream_t stream);
 
 /*
  * _scatter_unsort (models/lfm2.py:621-622) and the score-weighted sum over the
@@ -397,7 +428,7 @@ int mq_moe_combine(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scor
 int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t tokens,
                       int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
                       mq_bf16* scores, int32_t* sorted_ids, int32_t* order, int32_t* inverse,
-                      int32_t* rows, hipStream_t stream);
+                      int32_t* rows, int32_t* expert_offsets, hipStream_t stream);
 
 /*
  * mq_moe_combine, then the residual add and the RMSNorm that follow the MoE

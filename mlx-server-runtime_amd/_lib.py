@@ -52,6 +52,7 @@ EXPORTS = (
     "mq_gather_qmm_swiglu_supported",
     "mq_gather_qmm_swiglu",
     "mq_quantized_matmul_noalloc",
+    "mq_gather_qmm_segments",
     "mq_hbm_read",          # include/mq_measure.h
 )
 
@@ -92,9 +93,10 @@ def _declare(L: ctypes.CDLL) -> None:
                                            ctypes.c_float, _p, ctypes.c_size_t, _p, _p]
     L.mq_silu_mul.argtypes = [_p, _p, _i64, _i64, _p]
     L.mq_moe_route.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p]
-    L.mq_moe_sort.argtypes = [_p, _i64, _int, _int, _p, _p, _p, _p, _p]
+    L.mq_moe_sort.argtypes = [_p, _i64, _int, _int, _p, _p, _p, _p, _p, _p]
     L.mq_moe_combine.argtypes = [_p, _p, _p, _p, _i64, _int, _i64, _p]
-    L.mq_moe_route_sort.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p, _p, _p, _p, _p]
+    L.mq_moe_route_sort.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p, _p, _p, _p, _p,
+                                    _p]
     L.mq_quantized_matmul_swiglu_supported.argtypes = [_i64, _i64, _i64, _int, _int]
     L.mq_quantized_matmul_swiglu.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _p]
     L.mq_rms_norm_quantized_matmul_supported.argtypes = [_i64, _i64, _i64, _int, _int, _int]
@@ -115,6 +117,8 @@ def _declare(L: ctypes.CDLL) -> None:
                                        _i64, _int, _int, _p]
     L.mq_quantized_matmul_noalloc.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int,
                                               _int, _int, _p]
+    L.mq_gather_qmm_segments.argtypes = [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, _int, _int, _int, _p]
     L.mq_hbm_read.argtypes = [_p, ctypes.c_size_t, _p, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int

@@ -331,14 +331,18 @@ def rms_norm_quantized_matmul(a: torch.Tensor, norm_weight: torch.Tensor, eps: f
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                lhs_indices: torch.Tensor | None = None, rhs_indices: torch.Tensor | None = None,
                transpose: bool = True, group_size: int = 64, bits: int = 4, mode: str = "affine",
-               sorted_indices: bool = False) -> torch.Tensor:
+               sorted_indices: bool = False, expert_offsets: torch.Tensor | None = None
+               ) -> torch.Tensor:
     """mx.gather_qmm: out[b] = x[lhs[b]] @ dequantize(w[rhs[b]]).T, b over the index batch.
 
     x is [..., M, K] (its batch dims flattened are what lhs_indices index), w is
     [..., N, K*bits/32] (batch dims flattened are the experts rhs_indices
     index).  The output shape is broadcast(lhs_indices, rhs_indices) + [M, N];
     a missing lhs_indices means "every x batch in order" and broadcasts the same
-    way, as in mlx (models/lfm2.py:176-187, 202-218).
+    way, as in mlx (models/lfm2.py:176-187, 202-218).  With sorted_indices the
+    flat rhs must be non-decreasing (as MLX assumes); expert_offsets (int32
+    [E + 1], the segment starts expert_sort / route_sort return) spares the
+    kernel deriving the segments.
     """
     op = "gather_qmm"
     _check_mode(op, mode)
@@ -374,6 +378,15 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     xc = x.contiguous()
     y = torch.empty(tuple(out_batch) + (M, N), dtype=torch.bfloat16, device=dev)
     L = _lib.lib()
+    if expert_offsets is not None and sorted_indices:
+        if expert_offsets.dtype != torch.int32 or expert_offsets.numel() != E + 1:
+            raise ValueError(f"[{op}] expert_offsets must be int32 [{E + 1}]")
+        _require_gpu(op, expert_offsets=expert_offsets)
+        _lib.check(L.mq_gather_qmm_segments(
+            _ptr(xc), _ptr(lhs_flat), _ptr(rhs_flat), _ptr(expert_offsets.contiguous()),
+            _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(y),
+            T, M, N, K, E, n_xb, group_size, bits, 0, _stream(x)), op)
+        return y
     _lib.check(L.mq_gather_qmm(_ptr(xc), _ptr(lhs_flat), _ptr(rhs_flat), _ptr(w.contiguous()),
                                _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(y), T, M,
                                N, K, E, n_xb, group_size, bits, 1, int(bool(sorted_indices)),
@@ -390,7 +403,8 @@ def gather_swiglu_supported(T: int, M: int, N: int, K: int, group_size: int = 64
 def gather_qmm_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                       biases: torch.Tensor, lhs_indices: torch.Tensor | None,
                       rhs_indices: torch.Tensor, group_size: int = 64,
-                      bits: int = 4) -> torch.Tensor:
+                      bits: int = 4, expert_offsets: torch.Tensor | None = None
+                      ) -> torch.Tensor:
     """SwitchGLU's gate/up projections and silu(gate) * up (models/lfm2.py:208-214) for
     gathered pairs: w [E, 2N, K*bits/32] holds every expert's gate rows, then its up
     rows; x [n_x, M, K]; rhs_indices [T] (expert per pair), lhs_indices [T] (x batch
@@ -415,6 +429,17 @@ def gather_qmm_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         raise ValueError(f"[{op}] lhs_indices and rhs_indices differ in length")
     y = torch.empty(T, M, N, dtype=torch.bfloat16, device=x.device)
     L = _lib.lib()
+    if expert_offsets is not None:
+        # rows sorted by expert with the sort's segment offsets: the segment GEMM
+        # with SiLU * up in its epilogue (its GEMV form for decode-sized batches)
+        if expert_offsets.dtype != torch.int32 or expert_offsets.numel() != E + 1:
+            raise ValueError(f"[{op}] expert_offsets must be int32 [{E + 1}]")
+        _require_gpu(op, expert_offsets=expert_offsets)
+        _lib.check(L.mq_gather_qmm_segments(
+            _ptr(x.contiguous()), _ptr(lhs), _ptr(rhs), _ptr(expert_offsets.contiguous()),
+            _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(y),
+            T, M, N, K, E, n_xb, group_size, bits, 1, _stream(x)), op)
+        return y
     _lib.check(L.mq_gather_qmm_swiglu(_ptr(x.contiguous()), _ptr(lhs), _ptr(rhs),
                                       _ptr(w.contiguous()), _ptr(scales.contiguous()),
                                       _ptr(biases.contiguous()), _ptr(y), T, M, N, K, E, n_xb,

@@ -164,13 +164,21 @@ namespace {
 // epilogue (where mq_quantized_matmul itself runs that GEMV on the 2N rows),
 // 2 the skinny GEMM's K splits with a SwiGLU reduce (where mq_quantized_matmul
 // with its workspace splits K), 3 the unsplit one-tile skinny GEMM with the
-// SwiGLU in its epilogue, 0 not fused.
+// SwiGLU in its epilogue, 4 the large-M GEMM with the SwiGLU in its epilogue
+// (where mq_quantized_matmul runs that GEMM unsplit), 0 not fused.
 int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
   if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
   if (use_skinny(M, 2 * N, K, bits) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
   if (use_skinny(M, 2 * N, K, bits) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
+  // route 4 only where mq_quantized_matmul_ws itself runs the large-M GEMM,
+  // unsplit, on the 2N rows (the same kernel, so the same bits)
+  const int64_t N2 = 2 * N;
+  if (!dense_gemv(M, N2, K, bits) && !mq::qmv_fits(M, N2, K, bits, 1) &&
+      !use_skinny(M, N2, K, bits) && mq::qmm4_fits(M, N2, K, bits) &&
+      mq::qmm4_workspace_bytes(M, N2, K) == 0 && mq::qmm4_swiglu_fits(M, N, K, bits))
+    return 4;
   return 0;
 }
 
@@ -219,6 +227,9 @@ int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq
   if (route == 3)
     return hip_status(
         mq::launch_qmms_swiglu_direct(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+  if (route == 4)
+    return hip_status(mq::launch_qmm4_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream),
+                      op);
   const size_t need = mq::qmms_workspace_bytes(M, 2 * N, K, bits);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return fail(MQ_ERR_INVALID,
@@ -374,8 +385,6 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
     e = mq::launch_qmm4(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
-  } else if (mq::qmm2_fits(M, N, K, bits)) {
-    e = mq::launch_qmm2(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
   } else {
     e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
   }
@@ -425,11 +434,59 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
     e = mq::launch_qmvm(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
   } else if (few && mq::qmv_fits(M, N, K, bits, T)) {
     e = mq::launch_qmv(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
+  } else if (sorted_indices && mq::qmm4_gather_fits(T, M, N, K, E, x_batches, bits)) {
+    e = mq::launch_qmm4_gather(x, lhs_indices, rhs_indices, nullptr, wq, scales, biases, y, T, M,
+                               N, K, E, x_batches, bits, false, stream);
   } else {
     e = mq::launch_gather_qmm_rows(x, lhs_indices, rhs_indices, wq, scales, biases, y, T * M, N,
                                    K, E, x_batches * M, (int)M, bits, stream);
   }
   return hip_status(e, op);
+}
+
+int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
+                           const int32_t* rhs_indices, const int32_t* expert_offsets,
+                           const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases,
+                           mq_bf16* y, int64_t T, int64_t M, int64_t N, int64_t K, int64_t E,
+                           int64_t x_batches, int group_size, int bits, int swiglu,
+                           hipStream_t stream) {
+  const char* op = swiglu ? "gather_qmm_swiglu" : "gather_qmm";
+  if (!expert_offsets) return fail(MQ_ERR_INVALID, "[%s] expert_offsets is null.", op);
+  if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_dim(op, "T", T)) return rc;
+  if (int rc = check_dim(op, "M", M)) return rc;
+  if (int rc = check_dim(op, "N", swiglu ? 2 * N : N)) return rc;
+  if (int rc = check_dim(op, "E", E)) return rc;
+  if (int rc = check_dim(op, "x_batches", x_batches)) return rc;
+  if (T * M >= kMaxDim) return fail(MQ_ERR_INVALID, "[%s] T*M is too large.", op);
+  if (!lhs_indices && x_batches != T)
+    return fail(MQ_ERR_INVALID, "[%s] without lhs_indices x must have T=%lld batches, got %lld.",
+                op, (long long)T, (long long)x_batches);
+  if (T == 0 || M == 0 || N == 0) return ok();
+  if (E == 0) return fail(MQ_ERR_INVALID, "[%s] the expert table is empty.", op);
+  if (!x || !rhs_indices || !wq || !scales || !biases || !y)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x) || !aligned16(wq))
+    return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
+  // Decode-sized batches run as mq_gather_qmm (or its SwiGLU GEMV) does: the
+  // offsets are not needed there.
+  const bool fits = mq::qmm4_gather_fits(T, M, swiglu ? 2 * N : N, K, E, x_batches, bits);
+  if (T * M <= 64 || !fits) {
+    if (!swiglu)
+      return mq_gather_qmm(x, lhs_indices, rhs_indices, wq, scales, biases, y, T, M, N, K, E,
+                           x_batches, group_size, bits, 1, 1, stream);
+    if (mq_gather_qmm_swiglu_supported(T, M, N, K, group_size, bits))
+      return mq_gather_qmm_swiglu(x, lhs_indices, rhs_indices, wq, scales, biases, y, T, M, N,
+                                  K, E, x_batches, group_size, bits, stream);
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] T=%lld, M=%lld, N=%lld, K=%lld is not a fused shape; use "
+                "mq_gather_qmm_segments and mq_silu_mul.",
+                op, (long long)T, (long long)M, (long long)N, (long long)K);
+  }
+  return hip_status(mq::launch_qmm4_gather(x, lhs_indices, rhs_indices, expert_offsets, wq,
+                                           scales, biases, y, T, M, N, K, E, x_batches, bits,
+                                           swiglu != 0, stream),
+                    op);
 }
 
 int mq_gather_qmm_swiglu_supported(int64_t T, int64_t M, int64_t N, int64_t K, int group_size,
@@ -641,18 +698,18 @@ int mq_moe_route(const mq_bf16* logits, const float* expert_bias, int64_t tokens
 
 int mq_moe_sort(const int32_t* expert_ids, int64_t n, int top_k, int num_experts,
                 int32_t* sorted_ids, int32_t* order, int32_t* inverse, int32_t* rows,
-                hipStream_t stream) {
+                int32_t* expert_offsets, hipStream_t stream) {
   const char* op = "moe_sort";
   if (int rc = check_dim(op, "n", n)) return rc;
   if (top_k < 1) return fail(MQ_ERR_INVALID, "[%s] top_k=%d must be >= 1.", op, top_k);
   if (!mq::moe_sort_supported(n, num_experts))
     return fail(MQ_ERR_UNSUPPORTED, "[%s] %d experts (1..512), %lld entries (< 2^30).", op,
                 num_experts, (long long)n);
-  if (n == 0) return ok();
-  if (!expert_ids || !sorted_ids || !order || !inverse)
+  if (n == 0 && !expert_offsets) return ok();
+  if (n > 0 && (!expert_ids || !sorted_ids || !order || !inverse))
     return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
   return hip_status(mq::launch_moe_sort(expert_ids, n, top_k, num_experts, sorted_ids, order,
-                                        inverse, rows, stream),
+                                        inverse, rows, expert_offsets, stream),
                     op);
 }
 
@@ -676,7 +733,7 @@ int mq_moe_combine(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scor
 int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t tokens,
                       int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
                       mq_bf16* scores, int32_t* sorted_ids, int32_t* order, int32_t* inverse,
-                      int32_t* rows, hipStream_t stream) {
+                      int32_t* rows, int32_t* expert_offsets, hipStream_t stream) {
   const char* op = "moe_route_sort";
   if (int rc = check_dim(op, "tokens", tokens)) return rc;
   if (!mq::moe_route_supported(num_experts, top_k))
@@ -685,12 +742,15 @@ int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t t
   if (!mq::moe_sort_supported(tokens * top_k, num_experts))
     return fail(MQ_ERR_UNSUPPORTED, "[%s] %lld entries (< 2^30).", op,
                 (long long)(tokens * top_k));
-  if (tokens == 0) return ok();
+  if (tokens == 0)
+    return expert_offsets ? mq_moe_sort(nullptr, 0, top_k, num_experts, nullptr, nullptr,
+                                        nullptr, nullptr, expert_offsets, stream)
+                          : ok();
   if (!logits || !indices || !scores || !sorted_ids || !order || !inverse)
     return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
   return hip_status(mq::launch_moe_route_sort(logits, expert_bias, tokens, num_experts, top_k,
                                               norm_topk_prob != 0, indices, scores, sorted_ids,
-                                              order, inverse, rows, stream),
+                                              order, inverse, rows, expert_offsets, stream),
                     op);
 }
 

@@ -58,14 +58,8 @@ hipError_t launch_qmvm(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
 
-// 256x256-tile MFMA path for large M (qmm2_fits: >= 128 tiles, 32-bit offsets).
-bool qmm2_fits(int64_t M, int64_t N, int64_t K, int bits);
-hipError_t launch_qmm2(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
-                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, hipStream_t stream);
-
 // 256x256-tile MFMA path with weights dequantized in registers (qmm4_fits:
-// K a multiple of 512, >= 128 tiles, 32-bit offsets), one wave per SIMD, each
+// K an even number of groups, >= 128 tiles, 32-bit offsets), one wave per SIMD, each
 // owning the block's 256 rows for 64 columns (every code dequantized once per
 // block).  Few tiles and a long K: K is split over blocks through a float32
 // workspace of qmm4_workspace_bytes (without it the launch runs unsplit).
@@ -75,6 +69,26 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
+// The same kernel over rows sorted by expert (gather_qmm with sorted
+// indices): rows = T * Mb, row p = (batch p / Mb, row p % Mb) reads x batch
+// lhs[batch] (the batch itself without lhs) and expert rhs[batch]; tiles are
+// 256-row pieces of one expert's segment.  seg (E + 1 batch offsets of the
+// segments) or, when null, a scan of rhs (non-decreasing) gives the segments;
+// rows whose id names no expert are zero.  swiglu: every expert's matrix is
+// 2N rows (gate, then up) and y [T*Mb, N] = silu(gate) * up.
+bool qmm4_gather_fits(int64_t T, int64_t Mb, int64_t N, int64_t K, int64_t E,
+                      int64_t x_batches, int bits);
+hipError_t launch_qmm4_gather(const uint16_t* x, const int32_t* lhs, const int32_t* rhs,
+                              const int32_t* seg, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, uint16_t* y, int64_t T, int64_t Mb,
+                              int64_t N, int64_t K, int64_t E, int64_t x_batches, int bits,
+                              bool swiglu, hipStream_t stream);
+// The dense kernel on a gate|up matrix [2N, K] (gate rows first) with
+// silu(gate) * up in its epilogue: y [M, N] (unsplit launches only).
+bool qmm4_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits);
+hipError_t launch_qmm4_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N,
+                              int64_t K, int bits, hipStream_t stream);
 // y[i] = bf16(sum over s < splits of partial[s * MN + i] (in order) + bias[i % N])
 hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t* bias,
                                 uint16_t* y, int64_t MN, int64_t N, hipStream_t stream);
@@ -163,13 +177,14 @@ hipError_t launch_moe_route(const uint16_t* logits, const float* expert_bias, in
                             hipStream_t stream);
 bool moe_sort_supported(int64_t n, int E);
 hipError_t launch_moe_sort(const int32_t* ids, int64_t n, int k, int E, int32_t* sorted_ids,
-                           int32_t* order, int32_t* inverse, int32_t* rows, hipStream_t stream);
+                           int32_t* order, int32_t* inverse, int32_t* rows,
+                           int32_t* expert_offsets, hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t* y, const int32_t* inverse, const uint16_t* scores,
                               uint16_t* out, int64_t T, int k, int64_t H, hipStream_t stream);
 hipError_t launch_moe_route_sort(const uint16_t* logits, const float* expert_bias, int64_t T,
                                  int E, int k, bool normalize, int32_t* indices, uint16_t* scores,
                                  int32_t* sorted_ids, int32_t* order, int32_t* inverse,
-                                 int32_t* rows, hipStream_t stream);
+                                 int32_t* rows, int32_t* expert_offsets, hipStream_t stream);
 bool moe_combine_norm_supported(int64_t H);
 hipError_t launch_moe_combine_norm(const uint16_t* y, const int32_t* inverse,
                                    const uint16_t* scores, const uint16_t* residual,

@@ -170,7 +170,8 @@ __device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int
                                            int32_t* __restrict__ sorted_ids,
                                            int32_t* __restrict__ order,
                                            int32_t* __restrict__ inverse,
-                                           int32_t* __restrict__ rows) {
+                                           int32_t* __restrict__ rows,
+                                           int32_t* __restrict__ expert_offsets) {
   __shared__ int offset[kMaxBuckets];
   __shared__ int wave_count[kSortWaves][kMaxBuckets];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -208,6 +209,10 @@ __device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int
     }
   }
   __syncthreads();
+  // segment starts: expert e's pairs are sorted positions offset[e] ..
+  // offset[e + 1] - 1; offset[E] counts the pairs with a valid id
+  if (expert_offsets)
+    for (int e = tid; e < buckets; e += kSortThreads) expert_offsets[e] = offset[e];
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
   for (int c0 = 0; c0 < n; c0 += kSortThreads) {
     for (int e = lane; e < buckets; e += 64) wave_count[wave][e] = 0;
@@ -248,10 +253,16 @@ __device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int
   }
 }
 
+__global__ __launch_bounds__(256) void zero_i32_kernel(int32_t* __restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
     const int32_t* __restrict__ ids, int n, int k, int E, int32_t* __restrict__ sorted_ids,
-    int32_t* __restrict__ order, int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
-  sort_block(ids, n, k, E, sorted_ids, order, inverse, rows);
+    int32_t* __restrict__ order, int32_t* __restrict__ inverse, int32_t* __restrict__ rows,
+    int32_t* __restrict__ expert_offsets) {
+  sort_block(ids, n, k, E, sorted_ids, order, inverse, rows, expert_offsets);
 }
 
 // Route (one wave per token) and then sort, in one block: a decode step's
@@ -263,7 +274,8 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
     const uint16_t* __restrict__ logits, const float* __restrict__ expert_bias, int T, int E,
     int k, int normalize, int32_t* indices, uint16_t* __restrict__ scores,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ order,
-    int32_t* __restrict__ inverse, int32_t* __restrict__ rows) {
+    int32_t* __restrict__ inverse, int32_t* __restrict__ rows,
+    int32_t* __restrict__ expert_offsets) {
   __shared__ RouteScratch rs[kSortWaves];
   __shared__ int flat[64];  // the picks, for the one-wave sort
   const int n = T * k;
@@ -272,7 +284,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
                     rs[threadIdx.x >> 6], n <= 64 ? flat : nullptr);
   __syncthreads();
   if (n > 64) {
-    sort_block(indices, n, k, E, sorted_ids, order, inverse, rows);
+    sort_block(indices, n, k, E, sorted_ids, order, inverse, rows, expert_offsets);
     return;
   }
   // At most 64 pairs: one wave places each at its rank among the keys
@@ -293,6 +305,13 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
       inverse[i] = pos;
       if (rows) rows[pos] = i / k;
     }
+    // segment starts: the pairs whose bucket is below e
+    if (expert_offsets)
+      for (int e = i; e <= E; e += 64) {
+        int below = 0;
+        for (int j = 0; j < n; ++j) below += (int)((flat[j] >= 0 && flat[j] < E ? flat[j] : E) < e);
+        expert_offsets[e] = below;
+      }
   }
 }
 
@@ -405,17 +424,18 @@ __global__ __launch_bounds__(kNormThreads) void moe_combine_norm_kernel(
 hipError_t launch_moe_route_sort(const uint16_t* logits, const float* expert_bias, int64_t T,
                                  int E, int k, bool normalize, int32_t* indices, uint16_t* scores,
                                  int32_t* sorted_ids, int32_t* order, int32_t* inverse,
-                                 int32_t* rows, hipStream_t stream) {
+                                 int32_t* rows, int32_t* expert_offsets, hipStream_t stream) {
   if (T == 0) return hipSuccess;
   if (T > kRouteSortMaxTokens) {
     const hipError_t e =
         launch_moe_route(logits, expert_bias, T, E, k, normalize, indices, scores, stream);
     if (e != hipSuccess) return e;
-    return launch_moe_sort(indices, T * k, k, E, sorted_ids, order, inverse, rows, stream);
+    return launch_moe_sort(indices, T * k, k, E, sorted_ids, order, inverse, rows,
+                           expert_offsets, stream);
   }
   hipLaunchKernelGGL(moe_route_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, logits,
                      expert_bias, (int)T, E, k, normalize ? 1 : 0, indices, scores, sorted_ids,
-                     order, inverse, rows);
+                     order, inverse, rows, expert_offsets);
   return hipGetLastError();
 }
 
@@ -450,10 +470,18 @@ hipError_t launch_moe_route(const uint16_t* logits, const float* expert_bias, in
 bool moe_sort_supported(int64_t n, int E) { return E >= 1 && E <= kMaxExperts && n < (1 << 30); }
 
 hipError_t launch_moe_sort(const int32_t* ids, int64_t n, int k, int E, int32_t* sorted_ids,
-                           int32_t* order, int32_t* inverse, int32_t* rows, hipStream_t stream) {
-  if (n == 0) return hipSuccess;
+                           int32_t* order, int32_t* inverse, int32_t* rows,
+                           int32_t* expert_offsets, hipStream_t stream) {
+  if (n == 0) {
+    // no pairs: every segment is empty (a kernel, not a memset node, so that
+    // the call can be captured in a graph)
+    if (!expert_offsets) return hipSuccess;
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((E + 256) / 256), dim3(256), 0, stream,
+                       expert_offsets, E + 1);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, ids, (int)n, k, E,
-                     sorted_ids, order, inverse, rows);
+                     sorted_ids, order, inverse, rows, expert_offsets);
   return hipGetLastError();
 }
 

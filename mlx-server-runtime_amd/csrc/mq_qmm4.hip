@@ -36,6 +36,8 @@
 // and earlier (the next step's x tile), never those of this step or the
 // previous one.
 #include <algorithm>
+#include <climits>
+#include <type_traits>
 
 #include "mq_common.h"
 #include "mq_internal.h"
@@ -103,76 +105,272 @@ struct GroupAffine {
   float s, b;
 };
 
-template <int BITS>
-__global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ wq,
-    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
-    int M, int N, int K, int tiles_m, int tiles, int chunks_per_split) {
+// Arguments of one launch.  Dense: y[M, N] = x[M, K] @ W^T over tiles_m x
+// tiles_n tiles (K maybe split).  Gather (mx.gather_qmm over rows sorted by
+// expert): rows = T * Mb, row p = (batch t = p / Mb, row m = p % Mb) reads x row
+// lhs[t] * Mb + m (t * Mb + m without lhs) and expert rhs[t]'s matrix, and
+// writes y row p; tiles are whole 256-row pieces of one expert's segment.
+struct Qmm4Args {
+  const uint16_t* x;
+  const uint32_t* wq;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  const uint16_t* bias;
+  uint16_t* y;
+  float* partial;
+  int M, N, K;  // M: dense rows (gather: T * Mb)
+  int tiles_m, tiles_n, tiles, chunks_per_split;
+  // gather only
+  const int32_t* lhs;
+  const int32_t* rhs;
+  const int32_t* seg;  // E + 1 batch offsets of the expert segments, or null
+  int T, Mb, E, x_batches;
+};
+
+// Gather tile map, computed by each block from the expert segments: segment e
+// holds batches [start_e, start_(e+1)), i.e. ceil((start_(e+1) - start_e) * Mb
+// / BM) row tiles; the block's row tile rt is the (rt - pre_e)-th tile of the
+// expert e with pre_e <= rt < pre_(e+1) (exclusive prefix sums).  Out: e (-1
+// past the last tile), first row, valid rows, and lo/hi: the batches outside
+// [lo, hi) name no expert (ids < 0 sort first, ids >= E last) and give zeros.
+struct GatherTile {
+  int e, row0, rows, lo, hi, total;
+};
+
+__device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
+  // sh: LDS ints, 2 * (E + 1) + 8 of them
+  int* start = sh;              // [E + 1] segment starts (batches)
+  int* pre = sh + a.E + 1;      // [E + 1] exclusive tile prefix
+  int* misc = pre + a.E + 1;    // [8]
+  const int tid = threadIdx.x;
+  if (a.seg) {
+    for (int e = tid; e <= a.E; e += kThreads) start[e] = a.seg[e];
+  } else {
+    // start[e] = the first batch whose id is >= e: one coalesced pass over the
+    // sorted ids, each boundary (ids u < v at batches p - 1, p) giving
+    // start[e] = p for u < e <= v; experts past the largest id keep T
+    for (int e = tid; e <= a.E; e += kThreads) start[e] = a.T;
+    __syncthreads();
+    for (int p0 = 0; p0 < a.T; p0 += kThreads * 4) {
+      int v[4], u[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int p = p0 + q * kThreads + tid;
+        v[q] = p < a.T ? a.rhs[p] : INT_MAX;
+        u[q] = (p > 0 && p < a.T) ? a.rhs[p - 1] : INT_MIN;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int p = p0 + q * kThreads + tid;
+        if (p < a.T && u[q] < v[q])
+          for (int e = max(u[q] + 1, 0); e <= min(v[q], a.E); ++e) start[e] = p;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) misc[0] = start[0];  // batches before it have negative ids
+  __syncthreads();
+  // each thread counts the tiles of up to 4 experts: 4 tid .. 4 tid + 3
+  int mine[4], sum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = 4 * tid + q;
+    int t = 0;
+    if (e < a.E) {
+      const int lo = max(start[e], misc[0]);
+      const int rows = max(0, start[e + 1] - lo) * a.Mb;
+      t = (rows + BM - 1) / BM;
+    }
+    mine[q] = t;
+    sum += t;
+  }
+  // block exclusive scan of the per-thread sums (wave scan, then wave totals)
+  int incl = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if ((tid & 63) >= off) incl += v;
+  }
+  if ((tid & 63) == 63) misc[1 + (tid >> 6)] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < (tid >> 6); ++w) base += misc[1 + w];
+  int run = base + incl - sum;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = 4 * tid + q;
+    if (e < a.E) pre[e] = run;
+    run += mine[q];
+  }
+  if (tid == kThreads - 1) pre[min(a.E, 4 * kThreads)] = run;
+  if (tid == 0) misc[5] = -1;
+  __syncthreads();
+  const int total = pre[a.E];
+  for (int e = tid; e < a.E; e += kThreads)
+    if (pre[e] <= rt && rt < pre[e + 1]) misc[5] = e;
+  __syncthreads();
+  GatherTile g;
+  g.e = misc[5];
+  g.lo = misc[0];
+  g.hi = start[a.E];
+  g.total = total;
+  g.row0 = 0;
+  g.rows = 0;
+  if (g.e >= 0) {
+    const int lo = max(start[g.e], g.lo);
+    const int k = rt - pre[g.e];
+    g.row0 = lo * a.Mb + k * BM;
+    g.rows = min(BM, start[g.e + 1] * a.Mb - g.row0);
+  }
+  __syncthreads();  // the map's LDS is reused for x tiles
+  return g;
+}
+
+// SWIGLU: the matrix holds 2N rows, gate rows then up rows (the fused gate|up
+// projection); a block computes 128 gate columns and their 128 up columns --
+// lane (j = 0) and (j = 1) hold the same (row, column) of both -- and writes
+// y[., N] = silu(gate) * up, each rounded to bfloat16 as the unfused kernels
+// round (gate and up, then silu, then the product).
+template <int BITS, bool GATHER, bool SB16, bool SWIGLU>
+__global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
   extern __shared__ u32x4_t smem[];
   char* const lds = reinterpret_cast<char*>(smem);
   const int tid = threadIdx.x;
   const int l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = l >> 5;
+  const int N = a.N, K = a.K;  // N output columns
+  constexpr int kOutCols = SWIGLU ? BN / 2 : BN;  // output columns per block
+  const int NW = SWIGLU ? 2 * N : N;              // rows of the (expert's) matrix
 
-  // ---- tile order: XCD-contiguous runs of tile groups ----
-  const int nblk = gridDim.x;
-  const int per_xcd = nblk / 8, rem = nblk % 8;
-  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  const int idx = (xcd < rem ? xcd * (per_xcd + 1) : rem * (per_xcd + 1) + (xcd - rem) * per_xcd) + slot;
-  // With K split, idx = split * tiles + tile: a split's blocks are contiguous.
-  const int tile = idx % tiles, split = idx / tiles;
-  // group g: row blocks g*kGroupM .. +gm-1 x every column block, row fastest
-  const int tiles_n = tiles / tiles_m;
-  const int g = tile / (kGroupM * tiles_n), r = tile % (kGroupM * tiles_n);
-  const int gm = min(kGroupM, tiles_m - g * kGroupM);
-  const int bm = g * kGroupM + r % gm, bn = r / gm;
-  const int m0 = bm * BM, n0 = bn * BN;
-
+  int split = 0, bn, out_row0, rows_valid;
+  const uint32_t* wbank = a.wq;
+  const uint16_t* sbank = a.scales;
+  const uint16_t* bbank = a.biases;
   const int G = K / kGroup;
+  if constexpr (GATHER) {
+    // Blocks go to the 8 XCDs round-robin.  Each run of 8 * tiles_n blocks
+    // covers 8 row tiles, row tile 8g + x on XCD x with all its column tiles
+    // (the same expert and gathered x rows in one L2); the row tiles past the
+    // last one (the grid reserves an upper bound) are spread over every XCD.
+    const int run = 8 * a.tiles_n;
+    const int rt = (blockIdx.x / run) * 8 + blockIdx.x % 8;
+    bn = (blockIdx.x % run) / 8;
+    const GatherTile g = gather_tile(a, rt, reinterpret_cast<int*>(lds));
+    if (g.e < 0) {
+      // the first spare row tile zeroes the rows whose id names no expert
+      if (rt == g.total) {
+        const int n = bn * kOutCols + tid;
+        if (tid < kOutCols && n < N) {
+          for (int p = 0; p < g.lo * a.Mb; ++p) a.y[(int64_t)p * N + n] = 0;
+          for (int p = g.hi * a.Mb; p < a.T * a.Mb; ++p) a.y[(int64_t)p * N + n] = 0;
+        }
+      }
+      return;
+    }
+    out_row0 = g.row0;
+    rows_valid = g.rows;
+    wbank += (int64_t)g.e * NW * (K * BITS / 32);
+    sbank += (int64_t)g.e * NW * G;
+    bbank += (int64_t)g.e * NW * G;
+  } else {
+    // XCD-contiguous runs of the tile order below: consecutive idx on one XCD
+    const int nblk = gridDim.x;
+    const int per_xcd = nblk / 8, rem = nblk % 8;
+    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+    const int idx = (xcd < rem ? xcd * (per_xcd + 1) : rem * (per_xcd + 1) + (xcd - rem) * per_xcd) + slot;
+    // With K split, idx = split * tiles + tile: a split's blocks are contiguous.
+    const int tile = idx % a.tiles;
+    split = idx / a.tiles;
+    // group g: row blocks g*kGroupM .. +gm-1 x every column block, row fastest
+    const int g = tile / (kGroupM * a.tiles_n), r = tile % (kGroupM * a.tiles_n);
+    const int gm = min(kGroupM, a.tiles_m - g * kGroupM);
+    const int bm = g * kGroupM + r % gm;
+    bn = r / gm;
+    out_row0 = bm * BM;
+    rows_valid = min(BM, a.M - out_row0);
+  }
+  const int n0 = bn * kOutCols;
+  // matrix row of block column c (0..255): c itself past n0, or for SWIGLU
+  // gate row n0 + 32 (c / 64) + c % 32 when c % 64 < 32, else its up row
+  auto wrow = [&](int c, int& out_col) {
+    if constexpr (SWIGLU) {
+      out_col = n0 + 32 * (c >> 6) + (c & 31);
+      return ((c >> 5) & 1) * N + out_col;
+    } else {
+      out_col = n0 + c;
+      return out_col;
+    }
+  };
+  // MFMA row tiles holding valid rows (the same for every wave of the block)
+  const int live = __builtin_amdgcn_readfirstlane((rows_valid + 31) / 32);
+
   const int KT = K / BK;
-  const int c_begin = split * chunks_per_split;
-  const int c_end = min(KT / kSbChunk, c_begin + chunks_per_split);
+  const int chunks = (KT + kSbChunk - 1) / kSbChunk;
+  const int c_begin = split * a.chunks_per_split;
+  const int c_end = min(chunks, c_begin + a.chunks_per_split);
   const int kt0 = c_begin * kSbChunk;
-  const rsrc_t xrs = make_rsrc(x, (uint64_t)M * K * 2);
-  const rsrc_t wrs = make_rsrc(wq, (uint64_t)N * K * BITS / 8);
-  const rsrc_t srs = make_rsrc(scales, (uint64_t)N * G * 2);
-  const rsrc_t brs = make_rsrc(biases, (uint64_t)N * G * 2);
+  const int kt_end = min(KT, c_end * kSbChunk);
+  const int x_rows = GATHER ? a.x_batches * a.Mb : a.M;
+  const rsrc_t xrs = make_rsrc(a.x, (uint64_t)x_rows * K * 2);
+  const rsrc_t wrs = make_rsrc(wbank, (uint64_t)NW * K * BITS / 8);
+  const rsrc_t srs = make_rsrc(sbank, (uint64_t)NW * G * 2);
+  const rsrc_t brs = make_rsrc(bbank, (uint64_t)NW * G * 2);
 
   // x DMA: wave w, op i fills rows (8w + i)*8 .. +7 of a stage (1 KiB); lane l
   // writes physical chunk l % 8 of row l / 8, i.e. logical chunk (l%8) ^ f(row)
-  // with f(row) = (row >> 1) & 7.  Rows past M, and steps past K on the last
-  // row, lie beyond the descriptor's M*K*2 bytes and read as zeros.
+  // with f(row) = (row >> 1) & 7.  Rows past the tile's valid rows read as
+  // zeros (an offset past the descriptor; dense rows past M lie beyond it).
   uint32_t xoff[kXOps];
 #pragma unroll
   for (int i = 0; i < kXOps; ++i) {
     const int row = (wave * kXOps + i) * 8 + (l >> 3);
-    xoff[i] = (uint32_t)((m0 + row) * K + (((l & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
+    const uint32_t chunk = (uint32_t)(((l & 7) ^ ((row >> 1) & 7)) * 8);
+    if constexpr (GATHER) {
+      xoff[i] = kOutOfRange;
+      if (row < rows_valid) {
+        const int p = out_row0 + row;
+        const int t = p / a.Mb, m = p - t * a.Mb;
+        const int xb = a.lhs ? a.lhs[t] : t;
+        if (xb >= 0 && xb < a.x_batches)
+          xoff[i] = ((uint32_t)(xb * a.Mb + m) * (uint32_t)K + chunk) * 2u;
+      }
+    } else {
+      xoff[i] = (uint32_t)((out_row0 + row) * K + (int)chunk) * 2;
+    }
   }
-  // Codes: column n0 + 64*wave + 32j + l%32, half h of each group.
+  // Codes: block column 64*wave + 32j + l%32, half h of each group.
   constexpr int CB = BITS * 4;  // code bytes per lane per step: 16 (4-bit) / 32 (8-bit)
   constexpr int NC = BITS == 4 ? 2 : 4;  // 16-byte code loads per lane per step
   uint32_t coff[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wave * 64 + j * 32 + (l & 31);
-    coff[j] = n < N ? (uint32_t)(n * (K * BITS / 8) + h * CB) : kOutOfRange;
+    int oc;
+    const int n = wrow(wave * 64 + j * 32 + (l & 31), oc);
+    coff[j] = oc < N ? (uint32_t)(n * (K * BITS / 8) + h * CB) : kOutOfRange;
   }
-  // Scale/bias DMA: wave w loads both arrays for columns 64w + l.
+  // Scale/bias DMA: wave w loads both arrays for columns 64w + l.  SB16: one
+  // 16-byte operation per array per chunk (8 groups of a column together,
+  // LDS [array][column][group]); otherwise four 4-byte operations per array
+  // (rows of G groups, G even, are only 4-byte aligned; LDS
+  // [array][group pair][column]).
   uint32_t soff;
   {
-    const int n = n0 + wave * 64 + l;
-    soff = n < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
+    int oc;
+    const int n = wrow(wave * 64 + l, oc);
+    soff = oc < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
   }
-  const int sb_dst = kSbBase + wave * 1024;
   // A fragment rows 32i + l%32; logical chunk 4h + ks, stored at (4h + ks) ^ f
   // with f = (l >> 1) & 7 for every row tile: only bits 4-5 of the byte offset
   // depend on ks, so the k-slice ks reads at aoff ^ (ks << 4).
   const uint32_t aoff = (uint32_t)((l & 31) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
   uint32_t sbr[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) sbr[j] = kSbBase + (wave * 64 + j * 32 + (l & 31)) * 16;
+  for (int j = 0; j < 2; ++j) {
+    const int c = wave * 64 + j * 32 + (l & 31);
+    sbr[j] = kSbBase + (SB16 ? c * 16 : c * 4);
+  }
+  constexpr int kSbOps = SB16 ? 2 : 8;  // DMA operations per lane per scale chunk
 
   auto dma_x = [&](int kt, int stage) {
 #pragma unroll
@@ -181,8 +379,19 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(
             xoff[i] + kt * (BK * 2));
   };
   auto dma_sb = [&](int chunk, int buf) {
-    dma16(srs, (lds_t*)(lds + sb_dst + buf * kSbBytes), soff + chunk * (kSbChunk * 2));
-    dma16(brs, (lds_t*)(lds + sb_dst + buf * kSbBytes + kSbArray), soff + chunk * (kSbChunk * 2));
+    char* dst = lds + kSbBase + buf * kSbBytes;
+    if constexpr (SB16) {
+      dma16(srs, (lds_t*)(dst + wave * 1024), soff + chunk * (kSbChunk * 2));
+      dma16(brs, (lds_t*)(dst + kSbArray + wave * 1024), soff + chunk * (kSbChunk * 2));
+    } else {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_t*)(dst + d * 1024 + wave * 256), 4,
+                                                 soff + chunk * (kSbChunk * 2) + d * 4, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_t*)(dst + kSbArray + d * 1024 + wave * 256),
+                                                 4, soff + chunk * (kSbChunk * 2) + d * 4, 0, 0, 0);
+      }
+    }
   };
   auto load_codes = [&](u32x4_t (&cw)[2][NC / 2], int kt) {
 #pragma unroll
@@ -208,7 +417,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(
   auto read_sb = [&](int buf, int grp, GroupAffine (&g)[2]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const char* p = lds + sbr[j] + buf * kSbBytes + grp * 2;
+      const char* p = lds + sbr[j] + buf * kSbBytes +
+                      (SB16 ? grp * 2 : (grp >> 1) * 1024 + (grp & 1) * 2);
       g[j].s = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
       g[j].b = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + kSbArray));
     }
@@ -231,96 +441,155 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(
 #pragma unroll
   for (int j = 0; j < 2; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
 
-  int st = 0;  // stage holding x of the current step
-  for (int c = c_begin; c < c_end; ++c) {
+  // The K loop.  MASKED skips the MFMAs (and A reads) of row tiles past the
+  // tile's valid rows, at the price of a branch per row tile; full tiles take
+  // the branch-free body.
+  auto k_loop = [&](auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    int st = 0;  // stage holding x of the current step
+    for (int c = c_begin; c < c_end; ++c) {
 #pragma unroll
-    for (int u = 0; u < kSbChunk; ++u) {
-      const int kt = c * kSbChunk + u;
-      const uint32_t xa = st * kXStage + aoff;
-      bf16x8_t a[kRowTiles];
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(lds + xa + i * 4096);
-      load_codes(cw[(u + 2) % kCodeRing], kt + 2);
-      dma_x(kt + 3, (st + 3) % kXStages);
-      if (u == kSbChunk - 4) dma_sb(c + 1, (c + 1) & 1);
-
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bf16x8_t bq[2], an[kRowTiles];
-        if (ks < 3) {
-#pragma unroll
-          for (int i = 0; i < kRowTiles; ++i)
-            an[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ ((ks + 1) << 4)) + i * 4096);
+      for (int u = 0; u < kSbChunk; ++u) {
+        const int kt = c * kSbChunk + u;
+        if constexpr (!SB16) {
+          if (kt >= kt_end) break;  // a K of G % 8 != 0 groups ends mid-chunk
         }
+        const uint32_t xa = st * kXStage + aoff;
+        bf16x8_t a[kRowTiles];
 #pragma unroll
         for (int i = 0; i < kRowTiles; ++i)
+          if (!MASKED || i < live) a[i] = *reinterpret_cast<const bf16x8_t*>(lds + xa + i * 4096);
+        load_codes(cw[(u + 2) % kCodeRing], kt + 2);
+        dma_x(kt + 3, (st + 3) % kXStages);
+        if (u == kSbChunk - 4) dma_sb(c + 1, (c + 1) & 1);
+
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b0[j], acc[i][j], 0, 0, 0);
-        if (ks < 3) {
+        for (int ks = 0; ks < 4; ++ks) {
+          bf16x8_t bq[2], an[kRowTiles];
+          if (ks < 3) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
-        } else {
-          // next step: its scales (the next chunk's buffer after the last
-          // step of a chunk, DMA-ed four steps ago) and its first k-slice
-          if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
-          else read_sb(c & 1, u + 1, ga);
+            for (int i = 0; i < kRowTiles; ++i)
+              if (!MASKED || i < live)
+                an[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ ((ks + 1) << 4)) + i * 4096);
+          }
 #pragma unroll
-          for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
+          for (int i = 0; i < kRowTiles; ++i)
+            if (!MASKED || i < live) {
+#pragma unroll
+              for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b0[j], acc[i][j], 0, 0, 0);
+            }
+          if (ks < 3) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
+          } else {
+            // next step: its scales (the next chunk's buffer after the last
+            // step of a chunk, DMA-ed four steps ago) and its first k-slice
+            if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
+            else read_sb(c & 1, u + 1, ga);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
+          }
+#pragma unroll
+          for (int j = 0; j < 2; ++j) b0[j] = bq[j];
+          if (ks < 3) {
+#pragma unroll
+            for (int i = 0; i < kRowTiles; ++i) a[i] = an[i];
+          }
         }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) b0[j] = bq[j];
-        if (ks < 3) {
-#pragma unroll
-          for (int i = 0; i < kRowTiles; ++i) a[i] = an[i];
-        }
+        // the DMAs of this step and the previous one may still be in flight
+        // (more in the steps that load scales); x of the next step, issued two
+        // steps ago, and the scales read next step have landed
+        if (u == kSbChunk - 4 || u == kSbChunk - 3) step_barrier<2 * kXOps + kSbOps>();
+        else step_barrier<2 * kXOps>();
+        st = (st + 1) % kXStages;
       }
-      // the DMAs of this step and the previous one may still be in flight
-      // (two more in the steps that load scales); x of the next step, issued
-      // two steps ago, and the scales read next step have landed
-      if (u == kSbChunk - 4 || u == kSbChunk - 3) step_barrier<2 * kXOps + 2>();
-      else step_barrier<2 * kXOps>();
-      st = (st + 1) % kXStages;
     }
-  }
+  };
+  // Dense tiles past M read zero rows; only gather tiles (short expert
+  // segments) skip their empty row tiles.
+  if (GATHER && live < kRowTiles) k_loop(std::true_type{});
+  else k_loop(std::false_type{});
   // The prefetches of the last steps (past K, unused) must land before the
   // block's LDS is released.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4;
-  // a split of K writes float32 partial sums instead ----
-  const bool full_rows = m0 + BM <= M;
+  // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4 ----
+  const bool full_rows = rows_valid == BM;
+  if (a.partial) {
+    // a split of K writes its float32 partial sums straight from registers
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wave * 64 + j * 32 + (l & 31);
-    if (n >= N) continue;
-    if (partial) {
-      float* pc = partial + (int64_t)split * M * N + n;
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wave * 64 + j * 32 + (l & 31);
+      if (n >= N) continue;
+      float* pc = a.partial + (int64_t)split * a.M * N + n;
 #pragma unroll
       for (int i = 0; i < kRowTiles; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int mb = m0 + i * 32 + 8 * r + 4 * h;
-          float* p = pc + (int64_t)mb * N;
+          const int mb = i * 32 + 8 * r + 4 * h;
+          float* p = pc + (int64_t)(out_row0 + mb) * N;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (full_rows || mb + e < M) p[(int64_t)e * N] = acc[i][j][4 * r + e];
+            if (full_rows || mb + e < rows_valid) p[(int64_t)e * N] = acc[i][j][4 * r + e];
         }
+    }
+    return;
+  }
+  // bfloat16 output: the 256-row tile goes through LDS (the x stages; every
+  // wave's DMAs have landed once all have passed the barrier) so that rows
+  // leave as 16-byte stores instead of 2-byte ones per lane and value.
+  __syncthreads();
+  constexpr int kOutStride = kOutCols * 2 + 16;  // bytes per staged row (padding spreads banks)
+  static_assert(BM * kOutStride <= kLds, "the output tile must fit the LDS");
+  if constexpr (SWIGLU) {
+    const int c = wave * 32 + (l & 31);
+#pragma unroll
+    for (int i = 0; i < kRowTiles; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = i * 32 + 8 * r + 4 * h + e;
+          const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[i][0][4 * r + e]));
+          const float u = bf16_bits_to_f32(f32_to_bf16_bits(acc[i][1][4 * r + e]));
+          *reinterpret_cast<uint16_t*>(lds + m * kOutStride + c * 2) = silu_mul_bf16(g, u);
+        }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = wave * 64 + j * 32 + (l & 31);
+      const int n = n0 + c;
+      const float add = (a.bias && n < N) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < kRowTiles; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = i * 32 + 8 * r + 4 * h + e;
+            *reinterpret_cast<uint16_t*>(lds + m * kOutStride + c * 2) =
+                (uint16_t)f32_to_bf16_bits(acc[i][j][4 * r + e] + add);
+          }
+    }
+  }
+  __syncthreads();
+  // thread t stores 16-byte chunk t % CPR of rows (256 / CPR) q + t / CPR
+  constexpr int CPR = kOutCols / 8;  // chunks per row
+  const int cc = tid % CPR;
+  const int n = n0 + cc * 8;
+  const bool vec = (N % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
+#pragma unroll 4
+  for (int q = 0; q < BM * CPR / kThreads; ++q) {
+    const int row = q * (kThreads / CPR) + tid / CPR;
+    if (row >= rows_valid || n >= N) continue;
+    const char* src = lds + row * kOutStride + cc * 16;
+    uint16_t* dst = a.y + (int64_t)(out_row0 + row) * N + n;
+    if (vec) {
+      *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
     } else {
-      const float add = bias ? bf16_bits_to_f32(bias[n]) : 0.f;
-      uint16_t* yc = y + n;
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int mb = m0 + i * 32 + 8 * r + 4 * h;
-          uint16_t* p = yc + (int64_t)mb * N;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (full_rows || mb + e < M)
-              p[(int64_t)e * N] = (uint16_t)f32_to_bf16_bits(acc[i][j][4 * r + e] + add);
-        }
+      for (int e = 0; e < 8 && n + e < N; ++e)
+        dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
     }
   }
 }
@@ -332,20 +601,39 @@ int qmm4_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   constexpr int64_t kRound = 256;
   if (tiles >= kRound / 2) return 1;
-  const int64_t chunks = K / (kSbChunk * kGroup);
+  const int64_t chunks = (K / kGroup + kSbChunk - 1) / kSbChunk;
   return (int)std::max<int64_t>(1, std::min(kRound / tiles, chunks / 4));
+}
+
+template <bool GATHER, bool SWIGLU>
+hipError_t launch(const Qmm4Args& a, int bits, dim3 grid, hipStream_t stream) {
+  const bool sb16 = (a.K / kGroup) % kSbChunk == 0;
+  void (*kern)(Qmm4Args);
+  if (bits == 4)
+    kern = sb16 ? qmm4_kernel<4, GATHER, true, SWIGLU> : qmm4_kernel<4, GATHER, false, SWIGLU>;
+  else
+    kern = sb16 ? qmm4_kernel<8, GATHER, true, SWIGLU> : qmm4_kernel<8, GATHER, false, SWIGLU>;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), kLds, stream, a);
+  return hipGetLastError();
+}
+
+// 32-bit buffer offsets (with room for the kOutOfRange marker) for x, the
+// codes and the scales of one matrix; an even number of 64-element groups.
+bool offsets_fit(int64_t x_rows, int64_t N, int64_t K, int bits) {
+  const int64_t lim = (int64_t)1 << 31;
+  return K % (2 * kGroup) == 0 && (x_rows + BM) * K * 2 < lim && N * K * bits / 8 < lim &&
+         N * (K / kGroup) * 2 < lim;
 }
 
 }  // namespace
 
 bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits) {
-  // 32-bit buffer offsets (with room for the kOutOfRange marker) for x, the
-  // codes and the scales; whole 8-group scale chunks; >= 128 tiles, or >= 32
-  // when K is long enough to split over blocks.
+  // >= 128 tiles, or >= 32 when K is long enough to split over blocks
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int64_t lim = (int64_t)1 << 31;
-  return K % (kSbChunk * kGroup) == 0 && (M + BM) * K * 2 < lim && N * K * bits / 8 < lim &&
-         N * (K / kGroup) * 2 < lim && tiles < lim &&
+  return offsets_fit(M, N, K, bits) && tiles < ((int64_t)1 << 31) &&
          (tiles >= 128 || (tiles >= 32 && qmm4_splits(M, N, K) * tiles >= 128));
 }
 
@@ -359,23 +647,68 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
                        hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
-  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  const int tiles = tiles_m * tiles_n;
-  const int chunks = (int)(K / (kSbChunk * kGroup));
+  Qmm4Args a{};
+  a.x = x, a.wq = wq, a.scales = scales, a.biases = biases, a.bias = bias, a.y = y;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K;
+  a.tiles_m = (int)((M + BM - 1) / BM), a.tiles_n = (int)((N + BN - 1) / BN);
+  a.tiles = a.tiles_m * a.tiles_n;
+  const int chunks = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
   int S = qmm4_splits(M, N, K);
   if (S > 1 && (!workspace || workspace_bytes < qmm4_workspace_bytes(M, N, K))) S = 1;
-  const int per = (chunks + S - 1) / S;
-  S = (chunks + per - 1) / per;
-  float* part = S > 1 ? static_cast<float*>(workspace) : nullptr;
-  const dim3 grid((unsigned)(tiles * S));
-  auto kern = bits == 4 ? qmm4_kernel<4> : qmm4_kernel<8>;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), kLds, stream, x, wq, scales, biases, bias, y,
-                     part, (int)M, (int)N, (int)K, tiles_m, tiles, per);
-  if (S == 1) return hipGetLastError();
-  return launch_splitk_reduce(part, S, bias, y, M * N, N, stream);
+  a.chunks_per_split = (chunks + S - 1) / S;
+  S = (chunks + a.chunks_per_split - 1) / a.chunks_per_split;
+  a.partial = S > 1 ? static_cast<float*>(workspace) : nullptr;
+  const hipError_t e = launch<false, false>(a, bits, dim3((unsigned)(a.tiles * S)), stream);
+  if (e != hipSuccess || S == 1) return e;
+  return launch_splitk_reduce(a.partial, S, bias, y, M * N, N, stream);
+}
+
+bool qmm4_gather_fits(int64_t T, int64_t Mb, int64_t N, int64_t K, int64_t E,
+                      int64_t x_batches, int bits) {
+  const int64_t lim = (int64_t)1 << 31;
+  return E >= 1 && E <= 4 * kThreads && T * Mb < lim / 2 &&
+         offsets_fit(x_batches * Mb, N, K, bits);
+}
+
+hipError_t launch_qmm4_gather(const uint16_t* x, const int32_t* lhs, const int32_t* rhs,
+                              const int32_t* seg, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, uint16_t* y, int64_t T, int64_t Mb,
+                              int64_t N, int64_t K, int64_t E, int64_t x_batches, int bits,
+                              bool swiglu, hipStream_t stream) {
+  if (T == 0 || Mb == 0 || N == 0) return hipSuccess;
+  Qmm4Args a{};
+  a.x = x, a.wq = wq, a.scales = scales, a.biases = biases, a.y = y;
+  a.M = (int)(T * Mb), a.N = (int)N, a.K = (int)K;
+  const int out_cols = swiglu ? BN / 2 : BN;
+  a.tiles_n = (int)((N + out_cols - 1) / out_cols);
+  a.chunks_per_split = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
+  a.lhs = lhs, a.rhs = rhs, a.seg = seg;
+  a.T = (int)T, a.Mb = (int)Mb, a.E = (int)E, a.x_batches = (int)x_batches;
+  // every expert's segment adds at most one partial tile; one spare row tile
+  // zeroes the rows whose id names no expert
+  int64_t row_tiles = (T * Mb + BM - 1) / BM + std::min(E, T) + 1;
+  row_tiles = (row_tiles + 7) / 8 * 8;  // whole runs of 8 row tiles (one per XCD)
+  const dim3 grid((unsigned)(row_tiles * a.tiles_n));
+  return swiglu ? launch<true, true>(a, bits, grid, stream) : launch<true, false>(a, bits, grid, stream);
+}
+
+bool qmm4_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits) {
+  // the gate|up matrix (2N rows) in 128-column output tiles, unsplit
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN / 2 - 1) / (BN / 2));
+  return offsets_fit(M, 2 * N, K, bits) && tiles >= 128 && tiles < ((int64_t)1 << 31);
+}
+
+hipError_t launch_qmm4_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N,
+                              int64_t K, int bits, hipStream_t stream) {
+  if (M == 0 || N == 0) return hipSuccess;
+  Qmm4Args a{};
+  a.x = x, a.wq = wq, a.scales = scales, a.biases = biases, a.y = y;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K;
+  a.tiles_m = (int)((M + BM - 1) / BM), a.tiles_n = (int)((N + BN / 2 - 1) / (BN / 2));
+  a.tiles = a.tiles_m * a.tiles_n;
+  a.chunks_per_split = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
+  return launch<false, true>(a, bits, dim3((unsigned)a.tiles), stream);
 }
 
 }  // namespace mq

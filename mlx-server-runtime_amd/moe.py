@@ -52,8 +52,10 @@ def route(logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
     return idx, sc
 
 
-def expert_sort(indices: torch.Tensor, num_experts: int):
-    """indices int32 [T, k] -> (sorted_ids, order, inverse, rows), each int32 [T*k]."""
+def expert_sort(indices: torch.Tensor, num_experts: int, with_offsets: bool = False):
+    """indices int32 [T, k] -> (sorted_ids, order, inverse, rows), each int32 [T*k]
+    (+ offsets int32 [num_experts + 1], where each expert's run of sorted_ids
+    starts, with_offsets)."""
     op = "moe_sort"
     _require_gpu(op, indices=indices)
     if indices.dtype != torch.int32:
@@ -62,10 +64,12 @@ def expert_sort(indices: torch.Tensor, num_experts: int):
     flat = indices.contiguous().reshape(-1)
     n = flat.numel()
     outs = [torch.empty(n, dtype=torch.int32, device=flat.device) for _ in range(4)]
+    offs = (torch.empty(num_experts + 1, dtype=torch.int32, device=flat.device)
+            if with_offsets else None)
     L = _lib.lib()
     _lib.check(L.mq_moe_sort(_ptr(flat), n, k, num_experts, *(_ptr(t) for t in outs),
-                             _stream(flat)), op)
-    return tuple(outs)
+                             _ptr(offs), _stream(flat)), op)
+    return (*outs, offs) if with_offsets else tuple(outs)
 
 
 def combine(y: torch.Tensor, inverse: torch.Tensor | None, scores: torch.Tensor) -> torch.Tensor:
@@ -80,10 +84,11 @@ def combine(y: torch.Tensor, inverse: torch.Tensor | None, scores: torch.Tensor)
 
 
 def route_sort(logits: torch.Tensor, top_k: int, num_experts: int,
-               norm_topk_prob: bool = True, expert_bias: torch.Tensor | None = None):
+               norm_topk_prob: bool = True, expert_bias: torch.Tensor | None = None,
+               with_offsets: bool = False):
     """route(...) then expert_sort(indices, num_experts), in one launch when
     logits has at most 64 rows -> (indices, scores, sorted_ids, order, inverse,
-    rows)."""
+    rows) (+ the experts' segment offsets [num_experts + 1], with_offsets)."""
     op = "moe_route_sort"
     _require_gpu(op, logits=logits, expert_bias=expert_bias)
     _check_bf16(op, "logits", logits)
@@ -97,11 +102,12 @@ def route_sort(logits: torch.Tensor, top_k: int, num_experts: int,
     idx = torch.empty(T, top_k, dtype=torch.int32, device=dev)
     sc = torch.empty(T, top_k, dtype=torch.bfloat16, device=dev)
     outs = [torch.empty(T * top_k, dtype=torch.int32, device=dev) for _ in range(4)]
+    offs = torch.empty(E + 1, dtype=torch.int32, device=dev) if with_offsets else None
     L = _lib.lib()
     _lib.check(L.mq_moe_route_sort(_ptr(logits.contiguous()), _ptr(expert_bias), T, E, top_k,
                                    int(bool(norm_topk_prob)), _ptr(idx), _ptr(sc),
-                                   *(_ptr(t) for t in outs), _stream(logits)), op)
-    return (idx, sc, *outs)
+                                   *(_ptr(t) for t in outs), _ptr(offs), _stream(logits)), op)
+    return (idx, sc, *outs, offs) if with_offsets else (idx, sc, *outs)
 
 
 def _combine_args(op, y, inverse, scores):
@@ -152,21 +158,27 @@ class QExperts:
     def num_experts(self) -> int:
         return self.wq.shape[0]
 
-    def __call__(self, x, lhs=None, rhs=None, sorted_indices=False):
+    def __call__(self, x, lhs=None, rhs=None, sorted_indices=False, offsets=None):
         return core.gather_qmm(x, self.wq, self.scales, self.biases, lhs_indices=lhs,
                                rhs_indices=rhs, transpose=True, group_size=self.group_size,
-                               bits=self.bits, sorted_indices=sorted_indices)
+                               bits=self.bits, sorted_indices=sorted_indices,
+                               expert_offsets=offsets)
 
-    def swiglu(self, x, lhs, rhs, sorted_indices=False):
+    def swiglu(self, x, lhs, rhs, sorted_indices=False, offsets=None):
         """silu(gate) * up of a gate|up bank (every expert: gate rows, then up rows)
         for the pairs (lhs, rhs): the fused kernel where it takes the shape, else
         gather_qmm then silu_mul -- the same bits either way."""
         T, M, K = rhs.numel(), x.shape[-2], x.shape[-1]
         N = self.wq.shape[1] // 2
+        if offsets is not None and sorted_indices and T * M > 64:
+            # the expert-segment GEMM with SiLU * up in its epilogue
+            return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
+                                          self.group_size, self.bits, expert_offsets=offsets)
         if core.gather_swiglu_supported(T, M, N, K, self.group_size, self.bits):
             return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
                                           self.group_size, self.bits)
-        return silu_mul(self(x, lhs=lhs, rhs=rhs, sorted_indices=sorted_indices))
+        return silu_mul(self(x, lhs=lhs, rhs=rhs, sorted_indices=sorted_indices,
+                             offsets=offsets))
 
 
 class MoEBlock:
@@ -187,10 +199,14 @@ class MoEBlock:
         logits = self.gate(xt)
         xb = xt.reshape(T, 1, H)
         if T * self.top_k >= 64:  # the reference sorts at >= 64 pairs (lfm2.py:204)
-            _, sc, sorted_ids, _, inverse, rows = route_sort(
-                logits, self.top_k, self.num_experts, self.norm_topk_prob, self.expert_bias)
-            act = self.gate_up.swiglu(xb, rows, sorted_ids, sorted_indices=True)
-            y = self.down(act, rhs=sorted_ids, sorted_indices=True)
+            # the segment offsets feed the sorted GEMM; decode-sized batches
+            # (<= 64 pairs) run per-pair GEMVs that do not read them
+            sort = route_sort(logits, self.top_k, self.num_experts, self.norm_topk_prob,
+                              self.expert_bias, with_offsets=T * self.top_k > 64)
+            _, sc, sorted_ids, _, inverse, rows = sort[:6]
+            offs = sort[6] if len(sort) > 6 else None
+            act = self.gate_up.swiglu(xb, rows, sorted_ids, sorted_indices=True, offsets=offs)
+            y = self.down(act, rhs=sorted_ids, sorted_indices=True, offsets=offs)
         else:
             idx, sc = route(logits, self.top_k, self.norm_topk_prob, self.expert_bias)
             inverse = None

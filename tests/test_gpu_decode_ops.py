@@ -74,7 +74,8 @@ def test_rms_norm_batched_shape(ops):
                                         (16, 4739, 3584, 4), (32, 14336, 4096, 4),
                                         (16, 24000, 512, 4), (32, 20000, 1024, 8),
                                         (16, 4739, 3584, 8), (16, 18944, 3584, 8),
-                                        (12, 9475, 3584, 8)])
+                                        (12, 9475, 3584, 8), (512, 18944, 3584, 4),
+                                        (2048, 4739, 3584, 8), (300, 9476, 2048, 4)])
 def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     """The gate|up GEMV with silu(gate) * up in its epilogue: bit-equal to the
     GEMV followed by silu_mul.  N = 18948, 1025 and 2049 leave a partial last
@@ -82,7 +83,9 @@ def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     32 rows the skinny GEMM: K split with the SwiGLU in the reduce (4739) or
     unsplit with it in the GEMM's epilogue (9475 ends in a 3-column tile;
     24000 and 20000 take blocks of 6 and 5 waves).  8-bit batches of 9-16 rows
-    take the skinny GEMM's 32-row tile too."""
+    take the skinny GEMM's 32-row tile too.  Prefill-sized M (300, 512, 2048)
+    take the large-M GEMM with SiLU * up in its epilogue (4739 and 9476 leave
+    partial 128-column tiles, 300 a partial row tile)."""
     core = importlib.import_module("mlx-server-runtime_amd.core")
     assert core.swiglu_supported(M, N, K, 64, bits)
     g = _gen(N + K + bits)

@@ -64,18 +64,22 @@ def test_route(moe, T, E, k, norm, with_bias):
                                    (2000, 6, 512)])
 def test_expert_sort(moe, T, k, E):
     ids = torch.randint(0, E, (T, k), generator=_gen(T + k), device=DEV, dtype=torch.int32)
-    sorted_ids, order, inverse, rows = moe.expert_sort(ids, E)
+    sorted_ids, order, inverse, rows, offs = moe.expert_sort(ids, E, with_offsets=True)
     flat = ids.reshape(-1).long()
     ref_order = torch.argsort(flat, stable=True)
     assert torch.equal(order.long(), ref_order)
     assert torch.equal(sorted_ids.long(), flat[ref_order])
     assert torch.equal(inverse.long(), torch.argsort(ref_order, stable=True))
     assert torch.equal(rows.long(), ref_order // k)
+    # segment starts: expert e's run begins after every smaller id
+    ref_offs = torch.searchsorted(flat[ref_order], torch.arange(E + 1, device=DEV))
+    assert torch.equal(offs.long(), ref_offs)
 
 
 def test_expert_sort_out_of_range_ids_go_last(moe):
     ids = torch.tensor([[3, -1], [7, 0], [8, 3]], dtype=torch.int32, device=DEV)  # E = 8
-    sorted_ids, order, inverse, rows = moe.expert_sort(ids, 8)
+    sorted_ids, order, inverse, rows, offs = moe.expert_sort(ids, 8, with_offsets=True)
+    assert offs.tolist() == [0, 1, 1, 1, 3, 3, 3, 3, 4]  # the ids -1 and 8 follow offs[8]
     assert sorted_ids.tolist() == [0, 3, 3, 7, -1, 8]
     assert order.tolist() == [3, 0, 5, 2, 1, 4]
     assert rows.tolist() == [1, 0, 2, 1, 0, 2]
@@ -110,8 +114,9 @@ def test_route_sort_equals_route_then_sort(moe, T, E, k):
     bias = torch.randn(E, generator=_gen(2), device=DEV) * 0.01
     for b in (None, bias):
         idx, sc = moe.route(logits, k, True, b)
-        ref = (idx, sc) + moe.expert_sort(idx, E)
-        got = moe.route_sort(logits, k, E, True, b)
+        ref = (idx, sc) + moe.expert_sort(idx, E, with_offsets=True)
+        got = moe.route_sort(logits, k, E, True, b, with_offsets=True)
+        assert len(got) == len(ref) == 7
         for a, r in zip(got, ref):
             assert torch.equal(a, r)
 
@@ -329,3 +334,30 @@ def test_qwen3_30b_a3b_shape_decoder_batch_8(mq):
           f"{match}/{total}, worst margin {worst:.3f} std")
     assert e.median() <= 2.5e-2 and (e <= 3e-2).float().mean() >= 0.75, e
     assert match >= 0.8 * total and worst <= 0.3, (match, total, worst)
+
+
+@pytest.mark.parametrize("K", [2048, 768])
+def test_gather_segments_equals_gather(moe, mq, K):
+    """gather_qmm given the sort's segment offsets (mq_gather_qmm_segments) equals
+    gather_qmm deriving the segments itself, bit for bit: 2048 tokens routed to
+    8 of 128 experts, the x rows gathered through the sort's rows."""
+    E, k, N, T = 128, 8, 512, 2048
+    g = _gen(K)
+    logits = torch.randn(T, E, generator=g, device=DEV).to(torch.bfloat16)
+    _, _, sorted_ids, _, _, rows, offs = moe.route_sort(logits, k, E, with_offsets=True)
+    w = (torch.randn(E * N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = (t.reshape(E, N, -1) for t in mq.quantize(w, 64, 4))
+    x = torch.randn(T, 1, K, generator=g, device=DEV).to(torch.bfloat16)
+    a = mq.gather_qmm(x, wq, sc, bi, lhs_indices=rows, rhs_indices=sorted_ids,
+                      sorted_indices=True, expert_offsets=offs)
+    b = mq.gather_qmm(x, wq, sc, bi, lhs_indices=rows, rhs_indices=sorted_ids,
+                      sorted_indices=True)
+    assert torch.equal(a, b)
+    c = mq.gather_qmm(x, wq, sc, bi, lhs_indices=rows, rhs_indices=sorted_ids)  # unsorted path
+    assert float((a.float() - c.float()).abs().max() / c.float().abs().max()) <= 1e-2
+    # the same bank read as gate | up halves: SiLU * up in the GEMM's epilogue
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    ops = importlib.import_module("mlx-server-runtime_amd.decode_ops")
+    f = core.gather_qmm_swiglu(x, wq, sc, bi, rows, sorted_ids, 64, 4, expert_offsets=offs)
+    assert f.shape == (T * k, 1, N // 2)
+    assert torch.equal(f.reshape(-1, N // 2), ops.silu_mul(a.reshape(-1, N)))

@@ -439,6 +439,38 @@ def test_gather_moe_shape_prefill_sampled(mq, orc, bits):
     assert_close(y[torch.from_numpy(rows).to(DEV)], ref)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("K,Mb", [(768, 1), (1024, 1), (768, 3)])
+def test_gather_sorted_expert_segments(mq, orc, bits, K, Mb):
+    """The expert-segment GEMM behind sorted gather_qmm: segments of 0, 1, 255,
+    256, 257 and 700 batches (whole and partial 256-row tiles, empty experts),
+    ids below 0 first and at or above E last (their rows are zero), x batches
+    gathered through lhs (one of them out of range: zero rows), K of 12 groups
+    (a partial scale chunk) and 16, and Mb rows per batch."""
+    rng = np.random.default_rng(5 + K + Mb + bits)
+    E, N = 12, 320
+    sizes = [256, 0, 1, 700, 255, 0, 257, 37, 3, 0, 90, 256]
+    rhs = np.concatenate([np.full(3, -1)] + [np.full(n, e) for e, n in enumerate(sizes)]
+                         + [np.full(4, E)]).astype(np.int32)
+    T = rhs.shape[0]
+    wq, s, b = _experts(orc, rng, E, N, K, bits)
+    xb = 40
+    x = rand_bf16(orc, rng, (xb, Mb, K), 1.0)
+    lhs = rng.integers(0, xb, T).astype(np.int32)
+    lhs[7] = xb  # out of range: its rows are zero
+    y = mq.gather_qmm(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b),
+                      lhs_indices=torch.from_numpy(lhs).to(DEV),
+                      rhs_indices=torch.from_numpy(rhs).to(DEV), group_size=64, bits=bits,
+                      sorted_indices=True)
+    assert y.shape == (T, Mb, N)
+    valid = (rhs >= 0) & (rhs < E) & (lhs < xb)
+    yh = bits_host(y)
+    assert np.all(yh[~valid] == 0)
+    ref = orc.gather_qmm(x, wq, s, b, rhs[valid], lhs_indices=lhs[valid], group_size=64,
+                         bits=bits)
+    assert_close(y[torch.from_numpy(np.nonzero(valid)[0]).to(DEV)], ref)
+
+
 # ------------------------------------------------------------ modules
 
 

@@ -45,7 +45,7 @@ def test_header_declares_the_abi():
         "mq_quantized_matmul_swiglu_ws", "mq_quantized_matmul_add_rms_norm_supported",
         "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm",
         "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu", "mq_hbm_read",
-        "mq_quantized_matmul_noalloc"])
+        "mq_quantized_matmul_noalloc", "mq_gather_qmm_segments"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -126,15 +126,25 @@ def test_decoder_entry_validation(mq):
     assert L.mq_moe_route(null, null, 4, 600, 8, 1, null, null, null) == -2    # too many experts
     assert L.mq_moe_route(null, null, 4, 8, 9, 1, null, null, null) == -2      # k > E
     assert L.mq_moe_route(null, null, 0, 128, 8, 1, null, null, null) == 0
-    assert L.mq_moe_sort(null, 64, 8, 128, null, null, null, null, null) == -1
-    assert L.mq_moe_sort(null, 64, 0, 128, null, null, null, null, null) == -1
-    assert L.mq_moe_sort(null, 0, 8, 128, null, null, null, null, null) == 0
+    assert L.mq_moe_sort(null, 64, 8, 128, null, null, null, null, null, null) == -1
+    assert L.mq_moe_sort(null, 64, 0, 128, null, null, null, null, null, null) == -1
+    assert L.mq_moe_sort(null, 0, 8, 128, null, null, null, null, null, null) == 0
     assert L.mq_moe_combine(null, null, null, null, 4, 8, 2044, null) == -2    # hidden % 8
     assert L.mq_moe_combine(null, null, null, null, 0, 8, 2048, null) == 0
     rs = L.mq_moe_route_sort
-    assert rs(null, null, 4, 128, 8, 1, null, null, null, null, null, null, null) == -1
-    assert rs(null, null, 4, 600, 8, 1, null, null, null, null, null, null, null) == -2
-    assert rs(null, null, 0, 128, 8, 1, null, null, null, null, null, null, null) == 0
+    assert rs(null, null, 4, 128, 8, 1, null, null, null, null, null, null, null, null) == -1
+    assert rs(null, null, 4, 600, 8, 1, null, null, null, null, null, null, null, null) == -2
+    assert rs(null, null, 0, 128, 8, 1, null, null, null, null, null, null, null, null) == 0
+    seg = L.mq_gather_qmm_segments
+    assert seg(null, null, null, null, null, null, null, null, 300, 1, 64, 512, 8, 300, 64, 4,
+               0, null) == -1                                                   # no offsets
+    one = ctypes.c_void_p(16)  # never dereferenced: validation fails before any launch
+    assert seg(null, null, null, one, null, null, null, null, 300, 1, 64, 512, 8, 300, 64, 4,
+               0, null) == -1                                                   # null pointers
+    assert seg(null, null, null, one, null, null, null, null, 300, 1, 64, 512, 8, 300, 32, 4,
+               1, null) == -2                                                   # group size
+    assert seg(null, null, null, one, null, null, null, null, 0, 1, 64, 512, 8, 0, 64, 4,
+               1, null) == 0
     sup = L.mq_quantized_matmul_swiglu_supported
     assert sup(1, 18944, 3584, 64, 4) == 1 and sup(2, 18944, 3584, 64, 8) == 1
     assert sup(4, 18944, 3584, 64, 4) == 0                                      # M > 2
