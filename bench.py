@@ -67,6 +67,8 @@ def parse():
                     help="eager launches of the headline kernel + a 128 MiB copy (rocprofv3 runs)")
     ap.add_argument("--profile-shape", default=None, metavar="M,K,N,BITS",
                     help="eager launches of quantized_matmul at one shape (rocprofv3 runs)")
+    ap.add_argument("--profile-gather", action="store_true",
+                    help="eager launches of the MoE-prefill expert GEMMs (rocprofv3 runs)")
     ap.add_argument("--decode-only", type=int, default=None, metavar="BATCH",
                     help="only one decode benchmark: 7B at batch 1 or 32, or the MoE model "
                          "at batch 8 (rocprofv3 runs)")
@@ -327,7 +329,7 @@ def sweep(mq, torch):
     return rows
 
 
-def gather_sweep(mq, torch):
+def gather_sweep(mq, torch, eager_launches: int = 0):
     """The expert GEMMs of one MoE layer's prefill at the Qwen3-30B-A3B shape:
     8 x 512 tokens routed to 8 of 128 experts (uniform random), the 32768
     (token, expert) pairs sorted by expert (models/lfm2.py:204,613-618), then
@@ -356,6 +358,15 @@ def gather_sweep(mq, torch):
             mq.gather_qmm(xin, wq, sc, bi, lhs_indices=lhs_i, rhs_indices=rhs, group_size=64,
                           bits=4, sorted_indices=True, expert_offsets=seg)
 
+        if eager_launches:  # for rocprofv3: plain launches, no graph, no timing
+            for i in range(eager_launches):
+                launch(i)
+                if name == "gate|up":
+                    core = importlib.import_module("mlx-server-runtime_amd.core")
+                    core.gather_qmm_swiglu(x, wq, sc, bi, lhs, rhs, 64, 4, expert_offsets=offs)
+            torch.cuda.synchronize()
+            rows.append({"gemm": name, "launches": eager_launches})
+            continue
         ms, _ = time_graph(torch, launch, 8, warmup=2, reps=4)
         ms_derive, _ = time_graph(torch, lambda i: launch(i, seg=None), 8, warmup=2, reps=4)
         flops = 2.0 * T * k * N * K
@@ -366,6 +377,14 @@ def gather_sweep(mq, torch):
                      "us_segments_derived": round(ms_derive * 1e3, 2),
                      "GBps": round((wbytes + 2 * T * k * (N + K)) / (ms * 1e-3) / 1e9, 1),
                      "bound": "mfma", "frac": round(tfl / BF16_PEAK_TFLOPS, 4)})
+        if name == "gate|up":
+            # the form the MoE block runs: SiLU * up in the GEMM's epilogue
+            core = importlib.import_module("mlx-server-runtime_amd.core")
+            fms, _ = time_graph(torch, lambda i: core.gather_qmm_swiglu(
+                x, wq, sc, bi, lhs, rhs, 64, 4, expert_offsets=offs), 8, warmup=2, reps=4)
+            rows[-1]["us_with_swiglu_epilogue"] = round(fms * 1e3, 2)
+            rows[-1]["frac_with_swiglu_epilogue"] = round(
+                flops / (fms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)
         del wq, sc, bi
     torch.cuda.empty_cache()
     return rows
@@ -394,6 +413,11 @@ def main():
             mq.quantized_matmul(px, wq, s, b, transpose=True, group_size=64, bits=pbits)
         torch.cuda.synchronize()
         print(json.dumps({"profile_shape": [pM, pK, pN, pbits], "launches": args.warmup + args.steps}))
+        return
+
+    if args.profile_gather:
+        rows = gather_sweep(mq, torch, eager_launches=args.warmup + args.steps)
+        print(json.dumps({"profile_gather": rows}))
         return
 
     if args.decode_only is not None:

@@ -1,19 +1,24 @@
-// Large-M quantized matmul, one wave per SIMD:
+// Large-M quantized matmul, two waves per SIMD:
 //   y[m, n] = sum_k x[m, k] * (s*q + b)[n, k]  (+ bias[n])
 // mx.quantized_matmul(x, w, scales, biases, transpose=True) for prefill-sized
-// M (python/mlx_worker/native_mlx/models/qwen2.py:76-78,115,134,227).
+// M (python/mlx_worker/native_mlx/models/qwen2.py:76-78,115,134,227), and
+// gather_qmm over experts' row segments (mx.gather_qmm with sorted_indices, as
+// python/mlx_worker/native_mlx/models/lfm2.py:176-187 calls it).
 //
-// MFMA-bound.  A 256-thread block owns a 256x256 output tile and walks K in
-// steps of 64 (one quantization group).  Each of its 4 waves -- one per SIMD --
-// computes the whole 256-row M tile for 64 columns: 8x2
-// v_mfma_f32_32x32x16_bf16 per 16-wide k slice, 256 float32 accumulators per
+// MFMA-bound.  A 512-thread block owns a 256x256 output tile and walks K in
+// steps of 64 (one quantization group).  Each of its 8 waves -- two per SIMD --
+// computes the whole 256-row M tile for 32 columns: 8
+// v_mfma_f32_32x32x16_bf16 per 16-wide k slice, 128 float32 accumulators per
 // lane.  So every code of the block's 256 columns is dequantized exactly once
 // per block (256 MACs per dequantized weight): the weights' VALU work per MFMA
 // is half what a 2x4 wave grid (128 rows per wave, each column dequantized by
-// two waves) spends.
+// two waves) spends; the price is that every wave reads the whole x tile from
+// LDS (256 rows x 64 k per step), which the LDS's read bandwidth carries.
+// The second wave per SIMD covers the other's stalls (dequantization, LDS
+// reads, the barrier); 8 waves measured 4-11% faster than 4 waves of 64
+// columns on every shape this kernel serves.
 //
-// With one wave per SIMD nothing else hides a stall, so every load is issued
-// well ahead of its use:
+// Every load is still issued well ahead of its use:
 // * x never passes through registers on its way in: each step's 256x64 tile is
 //   copied HBM -> LDS by buffer_load_dwordx4 ... lds (every lane writes 16
 //   bytes at M0 + 16*lane), three steps ahead, into one of four 32 KiB stages.
@@ -32,6 +37,8 @@
 // * Tiles run in groups of 4 row blocks x every column block, the row blocks
 //   fastest: the 32 blocks an XCD runs at once cover 4 row blocks x 8 column
 //   blocks, so they share x rows and codes in that XCD's L2.
+// * The output tile is staged through LDS as bfloat16 and written as 16-byte
+//   row chunks.
 // One barrier per step; the wait before it covers the DMAs of two steps ago
 // and earlier (the next step's x tile), never those of this step or the
 // previous one.
@@ -46,10 +53,8 @@ namespace mq {
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int kThreads = 256;
 constexpr int kRowTiles = BM / 32;               // 8 MFMA row tiles per wave
 constexpr int kXStage = BM * BK * 2;             // 32 KiB of x per step
-constexpr int kXOps = kXStage / (kThreads * 16); // 8 DMA operations per lane per step
 constexpr int kSbChunk = 8;                      // groups per scale/bias chunk
 constexpr int kSbArray = BN * kSbChunk * 2;      // 4 KiB: one array, one chunk
 constexpr int kSbBytes = 2 * kSbArray;           // scales + biases of a chunk
@@ -137,11 +142,12 @@ struct GatherTile {
   int e, row0, rows, lo, hi, total;
 };
 
+template <int kThreads>
 __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
-  // sh: LDS ints, 2 * (E + 1) + 8 of them
+  // sh: LDS ints, 2 * (E + 1) + 10 of them; E <= 4 * kThreads
   int* start = sh;              // [E + 1] segment starts (batches)
   int* pre = sh + a.E + 1;      // [E + 1] exclusive tile prefix
-  int* misc = pre + a.E + 1;    // [8]
+  int* misc = pre + a.E + 1;    // [10]: lo, wave totals, the tile's expert
   const int tid = threadIdx.x;
   if (a.seg) {
     for (int e = tid; e <= a.E; e += kThreads) start[e] = a.seg[e];
@@ -203,14 +209,14 @@ __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
     run += mine[q];
   }
   if (tid == kThreads - 1) pre[min(a.E, 4 * kThreads)] = run;
-  if (tid == 0) misc[5] = -1;
+  if (tid == 0) misc[9] = -1;
   __syncthreads();
   const int total = pre[a.E];
   for (int e = tid; e < a.E; e += kThreads)
-    if (pre[e] <= rt && rt < pre[e + 1]) misc[5] = e;
+    if (pre[e] <= rt && rt < pre[e + 1]) misc[9] = e;
   __syncthreads();
   GatherTile g;
-  g.e = misc[5];
+  g.e = misc[9];
   g.lo = misc[0];
   g.hi = start[a.E];
   g.total = total;
@@ -226,13 +232,19 @@ __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
   return g;
 }
 
+// WAVES waves (4: one per SIMD, or 8: two) split the block's 256 columns: each
+// owns all 256 rows of 256 / WAVES columns (NJ = 8 / WAVES MFMA column tiles),
+// so every code of the block is dequantized once whatever WAVES is.
 // SWIGLU: the matrix holds 2N rows, gate rows then up rows (the fused gate|up
-// projection); a block computes 128 gate columns and their 128 up columns --
-// lane (j = 0) and (j = 1) hold the same (row, column) of both -- and writes
-// y[., N] = silu(gate) * up, each rounded to bfloat16 as the unfused kernels
-// round (gate and up, then silu, then the product).
-template <int BITS, bool GATHER, bool SB16, bool SWIGLU>
-__global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
+// projection); block columns 0..127 are 128 gate columns and 128..255 their up
+// columns; the epilogue pairs them and writes y[., N] = silu(gate) * up, each
+// rounded to bfloat16 as the unfused kernels round (gate and up, then silu,
+// then the product).
+template <int BITS, bool GATHER, bool SB16, bool SWIGLU, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
+  constexpr int kThreads = 64 * WAVES;
+  constexpr int NJ = 8 / WAVES;                     // 32-column MFMA tiles per wave
+  constexpr int kXOps = kXStage / (kThreads * 16);  // x DMA operations per lane per step
   extern __shared__ u32x4_t smem[];
   char* const lds = reinterpret_cast<char*>(smem);
   const int tid = threadIdx.x;
@@ -256,7 +268,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
     const int run = 8 * a.tiles_n;
     const int rt = (blockIdx.x / run) * 8 + blockIdx.x % 8;
     bn = (blockIdx.x % run) / 8;
-    const GatherTile g = gather_tile(a, rt, reinterpret_cast<int*>(lds));
+    const GatherTile g = gather_tile<kThreads>(a, rt, reinterpret_cast<int*>(lds));
     if (g.e < 0) {
       // the first spare row tile zeroes the rows whose id names no expert
       if (rt == g.total) {
@@ -292,11 +304,11 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
   }
   const int n0 = bn * kOutCols;
   // matrix row of block column c (0..255): c itself past n0, or for SWIGLU
-  // gate row n0 + 32 (c / 64) + c % 32 when c % 64 < 32, else its up row
+  // gate row n0 + c for c < 128, else the up row of output column n0 + c - 128
   auto wrow = [&](int c, int& out_col) {
     if constexpr (SWIGLU) {
-      out_col = n0 + 32 * (c >> 6) + (c & 31);
-      return ((c >> 5) & 1) * N + out_col;
+      out_col = n0 + (c & 127);
+      return (c >> 7) * N + out_col;
     } else {
       out_col = n0 + c;
       return out_col;
@@ -339,38 +351,39 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
       xoff[i] = (uint32_t)((out_row0 + row) * K + (int)chunk) * 2;
     }
   }
-  // Codes: block column 64*wave + 32j + l%32, half h of each group.
+  // Codes: block column 32 NJ wave + 32j + l%32, half h of each group.
   constexpr int CB = BITS * 4;  // code bytes per lane per step: 16 (4-bit) / 32 (8-bit)
   constexpr int NC = BITS == 4 ? 2 : 4;  // 16-byte code loads per lane per step
-  uint32_t coff[2];
+  uint32_t coff[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     int oc;
-    const int n = wrow(wave * 64 + j * 32 + (l & 31), oc);
+    const int n = wrow(wave * 32 * NJ + j * 32 + (l & 31), oc);
     coff[j] = oc < N ? (uint32_t)(n * (K * BITS / 8) + h * CB) : kOutOfRange;
   }
-  // Scale/bias DMA: wave w loads both arrays for columns 64w + l.  SB16: one
-  // 16-byte operation per array per chunk (8 groups of a column together,
-  // LDS [array][column][group]); otherwise four 4-byte operations per array
-  // (rows of G groups, G even, are only 4-byte aligned; LDS
-  // [array][group pair][column]).
+  // Scale/bias DMA, as wave operations o of 64 lanes (column block cb of 64
+  // columns, lane l taking column 64 cb + l); wave w issues o = w, w + WAVES,
+  // ..., all with cb = w % 4.  SB16: 8 operations per chunk, o = 4a + cb, one
+  // 16-byte load per lane (8 groups of a column; LDS [array][column][group]);
+  // otherwise 32, o = 16a + 4d + cb, dword d of 4 (rows of G groups, G even,
+  // are only 4-byte aligned; LDS [array][group pair][column]).
+  constexpr int kSbOps = (SB16 ? 8 : 32) / WAVES;  // DMA operations per lane per chunk
   uint32_t soff;
   {
     int oc;
-    const int n = wrow(wave * 64 + l, oc);
+    const int n = wrow((wave & 3) * 64 + l, oc);
     soff = oc < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
   }
   // A fragment rows 32i + l%32; logical chunk 4h + ks, stored at (4h + ks) ^ f
   // with f = (l >> 1) & 7 for every row tile: only bits 4-5 of the byte offset
   // depend on ks, so the k-slice ks reads at aoff ^ (ks << 4).
   const uint32_t aoff = (uint32_t)((l & 31) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
-  uint32_t sbr[2];
+  uint32_t sbr[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int c = wave * 64 + j * 32 + (l & 31);
+  for (int j = 0; j < NJ; ++j) {
+    const int c = wave * 32 * NJ + j * 32 + (l & 31);
     sbr[j] = kSbBase + (SB16 ? c * 16 : c * 4);
   }
-  constexpr int kSbOps = SB16 ? 2 : 8;  // DMA operations per lane per scale chunk
 
   auto dma_x = [&](int kt, int stage) {
 #pragma unroll
@@ -380,43 +393,45 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
   };
   auto dma_sb = [&](int chunk, int buf) {
     char* dst = lds + kSbBase + buf * kSbBytes;
-    if constexpr (SB16) {
-      dma16(srs, (lds_t*)(dst + wave * 1024), soff + chunk * (kSbChunk * 2));
-      dma16(brs, (lds_t*)(dst + kSbArray + wave * 1024), soff + chunk * (kSbChunk * 2));
-    } else {
+    const uint32_t src = soff + chunk * (kSbChunk * 2);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_t*)(dst + d * 1024 + wave * 256), 4,
-                                                 soff + chunk * (kSbChunk * 2) + d * 4, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_t*)(dst + kSbArray + d * 1024 + wave * 256),
-                                                 4, soff + chunk * (kSbChunk * 2) + d * 4, 0, 0, 0);
+    for (int t = 0; t < kSbOps; ++t) {
+      const int o = wave + WAVES * t;
+      if constexpr (SB16) {
+        const int arr = o >> 2, cb = o & 3;
+        dma16(arr ? brs : srs, (lds_t*)(dst + arr * kSbArray + cb * 1024), src);
+      } else {
+        const int arr = o >> 4, d = (o >> 2) & 3, cb = o & 3;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arr ? brs : srs,
+                                                 (lds_t*)(dst + arr * kSbArray + d * 1024 + cb * 256),
+                                                 4, src + d * 4, 0, 0, 0);
       }
     }
   };
-  auto load_codes = [&](u32x4_t (&cw)[2][NC / 2], int kt) {
+  auto load_codes = [&](u32x4_t (&cw)[NJ][NC / 2], int kt) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int p = 0; p < NC / 2; ++p) cw[j][p] = buf_load16(wrs, coff[j] + kt * (BK * BITS / 8) + p * 16);
   };
 
-  f32x16_t acc[kRowTiles][2];
+  f32x16_t acc[kRowTiles][NJ];
 #pragma unroll
   for (int i = 0; i < kRowTiles; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  u32x4_t cw[kCodeRing][2][NC / 2];
-  auto dequant_frag = [&](const u32x4_t (&q)[2][NC / 2], int j, int ks, const GroupAffine& g) {
+  u32x4_t cw[kCodeRing][NJ][NC / 2];
+  auto dequant_frag = [&](const u32x4_t (&q)[NJ][NC / 2], int j, int ks, const GroupAffine& g) {
     const u32x4_t& w = q[j][BITS == 4 ? 0 : ks >> 1];
     if constexpr (BITS == 4) return dequant8<4>(w[ks], 0u, g.s, g.b);
     else return dequant8<8>(w[(ks & 1) * 2], w[(ks & 1) * 2 + 1], g.s, g.b);
   };
-  auto read_sb = [&](int buf, int grp, GroupAffine (&g)[2]) {
+  auto read_sb = [&](int buf, int grp, GroupAffine (&g)[NJ]) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const char* p = lds + sbr[j] + buf * kSbBytes +
                       (SB16 ? grp * 2 : (grp >> 1) * 1024 + (grp & 1) * 2);
       g[j].s = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
@@ -435,11 +450,11 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
   step_barrier<2 * kXOps>();
   // B fragments of k-slice 0 are always dequantized one step early, at the end
   // of the previous step, so each step opens with MFMAs instead of VALU.
-  GroupAffine ga[2];
+  GroupAffine ga[NJ];
   read_sb(c_begin & 1, 0, ga);
-  bf16x8_t b0[2];
+  bf16x8_t b0[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
+  for (int j = 0; j < NJ; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
 
   // The K loop.  MASKED skips the MFMAs (and A reads) of row tiles past the
   // tile's valid rows, at the price of a branch per row tile; full tiles take
@@ -465,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
 
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          bf16x8_t bq[2], an[kRowTiles];
+          bf16x8_t bq[NJ], an[kRowTiles];
           if (ks < 3) {
 #pragma unroll
             for (int i = 0; i < kRowTiles; ++i)
@@ -476,22 +491,22 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
           for (int i = 0; i < kRowTiles; ++i)
             if (!MASKED || i < live) {
 #pragma unroll
-              for (int j = 0; j < 2; ++j)
+              for (int j = 0; j < NJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b0[j], acc[i][j], 0, 0, 0);
             }
           if (ks < 3) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
+            for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
           } else {
             // next step: its scales (the next chunk's buffer after the last
             // step of a chunk, DMA-ed four steps ago) and its first k-slice
             if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
             else read_sb(c & 1, u + 1, ga);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
+            for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
           }
 #pragma unroll
-          for (int j = 0; j < 2; ++j) b0[j] = bq[j];
+          for (int j = 0; j < NJ; ++j) b0[j] = bq[j];
           if (ks < 3) {
 #pragma unroll
             for (int i = 0; i < kRowTiles; ++i) a[i] = an[i];
@@ -519,8 +534,8 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
   if (a.partial) {
     // a split of K writes its float32 partial sums straight from registers
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wave * 64 + j * 32 + (l & 31);
+    for (int j = 0; j < NJ; ++j) {
+      const int n = n0 + wave * 32 * NJ + j * 32 + (l & 31);
       if (n >= N) continue;
       float* pc = a.partial + (int64_t)split * a.M * N + n;
 #pragma unroll
@@ -536,14 +551,22 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
     }
     return;
   }
-  // bfloat16 output: the 256-row tile goes through LDS (the x stages; every
-  // wave's DMAs have landed once all have passed the barrier) so that rows
-  // leave as 16-byte stores instead of 2-byte ones per lane and value.
+  // bfloat16 output: the 256 x 256 tile of block columns goes through LDS
+  // (the x stages; every wave's DMAs have landed once all have passed the
+  // barrier) so that rows leave as 16-byte stores instead of 2-byte ones per
+  // lane and value.  SWIGLU stages the gate and up columns (rounded to
+  // bfloat16, as the unfused GEMM stores them) and pairs them on the way out.
   __syncthreads();
-  constexpr int kOutStride = kOutCols * 2 + 16;  // bytes per staged row (padding spreads banks)
-  static_assert(BM * kOutStride <= kLds, "the output tile must fit the LDS");
-  if constexpr (SWIGLU) {
-    const int c = wave * 32 + (l & 31);
+  constexpr int kStageStride = BN * 2 + 16;  // bytes per staged row (padding spreads banks)
+  static_assert(BM * kStageStride <= kLds, "the output tile must fit the LDS");
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = wave * 32 * NJ + j * 32 + (l & 31);
+    float add = 0.f;
+    if constexpr (!SWIGLU) {
+      const int n = n0 + c;
+      add = (a.bias && n < N) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
+    }
 #pragma unroll
     for (int i = 0; i < kRowTiles; ++i)
 #pragma unroll
@@ -551,31 +574,14 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int m = i * 32 + 8 * r + 4 * h + e;
-          const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[i][0][4 * r + e]));
-          const float u = bf16_bits_to_f32(f32_to_bf16_bits(acc[i][1][4 * r + e]));
-          *reinterpret_cast<uint16_t*>(lds + m * kOutStride + c * 2) = silu_mul_bf16(g, u);
+          *reinterpret_cast<uint16_t*>(lds + m * kStageStride + c * 2) =
+              (uint16_t)f32_to_bf16_bits(acc[i][j][4 * r + e] + add);
         }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = wave * 64 + j * 32 + (l & 31);
-      const int n = n0 + c;
-      const float add = (a.bias && n < N) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int m = i * 32 + 8 * r + 4 * h + e;
-            *reinterpret_cast<uint16_t*>(lds + m * kOutStride + c * 2) =
-                (uint16_t)f32_to_bf16_bits(acc[i][j][4 * r + e] + add);
-          }
-    }
   }
   __syncthreads();
-  // thread t stores 16-byte chunk t % CPR of rows (256 / CPR) q + t / CPR
-  constexpr int CPR = kOutCols / 8;  // chunks per row
+  // thread t stores 16-byte chunk t % CPR of rows (kThreads / CPR) q + t / CPR
+  constexpr int kOutCols_ = SWIGLU ? BN / 2 : BN;
+  constexpr int CPR = kOutCols_ / 8;  // chunks per output row
   const int cc = tid % CPR;
   const int n = n0 + cc * 8;
   const bool vec = (N % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
@@ -583,13 +589,21 @@ __global__ __launch_bounds__(kThreads, 1) void qmm4_kernel(const Qmm4Args a) {
   for (int q = 0; q < BM * CPR / kThreads; ++q) {
     const int row = q * (kThreads / CPR) + tid / CPR;
     if (row >= rows_valid || n >= N) continue;
-    const char* src = lds + row * kOutStride + cc * 16;
+    const char* src = lds + row * kStageStride + cc * 16;
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
+    if constexpr (SWIGLU) {
+      const u32x4_t up = *reinterpret_cast<const u32x4_t*>(src + (BN / 2) * 2);
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        v[w] = (uint32_t)silu_mul_bf16(lo_bf16(v[w]), lo_bf16(up[w])) |
+               ((uint32_t)silu_mul_bf16(hi_bf16(v[w]), hi_bf16(up[w])) << 16);
+    }
     uint16_t* dst = a.y + (int64_t)(out_row0 + row) * N + n;
     if (vec) {
-      *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
+      *reinterpret_cast<u32x4_t*>(dst) = v;
     } else {
-      for (int e = 0; e < 8 && n + e < N; ++e)
-        dst[e] = reinterpret_cast<const uint16_t*>(src)[e];
+      const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
+      for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = vs[e];
     }
   }
 }
@@ -605,18 +619,22 @@ int qmm4_splits(int64_t M, int64_t N, int64_t K) {
   return (int)std::max<int64_t>(1, std::min(kRound / tiles, chunks / 4));
 }
 
+constexpr int kWaves = 8;  // waves per block: two per SIMD
+
 template <bool GATHER, bool SWIGLU>
 hipError_t launch(const Qmm4Args& a, int bits, dim3 grid, hipStream_t stream) {
   const bool sb16 = (a.K / kGroup) % kSbChunk == 0;
   void (*kern)(Qmm4Args);
   if (bits == 4)
-    kern = sb16 ? qmm4_kernel<4, GATHER, true, SWIGLU> : qmm4_kernel<4, GATHER, false, SWIGLU>;
+    kern = sb16 ? qmm4_kernel<4, GATHER, true, SWIGLU, kWaves>
+                : qmm4_kernel<4, GATHER, false, SWIGLU, kWaves>;
   else
-    kern = sb16 ? qmm4_kernel<8, GATHER, true, SWIGLU> : qmm4_kernel<8, GATHER, false, SWIGLU>;
+    kern = sb16 ? qmm4_kernel<8, GATHER, true, SWIGLU, kWaves>
+                : qmm4_kernel<8, GATHER, false, SWIGLU, kWaves>;
   const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), kLds, stream, a);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * kWaves), kLds, stream, a);
   return hipGetLastError();
 }
 
@@ -666,7 +684,7 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
 bool qmm4_gather_fits(int64_t T, int64_t Mb, int64_t N, int64_t K, int64_t E,
                       int64_t x_batches, int bits) {
   const int64_t lim = (int64_t)1 << 31;
-  return E >= 1 && E <= 4 * kThreads && T * Mb < lim / 2 &&
+  return E >= 1 && E <= 4 * 64 * kWaves && T * Mb < lim / 2 &&
          offsets_fit(x_batches * Mb, N, K, bits);
 }
 
