@@ -15,9 +15,13 @@
  *   - Weight format (MLX "affine"): wq uint32 [rows, K*bits/32] with codes
  *     packed LSB-first (code j of a word at bits [j*bits, (j+1)*bits));
  *     scales and biases bfloat16 [rows, K/group_size]; w = scale*q + bias.
- *   - Supported here: bits 4 or 8, group_size 64, transpose = 1.  MLX's other
- *     settings (bits 2/3/5/6, group_size 32/128, transpose = 0) return
+ *   - Supported here: bits 4 or 8, group_size 32, 64 or 128, transpose = 1.
+ *     MLX's other settings (bits 2/3/5/6, transpose = 0) return
  *     MQ_ERR_UNSUPPORTED; anything MLX itself rejects returns MQ_ERR_INVALID.
+ *     The fused entry points (SwiGLU, RMSNorm, add + RMSNorm, the SwiGLU
+ *     epilogue of mq_gather_qmm_segments) take group_size 64 only (their
+ *     *_supported queries say 0 otherwise); a matmul of more than 8 rows with
+ *     group_size 32 needs K to be a multiple of 64 (else MQ_ERR_UNSUPPORTED).
  *   - Pointers that feed 16-byte loads (x, wq, w, out, y rows) must be 16-byte
  *     aligned.
  *   - Return value: MQ_OK, or a negative code with a message available from

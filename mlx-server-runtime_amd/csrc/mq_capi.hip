@@ -65,9 +65,6 @@ int check_quant(const char* op, int64_t K, int group_size, int bits) {
   if (bits != 4 && bits != 8)
     return fail(MQ_ERR_UNSUPPORTED, "[%s] bits=%d is not implemented on this backend (4 or 8).",
                 op, bits);
-  if (group_size != 64)
-    return fail(MQ_ERR_UNSUPPORTED,
-                "[%s] group_size=%d is not implemented on this backend (64).", op, group_size);
   if (K <= 0 || K % group_size != 0)
     return fail(MQ_ERR_INVALID,
                 "[%s] The last dimension of the matrix needs to be divisible by the "
@@ -88,14 +85,18 @@ int check_dim(const char* op, const char* name, int64_t v) {
 // faster (M = 16, K = 3584: N = 18944 29.4 us against 34.6, N = 4608
 // 11.4 us against 14.1), so there it only serves shapes the skinny GEMM
 // does not fit.
-bool dense_gemv(int64_t M, int64_t N, int64_t K, int bits) {
-  return mq::qmvm_fits(M, N, K, bits, 1) && (M <= 8 || !mq::qmms_fits(M, N, K, bits));
+// The matrix-core GEMV, the skinny GEMM and the large-M GEMM read one scale
+// per 64-wide k step (group size 64); other group sizes run the dot2 GEMV
+// (M <= 8) or the 128 x 128 MFMA GEMM, which both index scales by group.
+bool dense_gemv(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+  return group_size == 64 && mq::qmvm_fits(M, N, K, bits, 1) &&
+         (M <= 8 || !mq::qmms_fits(M, N, K, bits));
 }
 
 // Skinny MFMA kernel for M above the GEMV range and up to two 128-row tiles.
-bool use_skinny(int64_t M, int64_t N, int64_t K, int bits) {
-  return M <= 256 && !dense_gemv(M, N, K, bits) &&
-         !mq::qmv_fits(M, N, K, bits, 1) && mq::qmms_fits(M, N, K, bits);
+bool use_skinny(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+  return group_size == 64 && M <= 256 && !dense_gemv(M, N, K, bits, 64) &&
+         !mq::qmv_fits(M, N, K, bits, 1, 64) && mq::qmms_fits(M, N, K, bits);
 }
 
 }  // namespace
@@ -115,7 +116,8 @@ int mq_quantize(const mq_bf16* w, uint32_t* wq, mq_bf16* scales, mq_bf16* biases
   if (!w || !wq || !scales || !biases) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
   if (!aligned16(w) || !aligned16(wq))
     return fail(MQ_ERR_INVALID, "[%s] w and wq must be 16-byte aligned.", op);
-  return hip_status(mq::launch_quantize(w, wq, scales, biases, rows, K, bits, stream), op);
+  return hip_status(mq::launch_quantize(w, wq, scales, biases, rows, K, group_size, bits, stream),
+                    op);
 }
 
 int mq_dequantize(const uint32_t* wq, const mq_bf16* scales, const mq_bf16* biases, mq_bf16* out,
@@ -128,7 +130,9 @@ int mq_dequantize(const uint32_t* wq, const mq_bf16* scales, const mq_bf16* bias
   if (!aligned16(wq) || !aligned16(out))
     return fail(MQ_ERR_INVALID, "[%s] wq and out must be 16-byte aligned.", op);
   return hip_status(
-      mq::launch_dequantize(wq, scales, biases, nullptr, rows, rows, out, K, bits, stream), op);
+      mq::launch_dequantize(wq, scales, biases, nullptr, rows, rows, out, K, group_size, bits,
+                            stream),
+      op);
 }
 
 int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
@@ -144,15 +148,17 @@ int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
   if (!aligned16(wq) || !aligned16(out))
     return fail(MQ_ERR_INVALID, "[%s] wq and out must be 16-byte aligned.", op);
   return hip_status(
-      mq::launch_dequantize(wq, scales, biases, ids, n_ids, rows, out, K, bits, stream), op);
+      mq::launch_dequantize(wq, scales, biases, ids, n_ids, rows, out, K, group_size, bits,
+                            stream),
+      op);
 }
 
 size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size,
                                      int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
-  if (use_skinny(M, N, K, bits)) return mq::qmms_workspace_bytes(M, N, K, bits);
-  if (dense_gemv(M, N, K, bits) || mq::qmv_fits(M, N, K, bits, 1)) return 0;
+  if (use_skinny(M, N, K, bits, 64)) return mq::qmms_workspace_bytes(M, N, K, bits);
+  if (dense_gemv(M, N, K, bits, 64) || mq::qmv_fits(M, N, K, bits, 1, 64)) return 0;
   if (mq::qmm4_fits(M, N, K, bits)) return mq::qmm4_workspace_bytes(M, N, K);
   return 0;
 }
@@ -170,13 +176,13 @@ int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
   if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
-  if (use_skinny(M, 2 * N, K, bits) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
-  if (use_skinny(M, 2 * N, K, bits) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
+  if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
+  if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
   // route 4 only where mq_quantized_matmul_ws itself runs the large-M GEMM,
   // unsplit, on the 2N rows (the same kernel, so the same bits)
   const int64_t N2 = 2 * N;
-  if (!dense_gemv(M, N2, K, bits) && !mq::qmv_fits(M, N2, K, bits, 1) &&
-      !use_skinny(M, N2, K, bits) && mq::qmm4_fits(M, N2, K, bits) &&
+  if (!dense_gemv(M, N2, K, bits, 64) && !mq::qmv_fits(M, N2, K, bits, 1, 64) &&
+      !use_skinny(M, N2, K, bits, 64) && mq::qmm4_fits(M, N2, K, bits) &&
       mq::qmm4_workspace_bytes(M, N2, K) == 0 && mq::qmm4_swiglu_fits(M, N, K, bits))
     return 4;
   return 0;
@@ -187,7 +193,7 @@ int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
 bool add_norm_fusable(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return false;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64 || N % 8 || N > 8192) return false;
-  return use_skinny(M, N, K, bits) && mq::qmms_split_fusable(M, N, K, bits);
+  return use_skinny(M, N, K, bits, 64) && mq::qmms_split_fusable(M, N, K, bits);
 }
 }  // namespace
 
@@ -370,23 +376,29 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
                 (long long)M);
   hipError_t e;
   const mq::GatherMap g1{nullptr, nullptr, 1, 1, 1};
-  if (dense_gemv(M, N, K, bits) &&
-      (use_matrix_core_gemv(M, N, K) || !mq::qmv_fits(M, N, K, bits, 1))) {
+  if (dense_gemv(M, N, K, bits, group_size) &&
+      (use_matrix_core_gemv(M, N, K) || !mq::qmv_fits(M, N, K, bits, 1, group_size))) {
     e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
-  } else if (mq::qmv_fits(M, N, K, bits, 1)) {
-    e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
-  } else if (use_skinny(M, N, K, bits)) {
+  } else if (mq::qmv_fits(M, N, K, bits, 1, group_size)) {
+    e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, group_size,
+                       stream);
+  } else if (use_skinny(M, N, K, bits, group_size)) {
     if (workspace && !aligned16(workspace))
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
     e = mq::launch_qmms(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
-  } else if (mq::qmm4_fits(M, N, K, bits)) {
+  } else if (group_size == 64 && mq::qmm4_fits(M, N, K, bits)) {
     if (workspace && !aligned16(workspace))
       return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
     e = mq::launch_qmm4(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
                         workspace_bytes, stream);
   } else {
-    e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, stream);
+    if (K % 64)
+      return fail(MQ_ERR_UNSUPPORTED,
+                  "[%s] M=%lld rows with K=%lld (not a multiple of 64) are not implemented on "
+                  "this backend.",
+                  op, (long long)M, (long long)K);
+    e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, group_size, bits, stream);
   }
   return hip_status(e, op);
 }
@@ -429,17 +441,24 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
   // (measured on the 128-expert, 2048 x 768 banks at 64 pairs: 25 % faster
   // decode).
   const bool dot2_rows = M <= 2 && T > 1;
-  if (few && mq::qmvm_fits(M, N, K, bits, T) &&
-      ((use_matrix_core_gemv(M, N, K) && !dot2_rows) || !mq::qmv_fits(M, N, K, bits, T))) {
+  if (few && group_size == 64 && mq::qmvm_fits(M, N, K, bits, T) &&
+      ((use_matrix_core_gemv(M, N, K) && !dot2_rows) || !mq::qmv_fits(M, N, K, bits, T, 64))) {
     e = mq::launch_qmvm(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
-  } else if (few && mq::qmv_fits(M, N, K, bits, T)) {
-    e = mq::launch_qmv(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, stream);
-  } else if (sorted_indices && mq::qmm4_gather_fits(T, M, N, K, E, x_batches, bits)) {
+  } else if (few && mq::qmv_fits(M, N, K, bits, T, group_size)) {
+    e = mq::launch_qmv(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, group_size,
+                       stream);
+  } else if (sorted_indices && group_size == 64 &&
+             mq::qmm4_gather_fits(T, M, N, K, E, x_batches, bits)) {
     e = mq::launch_qmm4_gather(x, lhs_indices, rhs_indices, nullptr, wq, scales, biases, y, T, M,
                                N, K, E, x_batches, bits, false, stream);
   } else {
+    if (K % 64)
+      return fail(MQ_ERR_UNSUPPORTED,
+                  "[%s] T*M=%lld rows with K=%lld (not a multiple of 64) are not implemented on "
+                  "this backend.",
+                  op, (long long)(T * M), (long long)K);
     e = mq::launch_gather_qmm_rows(x, lhs_indices, rhs_indices, wq, scales, biases, y, T * M, N,
-                                   K, E, x_batches * M, (int)M, bits, stream);
+                                   K, E, x_batches * M, (int)M, group_size, bits, stream);
   }
   return hip_status(e, op);
 }
@@ -470,7 +489,8 @@ int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
     return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
   // Decode-sized batches run as mq_gather_qmm (or its SwiGLU GEMV) does: the
   // offsets are not needed there.
-  const bool fits = mq::qmm4_gather_fits(T, M, swiglu ? 2 * N : N, K, E, x_batches, bits);
+  const bool fits = group_size == 64 &&
+                    mq::qmm4_gather_fits(T, M, swiglu ? 2 * N : N, K, E, x_batches, bits);
   if (T * M <= 64 || !fits) {
     if (!swiglu)
       return mq_gather_qmm(x, lhs_indices, rhs_indices, wq, scales, biases, y, T, M, N, K, E,

@@ -20,18 +20,22 @@ struct GatherMap {
   int64_t x_batches;    // batches in x
 };
 
+// Group sizes 32, 64 and 128 (K a multiple of the group size).
 hipError_t launch_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
-                           int64_t rows, int64_t K, int bits, hipStream_t stream);
+                           int64_t rows, int64_t K, int group_size, int bits, hipStream_t stream);
 hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
                              const int32_t* row_ids, int64_t n_out_rows, int64_t n_rows,
-                             uint16_t* out, int64_t K, int bits, hipStream_t stream);
+                             uint16_t* out, int64_t K, int group_size, int bits,
+                             hipStream_t stream);
 
 // y[t][m][n] = x[lhs[t]][m] . dequant(w[rhs[t]][n]) (+ bias[n]); valid when
-// qmv_fits(M, N, K, bits, T) (at most 8 rows, x staged within the LDS budget).
-bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
+// qmv_fits(M, N, K, bits, T, group_size) (at most 8 rows, x and the scales
+// staged within the LDS budget; group size 32, 64 or 128).
+bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T, int group_size);
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                      int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
+                      int64_t N, int64_t K, int bits, const GatherMap& g, int group_size,
+                      hipStream_t stream);
 // Gathered SwiGLU GEMV: y [T, M, N] per (batch, expert) pair of g; every
 // expert's matrix is 2N rows (gate rows, then up rows).
 bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
@@ -124,10 +128,10 @@ hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
-// MFMA path, any M.
+// MFMA path, any M, group size 32, 64 or 128.
 hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                      int64_t N, int64_t K, int bits, hipStream_t stream);
+                      int64_t N, int64_t K, int group_size, int bits, hipStream_t stream);
 // MFMA gather over flattened rows r = t*rows_per_batch + m: x row
 // lhs[t]*rows_per_batch + m (x_rows rows in x) times expert rhs[t]; the rows of
 // one expert inside a row tile share one pass over the weights.
@@ -135,7 +139,7 @@ hipError_t launch_gather_qmm_rows(const uint16_t* x, const int32_t* lhs, const i
                                   const uint32_t* wq, const uint16_t* scales,
                                   const uint16_t* biases, uint16_t* y, int64_t rows, int64_t N,
                                   int64_t K, int64_t E, int64_t x_rows, int rows_per_batch,
-                                  int bits, hipStream_t stream);
+                                  int group_size, int bits, hipStream_t stream);
 
 // Decoder-step kernels (mq_decoder.hip).  KV pages: bfloat16
 // [num_pages, page_size, nkv, head_dim]; page table int32 [B, pages_per_seq];

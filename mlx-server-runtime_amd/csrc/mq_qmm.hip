@@ -10,8 +10,10 @@
 //               QuantizedSwitchLinear (models/lfm2.py:176-187) after the expert
 //               sort of models/lfm2.py:613-618.
 //
-// Tiling: a 256-thread block owns a 128x128 output tile; K advances 64 at a time
-// (one quantization group, so one scale/bias per weight row per step).  Each
+// Tiling: a 256-thread block owns a 128x128 output tile; K advances 64 at a time.
+// A thread's codes for a step (32 4-bit or 16 8-bit: half or a quarter of the
+// step) lie in one quantization group at group sizes 32, 64 and 128, so each
+// takes one scale/bias, group (64 kt + its offset in the step) >> lgs.  Each
 // step the packed codes of the 128 weight rows (4 KiB at 4-bit) are dequantized
 // to bfloat16 (fma(s, q, b), one rounding) straight into LDS next to the
 // activation tile; the four waves (2x2) each run 2x2 v_mfma_f32_32x32x16_bf16
@@ -43,7 +45,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int M, int N, int K,
     const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, int rows_per_batch,
-    int64_t E, int64_t x_rows) {
+    int64_t E, int64_t x_rows, int lgs) {
   __shared__ u32x4_t As[BM * 8];
   __shared__ u32x4_t Bs[BN * 8];
   __shared__ int tile_expert[BM];
@@ -56,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(
   const int wm = wave >> 1, wn = wave & 1;
   const int n0 = blockIdx.x * BN;
   const int m0 = blockIdx.y * BM;
-  const int G = K / kGroup;
+  const int G = K >> lgs;  // groups per row (group size 1 << lgs)
   const int Kw = K * BITS / 32;  // words per weight row
   const int KT = K / BK;
 
@@ -161,8 +163,9 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(
         br_[i] = 0;
         if (won[i]) {
           wr_[i] = load_stream_u4(wsrc[i] + kt * (BK * BITS / 128));
-          sr_[i] = ssrc[i][kt];
-          br_[i] = bsrc[i][kt];
+          const int grp = (kt * BK + wpart[i] * (128 / BITS)) >> lgs;
+          sr_[i] = ssrc[i][grp];
+          br_[i] = bsrc[i][grp];
         }
       }
     };
@@ -256,15 +259,17 @@ __global__ __launch_bounds__(kThreads) void qmm_kernel(
 
 hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                      int64_t N, int64_t K, int bits, hipStream_t stream) {
+                      int64_t N, int64_t K, int group_size, int bits, hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
+  if (K % BK) return hipErrorInvalidValue;  // whole 64-wide steps (checked by the caller)
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  const int lgs = __builtin_ctz((unsigned)group_size);
   if (bits == 4)
     hipLaunchKernelGGL((qmm_kernel<4, false>), grid, dim3(kThreads), 0, stream, x, wq, scales,
-                       biases, bias, y, (int)M, (int)N, (int)K, nullptr, nullptr, 1, 1, M);
+                       biases, bias, y, (int)M, (int)N, (int)K, nullptr, nullptr, 1, 1, M, lgs);
   else
     hipLaunchKernelGGL((qmm_kernel<8, false>), grid, dim3(kThreads), 0, stream, x, wq, scales,
-                       biases, bias, y, (int)M, (int)N, (int)K, nullptr, nullptr, 1, 1, M);
+                       biases, bias, y, (int)M, (int)N, (int)K, nullptr, nullptr, 1, 1, M, lgs);
   return hipGetLastError();
 }
 
@@ -272,17 +277,19 @@ hipError_t launch_gather_qmm_rows(const uint16_t* x, const int32_t* lhs, const i
                                   const uint32_t* wq, const uint16_t* scales,
                                   const uint16_t* biases, uint16_t* y, int64_t rows, int64_t N,
                                   int64_t K, int64_t E, int64_t x_rows, int rows_per_batch,
-                                  int bits, hipStream_t stream) {
+                                  int group_size, int bits, hipStream_t stream) {
   if (rows == 0 || N == 0) return hipSuccess;
+  if (K % BK) return hipErrorInvalidValue;  // whole 64-wide steps (checked by the caller)
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((rows + BM - 1) / BM));
+  const int lgs = __builtin_ctz((unsigned)group_size);
   if (bits == 4)
     hipLaunchKernelGGL((qmm_kernel<4, true>), grid, dim3(kThreads), 0, stream, x, wq, scales,
                        biases, nullptr, y, (int)rows, (int)N, (int)K, lhs, rhs, rows_per_batch,
-                       E, x_rows);
+                       E, x_rows, lgs);
   else
     hipLaunchKernelGGL((qmm_kernel<8, true>), grid, dim3(kThreads), 0, stream, x, wq, scales,
                        biases, nullptr, y, (int)rows, (int)N, (int)K, lhs, rhs, rows_per_batch,
-                       E, x_rows);
+                       E, x_rows, lgs);
   return hipGetLastError();
 }
 

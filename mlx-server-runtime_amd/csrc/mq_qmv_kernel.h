@@ -94,10 +94,12 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
     const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* bias, uint16_t* y, int M, int N, int K,
     const int32_t* __restrict__ lhs, const int32_t* __restrict__ rhs, int64_t E,
-    int64_t x_batches, NormIn nrm) {
+    int64_t x_batches, NormIn nrm, int lcpg) {
   constexpr int EPC = 128 / BITS;      // elements per 16-byte chunk
   constexpr int UPC = EPC / 8;         // 8-element units per chunk (4 or 2)
-  constexpr int CPG = kGroup / EPC;    // chunks per group (2 or 4)
+  // Chunks per group, 1 << lcpg: 1, 2 or 4 at 4 bits and 2, 4 or 8 at 8 bits
+  // for group sizes 32, 64 and 128 (TPR is a multiple of it).
+  constexpr int CPG_MIN = 32 / EPC < 1 ? 1 : 32 / EPC;
   constexpr int SLOTS = kBlock / TPR;  // row slots per block
   constexpr int RPB = SLOTS * R;       // rows per block
   constexpr int WPR = TPR > 64 ? TPR / 64 : 1;  // waves per row (TPR > 64)
@@ -108,10 +110,10 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   __shared__ float red[WPR > 1 ? kBlock / 64 * R * MT : EPI == 1 ? RPB * MT : 1];
 
   const int C = K / EPC;                // chunks per row
-  const int G = K / kGroup;             // groups per row
+  const int G = C >> lcpg;              // groups per row
   const int NJ = (C + TPR - 1) / TPR;   // slots used (<= S)
   const int CP = NJ * TPR;              // chunks per row, padded
-  const int GP = CP / CPG;              // groups per row, padded
+  const int GP = CP >> lcpg;            // groups per row, padded
   const int64_t t = blockIdx.y;
   int64_t xb = t, e = 0;
   const int slot = threadIdx.x / TPR;
@@ -194,15 +196,19 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
   {
     // A fixed number of operations per wave, so that every wait below counts
     // exactly: the most this instance can need (a row has at most S*TPR
-    // chunks, so RPB*G + GP <= (RPB + 1) * S*TPR/CPG entries); extra ones
-    // repeat the last.  Each is a VMEM instruction in a congested queue.
-    constexpr int SB_WORDS_MAX = ((RPB + 1) * (S * TPR / CPG) + 1) / 2;
+    // chunks, so RPB*G + GP <= (RPB + 1) * S*TPR/CPG entries, most at the
+    // smallest group size); a wave stops after the operations this shape
+    // needs, the last of them repeated where the waves' shares differ.  Each
+    // is a VMEM instruction in a congested queue.
+    constexpr int SB_WORDS_MAX = ((RPB + 1) * (S * TPR / CPG_MIN) + 1) / 2;
     constexpr int OPS_PER_WAVE = (2 * ((SB_WORDS_MAX + 63) / 64) + kBlock / 64 - 1) / (kBlock / 64);
     constexpr int NQ = OPS_PER_WAVE < kSbOpsPerWave ? OPS_PER_WAVE : kSbOpsPerWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ln = threadIdx.x & 63;
     const int ops = (sb_words + 63) / 64;  // wave-wide 4-byte DMA operations per array
+    const int nq = (2 * ops + kBlock / 64 - 1) / (kBlock / 64);  // <= NQ (checked on the host)
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
+      if (q >= nq) break;  // uniform
       const int o = min(wave + q * (kBlock / 64), 2 * ops - 1);
       const bool is_b = o >= ops;
       const int oo = is_b ? o - ops : o;
@@ -322,8 +328,9 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
 
   const u32x4_t* xlane = xl + lane;
   const float* xslane = xsum + lane;
-  const uint16_t* slane = sl + slot * R * G + lane / CPG;
-  const uint16_t* blane = bl + slot * R * G + lane / CPG;
+  const uint16_t* slane = sl + slot * R * G + (lane >> lcpg);
+  const uint16_t* blane = bl + slot * R * G + (lane >> lcpg);
+  const int gstep = TPR >> lcpg;  // groups per chunk slot
 #pragma unroll
   for (int j = 0; j < S; ++j) {
     if (j + D < S) issue(j + D);
@@ -356,8 +363,8 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
                           xv[wi / 2][(wi % 2) * 2 + 1], d);
           }
         }
-        const float sc = bf16_bits_to_f32(slane[r * G + jj * (TPR / CPG)]);
-        const float bi = bf16_bits_to_f32(blane[r * G + jj * (TPR / CPG)]);
+        const float sc = bf16_bits_to_f32(slane[r * G + jj * gstep]);
+        const float bi = bf16_bits_to_f32(blane[r * G + jj * gstep]);
         if (j < NJ && m < M) {  // uniform
           if constexpr (BITS == 4) {
             acc[r][m] = fmaf(sc, d, acc[r][m]);
@@ -435,12 +442,12 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(
 
 // x units, chunk sums, then scales and biases: each array ceil((RPB*G + GP) / 2)
 // words rounded up to whole 64-lane DMA operations.
-inline int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R) {
+inline int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R, int gs) {
   const int epc = 128 / bits;
   const int64_t C = K / epc;
   const int64_t CP = (C + tpr - 1) / tpr * tpr;
-  const int64_t G = K / kGroup;
-  const int64_t GP = CP / (kGroup / epc);
+  const int64_t G = K / gs;
+  const int64_t GP = CP / (gs / epc);
   const int64_t RPB = (kBlock / tpr) * R;
   const int64_t sb_words = (RPB * G + GP + 1) / 2;
   return MT * CP * 16 * (epc / 8) + MT * CP * 4 + 2 * ((sb_words + 63) / 64) * 256;
@@ -449,34 +456,35 @@ inline int64_t lds_bytes(int bits, int tpr, int64_t MT, int64_t K, int R) {
 template <int BITS, int TPR, int R, int S, int MT, int XU, bool GATHER, int EPI, bool NORM>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-               const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
+               const GatherMap& g, const NormIn& nrm, int gs, hipStream_t stream) {
   const int64_t rows_per_block = (kBlock / TPR) * R / (EPI == 1 ? 2 : 1);
-  const size_t lds = (size_t)lds_bytes(BITS, TPR, MT, K, R);
+  const size_t lds = (size_t)lds_bytes(BITS, TPR, MT, K, R, gs);
   const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block), (unsigned)g.T);
+  const int lcpg = __builtin_ctz((unsigned)(gs / (128 / BITS)));  // log2 chunks per group
   hipLaunchKernelGGL((qmv_kernel<BITS, TPR, R, S, MT, XU, GATHER, EPI, NORM>), grid, dim3(kBlock),
                      lds, stream, x, wq, s, b, bias, y, (int)M, (int)N, (int)K, g.lhs, g.rhs, g.E,
-                     g.x_batches, nrm);
+                     g.x_batches, nrm, lcpg);
   return hipGetLastError();
 }
 
 template <int BITS, int TPR, int R, int S, int MT, bool GATHER, int EPI, bool NORM>
 hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                  const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
+                  const GatherMap& g, const NormIn& nrm, int gs, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t CP = (K / EPC + TPR - 1) / TPR * TPR;
   const int64_t units = (MT * CP * (EPC / 8) + kBlock - 1) / kBlock;  // x units per thread
   if (units <= 2)
-    return run<BITS, TPR, R, S, MT, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+    return run<BITS, TPR, R, S, MT, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs,
                                                           stream);
   if (units <= 4)
-    return run<BITS, TPR, R, S, MT, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+    return run<BITS, TPR, R, S, MT, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs,
                                                           stream);
   if constexpr (NORM) {
     return hipErrorInvalidValue;  // rows of <= 8192 (excluded by qmv_norm_fits)
   } else {
     if (units <= 12)
-      return run<BITS, TPR, R, S, MT, 12, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+      return run<BITS, TPR, R, S, MT, 12, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs,
                                                              stream);
     return hipErrorInvalidValue;  // excluded by qmv_fits
   }
@@ -485,23 +493,23 @@ hipError_t run_xu(const uint16_t* x, const uint32_t* wq, const uint16_t* s, cons
 template <int BITS, int TPR, int R, int S, bool GATHER, int EPI, bool NORM>
 hipError_t run_mt(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                  const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
+                  const GatherMap& g, const NormIn& nrm, int gs, hipStream_t stream) {
   if (M <= 1)
-    return run_xu<BITS, TPR, R, S, 1, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+    return run_xu<BITS, TPR, R, S, 1, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs,
                                                          stream);
   if constexpr (NORM) {
     return hipErrorInvalidValue;  // one row (excluded by qmv_norm_fits)
   } else {
     if (M <= 2)
-      return run_xu<BITS, TPR, R, S, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+      return run_xu<BITS, TPR, R, S, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs,
                                                            stream);
     if constexpr (EPI == 1) {
       return hipErrorInvalidValue;  // SwiGLU: M <= 2 (excluded by qmv_swiglu_fits)
     } else {
       if (M <= 4)
         return run_xu<BITS, TPR, R, S, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g,
-                                                             nrm, stream);
-      return run_xu<BITS, TPR, R, S, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm,
+                                                             nrm, gs, stream);
+      return run_xu<BITS, TPR, R, S, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs,
                                                            stream);
     }
   }
@@ -524,15 +532,15 @@ inline int pick_tpr(int64_t C, int64_t N, int64_t T) {
 // (RPB * G + GP entries per array, kSbOpsPerWave operations per wave), the
 // LDS budget, and at least min_blocks blocks.
 inline bool rows_fit(int R, int bits, int tpr, int64_t M, int64_t N, int64_t K, int64_t T,
-                     int64_t min_blocks) {
+                     int64_t min_blocks, int gs) {
   const int epc = 128 / bits;
-  const int64_t C = K / epc, G = K / kGroup;
-  const int64_t CP = (C + tpr - 1) / tpr * tpr, GP = CP / (kGroup / epc);
+  const int64_t C = K / epc, G = K / gs;
+  const int64_t CP = (C + tpr - 1) / tpr * tpr, GP = CP / (gs / epc);
   const int64_t rpb = (kBlock / tpr) * R;
   const int64_t mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const int64_t sb_words = (rpb * G + GP + 1) / 2;
   return 2 * ((sb_words + 63) / 64) <= kSbOpsPerWave * (kBlock / 64) &&
-         lds_bytes(bits, tpr, mt, K, R) <= (R >= 4 ? kFourRowLdsBudget : kTwoRowLdsBudget) &&
+         lds_bytes(bits, tpr, mt, K, R, gs) <= (R >= 4 ? kFourRowLdsBudget : kTwoRowLdsBudget) &&
          (N + rpb - 1) / rpb * T >= min_blocks;
 }
 
@@ -544,31 +552,31 @@ inline bool rows_fit(int R, int bits, int tpr, int64_t M, int64_t N, int64_t K, 
 template <int BITS, bool GATHER, int EPI, bool NORM>
 hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                     const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                    const GatherMap& g, const NormIn& nrm, hipStream_t stream) {
+                    const GatherMap& g, const NormIn& nrm, int gs, hipStream_t stream) {
   constexpr int EPC = 128 / BITS;
   const int64_t C = K / EPC;
   const int tpr = pick_tpr(C, EPI == 1 ? 2 * N : N, g.T);
   const int slots = (int)((C + tpr - 1) / tpr);
   switch (tpr) {
     case 8:
-      return run_mt<BITS, 8, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      return run_mt<BITS, 8, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
     // Chunk slots per lane S: the instantiated S >= NJ closest to it (slots
     // past NJ cost arithmetic on zeros, not memory traffic).  The S values
     // cover the model shapes exactly: K = 3584 / 18944 / 2048 / 768 at 4 and
     // 8 bits.
     case 16:
-      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      return run_mt<BITS, 16, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 2) return run_mt<BITS, 16, 1, 2, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      if (slots <= 3) return run_mt<BITS, 16, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      if (slots <= 4) return run_mt<BITS, 16, 1, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      if (slots <= 7) return run_mt<BITS, 16, 1, 7, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      return run_mt<BITS, 16, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
     case 32:
-      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      return run_mt<BITS, 32, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 4) return run_mt<BITS, 32, 1, 4, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      if (slots <= 7) return run_mt<BITS, 32, 1, 7, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      return run_mt<BITS, 32, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
     case 64:
-      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-      return run_mt<BITS, 64, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+      if (slots <= 5) return run_mt<BITS, 64, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+      return run_mt<BITS, 64, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
     default:
       if constexpr (EPI == 1) {
         return hipErrorInvalidValue;  // SwiGLU: one wave per row at most
@@ -578,16 +586,16 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
           // block stages all of x (long rows: up to 40 KB), so rows per block
           // divide that L2 traffic, and fewer blocks fit one round of
           // residency (2 or 3 per CU at these LDS sizes).
-          if (slots <= 5 && M == 1 && rows_fit(4, BITS, 128, M, N, K, g.T, 256))
-            return run_mt<BITS, 128, 4, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-          if (slots <= 5 && rows_fit(2, BITS, 128, M, N, K, g.T, 512))
-            return run_mt<BITS, 128, 2, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-          if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-          return run_mt<BITS, 128, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+          if (slots <= 5 && M == 1 && rows_fit(4, BITS, 128, M, N, K, g.T, 256, gs))
+            return run_mt<BITS, 128, 4, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+          if (slots <= 5 && rows_fit(2, BITS, 128, M, N, K, g.T, 512, gs))
+            return run_mt<BITS, 128, 2, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+          if (slots <= 5) return run_mt<BITS, 128, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+          return run_mt<BITS, 128, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
         }
-        if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-        if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
-        if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, stream);
+        if (slots <= 3) return run_mt<BITS, 256, 1, 3, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+        if (slots <= 5) return run_mt<BITS, 256, 1, 5, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
+        if (slots <= 8) return run_mt<BITS, 256, 1, 8, GATHER, EPI, NORM>(x, wq, s, b, bias, y, M, N, K, g, nrm, gs, stream);
         return hipErrorInvalidValue;  // excluded by qmv_fits
       }
   }
@@ -601,5 +609,5 @@ hipError_t run_bits(const uint16_t* x, const uint32_t* wq, const uint16_t* s, co
 #define MQ_QMV_INSTANCE(BITS, GATHER, EPI, NORM)                                             \
   template hipError_t qmv::run_bits<BITS, GATHER, EPI, NORM>(                               \
       const uint16_t*, const uint32_t*, const uint16_t*, const uint16_t*, const uint16_t*, \
-      uint16_t*, int64_t, int64_t, int64_t, const GatherMap&, const qmv::NormIn&,          \
+      uint16_t*, int64_t, int64_t, int64_t, const GatherMap&, const qmv::NormIn&, int,     \
       hipStream_t)

@@ -1,6 +1,6 @@
 // Affine quantize / dequantize kernels for gfx950.
 //
-// quantize: mx.quantize(w, group_size=64, bits, mode="affine") as called by
+// quantize: mx.quantize(w, group_size, bits, mode="affine") as called by
 //   QuantizedSwitchLinear (python/mlx_worker/native_mlx/models/lfm2.py:142-151)
 //   and by nn.quantize (models/qwen2.py:318-324).  Bit-exact with the float32
 //   algorithm: min/max per group, scale = max((max-min)/(2^b-1), 1e-7) signed
@@ -10,26 +10,29 @@
 //   element-wise ops MLX evaluates in the bfloat16 output dtype.  With a row
 //   index list it is the quantized embedding lookup (models/qwen2.py:185).
 //
-// Layout: one group of 64 bf16 weights = 128 contiguous bytes.  quantize gives
-// each group to 8 lanes (16 bytes each, one coalesced 128-byte segment per
-// group); dequantize gives each lane one 16-byte chunk of packed codes.
+// Group sizes 32, 64 and 128 (the values MLX accepts).  Layout: a group of GS
+// bf16 weights is 2*GS contiguous bytes.  quantize gives each group to GS/8
+// lanes (16 bytes each, one coalesced segment per group); dequantize gives
+// each lane one 16-byte chunk of packed codes (32 4-bit or 16 8-bit codes:
+// never more than one group).
 #include "mq_common.h"
 #include "mq_internal.h"
 
 namespace mq {
 namespace {
 
-template <int BITS>
+template <int BITS, int GS>
 __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restrict__ w,
                                                        uint32_t* __restrict__ wq,
                                                        uint16_t* __restrict__ scales,
                                                        uint16_t* __restrict__ biases,
                                                        int64_t n_groups) {
-  const int64_t gid = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
-  const int sub = threadIdx.x & 7;
+  constexpr int LPG = GS / 8;  // lanes per group
+  const int64_t gid = (int64_t)blockIdx.x * (256 / LPG) + threadIdx.x / LPG;
+  const int sub = threadIdx.x % LPG;
   const bool ok = gid < n_groups;
   u32x4_t v = {0u, 0u, 0u, 0u};
-  if (ok) v = *reinterpret_cast<const u32x4_t*>(w + gid * kGroup + sub * 8);
+  if (ok) v = *reinterpret_cast<const u32x4_t*>(w + gid * GS + sub * 8);
   float f[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -43,7 +46,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
     w_min = (f[i] < w_min) ? f[i] : w_min;
   }
 #pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
+  for (int off = 1; off < LPG; off <<= 1) {
     const float omax = __shfl_xor(w_max, off, 64);
     const float omin = __shfl_xor(w_min, off, 64);
     w_max = (w_max < omax) ? omax : w_max;
@@ -74,12 +77,12 @@ __global__ __launch_bounds__(256) void quantize_kernel(const uint16_t* __restric
     uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) word |= code[i] << (4 * i);
-    wq[gid * 8 + sub] = word;
+    wq[gid * (GS / 8) + sub] = word;
   } else {
     u32x2_t words;
     words[0] = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
     words[1] = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
-    *reinterpret_cast<u32x2_t*>(wq + gid * 16 + sub * 2) = words;
+    *reinterpret_cast<u32x2_t*>(wq + gid * (GS / 4) + sub * 2) = words;
   }
   if (sub == 0) {
     scales[gid] = (uint16_t)f32_to_bf16_bits(scale);
@@ -97,7 +100,7 @@ template <int BITS>
 __global__ __launch_bounds__(256) void dequantize_kernel(
     const uint32_t* __restrict__ wq, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const int32_t* __restrict__ row_ids, int64_t n_out_rows,
-    int64_t n_rows, uint16_t* __restrict__ out, int64_t K) {
+    int64_t n_rows, uint16_t* __restrict__ out, int64_t K, int lgs) {
   constexpr int EPC = 128 / BITS;  // elements per 16-byte chunk
   const int64_t cpr = K / EPC;     // chunks per row
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
     return;
   }
   const u32x4_t v = *reinterpret_cast<const u32x4_t*>(wq + srow * (K * BITS / 32) + c * 4);
-  const int64_t g = srow * (K / kGroup) + (c * EPC) / kGroup;
+  const int64_t g = srow * (K >> lgs) + ((c * EPC) >> lgs);  // group size 1 << lgs
   const float s = bf16_bits_to_f32(scales[g]);
   const float b = bf16_bits_to_f32(biases[g]);
   uint32_t packed[EPC / 2];
@@ -133,31 +136,33 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
 }  // namespace
 
 hipError_t launch_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
-                           int64_t rows, int64_t K, int bits, hipStream_t stream) {
-  const int64_t n_groups = rows * (K / kGroup);
+                           int64_t rows, int64_t K, int group_size, int bits, hipStream_t stream) {
+  const int64_t n_groups = rows * (K / group_size);
   if (n_groups == 0) return hipSuccess;
-  const dim3 grid((unsigned)((n_groups + 31) / 32));
-  if (bits == 4)
-    hipLaunchKernelGGL(quantize_kernel<4>, grid, dim3(256), 0, stream, w, wq, scales, biases,
-                       n_groups);
-  else
-    hipLaunchKernelGGL(quantize_kernel<8>, grid, dim3(256), 0, stream, w, wq, scales, biases,
-                       n_groups);
+  const int64_t per_block = 256 / (group_size / 8);
+  const dim3 grid((unsigned)((n_groups + per_block - 1) / per_block));
+  void (*kern)(const uint16_t*, uint32_t*, uint16_t*, uint16_t*, int64_t);
+  if (group_size == 32) kern = bits == 4 ? quantize_kernel<4, 32> : quantize_kernel<8, 32>;
+  else if (group_size == 64) kern = bits == 4 ? quantize_kernel<4, 64> : quantize_kernel<8, 64>;
+  else kern = bits == 4 ? quantize_kernel<4, 128> : quantize_kernel<8, 128>;
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, w, wq, scales, biases, n_groups);
   return hipGetLastError();
 }
 
 hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
                              const int32_t* row_ids, int64_t n_out_rows, int64_t n_rows,
-                             uint16_t* out, int64_t K, int bits, hipStream_t stream) {
+                             uint16_t* out, int64_t K, int group_size, int bits,
+                             hipStream_t stream) {
   const int64_t total = n_out_rows * (K * bits / 128);
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256));
+  const int lgs = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
   if (bits == 4)
     hipLaunchKernelGGL(dequantize_kernel<4>, grid, dim3(256), 0, stream, wq, scales, biases,
-                       row_ids, n_out_rows, n_rows, out, K);
+                       row_ids, n_out_rows, n_rows, out, K, lgs);
   else
     hipLaunchKernelGGL(dequantize_kernel<8>, grid, dim3(256), 0, stream, wq, scales, biases,
-                       row_ids, n_out_rows, n_rows, out, K);
+                       row_ids, n_out_rows, n_rows, out, K, lgs);
   return hipGetLastError();
 }
 

@@ -170,8 +170,9 @@ class QExperts:
         gather_qmm then silu_mul -- the same bits either way."""
         T, M, K = rhs.numel(), x.shape[-2], x.shape[-1]
         N = self.wq.shape[1] // 2
-        if offsets is not None and sorted_indices and T * M > 64:
-            # the expert-segment GEMM with SiLU * up in its epilogue
+        if offsets is not None and sorted_indices and T * M > 64 and self.group_size == 64:
+            # the expert-segment GEMM with SiLU * up in its epilogue (it reads one
+            # scale per 64-wide k step: group size 64 only)
             return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
                                           self.group_size, self.bits, expert_offsets=offsets)
         if core.gather_swiglu_supported(T, M, N, K, self.group_size, self.bits):

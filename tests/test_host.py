@@ -141,8 +141,8 @@ def test_decoder_entry_validation(mq):
     one = ctypes.c_void_p(16)  # never dereferenced: validation fails before any launch
     assert seg(null, null, null, one, null, null, null, null, 300, 1, 64, 512, 8, 300, 64, 4,
                0, null) == -1                                                   # null pointers
-    assert seg(null, null, null, one, null, null, null, null, 300, 1, 64, 512, 8, 300, 32, 4,
-               1, null) == -2                                                   # group size
+    assert seg(one, null, one, one, one, one, one, one, 300, 1, 64, 512, 8, 300, 32, 4,
+               1, null) == -2                      # SiLU * up epilogue: group size 64 only
     assert seg(null, null, null, one, null, null, null, null, 0, 1, 64, 512, 8, 0, 64, 4,
                1, null) == 0
     sup = L.mq_quantized_matmul_swiglu_supported
@@ -208,7 +208,16 @@ def test_capi_invalid_and_unsupported_codes(mq):
     assert b"supported bits" in L.mq_last_error()
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 2, 1, null) == -2
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 48, 4, 1, null) == -1
-    assert qmm(null, null, null, null, null, null, 1, 8, 64, 32, 4, 1, null) == -2
+    # group sizes 32 and 128 pass the checks (null pointers are then the error)
+    assert qmm(null, null, null, null, null, null, 1, 8, 64, 32, 4, 1, null) == -1
+    assert b"null" in L.mq_last_error()
+    assert qmm(null, null, null, null, null, null, 1, 8, 128, 128, 8, 1, null) == -1
+    assert qmm(null, null, null, null, null, null, 1, 8, 96, 128, 4, 1, null) == -1
+    assert b"divisible" in L.mq_last_error()
+    # group size 32 with K = 96: the GEMV takes it, the 64-step GEMMs do not
+    one = ctypes.c_void_p(16)  # never dereferenced: validation fails before any launch
+    assert qmm(one, one, one, one, null, one, 16, 8, 96, 32, 4, 1, null) == -2
+    assert b"multiple of 64" in L.mq_last_error()
     assert qmm(null, null, null, null, null, null, 1, 8, 96, 64, 4, 1, null) == -1
     assert b"divisible" in L.mq_last_error()
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 4, 0, null) == -2
