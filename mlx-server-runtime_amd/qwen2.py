@@ -352,12 +352,24 @@ class Qwen2Model:
                                      self._next_norm(li))
 
     # ------------------------------------------------------------ prefill
-    def prefill(self, ids: torch.Tensor, cache: PagedKV, start: int = 0,
-                rows: torch.Tensor | None = None, all_positions: bool = False) -> torch.Tensor:
+    def prefill(self, ids: torch.Tensor, cache: PagedKV, start: int | torch.Tensor = 0,
+                rows: torch.Tensor | None = None, all_positions: bool = False,
+                lengths: torch.Tensor | None = None) -> torch.Tensor:
         """ids [B, T] at positions start..start+T-1 of cache rows `rows` (default
         0..B-1), attending to the cached positions 0..start-1 as well ->
         logits [B, vocab] of the last position (or [B, T, vocab] with all_positions);
-        writes K/V of the new positions into the pages."""
+        writes K/V of the new positions into the pages.
+
+        Ragged batches (the reference's step layout, executor.py:335-346): start
+        may be int64 [B] (each row's cached length) and lengths int64 [B] (each
+        row's new tokens, 1..T).  Row b's tokens past lengths[b] are padding: they
+        sit at the row's last position (as the reference repeats it), are neither
+        written to the pages nor attended to by other tokens, and the logits
+        returned are those of each row's last valid token (executor.py:406-414).
+        A row with one new token on top of its cache is a decode row, so one call
+        also serves a mixed prefill/decode step."""
+        if not isinstance(start, int) or lengths is not None:
+            return self._prefill_ragged(ids, cache, start, rows, all_positions, lengths)
         c = self.cfg
         B, T = ids.shape
         dev = ids.device
@@ -396,6 +408,59 @@ class Qwen2Model:
             o = layer.o(a.transpose(1, 2).reshape(B, T, nh * d).to(torch.bfloat16))
             x, h = self._ffn(li, h, o)
         return self._head(x if all_positions else x[:, -1])
+
+    def _prefill_ragged(self, ids, cache, start, rows, all_positions, lengths):
+        c = self.cfg
+        B, T = ids.shape
+        dev = ids.device
+        d, nh, nkv = c.head_dim, c.num_attention_heads, c.num_key_value_heads
+        rep = nh // nkv
+        rows = torch.arange(B, device=dev) if rows is None else rows.to(dev).long()
+        starts = (torch.full((B,), start, dtype=torch.long) if isinstance(start, int)
+                  else torch.as_tensor(start)).to(dev).long().reshape(B)
+        lens = (torch.full((B,), T, dtype=torch.long) if lengths is None
+                else torch.as_tensor(lengths)).to(dev).long().reshape(B)
+        if bool(((lens < 1) | (lens > T) | (starts < 0)).any()):
+            raise ValueError(f"lengths must lie in 1..{T} and starts be >= 0")
+        S = int((starts + lens).max())
+        if S > cache.capacity:
+            raise ValueError(f"positions up to {S} exceed the cache capacity {cache.capacity}")
+        j = torch.arange(T, device=dev)
+        valid = j[None, :] < lens[:, None]                                  # [B, T]
+        pos = starts[:, None] + torch.minimum(j[None, :], lens[:, None] - 1)  # [B, T]
+        vb, vj = valid.nonzero(as_tuple=True)
+        slots = cache.slots(rows[vb], pos[vb, vj])
+        cos, sin = rope_tables(c, S, dev)
+        cs, sn = cos[pos][:, None], sin[pos][:, None]                       # [B, 1, T, d/2]
+        # query (b, j) sees the keys of its row at positions <= pos[b, j]; a
+        # padding query repeats the row's last valid one
+        keyp = torch.arange(S, device=dev)
+        mask = torch.zeros(B, 1, T, S, device=dev).masked_fill_(
+            (keyp[None, None, :] > pos[:, :, None])[:, None], float("-inf"))
+        h = self._embed(ids.reshape(-1)).reshape(B, T, c.hidden_size)
+        x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
+        for li, layer in enumerate(self.layers):
+            qkv = layer.qkv(x)
+            q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
+            q, k = q.reshape(B, T, nh, d), k.reshape(B, T, nkv, d)
+            if layer.q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
+                q = fused_rms_norm(q, layer.q_norm, c.rms_norm_eps)
+                k = fused_rms_norm(k, layer.k_norm, c.rms_norm_eps)
+            q = apply_rope(q.float().transpose(1, 2), cs, sn)
+            k = apply_rope(k.float().transpose(1, 2), cs, sn).to(torch.bfloat16)
+            v = v.reshape(B, T, nkv, d)
+            cache.write(li, slots, k.transpose(1, 2)[vb, vj], v[vb, vj])
+            kk, vv = cache.gather_rows(li, rows, S)
+            q = q.to(torch.bfloat16).float()
+            kk = kk.float().repeat_interleave(rep, dim=1)
+            vv = vv.float().repeat_interleave(rep, dim=1)
+            s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + mask
+            a = torch.matmul(torch.softmax(s, dim=-1), vv)
+            o = layer.o(a.transpose(1, 2).reshape(B, T, nh * d).to(torch.bfloat16))
+            x, h = self._ffn(li, h, o)
+        if all_positions:
+            return self._head(x)
+        return self._head(x[torch.arange(B, device=dev), lens - 1])
 
     # ------------------------------------------------------------ decode
     def decode_step(self, tok: torch.Tensor, pos: torch.Tensor, cache: PagedKV,
@@ -441,12 +506,16 @@ class Qwen2Model:
 
     def generate(self, prompt: torch.Tensor, n_new: int, max_len: int | None = None,
                  use_graph: bool = True, logits_out: list | None = None,
-                 prefix_len: int = 0, page_size: int = 16) -> torch.Tensor:
+                 prefix_len: int = 0, page_size: int = 16,
+                 lengths: torch.Tensor | None = None) -> torch.Tensor:
         """Greedy decode: prompt [B, T] -> new tokens [B, n_new] (int64).  With
         logits_out, each step's logits [B, vocab] are appended to it.  With
         prefix_len > 0 the rows' first prefix_len prompt tokens are equal (the
         caller's promise): they are prefilled once, from row 0, into pages every
-        row shares, and each row prefills only its own suffix."""
+        row shares, and each row prefills only its own suffix.  With lengths
+        (int64 [B], prefix_len < lengths[b] <= T) row b's prompt is its first
+        lengths[b] tokens (the rest padding); its first new token follows its
+        last prompt token and its decode steps continue from there."""
         B, T = prompt.shape
         dev = prompt.device
         max_len = max_len or (T + n_new)
@@ -455,12 +524,20 @@ class Qwen2Model:
         out = torch.empty(B, n_new, dtype=torch.int64, device=dev)
         if prefix_len:
             self.prefill(prompt[:1, :prefix_len], cache, rows=torch.zeros(1, dtype=torch.long))
-        logits = self.prefill(prompt[:, prefix_len:], cache, start=prefix_len)
+        if lengths is None:
+            logits = self.prefill(prompt[:, prefix_len:], cache, start=prefix_len)
+            pos = torch.full((B,), T, dtype=torch.int64, device=dev)
+        else:
+            lens = torch.as_tensor(lengths).to(dev).long().reshape(B)
+            if bool(((lens <= prefix_len) | (lens > T)).any()):
+                raise ValueError(f"lengths must lie in {prefix_len + 1}..{T}")
+            logits = self.prefill(prompt[:, prefix_len:], cache, start=prefix_len,
+                                  lengths=lens - prefix_len)
+            pos = lens.clone()
         if logits_out is not None:
             logits_out.append(logits.clone())
         out[:, 0] = logits.float().argmax(-1)
         tok = out[:, 0].clone()
-        pos = torch.full((B,), T, dtype=torch.int64, device=dev)
         step = lambda: self.decode_step(tok, pos, cache, cos, sin)  # noqa: E731
         if use_graph and n_new > 1:
             g, static_logits = self._capture(step)
