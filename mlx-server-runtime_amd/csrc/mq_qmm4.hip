@@ -608,15 +608,18 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
   }
 }
 
-// K splits for a launch: 1 when the tiles fill one round of the GPU (one
+// K splits for a launch: 1 when the tiles fill half a round of the GPU (one
 // block per CU); otherwise the most splits that keep the grid within one
-// round, each at least 4 scale chunks (2048 K) long.
+// round, each at least 2 scale chunks (1024 K) long.  Measured at M = 512
+// (7B prefill of one 512-token prompt): the down projection 18944 -> 3584 in
+// 28 tiles x 9 splits takes 81 us where the 128 x 128 GEMM took 431 us, and
+// q/k/v 3584 -> 4608 in 36 tiles x 3 splits 47 us (85 us).
 int qmm4_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   constexpr int64_t kRound = 256;
   if (tiles >= kRound / 2) return 1;
   const int64_t chunks = (K / kGroup + kSbChunk - 1) / kSbChunk;
-  return (int)std::max<int64_t>(1, std::min(kRound / tiles, chunks / 4));
+  return (int)std::max<int64_t>(1, std::min(kRound / tiles, chunks / 2));
 }
 
 constexpr int kWaves = 8;  // waves per block: two per SIMD
@@ -649,10 +652,10 @@ bool offsets_fit(int64_t x_rows, int64_t N, int64_t K, int bits) {
 }  // namespace
 
 bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits) {
-  // >= 128 tiles, or >= 32 when K is long enough to split over blocks
+  // >= 128 tiles, or >= 8 whose K splits give >= 64 blocks
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   return offsets_fit(M, N, K, bits) && tiles < ((int64_t)1 << 31) &&
-         (tiles >= 128 || (tiles >= 32 && qmm4_splits(M, N, K) * tiles >= 128));
+         (tiles >= 128 || (tiles >= 8 && qmm4_splits(M, N, K) * tiles >= 64));
 }
 
 size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K) {

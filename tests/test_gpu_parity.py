@@ -333,6 +333,23 @@ def test_sweep_shape_sampled_rows(mq, orc, bits, KN, M):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("KN", [(3584, 4608), (3584, 3584), (18944, 3584), (3584, 18944)])
+@pytest.mark.parametrize("M", [300, 512])
+def test_mid_m_split_plans_sampled_rows(mq, orc, bits, KN, M):
+    """A prefill chunk of 300 / 512 rows at the 7B shapes: few 256 x 256 tiles,
+    so the large-M GEMM splits K over blocks (up to 9 splits of the down
+    projection) and the fixed-order reduce adds the partial sums; sampled rows
+    (the first and last of each row tile among them) against the oracle."""
+    K, N = KN
+    wq, s, b = _sweep_weights(orc, K, N, bits)
+    rng = np.random.default_rng(11 + M + K + bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
+    rows = np.unique(np.r_[0, 255, min(256, M - 1), M - 1, rng.integers(0, M, 4)])
+    assert_close(y[torch.from_numpy(rows).to(DEV)], orc.qmm(x[rows], wq, s, b, 64, bits))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("M", [512, 4096])
 def test_group_tail_k_sampled_rows(mq, orc, bits, M):
     """K = 11008 (a down projection whose K is not a multiple of 512): the
