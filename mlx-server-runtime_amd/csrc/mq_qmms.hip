@@ -159,6 +159,11 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   // step kt - 1 and kt MI DMAs and NC code loads (and, at a chunk's first
   // step, two scale/bias loads, which only add to the count).
   constexpr int kInFlight = NC + 2 * (MI + NC);
+  // The split's first step is the exception: x of its second step was
+  // issued by the prologue, which loads no codes after it, so only the
+  // prologue's last x DMA, this step's scale/bias loads, x DMA and codes
+  // follow it (8-bit: 2 fewer than kInFlight).
+  constexpr int kFirstInFlight = 2 * MI + 2 + NC < kInFlight ? 2 * MI + 2 + NC : kInFlight;
 
   f32x16_t acc[MI];
 #pragma unroll
@@ -211,7 +216,8 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
       }
       // refill the slot just consumed with the codes kPrefetch steps ahead
       load_codes(q, kt + kPrefetch);
-      step_barrier<kInFlight>();
+      if (u == 0 && c == c_begin) step_barrier<kFirstInFlight>();  // uniform
+      else step_barrier<kInFlight>();
       st = (st + 1) & 3;
     }
     sv = svn;
