@@ -37,8 +37,13 @@ namespace {
 constexpr int BN = 128;  // columns of a 4-wave block
 constexpr int BK = 64;
 constexpr int kChunk = 8;     // groups per scale/bias load
-constexpr int kPrefetch = 4;  // steps of codes in flight per lane (divides kChunk)
-constexpr int kStages = 4;    // x stages: the DMA runs 3 steps ahead
+// Pipeline depths: codes kPrefetch steps ahead (divides kChunk), x kXAhead
+// steps ahead in kXStages LDS stages (a power of two above kXAhead).  Measured
+// on the M = 16/32 7B shapes: x 4-7 steps ahead in 8 stages changed nothing
+// (+-1 %), codes 8 steps ahead were 5-8 % slower, 2 ahead slower still.
+constexpr int kPrefetch = 4;
+constexpr int kXAhead = 3;
+constexpr int kXStages = 4;
 
 typedef __attribute__((address_space(3))) void lds_t;
 
@@ -97,6 +102,10 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
     int M, int N, int K, int tiles_n, int tiles_m, int chunks_per_split) {
   constexpr int BM = 32 * MI;
+  constexpr int P = kXAhead;   // x DMA steps ahead
+  constexpr int S = kXStages;  // x stages
+  static_assert(kChunk % kPrefetch == 0 && (S & (S - 1)) == 0 && S > P && P >= 2 && P <= kChunk,
+                "pipeline");
   constexpr int kXStage = BM * BK * 2;
   constexpr int CB = BITS * 4;           // code bytes per lane per step
   constexpr int NC = BITS == 4 ? 1 : 2;  // 16-byte code loads per lane per step
@@ -154,16 +163,34 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
     for (int p = 0; p < NC; ++p) cw[p] = buf_load16(wrs, coff + kt * (BK * BITS / 8) + p * 16);
     __asm__ volatile("" ::: "memory");
   };
-  // At the end of step kt the x DMA of step kt + 1 (issued in step kt - 2)
-  // must have landed; issued after it: the codes of step kt + 2, then per
-  // step kt - 1 and kt MI DMAs and NC code loads (and, at a chunk's first
-  // step, two scale/bias loads, which only add to the count).
-  constexpr int kInFlight = NC + 2 * (MI + NC);
-  // The split's first step is the exception: x of its second step was
-  // issued by the prologue, which loads no codes after it, so only the
-  // prologue's last x DMA, this step's scale/bias loads, x DMA and codes
-  // follow it (8-bit: 2 fewer than kInFlight).
-  constexpr int kFirstInFlight = 2 * MI + 2 + NC < kInFlight ? 2 * MI + 2 + NC : kInFlight;
+  // At the end of step kt the x DMA of step kt + 1 (issued in step
+  // kt + 1 - P) must have landed; issued after it: the codes of that step,
+  // then per step kt + 2 - P .. kt MI DMAs and NC code loads (and, at a
+  // chunk's first step, two scale/bias loads, which only add to the count).
+  constexpr int kInFlight = NC + (P - 1) * (MI + NC);
+  // A split's first P - 1 steps are the exception: x of step j + 1 (j < P - 1)
+  // was issued by the prologue, which loads no codes after its x DMAs, so
+  // only the prologue's later x DMAs, the first step's scale/bias loads and
+  // steps 0..j's x DMAs and codes follow it.
+  constexpr auto first_count = [](int u) {
+    const int a = (P - 1) * MI + (u + 1) * NC + 2;
+    return u <= P - 2 && a < kInFlight ? a : kInFlight;
+  };
+  // the barrier of step u of a split's first chunk (u is a constant after
+  // the unrolling, so the switch folds away)
+  auto first_barrier = [&](int u) {
+    switch (u) {
+      case 0: step_barrier<first_count(0)>(); break;
+      case 1: step_barrier<first_count(1)>(); break;
+      case 2: step_barrier<first_count(2)>(); break;
+      case 3: step_barrier<first_count(3)>(); break;
+      case 4: step_barrier<first_count(4)>(); break;
+      case 5: step_barrier<first_count(5)>(); break;
+      case 6: step_barrier<first_count(6)>(); break;
+      default: step_barrier<first_count(7)>(); break;
+    }
+  };
+  static_assert(kChunk == 8, "first_barrier covers one chunk of 8 steps");
 
   f32x16_t acc[MI];
 #pragma unroll
@@ -171,16 +198,15 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
 
-  // ---- prologue: codes of the first kPrefetch steps, x of the first 3 ----
+  // ---- prologue: codes of the first kPrefetch steps, x of the first P ----
   const int kt0 = c_begin * kChunk;
   u32x4_t sv = buf_load16(srs, soff + c_begin * 16), bv = buf_load16(brs, soff + c_begin * 16);
   u32x4_t cw[kPrefetch][NC];
 #pragma unroll
   for (int p = 0; p < kPrefetch; ++p) load_codes(cw[p], kt0 + p);
-  dma_x(kt0, 0);
-  dma_x(kt0 + 1, 1);
-  dma_x(kt0 + 2, 2);
-  step_barrier<2 * MI>();
+#pragma unroll
+  for (int p = 0; p < P; ++p) dma_x(kt0 + p, p);
+  step_barrier<(P - 1) * MI>();
 
   int st = 0;  // stage of the current step's x tile
   for (int c = c_begin; c < c_end; ++c) {
@@ -194,7 +220,7 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
         bvn = buf_load16(brs, soff + (c + 1) * 16);
         __asm__ volatile("" ::: "memory");
       }
-      dma_x(kt + 3, (st + 3) & 3);
+      dma_x(kt + P, (st + P) & (S - 1));
 
       const float s = bf16_bits_to_f32((sv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
       const float b = bf16_bits_to_f32((bv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
@@ -216,9 +242,9 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
       }
       // refill the slot just consumed with the codes kPrefetch steps ahead
       load_codes(q, kt + kPrefetch);
-      if (u == 0 && c == c_begin) step_barrier<kFirstInFlight>();  // uniform
+      if (c == c_begin) first_barrier(u);  // uniform
       else step_barrier<kInFlight>();
-      st = (st + 1) & 3;
+      st = (st + 1) & (S - 1);
     }
     sv = svn;
     bv = bvn;
@@ -467,7 +493,7 @@ hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
-  const int lds = kStages * 32 * MI * BK * 2;
+  const int lds = kXStages * 32 * MI * BK * 2;
   hipLaunchKernelGGL((qmms_kernel<BITS, MI, PARTIAL, EPI, W>), grid, dim3(64 * W), lds, stream,
                      x, wq, scales, biases, bias, y, partial, (int)M, (int)N, (int)K, p.tiles_n,
                      p.tiles_m, p.chunks_per_split);
