@@ -100,7 +100,9 @@ int mq_quantized_matmul(const mq_bf16* x, const uint32_t* wq, const mq_bf16* sca
  * Workspace, in bytes, that mq_quantized_matmul_ws can use for this shape
  * (0 = none).  Shapes whose output tiles cannot fill the GPU and have a long
  * K (the down projection at small M, and at M = 1-2K prefill chunks) split K
- * over blocks and need float32 partial sums.
+ * over blocks and need float32 partial sums; so do large-M shapes whose
+ * 256 x 256 tiles leave a short last round of the GPU (at most 85 of 256
+ * tiles): those tiles run as stream-K pieces.
  * MLX allocates such temporaries internally; this library allocates nothing,
  * so the caller provides them.  No counterpart in the reference: it serves
  * the same mx.quantized_matmul call sites as mq_quantized_matmul.
@@ -111,9 +113,9 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
  * mq_quantized_matmul with a caller-owned device workspace (16-byte aligned,
  * `workspace_bytes` long; NULL/0 allowed).  With at least
  * mq_quantized_matmul_workspace() bytes, K may be split over blocks; with
- * less it runs unsplit.  Results are identical run to run either way (the
- * partial sums are added in a fixed order).  Calls that share a workspace
- * must be ordered on one stream.
+ * less it runs unsplit (every large-M tile whole).  Results are identical run
+ * to run either way (the partial sums are added in a fixed order).  Calls
+ * that share a workspace must be ordered on one stream.
  */
 int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* scales,
                            const mq_bf16* biases, const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
@@ -128,9 +130,11 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
  * it is for callers that cannot allocate (code under HIP graph capture,
  * serving loops that forbid hipMalloc).  Same arguments, kernels, split plan
  * and results bit for bit as mq_quantized_matmul_ws with
- * mq_quantized_matmul_workspace() bytes.  Shapes whose plan needs more than
- * MQ_NOALLOC_SCRATCH_BYTES (mq_quantized_matmul_workspace) return
- * MQ_ERR_INVALID before any launch.  Every call on one GPU shares its array:
+ * mq_quantized_matmul_workspace() bytes.  A large-M stream-K plan that needs
+ * more than MQ_NOALLOC_SCRATCH_BYTES runs every tile whole instead (as
+ * mq_quantized_matmul_ws does without a workspace); other shapes whose plan
+ * needs more than MQ_NOALLOC_SCRATCH_BYTES (mq_quantized_matmul_workspace)
+ * return MQ_ERR_INVALID before any launch.  Every call on one GPU shares its array:
  * calls that overlap on one GPU (unordered streams) race; order them on one
  * stream.  The array is used on the device of `stream` (the current device
  * for the NULL stream).
@@ -311,8 +315,9 @@ int mq_silu_mul(const mq_bf16* gate_up, mq_bf16* out, int64_t rows, int64_t inte
  * GEMM's split-K plans (e.g. M = 32: its fixed-order reduce applies the
  * SwiGLU; needs mq_quantized_matmul_swiglu_workspace bytes, which is what
  * mq_quantized_matmul_workspace gives the unfused product); and for prefill
- * shapes the large-M GEMM runs unsplit (SiLU * up in its epilogue, no
- * workspace).
+ * shapes the large-M GEMM runs every tile whole (SiLU * up in its epilogue,
+ * no workspace; bit for bit mq_quantized_matmul_ws without a workspace,
+ * followed by mq_silu_mul).
  * mq_quantized_matmul_swiglu_supported says whether a shape is taken; others
  * return MQ_ERR_UNSUPPORTED.  mq_quantized_matmul_swiglu is the _ws form
  * without a workspace.

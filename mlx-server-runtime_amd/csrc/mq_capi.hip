@@ -165,6 +165,20 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
 
 }  // extern "C"
 
+namespace mq {
+// Whether mq_quantized_matmul_ws runs a shape with less workspace than
+// mq_quantized_matmul_workspace asks for: the large-M GEMM's stream-K plan,
+// which without its workspace runs every tile whole.
+bool qmm_workspace_optional(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return false;
+  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return false;
+  if (use_skinny(M, N, K, bits, 64) || dense_gemv(M, N, K, bits, 64) ||
+      mq::qmv_fits(M, N, K, bits, 1, 64))
+    return false;
+  return mq::qmm4_fits(M, N, K, bits) && mq::qmm4_stream_k(M, N, K);
+}
+}  // namespace mq
+
 namespace {
 // How mq_quantized_matmul_swiglu runs a shape: 1 the dot2 GEMV with the SwiGLU
 // epilogue (where mq_quantized_matmul itself runs that GEMV on the 2N rows),
@@ -178,12 +192,15 @@ int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
   if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
   if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
-  // route 4 only where mq_quantized_matmul_ws itself runs the large-M GEMM,
-  // unsplit, on the 2N rows (the same kernel, so the same bits)
+  // route 4 only where mq_quantized_matmul_ws runs the large-M GEMM on the 2N
+  // rows with no even K split: the fused kernel runs every tile whole, as
+  // mq_quantized_matmul_ws does without a workspace (the same kernel, so the
+  // same bits; with one, a stream-K plan may sum a short last round of tiles
+  // in pieces)
   const int64_t N2 = 2 * N;
   if (!dense_gemv(M, N2, K, bits, 64) && !mq::qmv_fits(M, N2, K, bits, 1, 64) &&
       !use_skinny(M, N2, K, bits, 64) && mq::qmm4_fits(M, N2, K, bits) &&
-      mq::qmm4_workspace_bytes(M, N2, K) == 0 && mq::qmm4_swiglu_fits(M, N, K, bits))
+      mq::qmm4_unsplit(M, N2, K) && mq::qmm4_swiglu_fits(M, N, K, bits))
     return 4;
   return 0;
 }

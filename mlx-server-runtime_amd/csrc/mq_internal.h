@@ -63,12 +63,20 @@ hipError_t launch_qmvm(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
 
 // 256x256-tile MFMA path with weights dequantized in registers (qmm4_fits:
-// K an even number of groups, >= 128 tiles, 32-bit offsets), one wave per SIMD, each
-// owning the block's 256 rows for 64 columns (every code dequantized once per
-// block).  Few tiles and a long K: K is split over blocks through a float32
-// workspace of qmm4_workspace_bytes (without it the launch runs unsplit).
+// K an even number of groups, >= 128 tiles or few tiles with K splits,
+// 32-bit offsets), two waves per SIMD, each owning the block's 256 rows for
+// 32 columns (every code dequantized once per block).  Few tiles and a long
+// K: K is split over blocks; a short last round of tiles: those tiles go to
+// stream-K blocks (qmm4_stream_k).  Both write float32 partial sums to a
+// workspace of qmm4_workspace_bytes; without it every tile runs whole.
+// qmm4_unsplit: the plan splits no tile's K evenly (the SwiGLU form's plan).
 bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits);
 size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K);
+bool qmm4_unsplit(int64_t M, int64_t N, int64_t K);
+bool qmm4_stream_k(int64_t M, int64_t N, int64_t K);
+// mq_quantized_matmul_ws takes the shape with less workspace than it asks for
+// (mq_capi.hip).
+bool qmm_workspace_optional(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                        int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,

@@ -54,7 +54,9 @@ extern "C" int mq_quantized_matmul_noalloc(const mq_bf16* x, const uint32_t* wq,
                                            const mq_bf16* bias_vec, mq_bf16* y, int64_t M,
                                            int64_t N, int64_t K, int group_size, int bits,
                                            int transpose, hipStream_t stream) {
-  const size_t need = mq_quantized_matmul_workspace(M, N, K, group_size, bits);
+  size_t need = mq_quantized_matmul_workspace(M, N, K, group_size, bits);
+  // a stream-K plan that does not fit the array runs every tile whole
+  if (need > kScratchBytes && mq::qmm_workspace_optional(M, N, K, group_size, bits)) need = 0;
   if (need > kScratchBytes) {
     char msg[256];
     snprintf(msg, sizeof(msg),

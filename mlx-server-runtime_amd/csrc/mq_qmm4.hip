@@ -125,6 +125,16 @@ struct Qmm4Args {
   float* partial;
   int M, N, K;  // M: dense rows (gather: T * Mb)
   int tiles_m, tiles_n, tiles, chunks_per_split;
+  // Dense K split: blocks below dp_blocks take (split, tile) pairs of
+  // dp_tiles x (K / chunks_per_split) (partial != null: their float32 sums go
+  // to partial[split][M][N]).  Blocks from dp_blocks on are stream-K blocks
+  // over the tiles from dp_tiles on: block b takes chunks [b sk_w, (b + 1)
+  // sk_w) of the flattened (tile, chunk) order of those tiles, a piece of at
+  // most two tiles, and writes each piece's float32 sums to
+  // sk_partial[(s * sk_pieces + p) * BM * BN] (stream-K tile s's piece p,
+  // 256 x 256, row-major); qmm4_sk_reduce adds a tile's pieces in order.
+  int dp_blocks, dp_tiles, sk_w, sk_units, sk_pieces;
+  float* sk_partial;
   // gather only
   const int32_t* lhs;
   const int32_t* rhs;
@@ -232,6 +242,15 @@ __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
   return g;
 }
 
+// Dense tile order: groups of kGroupM row blocks x every column block, row
+// blocks fastest.
+__device__ __forceinline__ void dense_tile(const Qmm4Args& a, int tile, int& bm, int& bn) {
+  const int g = tile / (kGroupM * a.tiles_n), r = tile % (kGroupM * a.tiles_n);
+  const int gm = min(kGroupM, a.tiles_m - g * kGroupM);
+  bm = g * kGroupM + r % gm;
+  bn = r / gm;
+}
+
 // WAVES waves (4: one per SIMD, or 8: two) split the block's 256 columns: each
 // owns all 256 rows of 256 / WAVES columns (NJ = 8 / WAVES MFMA column tiles),
 // so every code of the block is dequantized once whatever WAVES is.
@@ -255,11 +274,21 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
   constexpr int kOutCols = SWIGLU ? BN / 2 : BN;  // output columns per block
   const int NW = SWIGLU ? 2 * N : N;              // rows of the (expert's) matrix
 
-  int split = 0, bn, out_row0, rows_valid;
+  int bn = 0, out_row0 = 0, rows_valid = 0, c_begin = 0, c_end = 0;
   const uint32_t* wbank = a.wq;
   const uint16_t* sbank = a.scales;
   const uint16_t* bbank = a.biases;
   const int G = K / kGroup;
+  const int KT = K / BK;
+  const int chunks = (KT + kSbChunk - 1) / kSbChunk;
+  // A K split writes float32 sums: element (m, c) of the tile (row m, block
+  // column c) goes to pdst[(prow + m) * pld + pcol + c]; null: bfloat16 output
+  float* pdst = nullptr;
+  int64_t pld = 0;
+  int prow = 0, pcol = 0;
+  // stream-K block: chunks [sk_f, sk_end) of the flattened (tile, chunk) order
+  const bool sk = !GATHER && (int)blockIdx.x >= a.dp_blocks;
+  int sk_f = 0, sk_end = 0;
   if constexpr (GATHER) {
     // Blocks go to the 8 XCDs round-robin.  Each run of 8 * tiles_n blocks
     // covers 8 row tiles, row tile 8g + x on XCD x with all its column tiles
@@ -285,326 +314,353 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
     wbank += (int64_t)g.e * NW * (K * BITS / 32);
     sbank += (int64_t)g.e * NW * G;
     bbank += (int64_t)g.e * NW * G;
-  } else {
+    c_end = chunks;
+  } else if (!sk) {
     // XCD-contiguous runs of the tile order below: consecutive idx on one XCD
-    const int nblk = gridDim.x;
+    const int nblk = a.dp_blocks;
     const int per_xcd = nblk / 8, rem = nblk % 8;
     const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
     const int idx = (xcd < rem ? xcd * (per_xcd + 1) : rem * (per_xcd + 1) + (xcd - rem) * per_xcd) + slot;
     // With K split, idx = split * tiles + tile: a split's blocks are contiguous.
-    const int tile = idx % a.tiles;
-    split = idx / a.tiles;
-    // group g: row blocks g*kGroupM .. +gm-1 x every column block, row fastest
-    const int g = tile / (kGroupM * a.tiles_n), r = tile % (kGroupM * a.tiles_n);
-    const int gm = min(kGroupM, a.tiles_m - g * kGroupM);
-    const int bm = g * kGroupM + r % gm;
-    bn = r / gm;
+    const int tile = idx % a.dp_tiles, split = idx / a.dp_tiles;
+    int bm;
+    dense_tile(a, tile, bm, bn);
     out_row0 = bm * BM;
     rows_valid = min(BM, a.M - out_row0);
-  }
-  const int n0 = bn * kOutCols;
-  // matrix row of block column c (0..255): c itself past n0, or for SWIGLU
-  // gate row n0 + c for c < 128, else the up row of output column n0 + c - 128
-  auto wrow = [&](int c, int& out_col) {
-    if constexpr (SWIGLU) {
-      out_col = n0 + (c & 127);
-      return (c >> 7) * N + out_col;
-    } else {
-      out_col = n0 + c;
-      return out_col;
+    c_begin = split * a.chunks_per_split;
+    c_end = min(chunks, c_begin + a.chunks_per_split);
+    if (a.partial) {
+      pdst = a.partial + (int64_t)split * a.M * N;
+      pld = N, prow = out_row0, pcol = bn * kOutCols;
     }
-  };
-  // MFMA row tiles holding valid rows (the same for every wave of the block)
-  const int live = __builtin_amdgcn_readfirstlane((rows_valid + 31) / 32);
-
-  const int KT = K / BK;
-  const int chunks = (KT + kSbChunk - 1) / kSbChunk;
-  const int c_begin = split * a.chunks_per_split;
-  const int c_end = min(chunks, c_begin + a.chunks_per_split);
-  const int kt0 = c_begin * kSbChunk;
-  const int kt_end = min(KT, c_end * kSbChunk);
-  const int x_rows = GATHER ? a.x_batches * a.Mb : a.M;
-  const rsrc_t xrs = make_rsrc(a.x, (uint64_t)x_rows * K * 2);
-  const rsrc_t wrs = make_rsrc(wbank, (uint64_t)NW * K * BITS / 8);
-  const rsrc_t srs = make_rsrc(sbank, (uint64_t)NW * G * 2);
-  const rsrc_t brs = make_rsrc(bbank, (uint64_t)NW * G * 2);
-
-  // x DMA: wave w, op i fills rows (8w + i)*8 .. +7 of a stage (1 KiB); lane l
-  // writes physical chunk l % 8 of row l / 8, i.e. logical chunk (l%8) ^ f(row)
-  // with f(row) = (row >> 1) & 7.  Rows past the tile's valid rows read as
-  // zeros (an offset past the descriptor; dense rows past M lie beyond it).
-  uint32_t xoff[kXOps];
-#pragma unroll
-  for (int i = 0; i < kXOps; ++i) {
-    const int row = (wave * kXOps + i) * 8 + (l >> 3);
-    const uint32_t chunk = (uint32_t)(((l & 7) ^ ((row >> 1) & 7)) * 8);
-    if constexpr (GATHER) {
-      xoff[i] = kOutOfRange;
-      if (row < rows_valid) {
-        const int p = out_row0 + row;
-        const int t = p / a.Mb, m = p - t * a.Mb;
-        const int xb = a.lhs ? a.lhs[t] : t;
-        if (xb >= 0 && xb < a.x_batches)
-          xoff[i] = ((uint32_t)(xb * a.Mb + m) * (uint32_t)K + chunk) * 2u;
-      }
-    } else {
-      xoff[i] = (uint32_t)((out_row0 + row) * K + (int)chunk) * 2;
+  } else {
+    const int b = (int)blockIdx.x - a.dp_blocks;
+    sk_f = b * a.sk_w;
+    sk_end = min(a.sk_units, sk_f + a.sk_w);
+  }
+  for (;;) {  // one segment (a tile's chunk range) per pass; only stream-K blocks loop
+    if (sk) {
+      const int s = sk_f / chunks;
+      c_begin = sk_f - s * chunks;
+      c_end = min(chunks, c_begin + (sk_end - sk_f));
+      int bm;
+      dense_tile(a, a.dp_tiles + s, bm, bn);
+      out_row0 = bm * BM;
+      rows_valid = min(BM, a.M - out_row0);
+      // pieces of tile s come from blocks s*chunks/sk_w, ... in chunk order
+      const int piece = (int)blockIdx.x - a.dp_blocks - s * chunks / a.sk_w;
+      pdst = a.sk_partial + ((int64_t)s * a.sk_pieces + piece) * (BM * BN);
+      pld = BN, prow = 0, pcol = 0;
     }
-  }
-  // Codes: block column 32 NJ wave + 32j + l%32, half h of each group.
-  constexpr int CB = BITS * 4;  // code bytes per lane per step: 16 (4-bit) / 32 (8-bit)
-  constexpr int NC = BITS == 4 ? 2 : 4;  // 16-byte code loads per lane per step
-  uint32_t coff[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    int oc;
-    const int n = wrow(wave * 32 * NJ + j * 32 + (l & 31), oc);
-    coff[j] = oc < N ? (uint32_t)(n * (K * BITS / 8) + h * CB) : kOutOfRange;
-  }
-  // Scale/bias DMA, as wave operations o of 64 lanes (column block cb of 64
-  // columns, lane l taking column 64 cb + l); wave w issues o = w, w + WAVES,
-  // ..., all with cb = w % 4.  SB16: 8 operations per chunk, o = 4a + cb, one
-  // 16-byte load per lane (8 groups of a column; LDS [array][column][group]);
-  // otherwise 32, o = 16a + 4d + cb, dword d of 4 (rows of G groups, G even,
-  // are only 4-byte aligned; LDS [array][group pair][column]).
-  constexpr int kSbOps = (SB16 ? 8 : 32) / WAVES;  // DMA operations per lane per chunk
-  uint32_t soff;
-  {
-    int oc;
-    const int n = wrow((wave & 3) * 64 + l, oc);
-    soff = oc < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
-  }
-  // A fragment rows 32i + l%32; logical chunk 4h + ks, stored at (4h + ks) ^ f
-  // with f = (l >> 1) & 7 for every row tile: only bits 4-5 of the byte offset
-  // depend on ks, so the k-slice ks reads at aoff ^ (ks << 4).
-  const uint32_t aoff = (uint32_t)((l & 31) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
-  uint32_t sbr[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int c = wave * 32 * NJ + j * 32 + (l & 31);
-    sbr[j] = kSbBase + (SB16 ? c * 16 : c * 4);
-  }
-
-  auto dma_x = [&](int kt, int stage) {
-#pragma unroll
-    for (int i = 0; i < kXOps; ++i)
-      dma16(xrs, (lds_t*)(lds + stage * kXStage + (wave * kXOps + i) * 1024),
-            xoff[i] + kt * (BK * 2));
-  };
-  auto dma_sb = [&](int chunk, int buf) {
-    char* dst = lds + kSbBase + buf * kSbBytes;
-    const uint32_t src = soff + chunk * (kSbChunk * 2);
-#pragma unroll
-    for (int t = 0; t < kSbOps; ++t) {
-      const int o = wave + WAVES * t;
-      if constexpr (SB16) {
-        const int arr = o >> 2, cb = o & 3;
-        dma16(arr ? brs : srs, (lds_t*)(dst + arr * kSbArray + cb * 1024), src);
+    const int n0 = bn * kOutCols;
+    // matrix row of block column c (0..255): c itself past n0, or for SWIGLU
+    // gate row n0 + c for c < 128, else the up row of output column n0 + c - 128
+    auto wrow = [&](int c, int& out_col) {
+      if constexpr (SWIGLU) {
+        out_col = n0 + (c & 127);
+        return (c >> 7) * N + out_col;
       } else {
-        const int arr = o >> 4, d = (o >> 2) & 3, cb = o & 3;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(arr ? brs : srs,
-                                                 (lds_t*)(dst + arr * kSbArray + d * 1024 + cb * 256),
-                                                 4, src + d * 4, 0, 0, 0);
+        out_col = n0 + c;
+        return out_col;
+      }
+    };
+    // MFMA row tiles holding valid rows (the same for every wave of the block)
+    const int live = __builtin_amdgcn_readfirstlane((rows_valid + 31) / 32);
+
+    const int kt0 = c_begin * kSbChunk;
+    const int kt_end = min(KT, c_end * kSbChunk);
+    const int x_rows = GATHER ? a.x_batches * a.Mb : a.M;
+    const rsrc_t xrs = make_rsrc(a.x, (uint64_t)x_rows * K * 2);
+    const rsrc_t wrs = make_rsrc(wbank, (uint64_t)NW * K * BITS / 8);
+    const rsrc_t srs = make_rsrc(sbank, (uint64_t)NW * G * 2);
+    const rsrc_t brs = make_rsrc(bbank, (uint64_t)NW * G * 2);
+
+    // x DMA: wave w, op i fills rows (8w + i)*8 .. +7 of a stage (1 KiB); lane l
+    // writes physical chunk l % 8 of row l / 8, i.e. logical chunk (l%8) ^ f(row)
+    // with f(row) = (row >> 1) & 7.  Rows past the tile's valid rows read as
+    // zeros (an offset past the descriptor).
+    uint32_t xoff[kXOps];
+#pragma unroll
+    for (int i = 0; i < kXOps; ++i) {
+      const int row = (wave * kXOps + i) * 8 + (l >> 3);
+      const uint32_t chunk = (uint32_t)(((l & 7) ^ ((row >> 1) & 7)) * 8);
+      if constexpr (GATHER) {
+        xoff[i] = kOutOfRange;
+        if (row < rows_valid) {
+          const int p = out_row0 + row;
+          const int t = p / a.Mb, m = p - t * a.Mb;
+          const int xb = a.lhs ? a.lhs[t] : t;
+          if (xb >= 0 && xb < a.x_batches)
+            xoff[i] = ((uint32_t)(xb * a.Mb + m) * (uint32_t)K + chunk) * 2u;
+        }
+      } else {
+        xoff[i] = row < rows_valid ? (uint32_t)((out_row0 + row) * K + (int)chunk) * 2 : kOutOfRange;
       }
     }
-  };
-  auto load_codes = [&](u32x4_t (&cw)[NJ][NC / 2], int kt) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int p = 0; p < NC / 2; ++p) cw[j][p] = buf_load16(wrs, coff[j] + kt * (BK * BITS / 8) + p * 16);
-  };
-
-  f32x16_t acc[kRowTiles][NJ];
-#pragma unroll
-  for (int i = 0; i < kRowTiles; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  u32x4_t cw[kCodeRing][NJ][NC / 2];
-  auto dequant_frag = [&](const u32x4_t (&q)[NJ][NC / 2], int j, int ks, const GroupAffine& g) {
-    const u32x4_t& w = q[j][BITS == 4 ? 0 : ks >> 1];
-    if constexpr (BITS == 4) return dequant8<4>(w[ks], 0u, g.s, g.b);
-    else return dequant8<8>(w[(ks & 1) * 2], w[(ks & 1) * 2 + 1], g.s, g.b);
-  };
-  auto read_sb = [&](int buf, int grp, GroupAffine (&g)[NJ]) {
+    // Codes: block column 32 NJ wave + 32j + l%32, half h of each group.
+    constexpr int CB = BITS * 4;  // code bytes per lane per step: 16 (4-bit) / 32 (8-bit)
+    constexpr int NC = BITS == 4 ? 2 : 4;  // 16-byte code loads per lane per step
+    uint32_t coff[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const char* p = lds + sbr[j] + buf * kSbBytes +
-                      (SB16 ? grp * 2 : (grp >> 1) * 1024 + (grp & 1) * 2);
-      g[j].s = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
-      g[j].b = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + kSbArray));
+      int oc;
+      const int n = wrow(wave * 32 * NJ + j * 32 + (l & 31), oc);
+      coff[j] = oc < N ? (uint32_t)(n * (K * BITS / 8) + h * CB) : kOutOfRange;
     }
-  };
-
-  // ---- prologue: codes of this split's first two steps, its first scale
-  // chunk, x of its first three steps ----
-  load_codes(cw[0], kt0);
-  load_codes(cw[1], kt0 + 1);
-  dma_sb(c_begin, c_begin & 1);
-  dma_x(kt0, 0);
-  dma_x(kt0 + 1, 1);
-  dma_x(kt0 + 2, 2);
-  step_barrier<2 * kXOps>();
-  // B fragments of k-slice 0 are always dequantized one step early, at the end
-  // of the previous step, so each step opens with MFMAs instead of VALU.
-  GroupAffine ga[NJ];
-  read_sb(c_begin & 1, 0, ga);
-  bf16x8_t b0[NJ];
+    // Scale/bias DMA, as wave operations o of 64 lanes (column block cb of 64
+    // columns, lane l taking column 64 cb + l); wave w issues o = w, w + WAVES,
+    // ..., all with cb = w % 4.  SB16: 8 operations per chunk, o = 4a + cb, one
+    // 16-byte load per lane (8 groups of a column; LDS [array][column][group]);
+    // otherwise 32, o = 16a + 4d + cb, dword d of 4 (rows of G groups, G even,
+    // are only 4-byte aligned; LDS [array][group pair][column]).
+    constexpr int kSbOps = (SB16 ? 8 : 32) / WAVES;  // DMA operations per lane per chunk
+    uint32_t soff;
+    {
+      int oc;
+      const int n = wrow((wave & 3) * 64 + l, oc);
+      soff = oc < N ? (uint32_t)(n * G) * 2 : kOutOfRange;
+    }
+    // A fragment rows 32i + l%32; logical chunk 4h + ks, stored at (4h + ks) ^ f
+    // with f = (l >> 1) & 7 for every row tile: only bits 4-5 of the byte offset
+    // depend on ks, so the k-slice ks reads at aoff ^ (ks << 4).
+    const uint32_t aoff = (uint32_t)((l & 31) * 128 + ((h * 4) ^ ((l >> 1) & 7)) * 16);
+    uint32_t sbr[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
+    for (int j = 0; j < NJ; ++j) {
+      const int c = wave * 32 * NJ + j * 32 + (l & 31);
+      sbr[j] = kSbBase + (SB16 ? c * 16 : c * 4);
+    }
 
-  // The K loop.  MASKED skips the MFMAs (and A reads) of row tiles past the
-  // tile's valid rows, at the price of a branch per row tile; full tiles take
-  // the branch-free body.
-  auto k_loop = [&](auto masked) {
-    constexpr bool MASKED = decltype(masked)::value;
-    int st = 0;  // stage holding x of the current step
-    for (int c = c_begin; c < c_end; ++c) {
+    auto dma_x = [&](int kt, int stage) {
 #pragma unroll
-      for (int u = 0; u < kSbChunk; ++u) {
-        const int kt = c * kSbChunk + u;
-        if constexpr (!SB16) {
-          if (kt >= kt_end) break;  // a K of G % 8 != 0 groups ends mid-chunk
+      for (int i = 0; i < kXOps; ++i)
+        dma16(xrs, (lds_t*)(lds + stage * kXStage + (wave * kXOps + i) * 1024),
+              xoff[i] + kt * (BK * 2));
+    };
+    auto dma_sb = [&](int chunk, int buf) {
+      char* dst = lds + kSbBase + buf * kSbBytes;
+      const uint32_t src = soff + chunk * (kSbChunk * 2);
+#pragma unroll
+      for (int t = 0; t < kSbOps; ++t) {
+        const int o = wave + WAVES * t;
+        if constexpr (SB16) {
+          const int arr = o >> 2, cb = o & 3;
+          dma16(arr ? brs : srs, (lds_t*)(dst + arr * kSbArray + cb * 1024), src);
+        } else {
+          const int arr = o >> 4, d = (o >> 2) & 3, cb = o & 3;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(arr ? brs : srs,
+                                                   (lds_t*)(dst + arr * kSbArray + d * 1024 + cb * 256),
+                                                   4, src + d * 4, 0, 0, 0);
         }
-        const uint32_t xa = st * kXStage + aoff;
-        bf16x8_t a[kRowTiles];
-#pragma unroll
-        for (int i = 0; i < kRowTiles; ++i)
-          if (!MASKED || i < live) a[i] = *reinterpret_cast<const bf16x8_t*>(lds + xa + i * 4096);
-        load_codes(cw[(u + 2) % kCodeRing], kt + 2);
-        dma_x(kt + 3, (st + 3) % kXStages);
-        if (u == kSbChunk - 4) dma_sb(c + 1, (c + 1) & 1);
-
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          bf16x8_t bq[NJ], an[kRowTiles];
-          if (ks < 3) {
-#pragma unroll
-            for (int i = 0; i < kRowTiles; ++i)
-              if (!MASKED || i < live)
-                an[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ ((ks + 1) << 4)) + i * 4096);
-          }
-#pragma unroll
-          for (int i = 0; i < kRowTiles; ++i)
-            if (!MASKED || i < live) {
-#pragma unroll
-              for (int j = 0; j < NJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b0[j], acc[i][j], 0, 0, 0);
-            }
-          if (ks < 3) {
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
-          } else {
-            // next step: its scales (the next chunk's buffer after the last
-            // step of a chunk, DMA-ed four steps ago) and its first k-slice
-            if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
-            else read_sb(c & 1, u + 1, ga);
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
-          }
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) b0[j] = bq[j];
-          if (ks < 3) {
-#pragma unroll
-            for (int i = 0; i < kRowTiles; ++i) a[i] = an[i];
-          }
-        }
-        // the DMAs of this step and the previous one may still be in flight
-        // (more in the steps that load scales); x of the next step, issued two
-        // steps ago, and the scales read next step have landed
-        if (u == kSbChunk - 4 || u == kSbChunk - 3) step_barrier<2 * kXOps + kSbOps>();
-        else step_barrier<2 * kXOps>();
-        st = (st + 1) % kXStages;
       }
-    }
-  };
-  // Dense tiles past M read zero rows; only gather tiles (short expert
-  // segments) skip their empty row tiles.
-  if (GATHER && live < kRowTiles) k_loop(std::true_type{});
-  else k_loop(std::false_type{});
-  // The prefetches of the last steps (past K, unused) must land before the
-  // block's LDS is released.
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    auto load_codes = [&](u32x4_t (&cw)[NJ][NC / 2], int kt) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int p = 0; p < NC / 2; ++p) cw[j][p] = buf_load16(wrs, coff[j] + kt * (BK * BITS / 8) + p * 16);
+    };
 
-  // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4 ----
-  const bool full_rows = rows_valid == BM;
-  if (a.partial) {
-    // a split of K writes its float32 partial sums straight from registers
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int n = n0 + wave * 32 * NJ + j * 32 + (l & 31);
-      if (n >= N) continue;
-      float* pc = a.partial + (int64_t)split * a.M * N + n;
-#pragma unroll
-      for (int i = 0; i < kRowTiles; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int mb = i * 32 + 8 * r + 4 * h;
-          float* p = pc + (int64_t)(out_row0 + mb) * N;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (full_rows || mb + e < rows_valid) p[(int64_t)e * N] = acc[i][j][4 * r + e];
-        }
-    }
-    return;
-  }
-  // bfloat16 output: the 256 x 256 tile of block columns goes through LDS
-  // (the x stages; every wave's DMAs have landed once all have passed the
-  // barrier) so that rows leave as 16-byte stores instead of 2-byte ones per
-  // lane and value.  SWIGLU stages the gate and up columns (rounded to
-  // bfloat16, as the unfused GEMM stores them) and pairs them on the way out.
-  __syncthreads();
-  constexpr int kStageStride = BN * 2 + 16;  // bytes per staged row (padding spreads banks)
-  static_assert(BM * kStageStride <= kLds, "the output tile must fit the LDS");
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int c = wave * 32 * NJ + j * 32 + (l & 31);
-    float add = 0.f;
-    if constexpr (!SWIGLU) {
-      const int n = n0 + c;
-      add = (a.bias && n < N) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
-    }
+    f32x16_t acc[kRowTiles][NJ];
 #pragma unroll
     for (int i = 0; i < kRowTiles; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = i * 32 + 8 * r + 4 * h + e;
-          *reinterpret_cast<uint16_t*>(lds + m * kStageStride + c * 2) =
-              (uint16_t)f32_to_bf16_bits(acc[i][j][4 * r + e] + add);
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    u32x4_t cw[kCodeRing][NJ][NC / 2];
+    auto dequant_frag = [&](const u32x4_t (&q)[NJ][NC / 2], int j, int ks, const GroupAffine& g) {
+      const u32x4_t& w = q[j][BITS == 4 ? 0 : ks >> 1];
+      if constexpr (BITS == 4) return dequant8<4>(w[ks], 0u, g.s, g.b);
+      else return dequant8<8>(w[(ks & 1) * 2], w[(ks & 1) * 2 + 1], g.s, g.b);
+    };
+    auto read_sb = [&](int buf, int grp, GroupAffine (&g)[NJ]) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const char* p = lds + sbr[j] + buf * kSbBytes +
+                        (SB16 ? grp * 2 : (grp >> 1) * 1024 + (grp & 1) * 2);
+        g[j].s = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p));
+        g[j].b = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(p + kSbArray));
+      }
+    };
+
+    // ---- prologue: codes of this split's first two steps, its first scale
+    // chunk, x of its first three steps ----
+    load_codes(cw[0], kt0);
+    load_codes(cw[1], kt0 + 1);
+    dma_sb(c_begin, c_begin & 1);
+    dma_x(kt0, 0);
+    dma_x(kt0 + 1, 1);
+    dma_x(kt0 + 2, 2);
+    step_barrier<2 * kXOps>();
+    // B fragments of k-slice 0 are always dequantized one step early, at the end
+    // of the previous step, so each step opens with MFMAs instead of VALU.
+    GroupAffine ga[NJ];
+    read_sb(c_begin & 1, 0, ga);
+    bf16x8_t b0[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
+
+    // The K loop.  MASKED skips the MFMAs (and A reads) of row tiles past the
+    // tile's valid rows, at the price of a branch per row tile; full tiles take
+    // the branch-free body.
+    auto k_loop = [&](auto masked) {
+      constexpr bool MASKED = decltype(masked)::value;
+      int st = 0;  // stage holding x of the current step
+      for (int c = c_begin; c < c_end; ++c) {
+#pragma unroll
+        for (int u = 0; u < kSbChunk; ++u) {
+          const int kt = c * kSbChunk + u;
+          if constexpr (!SB16) {
+            if (kt >= kt_end) break;  // a K of G % 8 != 0 groups ends mid-chunk
+          }
+          const uint32_t xa = st * kXStage + aoff;
+          bf16x8_t a[kRowTiles];
+#pragma unroll
+          for (int i = 0; i < kRowTiles; ++i)
+            if (!MASKED || i < live) a[i] = *reinterpret_cast<const bf16x8_t*>(lds + xa + i * 4096);
+          load_codes(cw[(u + 2) % kCodeRing], kt + 2);
+          dma_x(kt + 3, (st + 3) % kXStages);
+          if (u == kSbChunk - 4) dma_sb(c + 1, (c + 1) & 1);
+
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            bf16x8_t bq[NJ], an[kRowTiles];
+            if (ks < 3) {
+#pragma unroll
+              for (int i = 0; i < kRowTiles; ++i)
+                if (!MASKED || i < live)
+                  an[i] = *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ ((ks + 1) << 4)) + i * 4096);
+            }
+#pragma unroll
+            for (int i = 0; i < kRowTiles; ++i)
+              if (!MASKED || i < live) {
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                  acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b0[j], acc[i][j], 0, 0, 0);
+              }
+            if (ks < 3) {
+#pragma unroll
+              for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
+            } else {
+              // next step: its scales (the next chunk's buffer after the last
+              // step of a chunk, DMA-ed four steps ago) and its first k-slice
+              if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
+              else read_sb(c & 1, u + 1, ga);
+#pragma unroll
+              for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) b0[j] = bq[j];
+            if (ks < 3) {
+#pragma unroll
+              for (int i = 0; i < kRowTiles; ++i) a[i] = an[i];
+            }
+          }
+          // the DMAs of this step and the previous one may still be in flight
+          // (more in the steps that load scales); x of the next step, issued two
+          // steps ago, and the scales read next step have landed
+          if (u == kSbChunk - 4 || u == kSbChunk - 3) step_barrier<2 * kXOps + kSbOps>();
+          else step_barrier<2 * kXOps>();
+          st = (st + 1) % kXStages;
         }
-  }
-  __syncthreads();
-  // thread t stores 16-byte chunk t % CPR of rows (kThreads / CPR) q + t / CPR
-  constexpr int kOutCols_ = SWIGLU ? BN / 2 : BN;
-  constexpr int CPR = kOutCols_ / 8;  // chunks per output row
-  const int cc = tid % CPR;
-  const int n = n0 + cc * 8;
-  const bool vec = (N % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
-#pragma unroll 4
-  for (int q = 0; q < BM * CPR / kThreads; ++q) {
-    const int row = q * (kThreads / CPR) + tid / CPR;
-    if (row >= rows_valid || n >= N) continue;
-    const char* src = lds + row * kStageStride + cc * 16;
-    u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
-    if constexpr (SWIGLU) {
-      const u32x4_t up = *reinterpret_cast<const u32x4_t*>(src + (BN / 2) * 2);
+      }
+    };
+    // Tiles of at most 192 valid rows (short expert segments, the last row
+    // tile) skip their empty MFMA row tiles; the branches cost more than one
+    // row tile's MFMAs (a dense sweep of masked tile heights measured a
+    // 224-row masked tile 6 % slower than a full 256-row one).
+    if (live <= kRowTiles - 2) k_loop(std::true_type{});
+    else k_loop(std::false_type{});
+    // The prefetches of the last steps (past K, unused) must land before the
+    // block's LDS is released.
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- epilogue: D[m][n], lane holds n = l%32, m = 8*(v/4) + 4*(l/32) + v%4 ----
+    const bool full_rows = rows_valid == BM;
+    if (pdst) {
+      // a K split writes its float32 partial sums straight from registers
 #pragma unroll
-      for (int w = 0; w < 4; ++w)
-        v[w] = (uint32_t)silu_mul_bf16(lo_bf16(v[w]), lo_bf16(up[w])) |
-               ((uint32_t)silu_mul_bf16(hi_bf16(v[w]), hi_bf16(up[w])) << 16);
-    }
-    uint16_t* dst = a.y + (int64_t)(out_row0 + row) * N + n;
-    if (vec) {
-      *reinterpret_cast<u32x4_t*>(dst) = v;
+      for (int j = 0; j < NJ; ++j) {
+        const int c = wave * 32 * NJ + j * 32 + (l & 31);
+        if (n0 + c >= N) continue;
+        float* pc = pdst + pcol + c;
+#pragma unroll
+        for (int i = 0; i < kRowTiles; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int mb = i * 32 + 8 * r + 4 * h;
+            float* p = pc + (int64_t)(prow + mb) * pld;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (full_rows || mb + e < rows_valid) p[(int64_t)e * pld] = acc[i][j][4 * r + e];
+          }
+      }
     } else {
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
-      for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = vs[e];
+      // bfloat16 output: the 256 x 256 tile of block columns goes through LDS
+      // (the x stages; every wave's DMAs have landed once all have passed the
+      // barrier) so that rows leave as 16-byte stores instead of 2-byte ones per
+      // lane and value.  SWIGLU stages the gate and up columns (rounded to
+      // bfloat16, as the unfused GEMM stores them) and pairs them on the way out.
+      __syncthreads();
+      constexpr int kStageStride = BN * 2 + 16;  // bytes per staged row (padding spreads banks)
+      static_assert(BM * kStageStride <= kLds, "the output tile must fit the LDS");
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int c = wave * 32 * NJ + j * 32 + (l & 31);
+        float add = 0.f;
+        if constexpr (!SWIGLU) {
+          const int n = n0 + c;
+          add = (a.bias && n < N) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < kRowTiles; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int m = i * 32 + 8 * r + 4 * h + e;
+              *reinterpret_cast<uint16_t*>(lds + m * kStageStride + c * 2) =
+                  (uint16_t)f32_to_bf16_bits(acc[i][j][4 * r + e] + add);
+            }
+      }
+      __syncthreads();
+      // thread t stores 16-byte chunk t % CPR of rows (kThreads / CPR) q + t / CPR
+      constexpr int kOutCols_ = SWIGLU ? BN / 2 : BN;
+      constexpr int CPR = kOutCols_ / 8;  // chunks per output row
+      const int cc = tid % CPR;
+      const int n = n0 + cc * 8;
+      const bool vec = (N % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
+#pragma unroll 4
+      for (int q = 0; q < BM * CPR / kThreads; ++q) {
+        const int row = q * (kThreads / CPR) + tid / CPR;
+        if (row >= rows_valid || n >= N) continue;
+        const char* src = lds + row * kStageStride + cc * 16;
+        u32x4_t v = *reinterpret_cast<const u32x4_t*>(src);
+        if constexpr (SWIGLU) {
+          const u32x4_t up = *reinterpret_cast<const u32x4_t*>(src + (BN / 2) * 2);
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            v[w] = (uint32_t)silu_mul_bf16(lo_bf16(v[w]), lo_bf16(up[w])) |
+                   ((uint32_t)silu_mul_bf16(hi_bf16(v[w]), hi_bf16(up[w])) << 16);
+        }
+        uint16_t* dst = a.y + (int64_t)(out_row0 + row) * N + n;
+        if (vec) {
+          *reinterpret_cast<u32x4_t*>(dst) = v;
+        } else {
+          const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
+          for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = vs[e];
+        }
+      }
     }
+    if (!sk) break;
+    sk_f += c_end - c_begin;
+    if (sk_f >= sk_end) break;
+    // the next segment's DMAs reuse the LDS: every wave's stores and reads of
+    // this one are done
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
 }
 
@@ -623,6 +679,106 @@ int qmm4_splits(int64_t M, int64_t N, int64_t K) {
 }
 
 constexpr int kWaves = 8;  // waves per block: two per SIMD
+constexpr int kMaxPieces = 8;  // stream-K pieces per tile
+
+// Stream-K tiles: y = the sum of a tile's pieces in piece order (+ bias),
+// rounded to bfloat16 -- the order is fixed by the plan, so results do not
+// depend on timing.  Grid (BM / 8, stream-K tiles) of 256 threads; thread t
+// adds 8 consecutive columns of tile row 8 * blockIdx.x + t / 32.
+__global__ __launch_bounds__(256) void qmm4_sk_reduce(const Qmm4Args a) {
+  const int s = blockIdx.y;
+  const int chunks = (a.K / BK + kSbChunk - 1) / kSbChunk;
+  const int first = s * chunks / a.sk_w;
+  const int pieces = (s * chunks + chunks - 1) / a.sk_w - first + 1;
+  int bm, bn;
+  dense_tile(a, a.dp_tiles + s, bm, bn);
+  const int r = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int c = (threadIdx.x & 31) * 8;
+  const int m = bm * BM + r, n = bn * BN + c;
+  if (m >= a.M || n >= a.N) return;
+  const float* p = a.sk_partial + (int64_t)s * a.sk_pieces * (BM * BN) + r * BN + c;
+  f32x4_t v[kMaxPieces][2];
+#pragma unroll
+  for (int q = 0; q < kMaxPieces; ++q)
+    if (q < pieces) {
+      v[q][0] = *reinterpret_cast<const f32x4_t*>(p + q * (BM * BN));
+      v[q][1] = *reinterpret_cast<const f32x4_t*>(p + q * (BM * BN) + 4);
+    }
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int q = 0; q < kMaxPieces; ++q)
+    if (q < pieces) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += v[q][e >> 2][e & 3];
+    }
+  uint16_t* dst = a.y + (int64_t)m * a.N + n;
+  uint16_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float b = (a.bias && n + e < a.N) ? bf16_bits_to_f32(a.bias[n + e]) : 0.f;
+    o[e] = (uint16_t)f32_to_bf16_bits(acc[e] + b);
+  }
+  if (n + 8 <= a.N && ((reinterpret_cast<uintptr_t>(dst) & 15) == 0)) {
+    *reinterpret_cast<u32x4_t*>(dst) = __builtin_bit_cast(u32x4_t, o);
+  } else {
+    for (int e = 0; e < 8 && n + e < a.N; ++e) dst[e] = o[e];
+  }
+}
+
+// How a dense launch covers its tiles.  The uniform plan runs every tile
+// whole, or (few tiles) split into S equal K ranges.  When the tiles fill
+// whole rounds of the GPU (one block per CU, 256 CUs) and leave a short last
+// round -- at most a third of the CUs busy -- the tiles of that last round go
+// to stream-K blocks instead: 256 blocks share their chunks equally, so the
+// launch takes its full rounds plus sk_w chunks, and a reduce adds the
+// pieces.  Measured (4-bit, against every tile whole): 296 tiles (M = 1024,
+// 3584 -> 18944) -15 %, 576 (M = 8192, 3584 -> 4608) -4 %, 592 (M = 2048,
+// 3584 -> 18944) -2 %, 2368 (M = 8192) +-0.  Longer last rounds, and launches
+// of fewer than 256 tiles, were slower (M = 2048, 3584 -> 4608 in 144 tiles
+// +17 %; 18944 -> 3584 in 112 tiles +5 %; 448 tiles +1-3 %): the float32
+// pieces' round trip through memory costs more than the idle CUs, which the
+// short last round runs at a higher clock.
+struct Plan {
+  int S;          // uniform K splits per tile
+  int dp_tiles;   // tiles run whole or uniformly split
+  int sk_tiles;   // the last tiles, run by stream-K blocks
+  int sk_w;       // chunks per stream-K block
+  int sk_blocks, sk_pieces;
+};
+
+Plan qmm4_plan(int64_t M, int64_t N, int64_t K) {
+  constexpr int64_t kRound = 256;
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int64_t chunks = (K / kGroup + kSbChunk - 1) / kSbChunk;
+  Plan p{};
+  p.S = qmm4_splits(M, N, K);
+  const int64_t cps = (chunks + p.S - 1) / p.S;
+  p.S = (int)((chunks + cps - 1) / cps);
+  p.dp_tiles = (int)tiles;
+  const int64_t makespan = p.S > 1 ? cps : (tiles + kRound - 1) / kRound * chunks;
+  const int64_t skt = tiles % kRound;
+  if (tiles < kRound || skt == 0 || skt > kRound / 3) return p;
+  const int64_t units = skt * chunks, w = (units + kRound - 1) / kRound;
+  if (w < 2 || w >= chunks || (tiles - skt) / kRound * chunks + w > makespan - 2) return p;
+  int64_t pieces = 0;
+  for (int64_t s = 0; s < skt; ++s)
+    pieces = std::max(pieces, ((s + 1) * chunks - 1) / w - s * chunks / w + 1);
+  if (pieces > kMaxPieces) return p;
+  p.S = 1;
+  p.dp_tiles = (int)(tiles - skt);
+  p.sk_tiles = (int)skt;
+  p.sk_w = (int)w;
+  p.sk_blocks = (int)((units + w - 1) / w);
+  p.sk_pieces = (int)pieces;
+  return p;
+}
+
+size_t plan_workspace(const Plan& p, int64_t M, int64_t N) {
+  if (p.sk_tiles) return (size_t)p.sk_tiles * p.sk_pieces * BM * BN * sizeof(float);
+  return p.S > 1 ? (size_t)p.S * M * N * sizeof(float) : 0;
+}
 
 template <bool GATHER, bool SWIGLU>
 hipError_t launch(const Qmm4Args& a, int bits, dim3 grid, hipStream_t stream) {
@@ -659,9 +815,12 @@ bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits) {
 }
 
 size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  const int S = qmm4_splits(M, N, K);
-  return S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+  return plan_workspace(qmm4_plan(M, N, K), M, N);
 }
+
+bool qmm4_unsplit(int64_t M, int64_t N, int64_t K) { return qmm4_splits(M, N, K) == 1; }
+
+bool qmm4_stream_k(int64_t M, int64_t N, int64_t K) { return qmm4_plan(M, N, K).sk_tiles > 0; }
 
 hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
@@ -674,14 +833,26 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
   a.tiles_m = (int)((M + BM - 1) / BM), a.tiles_n = (int)((N + BN - 1) / BN);
   a.tiles = a.tiles_m * a.tiles_n;
   const int chunks = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
-  int S = qmm4_splits(M, N, K);
-  if (S > 1 && (!workspace || workspace_bytes < qmm4_workspace_bytes(M, N, K))) S = 1;
-  a.chunks_per_split = (chunks + S - 1) / S;
-  S = (chunks + a.chunks_per_split - 1) / a.chunks_per_split;
-  a.partial = S > 1 ? static_cast<float*>(workspace) : nullptr;
-  const hipError_t e = launch<false, false>(a, bits, dim3((unsigned)(a.tiles * S)), stream);
-  if (e != hipSuccess || S == 1) return e;
-  return launch_splitk_reduce(a.partial, S, bias, y, M * N, N, stream);
+  Plan p = qmm4_plan(M, N, K);
+  // without the workspace the plan needs: every tile whole
+  if (!workspace || workspace_bytes < plan_workspace(p, M, N)) p = Plan{1, a.tiles, 0, 0, 0, 0};
+  a.chunks_per_split = (chunks + p.S - 1) / p.S;
+  a.partial = p.S > 1 ? static_cast<float*>(workspace) : nullptr;
+  a.dp_tiles = p.dp_tiles;
+  a.dp_blocks = p.dp_tiles * p.S;
+  a.sk_w = p.sk_w;
+  a.sk_units = p.sk_tiles * chunks;
+  a.sk_pieces = p.sk_pieces;
+  a.sk_partial = p.sk_tiles ? static_cast<float*>(workspace) : nullptr;
+  const hipError_t e =
+      launch<false, false>(a, bits, dim3((unsigned)(a.dp_blocks + p.sk_blocks)), stream);
+  if (e != hipSuccess) return e;
+  if (p.sk_tiles) {
+    hipLaunchKernelGGL(qmm4_sk_reduce, dim3(BM / 8, (unsigned)p.sk_tiles), dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
+  if (p.S == 1) return e;
+  return launch_splitk_reduce(a.partial, p.S, bias, y, M * N, N, stream);
 }
 
 bool qmm4_gather_fits(int64_t T, int64_t Mb, int64_t N, int64_t K, int64_t E,
@@ -729,6 +900,7 @@ hipError_t launch_qmm4_swiglu(const uint16_t* x, const uint32_t* wq, const uint1
   a.tiles_m = (int)((M + BM - 1) / BM), a.tiles_n = (int)((N + BN / 2 - 1) / (BN / 2));
   a.tiles = a.tiles_m * a.tiles_n;
   a.chunks_per_split = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
+  a.dp_tiles = a.dp_blocks = a.tiles;
   return launch<false, true>(a, bits, dim3((unsigned)a.tiles), stream);
 }
 

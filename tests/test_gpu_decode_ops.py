@@ -67,6 +67,23 @@ def test_rms_norm_batched_shape(ops):
     assert torch.equal(out, ref)
 
 
+def _qmm_whole_tiles(x, wq, sc, bi, bits):
+    """mq_quantized_matmul_ws without a workspace: the large-M GEMM runs every
+    tile whole."""
+    import ctypes
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    L = mq._lib.lib()
+    M, K = x.shape
+    N = wq.shape[0]
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    mq._lib.check(L.mq_quantized_matmul_ws(ptr(x), ptr(wq), ptr(sc), ptr(bi), None, ptr(y), M, N,
+                                           K, 64, bits, 1, None, ctypes.c_size_t(0),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                  "ws")
+    return y
+
+
 @pytest.mark.parametrize("M,N,K,bits", [(1, 18944, 3584, 4), (2, 18944, 3584, 8),
                                         (1, 18948, 3584, 4), (1, 1025, 16384, 4),
                                         (2, 2049, 8192, 8), (32, 18944, 3584, 4),
@@ -85,7 +102,8 @@ def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     24000 and 20000 take blocks of 6 and 5 waves).  8-bit batches of 9-16 rows
     take the skinny GEMM's 32-row tile too.  Prefill-sized M (300, 512, 2048)
     take the large-M GEMM with SiLU * up in its epilogue (4739 and 9476 leave
-    partial 128-column tiles, 300 a partial row tile)."""
+    partial 128-column tiles, 300 a partial row tile), against that GEMM with
+    every tile whole."""
     core = importlib.import_module("mlx-server-runtime_amd.core")
     assert core.swiglu_supported(M, N, K, 64, bits)
     g = _gen(N + K + bits)
@@ -93,7 +111,13 @@ def test_quantized_matmul_swiglu_equals_two_kernels(ops, M, N, K, bits):
     wq, sc, bi = core.quantize(w, 64, bits)
     x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
     out = core.quantized_matmul_swiglu(x, wq, sc, bi, 64, bits)
-    gu = core.quantized_matmul(x, wq, sc, bi, True, 64, bits)
+    if M <= 256:
+        gu = core.quantized_matmul(x, wq, sc, bi, True, 64, bits)
+    else:
+        # the large-M GEMM with every tile whole, as the fused form runs it
+        # (with a workspace a short last round of tiles may run as stream-K
+        # pieces, summed in another order)
+        gu = _qmm_whole_tiles(x, wq, sc, bi, bits)
     pad = -N % 8  # silu_mul takes widths of whole 8-element units; it is elementwise
     g, u = (F.pad(t, (0, pad)) for t in (gu[:, :N], gu[:, N:]))
     ref = ops.silu_mul(torch.cat([g, u], -1))[:, :N]

@@ -368,6 +368,50 @@ def test_group_tail_k_sampled_rows(mq, orc, bits, M):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
+def test_large_tiles_stream_k(mq, orc, bits):
+    """296 tiles of 256 x 256 (M = 900, N = 18900, K = 3584): one full round of
+    the GPU and a last round of 40 tiles, which run as stream-K pieces whose
+    float32 sums a reduce adds (with the bias) -- among them the partial last
+    column tile, in every row tile, and the 132-row last row tile.  Sampled
+    rows against the oracle, bit-identical results run to run, and the
+    whole-tile plan (no workspace) within one bfloat16 ulp of it (plus the
+    float32 reassociation error on sums that cancel)."""
+    import ctypes
+    M, N, K = 900, 18900, 3584
+    L = mq._lib.lib()
+    need = L.mq_quantized_matmul_workspace(M, N, K, 64, bits)
+    assert need >= 40 * 3 * 256 * 256 * 4, need  # the stream-K plan's pieces
+    rng = np.random.default_rng(717 + bits)
+    wq, s, b = quantized(orc, rng, N, K, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    args = (bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits)
+    y = mq.quantized_matmul(*args, bias=bf16_dev(bias))
+    for _ in range(3):
+        assert torch.equal(mq.quantized_matmul(*args, bias=bf16_dev(bias)).view(torch.int16),
+                           y.view(torch.int16))
+    rows = np.unique(np.r_[0, 255, 256, 767, 768, M - 1, rng.integers(0, M, 4)])
+    assert_close(y[torch.from_numpy(rows).to(DEV)],
+                 orc.qmm(x[rows], wq, s, b, 64, bits, bias=bias))
+    whole = torch.empty_like(y)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    mq._lib.check(L.mq_quantized_matmul_ws(ptr(args[0]), ptr(args[1]), ptr(args[2]),
+                                           ptr(args[3]), ptr(bf16_dev(bias)), ptr(whole), M, N,
+                                           K, 64, bits, 1, None, ctypes.c_size_t(0),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                  "ws")
+    torch.cuda.synchronize()
+    # two roundings of float32 sums that differ only in summation order: one
+    # bfloat16 ulp apart, plus the reassociation error of the float32 sums,
+    # which shows on results that cancel to near zero (measured: <= 6e-7
+    # where max |y| ~ 7)
+    mag = torch.maximum(y.float().abs(), whole.float().abs()).clamp_min(1e-30)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    slack = 2.0**-16 * float(whole.float().abs().max())
+    assert bool(((y.float() - whole.float()).abs() <= ulp + slack).all())
+
+
+@pytest.mark.parametrize("bits", [4, 8])
 def test_large_tiles_ragged_edges(mq, orc, bits):
     """M and N that are not multiples of the 256-row tiles, with enough tiles
     (5 x 26) for the large-tile kernel: rows of the last, partial M tile and

@@ -26,14 +26,14 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
 
 
-def _case(mq, L, M, N, K, bits, seed, bias):
+def _case(mq, L, M, N, K, bits, seed, bias, with_ws=True):
     core = importlib.import_module("mlx-server-runtime_amd.core")
     g = torch.Generator(device=DEV).manual_seed(seed)
     w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
     wq, sc, bi = core.quantize(w, 64, bits)
     x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
     bv = (torch.randn(N, generator=g, device=DEV) * 0.1).to(torch.bfloat16) if bias else None
-    need = L.mq_quantized_matmul_workspace(M, N, K, 64, bits)
+    need = L.mq_quantized_matmul_workspace(M, N, K, 64, bits) if with_ws else 0
     assert need <= SCRATCH_BYTES, need
     ws = torch.empty(need, dtype=torch.uint8, device=DEV) if need else None
     ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
@@ -62,6 +62,19 @@ def test_noalloc_equals_workspace_entry(bits):
     _case(mq, L, 16, 4608, 3584, bits, seed=3, bias=True)
     assert L.mq_quantized_matmul_workspace(1, 18944, 3584, 64, bits) == 0
     _case(mq, L, 1, 18944, 3584, bits, seed=4, bias=False)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_noalloc_stream_k_beyond_the_array_runs_whole_tiles(bits):
+    """M = 1024, 3584 -> 18944 (296 tiles of 256 x 256): the workspace entry's
+    stream-K plan wants more than the array holds, so the no-allocation entry
+    runs every tile whole -- bit-equal to the workspace entry without a
+    workspace."""
+    mq, L = _lib()
+    M, N, K = 1024, 18944, 3584
+    print(f"noalloc bits={bits}: M={M}, N={N}, K={K} (stream-K plan beyond the array)", flush=True)
+    assert L.mq_quantized_matmul_workspace(M, N, K, 64, bits) > SCRATCH_BYTES
+    _case(mq, L, M, N, K, bits, seed=5, bias=True, with_ws=False)
 
 
 def test_noalloc_refuses_beyond_the_array():
