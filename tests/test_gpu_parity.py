@@ -368,20 +368,22 @@ def test_group_tail_k_sampled_rows(mq, orc, bits, M):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_large_tiles_stream_k(mq, orc, bits):
-    """296 tiles of 256 x 256 (M = 900, N = 18900, K = 3584): one full round of
-    the GPU and a last round of 40 tiles, which run as stream-K pieces whose
-    float32 sums a reduce adds (with the bias) -- among them the partial last
-    column tile, in every row tile, and the 132-row last row tile.  Sampled
+@pytest.mark.parametrize("MNK", [(900, 18900, 3584), (1024, 18944, 3712)])
+def test_large_tiles_stream_k(mq, orc, bits, MNK):
+    """296 tiles of 256 x 256: one full round of the GPU and a last round of
+    40 tiles, which run as stream-K pieces whose float32 sums a reduce adds
+    (with the bias).  M = 900, N = 18900: the partial last column tile, in
+    every row tile, and the 132-row last row tile; K = 3712 (58 groups): the
+    last 512-wide chunk holds 2 groups, so pieces end inside a chunk.  Sampled
     rows against the oracle, bit-identical results run to run, and the
     whole-tile plan (no workspace) within one bfloat16 ulp of it (plus the
     float32 reassociation error on sums that cancel)."""
     import ctypes
-    M, N, K = 900, 18900, 3584
+    M, N, K = MNK
     L = mq._lib.lib()
     need = L.mq_quantized_matmul_workspace(M, N, K, 64, bits)
     assert need >= 40 * 3 * 256 * 256 * 4, need  # the stream-K plan's pieces
-    rng = np.random.default_rng(717 + bits)
+    rng = np.random.default_rng(717 + bits + K)
     wq, s, b = quantized(orc, rng, N, K, bits)
     x = rand_bf16(orc, rng, (M, K), 1.0)
     bias = rand_bf16(orc, rng, (N,), 0.5)
