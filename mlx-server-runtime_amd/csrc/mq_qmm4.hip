@@ -39,6 +39,9 @@
 //   blocks, so they share x rows and codes in that XCD's L2.
 // * The output tile is staged through LDS as bfloat16 and written as 16-byte
 //   row chunks.
+// * Few tiles and a long K split K evenly over blocks; a short last round of
+//   tiles (at most a third of the CUs) runs as stream-K pieces (qmm4_plan).
+//   Both write float32 partial sums that a reduce adds in a fixed order.
 // One barrier per step; the wait before it covers the DMAs of two steps ago
 // and earlier (the next step's x tile), never those of this step or the
 // previous one.
