@@ -413,6 +413,43 @@ def test_large_tiles_stream_k(mq, orc, bits, MNK):
     assert bool(((y.float() - whole.float()).abs() <= ulp + slack).all())
 
 
+def _random_shapes(n, seed):
+    """Seeded (M, N, K, group size, bits) across every dispatch range: the
+    GEMVs (M <= 8), the skinny GEMM (9..256 rows), the large-M GEMM with K
+    splits, whole tiles and stream-K tails (300..3100 rows), group sizes
+    32 / 64 / 128, N and M off the tile sizes."""
+    rng = np.random.default_rng(seed)
+    out = []
+    m_ranges = [(1, 8), (9, 32), (33, 256), (257, 1100), (1500, 3100)]
+    for i in range(n):
+        lo, hi = m_ranges[i % len(m_ranges)]
+        M = int(rng.integers(lo, hi + 1))
+        gs = int(rng.choice([64, 64, 32, 128]))
+        bits = int(rng.choice([4, 8]))
+        K = int(rng.choice([512, 1024, 2048, 3584, 4096, 5120]))
+        N = int(rng.choice([200, 1000, 2304, 4608, 9000, 18944]))
+        out.append((M, N, K, gs, bits))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,gs,bits", _random_shapes(30, 2026))
+def test_random_shapes_sampled_rows(mq, orc, M, N, K, gs, bits):
+    """Seeded shapes across the dispatch: sampled rows (first, last, the row
+    tile edges among them) against the oracle, with a bias."""
+    print(f"random shape M={M} N={N} K={K} gs={gs} bits={bits}", flush=True)
+    rng = np.random.default_rng(M * 7 + N * 3 + K + gs + bits)
+    wq, s, b = orc.quantize(rand_bf16(orc, rng, (N, K), 0.02), gs, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, gs, bits,
+                            bias=bf16_dev(bias))
+    assert y.shape == (M, N)
+    rows = np.unique(np.r_[0, M - 1, [r for r in (31, 32, 127, 128, 255, 256) if r < M],
+                           rng.integers(0, M, 3)]).astype(np.int64)
+    assert_close(y[torch.from_numpy(rows).to(DEV)],
+                 orc.qmm(x[rows], wq, s, b, gs, bits, bias=bias))
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_large_tiles_ragged_edges(mq, orc, bits):
     """M and N that are not multiples of the 256-row tiles, with enough tiles
