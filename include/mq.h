@@ -13,11 +13,21 @@
  *     `stream` (NULL = the default stream).
  *   - bfloat16 data is passed as raw 16-bit patterns (mq_bf16).
  *   - Weight format (MLX "affine"): wq uint32 [rows, K*bits/32] with codes
- *     packed LSB-first (code j of a word at bits [j*bits, (j+1)*bits));
- *     scales and biases bfloat16 [rows, K/group_size]; w = scale*q + bias.
- *   - Supported here: bits 4 or 8, group_size 32, 64 or 128, transpose = 1.
- *     MLX's other settings (bits 2/3/5/6, transpose = 0) return
- *     MQ_ERR_UNSUPPORTED; anything MLX itself rejects returns MQ_ERR_INVALID.
+ *     packed LSB-first as one bit stream per row (code k at bits
+ *     [k*bits, (k+1)*bits) of the row's words: 32/bits codes per word for 2,
+ *     4 and 8 bits; for 3, 5 and 6 bits MLX's 8, 8 and 4 codes per 3, 5 and
+ *     3 bytes, a code possibly straddling two words); scales and biases
+ *     bfloat16 [rows, K/group_size]; w = scale*q + bias.
+ *   - Supported here: bits 2, 3, 4, 5, 6 and 8 with group_size 32, 64 or 128
+ *     for mq_quantize, mq_dequantize and mq_embedding_lookup.  The matmul
+ *     kernels read 4- and 8-bit codes: mq_quantized_matmul_ws runs 2/3/5/6
+ *     bits by rewriting the codes one byte each into its workspace
+ *     (mq_quantized_matmul_workspace counts those bytes) and running the 8-bit
+ *     kernels with the same scales and biases; the other matmul entry points
+ *     return MQ_ERR_UNSUPPORTED for them (mq_repack_codes_u8 converts a
+ *     matrix once, e.g. at load time, to call them with bits = 8).  transpose
+ *     = 0 returns MQ_ERR_UNSUPPORTED; anything MLX itself rejects returns
+ *     MQ_ERR_INVALID.
  *     The fused entry points (SwiGLU, RMSNorm, add + RMSNorm, the SwiGLU
  *     epilogue of mq_gather_qmm_segments) take group_size 64 only (their
  *     *_supported queries say 0 otherwise); a matmul of more than 8 rows with
@@ -79,6 +89,18 @@ int mq_dequantize(const uint32_t* wq, const mq_bf16* scales, const mq_bf16* bias
 int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
                         const mq_bf16* scales, const mq_bf16* biases, int64_t rows, int64_t K,
                         int group_size, int bits, mq_bf16* out, hipStream_t stream);
+
+/*
+ * 2/3/5/6-bit codes wq [rows, K*bits/32] -> the same codes one byte each,
+ * wq8 [rows, K/4] (the 8-bit layout): with the unchanged scales and biases
+ * the matrix dequantizes to the same weights and runs on every 8-bit entry
+ * point.  No counterpart in MLX (its kernels read these widths directly); it
+ * is the load-time step a caller takes where a checkpoint's config.json
+ * "quantization" gives such bits for a path (models/qwen2.py:316-324,
+ * models/lfm2.py:579-589).  K a multiple of 32; wq8 16-byte aligned.
+ */
+int mq_repack_codes_u8(const uint32_t* wq, uint32_t* wq8, int64_t rows, int64_t K, int bits,
+                       hipStream_t stream);
 
 /*
  * mx.quantized_matmul(x, wq, scales, biases, transpose=True, group_size, bits)

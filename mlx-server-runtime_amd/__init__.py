@@ -7,7 +7,7 @@ Import by its directory name (it contains dashes):
     y = mq.quantized_matmul(x, wq, scales, biases, transpose=True, group_size=64, bits=4)
 
 Ops (mx.* names): quantize, dequantize, quantized_matmul, gather_qmm,
-embedding_lookup.  Decoder-step ops (decode_ops): rms_norm, rope_kv_append,
+embedding_lookup; repack_codes_u8 rewrites 2/3/5/6-bit codes one byte each.  Decoder-step ops (decode_ops): rms_norm, rope_kv_append,
 paged_decode_attention, silu_mul over a PagedKV cache; qwen2: the Qwen2-shaped
 decoder with greedy decode.  Modules (mlx.nn names): nn.QuantizedLinear,
 nn.QuantizedEmbedding, nn.QuantizedSwitchLinear, nn.SwitchGLU, nn.quantize.
@@ -16,7 +16,8 @@ there is no CPU fallback.
 """
 
 from . import _lib, core, decode_ops, nn
-from .core import dequantize, embedding_lookup, gather_qmm, quantize, quantized_matmul
+from .core import (dequantize, embedding_lookup, gather_qmm, quantize, quantized_matmul,
+                   repack_codes_u8)
 
 
 def library_path() -> str:
@@ -29,4 +30,4 @@ def version() -> tuple[int, int]:
 
 
 __all__ = ["core", "decode_ops", "nn", "quantize", "dequantize", "quantized_matmul", "gather_qmm",
-           "embedding_lookup", "library_path", "version"]
+           "embedding_lookup", "repack_codes_u8", "library_path", "version"]

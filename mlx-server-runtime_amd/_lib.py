@@ -25,6 +25,7 @@ EXPORTS = (
     "mq_quantize",
     "mq_dequantize",
     "mq_embedding_lookup",
+    "mq_repack_codes_u8",
     "mq_quantized_matmul",
     "mq_quantized_matmul_workspace",
     "mq_quantized_matmul_ws",
@@ -76,6 +77,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_quantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]
     L.mq_dequantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]
     L.mq_embedding_lookup.argtypes = [_p, _i64, _p, _p, _p, _i64, _i64, _int, _int, _p, _p]
+    L.mq_repack_codes_u8.argtypes = [_p, _p, _i64, _i64, _int, _p]
     L.mq_quantized_matmul.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int, _p]
     L.mq_quantized_matmul_workspace.argtypes = [_i64, _i64, _i64, _int, _int]
     L.mq_quantized_matmul_ws.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int,

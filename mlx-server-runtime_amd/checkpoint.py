@@ -222,6 +222,11 @@ class _Builder:
             raise WeightArtifactValidationError(
                 f"{path}: weight {tuple(wq.shape)} does not hold {K} {bits}-bit codes per row")
         wq = wq.view(torch.int32) if wq.dtype == torch.uint32 else wq
+        if bits not in (4, 8) and wq.is_cuda:
+            # the matmul kernels read 4- and 8-bit codes: 2/3/5/6-bit codes are
+            # rewritten one byte each, once here (same scales and biases, so
+            # the same dequantized weights)
+            wq, bits = core.repack_codes_u8(wq.contiguous(), bits), 8
         return QLinear(wq.contiguous(), s, b, bias, gs, bits)
 
     def experts(self, path: str, proj: str) -> QExperts:

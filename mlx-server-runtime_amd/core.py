@@ -12,9 +12,11 @@ graphs make (python/mlx_worker/native_mlx/models/qwen2.py, lfm2.py):
 Tensors live on a ROCm device: activations, scales and biases are bfloat16;
 packed weights are uint32 (int32 is accepted as the same bits).  Invalid
 arguments raise ValueError like MLX; settings MLX accepts but this backend
-does not implement (bits other than 4/8, group sizes other than 64,
-transpose=False, non-affine modes) raise NotImplementedError.  There is no CPU
-or PyTorch fallback.
+does not implement (transpose=False, non-affine modes) raise
+NotImplementedError.  Bits 2, 3, 5 and 6 quantize and dequantize natively;
+their matmuls run on the 8-bit kernels after the codes are rewritten one byte
+each (repack_codes_u8: per call here, once at load time in the model
+loader).  There is no CPU or PyTorch fallback.
 """
 
 from __future__ import annotations
@@ -122,8 +124,7 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4, mode: str = "
     w = w.contiguous()
     rows = w.numel() // K
     lead = tuple(w.shape[:-1])
-    wq = torch.empty(lead + (K * bits // 32 if bits in (2, 4, 8) else 0,), dtype=torch.int32,
-                     device=w.device)
+    wq = torch.empty(lead + (K * bits // 32,), dtype=torch.int32, device=w.device)
     s = torch.empty(lead + (K // group_size,), dtype=torch.bfloat16, device=w.device)
     b = torch.empty_like(s)
     L = _lib.lib()
@@ -145,6 +146,26 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, grou
     L = _lib.lib()
     _lib.check(L.mq_dequantize(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out), rows, K,
                                group_size, bits, _stream(w)), op)
+    return out
+
+
+def repack_codes_u8(w: torch.Tensor, bits: int) -> torch.Tensor:
+    """2/3/5/6-bit codes [..., K*bits/32] -> the same codes one byte each
+    [..., K/4] (the 8-bit layout; with the unchanged scales and biases the
+    matrix dequantizes to the same weights and runs on the 8-bit kernels)."""
+    op = "repack_codes_u8"
+    _require_gpu(op, w=w)
+    _check_codes(op, w)
+    if bits not in (2, 3, 5, 6):
+        raise ValueError(f"[{op}] only 2, 3, 5 and 6-bit codes are repacked, got bits={bits}")
+    if w.ndim < 1 or w.shape[-1] * 32 % bits or (w.shape[-1] * 32 // bits) % 32:
+        raise ValueError(f"[{op}] {tuple(w.shape)} does not hold a multiple of 32 {bits}-bit "
+                         "codes per row")
+    K = w.shape[-1] * 32 // bits
+    wc = w.contiguous()
+    rows = wc.numel() // w.shape[-1]
+    out = torch.empty(tuple(w.shape[:-1]) + (K // 4,), dtype=torch.int32, device=w.device)
+    _lib.check(_lib.lib().mq_repack_codes_u8(_ptr(wc), _ptr(out), rows, K, bits, _stream(w)), op)
     return out
 
 
@@ -354,6 +375,8 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
         raise NotImplementedError(f"[{op}] transpose=False is not implemented on this backend")
     if x.ndim < 2 or x.shape[-1] != K:
         raise ValueError(f"[{op}] x must be [..., M, {K}], got {tuple(x.shape)}")
+    if bits not in (4, 8):  # the expert kernels read word-aligned codes
+        w, bits = repack_codes_u8(w, bits), 8
     M = x.shape[-2]
     N = w.shape[-2]
     E = math.prod(w.shape[:-2])
@@ -420,6 +443,8 @@ def gather_qmm_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         raise ValueError(f"[{op}] x must be [..., M, {K}], got {tuple(x.shape)}")
     if w.ndim != 3 or w.shape[1] % 2:
         raise ValueError(f"[{op}] w must be [E, 2N, K*bits/32], got {tuple(w.shape)}")
+    if bits not in (4, 8):  # the expert kernels read word-aligned codes
+        w, bits = repack_codes_u8(w, bits), 8
     M, N, E = x.shape[-2], w.shape[1] // 2, w.shape[0]
     n_xb = math.prod(x.shape[:-2])
     rhs = rhs_indices.reshape(-1).to(torch.int32).contiguous()

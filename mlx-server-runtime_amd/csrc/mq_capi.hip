@@ -62,9 +62,6 @@ int check_quant(const char* op, int64_t K, int group_size, int bits) {
                 "[%s] The requested group size %d is not supported. The supported group sizes "
                 "are 32, 64 and 128.",
                 op, group_size);
-  if (bits != 4 && bits != 8)
-    return fail(MQ_ERR_UNSUPPORTED, "[%s] bits=%d is not implemented on this backend (4 or 8).",
-                op, bits);
   if (K <= 0 || K % group_size != 0)
     return fail(MQ_ERR_INVALID,
                 "[%s] The last dimension of the matrix needs to be divisible by the "
@@ -73,6 +70,23 @@ int check_quant(const char* op, int64_t K, int group_size, int bits) {
   if (K >= kMaxDim) return fail(MQ_ERR_INVALID, "[%s] K=%lld is too large.", op, (long long)K);
   return MQ_OK;
 }
+
+// 2, 3, 5 and 6 bits (codes as one bit stream per row): quantize, dequantize,
+// the embedding lookup and mq_quantized_matmul_ws (through its workspace) take
+// them; the other matmul entry points run word-aligned codes only.
+bool stream_bits(int bits) { return bits != 4 && bits != 8; }
+
+int check_word_bits(const char* op, int bits) {
+  if (stream_bits(bits))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] bits=%d codes run here as one byte each: repack them with "
+                "mq_repack_codes_u8 and call with bits=8 (or use mq_quantized_matmul_ws).",
+                op, bits);
+  return MQ_OK;
+}
+
+// Repacked 8-bit codes of an N x K matrix, at the start of the workspace.
+size_t repack_bytes(int64_t N, int64_t K) { return (size_t)((N * K + 255) / 256 * 256); }
 
 int check_dim(const char* op, const char* name, int64_t v) {
   if (v < 0 || v >= kMaxDim)
@@ -153,9 +167,28 @@ int mq_embedding_lookup(const int32_t* ids, int64_t n_ids, const uint32_t* wq,
       op);
 }
 
+int mq_repack_codes_u8(const uint32_t* wq, uint32_t* wq8, int64_t rows, int64_t K, int bits,
+                       hipStream_t stream) {
+  const char* op = "repack_codes_u8";
+  if (bits != 2 && bits != 3 && bits != 5 && bits != 6)
+    return fail(MQ_ERR_INVALID, "[%s] bits=%d: only 2, 3, 5 and 6-bit codes are repacked.", op,
+                bits);
+  if (K <= 0 || K % 32 || K >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] K=%lld must be a positive multiple of 32.", op,
+                (long long)K);
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (rows == 0) return ok();
+  if (!wq || !wq8) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(wq8)) return fail(MQ_ERR_INVALID, "[%s] wq8 must be 16-byte aligned.", op);
+  return hip_status(mq::launch_repack_u8(wq, wq8, rows, K, bits, stream), op);
+}
+
 size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_size,
                                      int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+  if ((bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
+      (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0)
+    return repack_bytes(N, K) + mq_quantized_matmul_workspace(M, N, K, group_size, 8);
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
   if (use_skinny(M, N, K, bits, 64)) return mq::qmms_workspace_bytes(M, N, K, bits);
   if (dense_gemv(M, N, K, bits, 64) || mq::qmv_fits(M, N, K, bits, 1, 64)) return 0;
@@ -233,6 +266,7 @@ int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq
                                   size_t workspace_bytes, hipStream_t stream) {
   const char* op = "quantized_matmul_swiglu";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_word_bits(op, bits)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", 2 * N)) return rc;
   if (M == 0 || N == 0) return ok();
@@ -291,6 +325,7 @@ int mq_quantized_matmul_add_rms_norm(const mq_bf16* x, const uint32_t* wq, const
                                      hipStream_t stream) {
   const char* op = "quantized_matmul_add_rms_norm";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_word_bits(op, bits)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", N)) return rc;
   if (M == 0 || N == 0) return ok();
@@ -339,6 +374,7 @@ int mq_rms_norm_quantized_matmul(const mq_bf16* a, const mq_bf16* residual, mq_b
                                  hipStream_t stream) {
   const char* op = "rms_norm_quantized_matmul";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_word_bits(op, bits)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", swiglu ? 2 * N : N)) return rc;
   if (M == 0 || N == 0) return ok();
@@ -391,6 +427,23 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
   if ((M + 127) / 128 > 65535)
     return fail(MQ_ERR_UNSUPPORTED, "[%s] M=%lld exceeds the launch grid (8388480 rows).", op,
                 (long long)M);
+  if (stream_bits(bits)) {
+    // codes rewritten one byte each into the workspace, then the 8-bit
+    // kernels with the rest of it (same scales and biases: the dequantized
+    // weights are those of the bits-wide codes)
+    const size_t rb = repack_bytes(N, K);
+    if (!workspace || workspace_bytes < rb || !aligned16(workspace))
+      return fail(MQ_ERR_UNSUPPORTED,
+                  "[%s] bits=%d needs a 16-byte aligned workspace of at least %zu bytes for its "
+                  "codes repacked to 8 bits (mq_quantized_matmul_workspace).",
+                  op, bits, rb);
+    uint32_t* wq8 = static_cast<uint32_t*>(workspace);
+    if (hipError_t e = mq::launch_repack_u8(wq, wq8, N, K, bits, stream); e != hipSuccess)
+      return hip_status(e, op);
+    return mq_quantized_matmul_ws(x, wq8, scales, biases, bias_vec, y, M, N, K, group_size, 8, 1,
+                                  static_cast<char*>(workspace) + rb, workspace_bytes - rb,
+                                  stream);
+  }
   hipError_t e;
   const mq::GatherMap g1{nullptr, nullptr, 1, 1, 1};
   if (dense_gemv(M, N, K, bits, group_size) &&
@@ -427,6 +480,7 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
                   hipStream_t stream) {
   const char* op = "gather_qmm";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_word_bits(op, bits)) return rc;
   if (int rc = check_dim(op, "T", T)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", N)) return rc;
@@ -489,6 +543,7 @@ int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
   const char* op = swiglu ? "gather_qmm_swiglu" : "gather_qmm";
   if (!expert_offsets) return fail(MQ_ERR_INVALID, "[%s] expert_offsets is null.", op);
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_word_bits(op, bits)) return rc;
   if (int rc = check_dim(op, "T", T)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", swiglu ? 2 * N : N)) return rc;
@@ -542,6 +597,7 @@ int mq_gather_qmm_swiglu(const mq_bf16* x, const int32_t* lhs_indices,
                          hipStream_t stream) {
   const char* op = "gather_qmm_swiglu";
   if (int rc = check_quant(op, K, group_size, bits)) return rc;
+  if (int rc = check_word_bits(op, bits)) return rc;
   if (int rc = check_dim(op, "T", T)) return rc;
   if (int rc = check_dim(op, "M", M)) return rc;
   if (int rc = check_dim(op, "N", N)) return rc;

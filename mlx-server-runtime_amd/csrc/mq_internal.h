@@ -27,6 +27,10 @@ hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* scales, const u
                              const int32_t* row_ids, int64_t n_out_rows, int64_t n_rows,
                              uint16_t* out, int64_t K, int group_size, int bits,
                              hipStream_t stream);
+// 2/3/5/6-bit stream codes [rows, K * bits / 32] -> one byte per code
+// [rows, K / 4] (the 8-bit layout; same scales and biases).
+hipError_t launch_repack_u8(const uint32_t* wq, uint32_t* wq8, int64_t rows, int64_t K, int bits,
+                            hipStream_t stream);
 
 // y[t][m][n] = x[lhs[t]][m] . dequant(w[rhs[t]][n]) (+ bias[n]); valid when
 // qmv_fits(M, N, K, bits, T, group_size) (at most 8 rows, x and the scales

@@ -24,10 +24,16 @@
  * Format (MLX "affine" mode): a row of K weights is split into K/group_size
  * groups.  Each group has one scale s and one bias b (stored in the weight
  * dtype, bfloat16 here) and the weight is w = s*q + b with an integer code q
- * in [0, 2^bits).  Codes are packed LSB-first, 32/bits codes per uint32 word:
- * code j of a word occupies bits [j*bits, (j+1)*bits).
+ * in [0, 2^bits).  Codes are packed LSB-first as one bit stream per row: code
+ * k of a row occupies bits [k*bits, (k+1)*bits) of the row's uint32 words
+ * read as a little-endian stream.  For 2, 4 and 8 bits that is 32/bits codes
+ * per word (code j of a word at bits [j*bits, (j+1)*bits)); for 3, 5 and 6
+ * bits MLX packs 8, 8 and 4 codes into 3, 5 and 3 bytes, which is the same
+ * stream, a code possibly straddling two words.  A group (>= 32 codes) always
+ * fills whole words.
  *
- * Pins (tests/test_oracle_pins.py): packing known-answer words, hand-derived
+ * Pins (tests/test_oracle_pins.py): packing known-answer words (every width,
+ * including codes that straddle a word boundary), hand-derived
  * dequantize values that separate one rounding from two, on-grid round trips
  * through quantize for both scale signs, brute-force nearest-code search, the
  * zero-exactness property of the edge refit, one-hot and all-zero-code
@@ -76,7 +82,8 @@ float orc_bf16_to_f32(uint16_t h) { return bf16_to_f32(h); }
 
 static int check_params(int64_t rows, int64_t K, int group_size, int bits) {
   if (rows < 0 || K <= 0) return ORC_EINVAL;
-  if (bits != 2 && bits != 4 && bits != 8) return ORC_EINVAL;
+  if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8)
+    return ORC_EINVAL;
   if (group_size != 32 && group_size != 64 && group_size != 128) return ORC_EINVAL;
   if (K % group_size) return ORC_EINVAL;
   return ORC_OK;
@@ -104,9 +111,9 @@ int orc_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size, int
   if (check_params(rows, K, group_size, bits)) return ORC_EINVAL;
   const float n_bins = (float)((1 << bits) - 1);
   const float eps = 1e-7f;
-  const int per_word = 32 / bits;
   const int64_t groups = K / group_size;
-  const int64_t words_per_row = K / per_word;
+  const int64_t words_per_row = K * bits / 32;
+  const int group_words = group_size * bits / 32;
   for (int64_t r = 0; r < rows; ++r) {
     for (int64_t g = 0; g < groups; ++g) {
       const uint16_t* src = w + r * K + g * group_size;
@@ -127,17 +134,18 @@ int orc_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size, int
         scale = edge / q0;
         bias = edge;
       }
-      uint32_t* dst = wq + r * words_per_row + g * (group_size / per_word);
-      for (int wd = 0; wd < group_size / per_word; ++wd) {
-        uint32_t word = 0;
-        for (int p = 0; p < per_word; ++p) {
-          float v = bf16_to_f32(src[wd * per_word + p]);
-          float q = rintf((v - bias) / scale);
-          q = (q < 0.0f) ? 0.0f : q;
-          q = (q > n_bins) ? n_bins : q;
-          word |= (uint32_t)q << (p * bits);
-        }
-        dst[wd] = word;
+      uint32_t* dst = wq + r * words_per_row + g * group_words;
+      for (int wd = 0; wd < group_words; ++wd) dst[wd] = 0;
+      for (int j = 0; j < group_size; ++j) {
+        float v = bf16_to_f32(src[j]);
+        float q = rintf((v - bias) / scale);
+        q = (q < 0.0f) ? 0.0f : q;
+        q = (q > n_bins) ? n_bins : q;
+        /* bit p of the group's stream; the high part of a straddling code
+         * goes to the next word */
+        const int p = j * bits;
+        dst[p >> 5] |= (uint32_t)q << (p & 31);
+        if ((p & 31) + bits > 32) dst[(p >> 5) + 1] |= (uint32_t)q >> (32 - (p & 31));
       }
       scales[r * groups + g] = f32_to_bf16(scale);
       biases[r * groups + g] = f32_to_bf16(bias);
@@ -148,10 +156,12 @@ int orc_quantize(const uint16_t* w, int64_t rows, int64_t K, int group_size, int
   return ORC_OK;
 }
 
+/* code k of a row: bits [k*bits, (k+1)*bits) of the row's word stream */
 static inline uint32_t code_at(const uint32_t* row_words, int64_t k, int bits) {
-  const int per_word = 32 / bits;
-  uint32_t word = row_words[k / per_word];
-  return (word >> ((k % per_word) * bits)) & ((1u << bits) - 1u);
+  const int64_t p = k * bits;
+  uint64_t v = row_words[p >> 5];
+  if ((p & 31) + bits > 32) v |= (uint64_t)row_words[(p >> 5) + 1] << 32;
+  return (uint32_t)(v >> (p & 31)) & ((1u << bits) - 1u);
 }
 
 /*
@@ -236,7 +246,7 @@ int orc_qmm_f32(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
   if (M < 0 || check_params(N, K, group_size, bits)) return ORC_EINVAL;
   const int64_t groups = K / group_size;
   const int64_t words_per_row = K * bits / 32;
-  const int per_word = 32 / bits;
+  const int per_word = 32 % bits ? 1 : 32 / bits;  /* word-aligned widths only */
   const uint32_t mask = (1u << bits) - 1u;
   float* xf = (float*)malloc(sizeof(float) * (size_t)(M * K + 1));
   if (!xf) return ORC_EINVAL;
@@ -253,8 +263,16 @@ int orc_qmm_f32(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
       for (int64_t g = 0; g < groups; ++g) {
         const float s = bf16_to_f32(scales[n * groups + g]);
         const float b = bf16_to_f32(biases[n * groups + g]);
-        const uint32_t* gw = rw + g * (group_size / per_word);
         const float* gx = xr + g * group_size;
+        if (32 % bits) {  /* 3, 5, 6 bits: codes from the stream */
+          for (int j = 0; j < group_size; ++j) {
+            float wv = (float)code_at(rw, g * group_size + j, bits) * s;
+            wv = wv + b;
+            acc = acc + gx[j] * wv;
+          }
+          continue;
+        }
+        const uint32_t* gw = rw + g * (group_size / per_word);
         for (int wd = 0; wd < group_size / per_word; ++wd) {
           uint32_t word = gw[wd];
           for (int p = 0; p < per_word; ++p) {

@@ -1,4 +1,5 @@
-"""Write known-answer fixtures for MLX affine quantization (tests/golden/kat_affine_b{4,8}.npz).
+"""Write known-answer fixtures for MLX affine quantization
+(tests/golden/kat_affine_b{2,3,4,5,6,8}.npz).
 
 Every expected value here is fixed by construction, not computed by the oracle
 or the HIP library:
@@ -12,6 +13,10 @@ or the HIP library:
 * Every product and sum of the on-grid weights is exact in bfloat16, so
   mx.dequantize must reproduce w bit for bit.
 * x holds small dyadic bfloat16 values (k/8), so x @ w^T is exact in float64.
+* Codes are packed as one LSB-first bit stream per row (code k at bits
+  [k*bits, (k+1)*bits) of the row's little-endian uint32 words), built here as
+  a Python integer per row: for 2, 4 and 8 bits that is 32/bits codes per
+  word; for 3, 5 and 6 bits it is MLX's 8, 8 and 4 codes per 3, 5 and 3 bytes.
 
 MLX itself is not available offline, so these pin the restatement's algorithm
 (sign/edge choice, refit, packing order, dequantize, matmul orientation) from
@@ -37,10 +42,22 @@ def exact_bf16_bits(v: np.ndarray) -> np.ndarray:
 
 
 def pack(codes: np.ndarray, bits: int) -> np.ndarray:
-    per = 32 // bits
-    c = codes.astype(np.uint64).reshape(codes.shape[:-1] + (codes.shape[-1] // per, per))
-    shifts = (np.arange(per, dtype=np.uint64) * bits)
-    return np.bitwise_or.reduce(c << shifts, axis=-1).astype(np.uint32)
+    lead, K = codes.shape[:-1], codes.shape[-1]
+    rows = []
+    for r in codes.reshape(-1, K):
+        stream = 0
+        for k, q in enumerate(r.tolist()):
+            assert 0 <= q < (1 << bits)
+            stream |= q << (k * bits)
+        rows.append(np.frombuffer(stream.to_bytes(K * bits // 8, "little"), "<u4"))
+    return np.stack(rows).astype(np.uint32).reshape(lead + (K * bits // 32,))
+
+
+# Per width: (scale exponents drawn from [lo, hi), significant fractional
+# steps of the scale, c_pos, c_neg).  c_pos > nmax/2 > c_neg, and |q - c| times
+# the scale's significand stays within bfloat16's 8 bits.
+SCALE_RULES = {2: (4, 7, 8, 2, 1), 3: (5, 8, 8, 5, 2), 4: (5, 8, 8, 9, 6),
+               5: (6, 9, 4, 18, 13), 6: (7, 10, 2, 36, 27), 8: (8, 11, 1, 130, 125)}
 
 
 def build_matrix(rng, rows: int, K: int, bits: int):
@@ -57,12 +74,11 @@ def build_matrix(rng, rows: int, K: int, bits: int):
             kind = kinds[(r * groups + g) % len(kinds)] if (r + g) % 7 else "pos"
             sl = slice(g * GS, (g + 1) * GS)
             if kind in ("pos", "neg"):
-                if bits == 4:
-                    s = 2.0 ** -int(rng.integers(5, 8)) * (1 + int(rng.integers(0, 8)) / 8)
-                    c_pos, c_neg = 9, 6
+                lo, hi, steps, c_pos, c_neg = SCALE_RULES[bits]
+                if bits == 8:
+                    s = 2.0 ** -int(rng.integers(lo, hi))
                 else:
-                    s = 2.0 ** -int(rng.integers(8, 11))
-                    c_pos, c_neg = 130, 125
+                    s = 2.0 ** -int(rng.integers(lo, hi)) * (1 + int(rng.integers(0, steps)) / steps)
                 q = rng.integers(0, nmax + 1, GS)
                 q[rng.integers(0, GS)] = 0
                 q[(rng.integers(1, GS) + 0) % GS] = nmax
@@ -90,7 +106,9 @@ def build_matrix(rng, rows: int, K: int, bits: int):
 
 def main() -> None:
     rng = np.random.default_rng(1234)
-    for bits in (4, 8):
+    # 4 and 8 first: the random stream (and so their fixtures) is unchanged
+    # by the widths added after them
+    for bits in (4, 8, 2, 3, 5, 6):
         rows, K, M = 12, 256, 3
         w, codes, scales, biases, checked = build_matrix(rng, rows, K, bits)
         x = rng.integers(-16, 17, (M, K)) / 8.0

@@ -1,0 +1,233 @@
+"""Bits 2, 3, 5 and 6 (the other widths mx.quantize accepts; mlx-community
+checkpoints carry them in config.json["quantization"], read per path at
+models/qwen2.py:279,321 and models/lfm2.py:579-589) through the C ABI against
+the oracle:
+
+* quantize and dequantize (the codes as one LSB-first bit stream per row),
+  the embedding lookup and the on-grid known-answer fixtures: bit-exact;
+* repack_codes_u8: the one-byte codes dequantize at 8 bits to exactly what the
+  stream codes dequantize to;
+* quantized_matmul (the codes repacked into the call's workspace, then the
+  8-bit kernels) at GEMV, skinny and large-M rows, and gather_qmm sorted and
+  unsorted: norm-wise relative error <= 1e-2 against the oracle (bfloat16
+  output, float32 accumulation);
+* a 2-layer Qwen2-shaped decoder and a Qwen3-MoE-shaped one at these widths
+  against the float32 restatement, and a 3-bit checkpoint through the loader
+  (which repacks the codes once at load).
+"""
+
+from __future__ import annotations
+
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import (DEV, assert_close, bf16_dev, bits_host, rand_bf16, u32_dev,
+                             u32_host)
+from test_oracle_pins import load_kat, unpack_stream
+
+pytestmark = pytest.mark.gpu
+
+WIDTHS = [2, 3, 5, 6]
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("shape", [(37, 256), (5, 3584), (3, 128)])
+def test_quantize_bit_exact(mq, orc, bits, gs, shape):
+    rng = np.random.default_rng(500 + 10 * bits + gs)
+    w = rand_bf16(orc, rng, shape, 0.02)
+    w[0, :gs] = 0                                        # zero group
+    w[-1, -gs:] = orc.f32_to_bf16(np.float32(0.0125))   # constant group
+    if shape[1] >= 2 * gs:                               # a one-signed group
+        w[1 % shape[0], gs:2 * gs] = orc.f32_to_bf16(
+            np.abs(rng.normal(0, 1, gs)).astype(np.float32))
+    wq, s, b = mq.quantize(bf16_dev(w), gs, bits)
+    rq, rs, rb = orc.quantize(w, gs, bits)
+    assert wq.shape == (shape[0], shape[1] * bits // 32)
+    assert np.array_equal(u32_host(wq), rq)
+    assert np.array_equal(bits_host(s), rs)
+    assert np.array_equal(bits_host(b), rb)
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_dequantize_bit_exact(mq, orc, bits, gs):
+    rng = np.random.default_rng(600 + 10 * bits + gs)
+    wq, s, b = orc.quantize(rand_bf16(orc, rng, (41, 384), 0.02), gs, bits)
+    out = mq.dequantize(u32_dev(wq), bf16_dev(s), bf16_dev(b), gs, bits)
+    assert np.array_equal(bits_host(out), orc.dequantize(wq, s, b, gs, bits))
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+def test_kat_fixtures_on_gpu(mq, orc, bits):
+    """On-grid weights (tests/golden/make_kat.py): quantize returns the
+    constructed codes, scales and biases; dequantize returns w."""
+    kat = load_kat(bits)
+    wq, s, b = mq.quantize(bf16_dev(kat["w"]), 64, bits)
+    assert np.array_equal(u32_host(wq), kat["wq"])
+    chk = kat["scale_checked"]
+    assert np.array_equal(bits_host(s)[chk], kat["scales"][chk])
+    assert np.array_equal(bits_host(b), kat["biases"])
+    deq = mq.dequantize(u32_dev(kat["wq"]), bf16_dev(kat["scales"]), bf16_dev(kat["biases"]), 64,
+                        bits)
+    assert np.array_equal(bits_host(deq), kat["deq"])
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+def test_embedding_lookup_bit_exact(mq, orc, bits):
+    rng = np.random.default_rng(700 + bits)
+    wq, s, b = orc.quantize(rand_bf16(orc, rng, (50, 256), 0.02), 64, bits)
+    ids = np.array([[3, 0, 49], [7, 7, 12]], np.int32)
+    out = mq.embedding_lookup(torch.from_numpy(ids).to(DEV), u32_dev(wq), bf16_dev(s),
+                              bf16_dev(b), 64, bits)
+    ref = orc.dequantize(wq, s, b, 64, bits)[ids.reshape(-1)].reshape(2, 3, 256)
+    assert np.array_equal(bits_host(out), ref)
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+def test_repack_keeps_codes(mq, orc, bits):
+    """One byte per code, the same code values; with the same scales and
+    biases the 8-bit matrix dequantizes to the stream matrix's weights."""
+    rng = np.random.default_rng(800 + bits)
+    wq, s, b = orc.quantize(rand_bf16(orc, rng, (19, 192), 0.02), 64, bits)
+    w8 = u32_host(mq.repack_codes_u8(u32_dev(wq), bits))
+    assert w8.shape == (19, 48)
+    assert np.array_equal(w8.view(np.uint8).reshape(19, 192), unpack_stream(wq, bits))
+    assert np.array_equal(orc.dequantize(w8, s, b, 64, 8), orc.dequantize(wq, s, b, 64, bits))
+
+
+@pytest.mark.parametrize("bits", WIDTHS)
+@pytest.mark.parametrize("M", [1, 3, 9, 32, 130, 600])
+def test_quantized_matmul_parity(mq, orc, bits, M):
+    K, N = 1024, 768
+    rng = np.random.default_rng(900 + 10 * bits + M)
+    wq, s, b = orc.quantize(rand_bf16(orc, rng, (N, K), 0.02), 64, bits)
+    x = rand_bf16(orc, rng, (M, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, 64, bits,
+                            bias=bf16_dev(bias))
+    assert y.shape == (M, N)
+    assert_close(y, orc.qmm(x, wq, s, b, 64, bits, bias=bias))
+
+
+@pytest.mark.parametrize("bits,gs", [(3, 32), (6, 128)])
+def test_quantized_matmul_group_sizes(mq, orc, bits, gs):
+    rng = np.random.default_rng(950 + bits + gs)
+    for M, K, N in [(1, 3584, 4608), (20, 512, 256)]:
+        wq, s, b = orc.quantize(rand_bf16(orc, rng, (N, K), 0.02), gs, bits)
+        x = rand_bf16(orc, rng, (M, K), 1.0)
+        y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, gs,
+                                bits)
+        assert_close(y, orc.qmm(x, wq, s, b, gs, bits))
+
+
+@pytest.mark.parametrize("bits", [3, 5])
+@pytest.mark.parametrize("T,sorted_", [(5, False), (300, True)])
+def test_gather_qmm_parity(mq, orc, bits, T, sorted_):
+    rng = np.random.default_rng(990 + T + bits)
+    E, N, K = 16, 192, 512
+    w = rand_bf16(orc, rng, (E * N, K), 0.02)
+    wq, s, b = orc.quantize(w, 64, bits)
+    wq, s, b = wq.reshape(E, N, -1), s.reshape(E, N, -1), b.reshape(E, N, -1)
+    rhs = rng.integers(0, E, T).astype(np.int32)
+    if sorted_:
+        rhs = np.sort(rhs)
+    x = rand_bf16(orc, rng, (T, 1, K), 1.0)
+    y = mq.gather_qmm(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b),
+                      rhs_indices=torch.from_numpy(rhs).to(DEV), group_size=64, bits=bits,
+                      sorted_indices=sorted_)
+    assert y.shape == (T, 1, N)
+    assert_close(y, orc.gather_qmm(x, wq, s, b, rhs, group_size=64, bits=bits))
+
+
+@pytest.mark.parametrize("bits", [3, 6])
+def test_decoder_bits(bits):
+    """A 2-layer Qwen2-shaped decoder quantized at 3 / 6 bits: its fused
+    entry points report these widths unsupported, so the model runs the
+    unfused kernels on codes repacked per call; prefill logits against the
+    float32 restatement, graph decode equal to eager decode."""
+    from test_gpu_qwen2 import _run
+
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config(256, 512, 4, 2, 2, 1000, bits=bits)
+    toks, toks_graph, e_pre, e_dec, (match, total, worst) = _run(cfg, 2, 12, 16)
+    m, _ = _run.last
+    assert m.layers[0].qkv.bits == bits
+    assert torch.equal(toks, toks_graph)
+    assert e_pre <= 3e-2 and e_dec <= 2e-2, (e_pre, e_dec)
+    assert match >= 0.9 * total and worst <= 0.05, (match, total, worst)
+
+
+@pytest.mark.parametrize("bits", [3, 6])
+@pytest.mark.parametrize("T", [3, 64])
+def test_moe_block_bits(mq, bits, T):
+    """Routed experts at 3 / 6 bits (banks repacked per call): T=3 is 24
+    pairs (per-pair GEMV), T=64 512 pairs (sorted segments, SiLU*up epilogue);
+    against the float32 restatement given the kernel's own routing."""
+    moe = importlib.import_module("mlx-server-runtime_amd.moe")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    from qwen2_reference import moe_reference
+
+    E, k, H, inter = 16, 8, 256, 128
+    cfg = q2.Qwen2Config(H, 4 * H, 4, 2, 1, 100, bits=bits)
+    g = torch.Generator(device=DEV).manual_seed(20 + bits)
+    block = moe.MoEBlock(q2._random_qlinear(g, E, H, cfg, False, DEV),
+                         q2._random_experts(g, E, 2 * inter, H, cfg, DEV),
+                         q2._random_experts(g, E, H, inter, cfg, DEV), k, True)
+    assert block.gate_up.bits == bits
+    x = torch.randn(T, H, generator=g, device=DEV).to(torch.bfloat16)
+    out = block(x)
+    idx, _ = moe.route(block.gate(x), k, True)
+    ref = moe_reference(mq, block, x, indices=idx)
+    err = float((out.float() - ref).abs().max() / ref.abs().max())
+    assert err < 2e-2, err
+
+
+def test_moe_decoder_bits():
+    """Qwen3-MoE shape at 3 bits, prefill against the float32 restatement.
+    Routing is a discrete choice: where two experts' gates nearly tie the two
+    can pick different experts for a token (~10 % on that position), so the
+    bounds are on the median and the share of positions, as for 4 bits."""
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    from qwen2_reference import reference_logits
+
+    cfg = q2.Qwen2Config(256, 512, 4, 2, 2, 1000, attention_bias=False, qk_norm=True,
+                         num_experts=8, num_experts_per_tok=2, moe_intermediate_size=128, bits=3)
+    m = q2.Qwen2Model.random(cfg, seed=4, device=DEV)
+    ids = torch.randint(0, 1000, (3, 24), generator=torch.Generator(device=DEV).manual_seed(6),
+                        device=DEV)
+    ours = m.prefill(ids, m.new_cache(3, 24), all_positions=True)
+    ref = reference_logits(mq, m, ids)
+    d = (ours.float() - ref).abs().amax(-1) / ref.abs().amax(-1)
+    assert d.median() <= 2.5e-2 and (d <= 3e-2).float().mean() >= 0.75, d
+    assert torch.equal(m.generate(ids, 6, use_graph=False), m.generate(ids, 6))
+
+
+def test_three_bit_checkpoint_loads_repacked(tmp_path):
+    """A checkpoint whose config.json says bits 3 (and one path 6): the loader
+    rewrites the codes one byte each at load (the layers run the 8-bit
+    kernels, fused entries included); logits against the 3-bit model it was
+    saved from and against the float32 restatement."""
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    ck = importlib.import_module("mlx-server-runtime_amd.checkpoint")
+    from qwen2_reference import reference_logits
+
+    cfg = q2.Qwen2Config(256, 512, 4, 2, 2, 1000, bits=3)
+    m = q2.Qwen2Model.random(cfg, seed=8, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(12)
+    w_d = (torch.randn(256, 512, generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    m.layers[1].down = q2.QLinear(*mq.quantize(w_d, 64, 6), None, 64, 6)
+    ck.save(m, tmp_path)
+    m2 = ck.load(tmp_path, device=DEV)
+    assert m2.layers[0].qkv.bits == 8 and m2.layers[1].down.bits == 8
+    ids = torch.randint(0, 1000, (2, 20), generator=gen, device=DEV)
+    a = m.prefill(ids, m.new_cache(2, 20), all_positions=True)
+    b = m2.prefill(ids, m2.new_cache(2, 20), all_positions=True)
+    assert float((a.float() - b.float()).abs().max() / b.float().abs().max()) <= 1e-2
+    ref = reference_logits(mq, m2, ids)
+    assert float((b.float() - ref).abs().max() / ref.abs().max()) <= 3e-2

@@ -34,7 +34,7 @@ def declared_functions():
 def test_header_declares_the_abi():
     assert declared_functions() == sorted([
         "mq_version", "mq_last_error", "mq_quantize", "mq_dequantize", "mq_embedding_lookup",
-        "mq_quantized_matmul", "mq_quantized_matmul_workspace", "mq_quantized_matmul_ws",
+        "mq_repack_codes_u8", "mq_quantized_matmul", "mq_quantized_matmul_workspace", "mq_quantized_matmul_ws",
         "mq_gather_qmm", "mq_rms_norm", "mq_rope_kv_append",
         "mq_paged_decode_attention_workspace", "mq_paged_decode_attention",
         "mq_decode_attention_step", "mq_silu_mul",
@@ -71,7 +71,10 @@ def test_workspace_query(mq):
     assert q(1, 3584, 18944, 64, 4) == 0      # GEMV
     assert q(4096, 3584, 18944, 64, 4) == 0   # large-M kernels, 224 tiles: no split
     assert q(2048, 3584, 18944, 64, 4) == 2 * 2048 * 3584 * 4   # 112 tiles: K in 2
-    assert q(64, 3584, 18944, 64, 3) == 0     # unsupported bits
+    # 3-bit codes: their one-byte repack (rounded to 256 bytes) ahead of the
+    # 8-bit plan's own workspace
+    assert q(64, 3584, 18944, 64, 3) == (3584 * 18944 + 255) // 256 * 256 + q(64, 3584, 18944, 64, 8)
+    assert q(1, 100, 96, 32, 5) == 9728 + q(1, 100, 96, 32, 8)
     assert q(64, 3584, 18900, 64, 4) == 0     # K not a group multiple
     assert q(0, 3584, 18944, 64, 4) == 0
 
@@ -203,10 +206,16 @@ def test_capi_invalid_and_unsupported_codes(mq):
     L = _L(mq)
     null = None
     qmm = L.mq_quantized_matmul
-    # bits MLX does not know -> invalid; bits MLX knows but not here -> unsupported
+    # bits MLX does not know -> invalid; 2/3/5/6 bits without the workspace
+    # their repacked codes need -> unsupported
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 7, 1, null) == -1
     assert b"supported bits" in L.mq_last_error()
-    assert qmm(null, null, null, null, null, null, 1, 8, 64, 64, 2, 1, null) == -2
+    sixteen = ctypes.c_void_p(16)  # never dereferenced: validation fails before any launch
+    assert qmm(sixteen, sixteen, sixteen, sixteen, null, sixteen, 1, 8, 64, 64, 2, 1, null) == -2
+    assert b"workspace" in L.mq_last_error()
+    ws = L.mq_quantized_matmul_ws
+    assert ws(sixteen, sixteen, sixteen, sixteen, null, sixteen, 1, 8, 64, 64, 3, 1, sixteen, 255,
+              null) == -2
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 48, 4, 1, null) == -1
     # group sizes 32 and 128 pass the checks (null pointers are then the error)
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 32, 4, 1, null) == -1
@@ -251,7 +260,13 @@ def test_capi_quantize_dequantize_validation(mq):
     null = None
     assert L.mq_quantize(null, null, null, null, 4, 100, 64, 4, null) == -1
     assert L.mq_quantize(null, null, null, null, 0, 128, 64, 4, null) == 0
-    assert L.mq_dequantize(null, null, null, null, 4, 128, 64, 6, null) == -2
+    assert L.mq_dequantize(null, null, null, null, 4, 128, 64, 6, null) == -1  # 6-bit: null ptrs
+    assert b"null" in L.mq_last_error()
+    rp = L.mq_repack_codes_u8
+    assert rp(null, null, 4, 128, 4, null) == -1      # 4-bit codes are not repacked
+    assert rp(null, null, 4, 100, 3, null) == -1      # K not a multiple of 32
+    assert rp(null, null, 0, 128, 3, null) == 0       # empty
+    assert rp(null, null, 2, 128, 5, null) == -1 and b"null" in L.mq_last_error()
     assert L.mq_embedding_lookup(null, 3, null, null, null, 10, 128, 64, 4, null, null) == -1
 
 

@@ -57,6 +57,61 @@ def test_pack_known_word_8bit(orc):
     assert out.tolist() == [[0.0, 1.0, 2.0, 254.0] * 16]
 
 
+# Widths that do not divide 32 continue the LSB-first stream across words
+# (MLX: 8 3-bit codes in 3 bytes, 4 6-bit codes in 3 bytes, 8 5-bit codes in
+# 5 bytes).  Words below are written out by hand from those byte patterns.
+STREAM_KATS = {
+    # 3-bit codes 0..7 -> octal 76543210 = bytes 88 C6 FA, repeated
+    3: ([0x88FAC688, 0xC688FAC6, 0xFAC688FA] * 2, list(range(8)) * 8),
+    # 6-bit codes 1..4 -> octal 04030201 = bytes 81 30 10, repeated
+    6: ([0x81103081, 0x30811030, 0x10308110] * 4, [1, 2, 3, 4] * 16),
+    # 5-bit: a 1 every 8th code sets stream bits 0, 40, 80, 120 of each 160
+    5: ([0x1, 0x100, 0x10000, 0x1000000, 0x0] * 2, ([1] + [0] * 7) * 8),
+    # 2-bit: byte E4 = codes 0, 1, 2, 3
+    2: ([0xE4E4E4E4] * 4, [0, 1, 2, 3] * 16),
+}
+
+
+@pytest.mark.parametrize("bits", sorted(STREAM_KATS))
+def test_pack_known_words_stream(orc, bits):
+    words, codes = STREAM_KATS[bits]
+    wq = np.array([words], np.uint32)
+    s = np.array([[bf16_bits(1.0)]], np.uint16)
+    b = np.array([[0]], np.uint16)
+    out = orc.bf16_to_f32(orc.dequantize(wq, s, b, 64, bits))
+    assert out.tolist() == [[float(c) for c in codes]]
+
+
+def test_pack_straddling_code(orc):
+    # 3-bit code 10 holds bits 30..32: two bits in word 0, one in word 1
+    wq = np.array([[0xC0000000, 0x1, 0, 0, 0, 0]], np.uint32)
+    s = np.array([[bf16_bits(1.0)]], np.uint16)
+    b = np.array([[0]], np.uint16)
+    out = orc.bf16_to_f32(orc.dequantize(wq, s, b, 64, 3))[0]
+    assert out[10] == 7.0 and np.count_nonzero(out) == 1
+    # quantize through the same boundary: zeros with 1.75 at k = 10 refit to
+    # scale -0.25 and bias 1.75 (the larger-magnitude edge), so the zeros are
+    # code 7 and k = 10 is code 0: every bit set but 30, 31 and 32
+    w = np.zeros((1, 64), np.uint16)
+    w[0, 10] = bf16_bits(1.75)
+    wq2, s2, b2 = orc.quantize(w, 64, 3)
+    assert wq2.tolist() == [[0x3FFFFFFF, 0xFFFFFFFE] + [0xFFFFFFFF] * 4]
+    assert s2[0, 0] == bf16_bits(-0.25) and b2[0, 0] == bf16_bits(1.75)
+    assert orc.bf16_to_f32(orc.dequantize(wq2, s2, b2, 64, 3)).tolist() == \
+        orc.bf16_to_f32(w).tolist()
+
+
+def unpack_stream(wq: np.ndarray, bits: int) -> np.ndarray:
+    """Codes [rows, K] of LSB-first stream-packed rows, through Python integers."""
+    rows = wq.reshape(-1, wq.shape[-1])
+    K = wq.shape[-1] * 32 // bits
+    out = np.empty((rows.shape[0], K), np.int64)
+    for r, row in enumerate(rows):
+        stream = int.from_bytes(row.astype("<u4").tobytes(), "little")
+        out[r] = [(stream >> (k * bits)) & ((1 << bits) - 1) for k in range(K)]
+    return out
+
+
 # -------------------------------------------------------------- dequantize
 
 
@@ -82,7 +137,7 @@ def test_dequantize_rounds_twice(orc):
     assert np.all(exact == 3.015625)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_dequantize_kat_fixture(orc, bits):
     kat = load_kat(bits)
     out = orc.dequantize(kat["wq"], kat["scales"], kat["biases"], 64, bits)
@@ -92,7 +147,7 @@ def test_dequantize_kat_fixture(orc, bits):
 # ---------------------------------------------------------------- quantize
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_quantize_on_grid_fixture(orc, bits):
     kat = load_kat(bits)
     wq, s, b = orc.quantize(kat["w"], 64, bits)
@@ -106,13 +161,12 @@ def test_quantize_on_grid_fixture(orc, bits):
     assert np.array_equal(orc.bf16_to_f32(deq), orc.bf16_to_f32(kat["w"]))
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_quantize_codes_are_nearest(orc, bits):
     rng = np.random.default_rng(7)
     w = orc.f32_to_bf16(rng.normal(0, 0.02, (33, 256)).astype(np.float32))
     wq, s, b, s32, b32 = orc.quantize(w, 64, bits, with_f32=True)
-    codes = np.stack([(wq >> np.uint32(j * bits)) & np.uint32((1 << bits) - 1)
-                      for j in range(32 // bits)], -1).reshape(33, 256).astype(np.float64)
+    codes = unpack_stream(wq, bits).astype(np.float64)
     wf = orc.bf16_to_f32(w).astype(np.float64).reshape(33, 4, 64)
     sg = s32.astype(np.float64)[..., None]
     bg = b32.astype(np.float64)[..., None]
@@ -146,7 +200,7 @@ def test_quantize_zero_is_exact(orc):
 def test_quantize_rejects_bad_params(orc):
     w = np.zeros((2, 64), np.uint16)
     with pytest.raises(ValueError):
-        orc.quantize(w, 64, 3)
+        orc.quantize(w, 64, 7)
     with pytest.raises(ValueError):
         orc.quantize(w, 48, 4)
     with pytest.raises(ValueError):
@@ -161,14 +215,14 @@ def _rand_quantized(orc, rng, N, K, bits):
     return orc.quantize(w, 64, bits)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_qmm_kat_fixture(orc, bits):
     kat = load_kat(bits)
     y = orc.qmm(kat["x"], kat["wq"], kat["scales"], kat["biases"], 64, bits)
     assert np.allclose(y, kat["y"], rtol=2e-7, atol=1e-6)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_qmm_one_hot_reads_dequantized_column(orc, bits):
     rng = np.random.default_rng(11)
     wq, s, b = _rand_quantized(orc, rng, 24, 192, bits)
@@ -193,7 +247,7 @@ def test_qmm_zero_codes_sum_biases(orc):
     assert np.allclose(y, ref, rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_qmm_matches_numpy_matmul(orc, bits):
     rng = np.random.default_rng(13)
     wq, s, b = _rand_quantized(orc, rng, 40, 320, bits)
@@ -228,7 +282,7 @@ def test_qmm_f32_variant_close_to_double(orc, bits):
 # ---------------------------------------------------------------- gather_qmm
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 def test_gather_kat_fixture(orc, bits):
     kat = load_kat(bits)
     y = orc.gather_qmm(kat["gx"], kat["gwq"], kat["gscales"], kat["gbiases"], kat["rhs"],
