@@ -15,7 +15,9 @@ q/k norms; models/lfm2.py:569-591 for per-path quantization overrides):
   [N, K*bits/32], `{path}.scales` / `{path}.biases` [N, K/group_size];
   mixture-of-experts banks are stacked per expert,
   `mlp.switch_mlp.{gate,up,down}_proj.*` [E, N, ...] (or per-expert
-  `mlp.experts.{e}.*`, stacked on load).
+  `mlp.experts.{e}.*`, stacked on load); codes at 2, 3, 5 or 6 bits are
+  rewritten one byte each on a GPU device (the layer then runs at 8 bits with
+  the same scales and biases: the same dequantized weights).
 
 Tensors are read with safetensors (no pickle), straight to the target device.
 Modules stored without `{path}.scales` (and every module of a checkpoint
