@@ -146,7 +146,8 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
 
 /*
  * mq_quantized_matmul_ws without a workspace argument and without any
- * allocation: the split-K partial sums live in a device array of this library
+ * allocation: the split-K partial sums (and, at 2/3/5/6 bits, the codes
+ * repacked one byte each) live in a device array of this library
  * (MQ_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; resolved
  * once per device on its first call there).  No counterpart in the reference:
  * it is for callers that cannot allocate (code under HIP graph capture,

@@ -60,9 +60,10 @@ extern "C" int mq_quantized_matmul_noalloc(const mq_bf16* x, const uint32_t* wq,
   if (need > kScratchBytes) {
     char msg[256];
     snprintf(msg, sizeof(msg),
-             "[quantized_matmul_noalloc] M=%lld, N=%lld, K=%lld needs %zu bytes of split-K "
-             "scratch; this entry point holds %zu per GPU (use mq_quantized_matmul_ws with a "
-             "caller workspace).",
+             "[quantized_matmul_noalloc] M=%lld, N=%lld, K=%lld needs %zu bytes of scratch "
+             "(split-K partial sums; at 2/3/5/6 bits also the codes repacked to 8 bits); this "
+             "entry point holds %zu per GPU (use mq_quantized_matmul_ws with a caller "
+             "workspace).",
              (long long)M, (long long)N, (long long)K, need, kScratchBytes);
     return mq::set_last_error(MQ_ERR_INVALID, msg);
   }

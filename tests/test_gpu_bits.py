@@ -18,6 +18,7 @@ the oracle:
 
 from __future__ import annotations
 
+import ctypes
 import importlib
 
 import numpy as np
@@ -231,3 +232,21 @@ def test_three_bit_checkpoint_loads_repacked(tmp_path):
     assert float((a.float() - b.float()).abs().max() / b.float().abs().max()) <= 1e-2
     ref = reference_logits(mq, m2, ids)
     assert float((b.float() - ref).abs().max() / ref.abs().max()) <= 3e-2
+
+
+def test_noalloc_stream_bits():
+    """mq_quantized_matmul_noalloc at 3 bits: the repacked codes (and any
+    split-K partial sums) in the per-GPU array, bit-equal to
+    mq_quantized_matmul_ws, on two calls in a row (the second smaller); a
+    matrix whose repacked codes exceed the array is refused before any launch."""
+    from test_zz_no_alloc import SCRATCH_BYTES, _case, _lib
+
+    mq, L = _lib()
+    _case(mq, L, 32, 1024, 2048, 3, seed=21, bias=True)
+    _case(mq, L, 8, 512, 1024, 3, seed=22, bias=False)
+    N, K = 4608, 4096
+    assert N * K > SCRATCH_BYTES
+    sixteen = ctypes.c_void_p(16)  # never dereferenced: refused before any launch
+    rc = L.mq_quantized_matmul_noalloc(sixteen, sixteen, sixteen, sixteen, None, sixteen, 4, N,
+                                       K, 64, 3, 1, None)
+    assert rc == -1 and b"repacked" in L.mq_last_error()
