@@ -650,7 +650,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
         }
         uint16_t* dst = a.y + (int64_t)(out_row0 + row) * N + n;
         if (vec) {
-          *reinterpret_cast<u32x4_t*>(dst) = v;
+          // nontemporal: the output streams out once (measured against plain
+          // stores: the MoE-prefill down projection 8 % faster, the dense and
+          // gate|up GEMMs 1-4 %)
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
         } else {
           const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
           for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = vs[e];
