@@ -432,6 +432,13 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
     // kernels with the rest of it (same scales and biases: the dequantized
     // weights are those of the bits-wide codes)
     const size_t rb = repack_bytes(N, K);
+    // the one refusal of the 8-bit path below, checked before the repack so
+    // that a failed call enqueues nothing
+    if (group_size != 64 && K % 64 && !mq::qmv_fits(M, N, K, 8, 1, group_size))
+      return fail(MQ_ERR_UNSUPPORTED,
+                  "[%s] M=%lld rows with K=%lld (not a multiple of 64) are not implemented on "
+                  "this backend.",
+                  op, (long long)M, (long long)K);
     if (!workspace || workspace_bytes < rb || !aligned16(workspace))
       return fail(MQ_ERR_UNSUPPORTED,
                   "[%s] bits=%d needs a 16-byte aligned workspace of at least %zu bytes for its "

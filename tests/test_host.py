@@ -216,6 +216,9 @@ def test_capi_invalid_and_unsupported_codes(mq):
     ws = L.mq_quantized_matmul_ws
     assert ws(sixteen, sixteen, sixteen, sixteen, null, sixteen, 1, 8, 64, 64, 3, 1, sixteen, 255,
               null) == -2
+    # group 32 with K = 96 beyond the GEMV's rows: refused before the repack
+    assert ws(sixteen, sixteen, sixteen, sixteen, null, sixteen, 16, 8, 96, 32, 3, 1, sixteen,
+              1 << 20, null) == -2 and b"multiple of 64" in L.mq_last_error()
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 48, 4, 1, null) == -1
     # group sizes 32 and 128 pass the checks (null pointers are then the error)
     assert qmm(null, null, null, null, null, null, 1, 8, 64, 32, 4, 1, null) == -1
