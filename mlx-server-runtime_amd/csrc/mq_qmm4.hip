@@ -655,8 +655,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
           // gate|up GEMMs 1-4 %)
           __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
         } else {
-          const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
-          for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = vs[e];
+          // constant indices into v: no copy of it on the stack
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
         }
       }
     }

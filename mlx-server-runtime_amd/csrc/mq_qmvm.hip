@@ -319,15 +319,31 @@ int pick_nw(int64_t K, int bits) {
   return T <= 32 ? 4 : T <= 64 ? 8 : 16;
 }
 
+// x registers a lane holds (16-byte units) and the most a block of NW waves
+// affords: 1024-thread blocks have 128 VGPRs.  Past it the kernel spills.
+constexpr int x_regs(int bits, int s, int mt) { return mt * ((s * (16 / bits) + 15) / 16); }
+constexpr int x_regs_max(int nw) { return nw == 16 ? 6 : 16; }
+
+// Instantiates only the row counts whose x registers fit (the rest would
+// spill and qmvm_fits refuses them).
+template <int BITS, int NW, int S, int MT>
+hipError_t run_fit(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                   const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                   const GatherMap& g, hipStream_t stream) {
+  if constexpr (x_regs(BITS, S, MT) <= x_regs_max(NW))
+    return run<BITS, NW, S, MT>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  return hipErrorInvalidValue;
+}
+
 template <int BITS, int NW, int S>
 hipError_t run_s(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                  const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                  const GatherMap& g, hipStream_t stream) {
-  if (M <= 1) return run<BITS, NW, S, 1>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 2) return run<BITS, NW, S, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 4) return run<BITS, NW, S, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if (M <= 8) return run<BITS, NW, S, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
-  if constexpr (BITS == 8) return run<BITS, NW, S, 16>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 1) return run_fit<BITS, NW, S, 1>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 2) return run_fit<BITS, NW, S, 2>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 4) return run_fit<BITS, NW, S, 4>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if (M <= 8) return run_fit<BITS, NW, S, 8>(x, wq, s, b, bias, y, M, N, K, g, stream);
+  if constexpr (BITS == 8) return run_fit<BITS, NW, S, 16>(x, wq, s, b, bias, y, M, N, K, g, stream);
   return hipErrorInvalidValue;
 }
 
@@ -352,8 +368,7 @@ bool qmvm_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T) {
   if (TS > kMaxS) return false;                                   // chunks per lane
   if ((K / kGroup) / 4 > 2 * (nw * 64 / kRows)) return false;     // scale loads per thread
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
-  const int64_t xregs = mt * (((TS <= 8 ? 8 : kMaxS) * (16 / bits) + 15) / 16);  // x units held
-  if (xregs > (nw == 16 ? 6 : 16)) return false;  // 1024-thread blocks have 128 VGPRs
+  if (x_regs(bits, TS <= 8 ? 8 : kMaxS, mt) > x_regs_max(nw)) return false;
   return layout(bits, nw, mt, (int)K).total <= 160 * 1024;
 }
 
