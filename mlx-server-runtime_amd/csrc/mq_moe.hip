@@ -52,12 +52,48 @@ __device__ __forceinline__ uint64_t route_key(float gate, int id) {
   return (uint64_t)m << 32 | (uint32_t)~(uint32_t)id;
 }
 
-// Token t's top-k by one whole wave.  The picks are the experts of rank < k,
-// rank = the number of experts with a larger gate, or an equal gate and a
-// smaller id (a larger route_key): the arg-max order taken k times
-// (descending gates, ties to the lower id), found without k dependent rounds
-// of lane shuffles.  PER =
-// experts per lane (E <= 64 * PER).
+// The gate whose route_key has high word m (route_key's map inverted; -0 comes
+// back as +0, which no gate is: a softmax term plus a bias rounds -0 to +0).
+__device__ __forceinline__ float key_gate(uint32_t m) {
+  return __uint_as_float((m >> 31) ? (m & 0x7fffffffu) : ~m);
+}
+
+// A 64-bit value moved by DPP, as two 32-bit moves; lanes the pattern leaves
+// out read 0, below every key.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, true);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf, true);
+  return (uint64_t)hi << 32 | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// The largest key of the wave, the same in every lane: DPP within rows of 16,
+// the row broadcasts into lane 63, then read from it.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+  v = max_u64(v, dpp_u64<0xb1>(v));        // quad_perm [1,0,3,2]
+  v = max_u64(v, dpp_u64<0x4e>(v));        // quad_perm [2,3,0,1]
+  v = max_u64(v, dpp_u64<0x141>(v));       // row_half_mirror
+  v = max_u64(v, dpp_u64<0x140>(v));       // row_mirror
+  v = max_u64(v, dpp_u64<0x142, 0xa>(v));  // row_bcast:15 into rows 1, 3
+  v = max_u64(v, dpp_u64<0x143, 0xc>(v));  // row_bcast:31 into rows 2, 3
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return (uint64_t)hi << 32 | lo;
+}
+
+// Up to this many picks, top-k takes k rounds of the wave arg-max; beyond,
+// each expert's rank is counted against every key (one pass over the LDS).
+constexpr int kArgmaxTopK = 16;
+
+// Token t's top-k by one whole wave: the arg-max order taken k times
+// (descending gates, ties to the lower expert id: the largest route_key
+// first).  Up to kArgmaxTopK picks, k rounds of a wave maximum over the keys,
+// the winning key removed after each; beyond, the picks are the experts of
+// rank < k, rank = the number of larger keys.  PER = experts per lane
+// (E <= 64 * PER).
 template <int PER>
 __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
                                             const float* __restrict__ expert_bias, int64_t t,
@@ -91,14 +127,42 @@ __device__ __forceinline__ void route_token(const uint16_t* __restrict__ logits,
     const int e = lane + 64 * j;
     v[j] = e < E ? v[j] * inv + (expert_bias ? expert_bias[e] : 0.f) : -INFINITY;
   }
-  // ranks against every gate of the token, staged in the wave's LDS as keys
-  const int EP = (E + 1) & ~1;
   uint64_t key[PER];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
+  for (int j = 0; j < PER; ++j)
     key[j] = lane + 64 * j < E ? route_key(v[j], lane + 64 * j) : 0ull;  // 0: below all
-    if (lane + 64 * j < EP) rs.key[lane + 64 * j] = key[j];
+  if (k <= kArgmaxTopK) {
+    // round r's winner goes to lane r; the total adds the picks in rank order
+    float total = 0.f, mine = 0.f;
+    int mine_id = 0;
+    for (int r = 0; r < k; ++r) {
+      uint64_t best = key[0];
+#pragma unroll
+      for (int j = 1; j < PER; ++j) best = max_u64(best, key[j]);
+      const uint64_t m = wave_max_key(best);
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (key[j] == m) key[j] = 0ull;  // keys are distinct (the id is in them)
+      const float g = key_gate((uint32_t)(m >> 32));
+      total += g;
+      if (lane == r) {
+        mine = g;
+        mine_id = (int)~(uint32_t)m;
+      }
+    }
+    if (lane < k) {
+      const float sc = normalize ? mine / (total + 1e-20f) : mine;
+      indices[t * k + lane] = mine_id;
+      if (flat) flat[t * k + lane] = mine_id;
+      scores[t * k + lane] = (uint16_t)f32_to_bf16_bits(sc);
+    }
+    return;
   }
+  // ranks against every gate of the token, staged in the wave's LDS as keys
+  const int EP = (E + 1) & ~1;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (lane + 64 * j < EP) rs.key[lane + 64 * j] = key[j];
   if (lane < kMaxTopK) {
     rs.pick_gate[lane] = -INFINITY;
     rs.pick_id[lane] = 0x7fffffff;
@@ -278,6 +342,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
     int32_t* __restrict__ expert_offsets) {
   __shared__ RouteScratch rs[kSortWaves];
   __shared__ int flat[64];  // the picks, for the one-wave sort
+  __shared__ int bucket_at[64];  // the sorted pairs' buckets
   const int n = T * k;
   for (int t = threadIdx.x >> 6; t < T; t += kSortWaves)
     route_token_any(logits, expert_bias, t, E, k, normalize, indices, scores,
@@ -305,13 +370,20 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
       inverse[i] = pos;
       if (rows) rows[pos] = i / k;
     }
-    // segment starts: the pairs whose bucket is below e
-    if (expert_offsets)
-      for (int e = i; e <= E; e += 64) {
-        int below = 0;
-        for (int j = 0; j < n; ++j) below += (int)((flat[j] >= 0 && flat[j] < E ? flat[j] : E) < e);
-        expert_offsets[e] = below;
+    if (expert_offsets) {
+      // segment starts: expert e's pairs begin at the first sorted position
+      // whose bucket is >= e, so the pair at sorted position p starts the
+      // experts in (bucket[p - 1], bucket[p]], and the experts past the last
+      // pair's bucket start at n
+      if (i < n) bucket_at[pos] = key >> 6;
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's stores are visible
+      if (i < n) {
+        const int b = bucket_at[i], prev = i > 0 ? bucket_at[i - 1] : -1;
+        for (int e = prev + 1; e <= b; ++e) expert_offsets[e] = i;
       }
+      const int last = n > 0 ? bucket_at[n - 1] : -1;
+      for (int e = last + 1 + i; e <= E; e += 64) expert_offsets[e] = n;
+    }
   }
 }
 

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import importlib
 
+import numpy as np
 import pytest
 import torch
 
@@ -58,6 +59,31 @@ def test_route(moe, T, E, k, norm, with_bias):
     assert bool(((sc.float() - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-7).all())
     # descending gate order
     assert bool((ref[:, :-1] >= ref[:, 1:]).all())
+
+
+@pytest.mark.parametrize("T,E,k", [(8, 128, 8), (70, 128, 8), (8, 128, 20), (3, 512, 16),
+                                   (5, 300, 17), (1, 64, 64), (2, 4, 4)])
+def test_route_ties_go_to_the_lower_id(moe, T, E, k):
+    """Logits from six values (many equal gates): the picks in the order of
+    (descending logit, ascending id) exactly -- the softmax keeps the logits'
+    order, equal logits give equal gates -- by moe.route and by the fused
+    route_sort (up to 64 tokens one launch), with k rounds of arg-max (k <= 16)
+    and with counted ranks (k > 16)."""
+    g = torch.Generator().manual_seed(T * E + k)
+    lv = torch.randint(0, 6, (T, E), generator=g).float() * 0.5
+    logits = lv.to(torch.bfloat16).to(DEV)
+    ids = torch.arange(E).expand(T, E)
+    ref = torch.from_numpy(np.lexsort((ids.numpy(), -lv.numpy()), axis=-1)[:, :k].copy())
+    idx, sc = moe.route(logits, k, True)
+    assert torch.equal(idx.cpu().long(), ref)
+    got = moe.route_sort(logits, k, E, True, with_offsets=True)
+    assert torch.equal(got[0].cpu().long(), ref) and torch.equal(got[1], sc)
+    gates = torch.softmax(lv, -1).gather(-1, ref)
+    gates = gates / (gates.sum(-1, keepdim=True) + 1e-20)
+    assert bool(((sc.cpu().float() - gates).abs() <= gates * 2.0 ** -7 + 1e-7).all())
+    flat = ref.reshape(-1)
+    offs = got[6].cpu().long()
+    assert torch.equal(offs, torch.searchsorted(torch.sort(flat).values, torch.arange(E + 1)))
 
 
 @pytest.mark.parametrize("T,k,E", [(8, 8, 128), (4096, 8, 128), (77, 3, 17), (1, 1, 1),
