@@ -65,12 +65,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
   __shared__ float red[kThreads / 64];
   const int64_t row = blockIdx.x;
   const int units = dim / 8;
-  u32x4_t hv[kNormMaxUnits];
+  u32x4_t hv[kNormMaxUnits], wv[kNormMaxUnits];
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < kNormMaxUnits; ++k) {
     const int u = threadIdx.x + k * kThreads;
     if (u < units) {
+      // the weights now, not after the reduction's barrier: one memory round
+      // trip less on the kernel's critical path
+      wv[k] = reinterpret_cast<const u32x4_t*>(w)[u];
       u32x4_t v = reinterpret_cast<const u32x4_t*>(x + row * dim)[u];
       if (res_in) {
         const u32x4_t r = reinterpret_cast<const u32x4_t*>(res_in + row * dim)[u];
@@ -99,12 +102,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
   for (int k = 0; k < kNormMaxUnits; ++k) {
     const int u = threadIdx.x + k * kThreads;
     if (u < units) {
-      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(w)[u];
       u32x4_t o;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        o[q] = pack_bf16x2(lo_bf16(hv[k][q]) * inv * lo_bf16(wv[q]),
-                           hi_bf16(hv[k][q]) * inv * hi_bf16(wv[q]));
+        o[q] = pack_bf16x2(lo_bf16(hv[k][q]) * inv * lo_bf16(wv[k][q]),
+                           hi_bf16(hv[k][q]) * inv * hi_bf16(wv[k][q]));
       reinterpret_cast<u32x4_t*>(out + row * dim)[u] = o;
     }
   }

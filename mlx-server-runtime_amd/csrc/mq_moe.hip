@@ -388,6 +388,42 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
 }
 
 // ---------------------------------------------------------------- combine
+// acc[0..8) += bf16(y[row_j][8u .. 8u+8) * score_j) over token t's k slots j
+// in slot order, row_j = inverse[t*k + j] (or t*k + j), clamped to y's rows.
+// The slots go 8 at a time: their rows and scores are loaded, then their y
+// units, before any is added, so a group costs two memory round trips, not
+// two per slot (slots past k reload slot k - 1 and are not added).
+__device__ __forceinline__ void combine_unit(const uint16_t* __restrict__ y,
+                                             const int32_t* __restrict__ inverse,
+                                             const uint16_t* __restrict__ scores, int64_t t, int k,
+                                             int H, int64_t y_rows, int u, float* acc) {
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    int64_t r[8];
+    float sc[8];
+    u32x4_t v[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int j = min(j0 + jj, k - 1);
+      int64_t rr = t * k + j;
+      if (inverse) rr = inverse[rr];
+      r[jj] = rr < 0 ? 0 : (rr >= y_rows ? y_rows - 1 : rr);
+      sc[jj] = bf16_bits_to_f32(scores[t * k + j]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) v[jj] = reinterpret_cast<const u32x4_t*>(y + r[jj] * H)[u];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (j0 + jj < k) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += bf16_bits_to_f32(f32_to_bf16_bits(lo_bf16(v[jj][q]) * sc[jj]));
+          acc[2 * q + 1] += bf16_bits_to_f32(f32_to_bf16_bits(hi_bf16(v[jj][q]) * sc[jj]));
+        }
+      }
+    }
+  }
+}
+
 // Grid (T, ceil(H / (8 * 256))), 256 threads, 8 elements per thread.
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ inverse,
@@ -397,18 +433,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   const int u = blockIdx.y * 256 + threadIdx.x;  // 8-element unit of the row
   if (u >= H / 8) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    int64_t r = t * k + j;
-    if (inverse) r = inverse[r];
-    r = r < 0 ? 0 : (r >= y_rows ? y_rows - 1 : r);
-    const float sc = bf16_bits_to_f32(scores[t * k + j]);
-    const u32x4_t v = reinterpret_cast<const u32x4_t*>(y + r * H)[u];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      acc[2 * q] += bf16_bits_to_f32(f32_to_bf16_bits(lo_bf16(v[q]) * sc));
-      acc[2 * q + 1] += bf16_bits_to_f32(f32_to_bf16_bits(hi_bf16(v[q]) * sc));
-    }
-  }
+  combine_unit(y, inverse, scores, t, k, H, y_rows, u, acc);
   u32x4_t o;
 #pragma unroll
   for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
@@ -432,26 +457,25 @@ __global__ __launch_bounds__(kNormThreads) void moe_combine_norm_kernel(
   __shared__ float red[kNormThreads / 64];
   const int64_t t = blockIdx.x;
   const int units = H / 8;
-  u32x4_t hv[kNormUnits];
+  u32x4_t hv[kNormUnits], rvs[kNormUnits], wvs[kNormUnits];
+  // the residual and the norm weights first: their loads overlap the expert
+  // rows' instead of following them (and the reduction's barrier)
+#pragma unroll
+  for (int pass = 0; pass < kNormUnits; ++pass) {
+    const int u = threadIdx.x + pass * kNormThreads;
+    if (u < units) {
+      rvs[pass] = reinterpret_cast<const u32x4_t*>(residual + t * H)[u];
+      wvs[pass] = reinterpret_cast<const u32x4_t*>(w)[u];
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int pass = 0; pass < kNormUnits; ++pass) {
     const int u = threadIdx.x + pass * kNormThreads;
     if (u < units) {
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int j = 0; j < k; ++j) {
-        int64_t r = t * k + j;
-        if (inverse) r = inverse[r];
-        r = r < 0 ? 0 : (r >= y_rows ? y_rows - 1 : r);
-        const float sc = bf16_bits_to_f32(scores[t * k + j]);
-        const u32x4_t v = reinterpret_cast<const u32x4_t*>(y + r * H)[u];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc[2 * q] += bf16_bits_to_f32(f32_to_bf16_bits(lo_bf16(v[q]) * sc));
-          acc[2 * q + 1] += bf16_bits_to_f32(f32_to_bf16_bits(hi_bf16(v[q]) * sc));
-        }
-      }
-      const u32x4_t rv = reinterpret_cast<const u32x4_t*>(residual + t * H)[u];
+      combine_unit(y, inverse, scores, t, k, H, y_rows, u, acc);
+      const u32x4_t rv = rvs[pass];
       u32x4_t h;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -480,7 +504,7 @@ __global__ __launch_bounds__(kNormThreads) void moe_combine_norm_kernel(
   for (int pass = 0; pass < kNormUnits; ++pass) {
     const int u = threadIdx.x + pass * kNormThreads;
     if (u < units) {
-      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(w)[u];
+      const u32x4_t wv = wvs[pass];
       u32x4_t o;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
