@@ -543,13 +543,14 @@ def test_gather_moe_shape_prefill_sampled(mq, orc, bits):
 @pytest.mark.parametrize("K,Mb", [(768, 1), (1024, 1), (768, 3)])
 def test_gather_sorted_expert_segments(mq, orc, bits, K, Mb):
     """The expert-segment GEMM behind sorted gather_qmm: segments of 0, 1, 255,
-    256, 257 and 700 batches (whole and partial 256-row tiles, empty experts),
+    256, 257, 288, 289 and 700 batches (whole and partial 256-row tiles, empty
+    experts),
     ids below 0 first and at or above E last (their rows are zero), x batches
     gathered through lhs (one of them out of range: zero rows), K of 12 groups
     (a partial scale chunk) and 16, and Mb rows per batch."""
     rng = np.random.default_rng(5 + K + Mb + bits)
-    E, N = 12, 320
-    sizes = [256, 0, 1, 700, 255, 0, 257, 37, 3, 0, 90, 256]
+    sizes = [256, 0, 1, 700, 255, 0, 257, 37, 3, 0, 90, 256, 288, 289]
+    E, N = len(sizes), 320
     rhs = np.concatenate([np.full(3, -1)] + [np.full(n, e) for e, n in enumerate(sizes)]
                          + [np.full(4, E)]).astype(np.int32)
     T = rhs.shape[0]
