@@ -450,12 +450,32 @@ __global__ __launch_bounds__(256) void splitk_reduce_add_norm(
     }
   }
   float ss = 0.f;
+  // Rows of at most 512 units (N <= 4096): the partial sums of both of a
+  // thread's units are requested before the first add (one round trip); a
+  // thread without a second unit reads its first unit's twice.
+  float acc2[2][8] = {};
+  const bool two = units <= 512;
+  if (two) {
+    const int u1 = threadIdx.x + 256 < units ? 256 * 8 : 0;
+    float acc16[16] = {};
+    add_splits<16, 8>(partial + m * N + threadIdx.x * 8, S, MN,
+                      {0, 1, 2, 3, 4, 5, 6, 7, u1, u1 + 1, u1 + 2, u1 + 3, u1 + 4, u1 + 5, u1 + 6,
+                       u1 + 7},
+                      acc16);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc2[0][e] = acc16[e], acc2[1][e] = acc16[8 + e];
+  }
 #pragma unroll
   for (int k = 0; k < kUnits; ++k) {
     const int u = threadIdx.x + k * 256;
     if (u < units) {
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      add_splits<8, 16>(partial + m * N + u * 8, S, MN, {0, 1, 2, 3, 4, 5, 6, 7}, acc);
+      if (two && k < 2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = acc2[k][e];
+      } else {
+        add_splits<8, 16>(partial + m * N + u * 8, S, MN, {0, 1, 2, 3, 4, 5, 6, 7}, acc);
+      }
       if (bias) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -715,10 +735,7 @@ hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                      ? run_mi<4, true>(x, wq, scales, biases, bias, y, part, M, N, K, p, stream)
                      : run_mi<8, true>(x, wq, scales, biases, bias, y, part, M, N, K, p, stream);
   if (e != hipSuccess) return e;
-  const int64_t MN = M * N;
-  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream, part,
-                     p.splits, bias, y, MN, (int)N);
-  return hipGetLastError();
+  return launch_splitk_reduce(part, p.splits, bias, y, M * N, N, stream);
 }
 
 }  // namespace mq
