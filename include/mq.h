@@ -58,7 +58,8 @@ typedef uint16_t mq_bf16; /* raw bfloat16 bits */
 #define MQ_ERR_UNSUPPORTED (-2) /* valid for MLX, not implemented here */
 #define MQ_ERR_HIP (-3)         /* the HIP runtime refused a launch */
 
-/* (major << 16) | minor */
+/* (major << 16) | minor.  2.0: mq_moe_sort and mq_moe_route_sort take an
+ * expert_offsets output before the stream argument (1.0 had none). */
 int mq_version(void);
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -148,8 +149,12 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
  * mq_quantized_matmul_ws without a workspace argument and without any
  * allocation: the split-K partial sums (and, at 2/3/5/6 bits, the codes
  * repacked one byte each) live in a device array of this library
- * (MQ_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; resolved
- * once per device on its first call there).  No counterpart in the reference:
+ * (MQ_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends).  Its
+ * device address is looked up (hipGetSymbolAddress) by the first call with
+ * work on a device and kept once the lookup succeeds (a failed lookup returns
+ * MQ_ERR_HIP and the next call retries); code that captures this entry point
+ * in a HIP graph makes one eager call on the device first, so that the
+ * lookup never happens during capture.  No counterpart in the reference:
  * it is for callers that cannot allocate (code under HIP graph capture,
  * serving loops that forbid hipMalloc).  Same arguments, kernels, split plan
  * and results bit for bit as mq_quantized_matmul_ws with
@@ -210,6 +215,15 @@ int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
                            mq_bf16* y, int64_t T, int64_t M, int64_t N, int64_t K, int64_t E,
                            int64_t x_batches, int group_size, int bits, int swiglu,
                            hipStream_t stream);
+
+/* 1 if mq_gather_qmm_segments takes these sizes (with swiglu, N is the
+ * output width: every expert's matrix is 2N rows), else 0.  Without swiglu
+ * every valid shape is taken (beyond the segment GEMM it runs as
+ * mq_gather_qmm); with swiglu, the segment GEMM's shapes and the decode-sized
+ * ones mq_gather_qmm_swiglu takes.  Host-only; no counterpart in the
+ * reference. */
+int mq_gather_qmm_segments_supported(int64_t T, int64_t M, int64_t N, int64_t K, int64_t E,
+                                     int64_t x_batches, int group_size, int bits, int swiglu);
 
 /*
  * SwitchGLU's gate and up projections and silu(gate) * up for gathered

@@ -54,6 +54,7 @@ EXPORTS = (
     "mq_gather_qmm_swiglu",
     "mq_quantized_matmul_noalloc",
     "mq_gather_qmm_segments",
+    "mq_gather_qmm_segments_supported",
     "mq_hbm_read",          # include/mq_measure.h
 )
 
@@ -121,6 +122,8 @@ def _declare(L: ctypes.CDLL) -> None:
                                               _int, _int, _p]
     L.mq_gather_qmm_segments.argtypes = [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
                                          _i64, _i64, _int, _int, _int, _p]
+    L.mq_gather_qmm_segments_supported.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64, _int,
+                                                   _int, _int]
     L.mq_hbm_read.argtypes = [_p, ctypes.c_size_t, _p, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int

@@ -423,6 +423,14 @@ def gather_swiglu_supported(T: int, M: int, N: int, K: int, group_size: int = 64
     return bool(_lib.lib().mq_gather_qmm_swiglu_supported(T, M, N, K, group_size, bits))
 
 
+def gather_segments_supported(T: int, M: int, N: int, K: int, E: int, x_batches: int,
+                              group_size: int = 64, bits: int = 4, swiglu: bool = False) -> bool:
+    """Whether gather_qmm / gather_qmm_swiglu with expert_offsets take these sizes
+    (swiglu: N is the output width of a 2N-row gate|up bank)."""
+    return bool(_lib.lib().mq_gather_qmm_segments_supported(T, M, N, K, E, x_batches, group_size,
+                                                            bits, int(bool(swiglu))))
+
+
 def gather_qmm_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                       biases: torch.Tensor, lhs_indices: torch.Tensor | None,
                       rhs_indices: torch.Tensor, group_size: int = 64,

@@ -117,7 +117,7 @@ bool use_skinny(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
 
 extern "C" {
 
-int mq_version(void) { return (1 << 16) | 0; }
+int mq_version(void) { return (2 << 16) | 0; }
 
 const char* mq_last_error(void) { return g_err; }
 
@@ -586,6 +586,21 @@ int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
                                            scales, biases, y, T, M, N, K, E, x_batches, bits,
                                            swiglu != 0, stream),
                     op);
+}
+
+int mq_gather_qmm_segments_supported(int64_t T, int64_t M, int64_t N, int64_t K, int64_t E,
+                                     int64_t x_batches, int group_size, int bits, int swiglu) {
+  if (bits != 2 && bits != 3 && bits != 4 && bits != 5 && bits != 6 && bits != 8) return 0;
+  if (group_size != 32 && group_size != 64 && group_size != 128) return 0;
+  if (T < 0 || M < 0 || N < 0 || K < 1 || E < 1 || x_batches < 0 || K % group_size) return 0;
+  if (T >= kMaxDim || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim || E >= kMaxDim ||
+      x_batches >= kMaxDim || T * M >= kMaxDim)
+    return 0;
+  if (!swiglu) return bits == 4 || bits == 8;
+  if (bits != 4 && bits != 8) return 0;
+  if (T * M > 64 && group_size == 64 && mq::qmm4_gather_fits(T, M, 2 * N, K, E, x_batches, bits))
+    return 1;
+  return mq_gather_qmm_swiglu_supported(T, M, N, K, group_size, bits);
 }
 
 int mq_gather_qmm_swiglu_supported(int64_t T, int64_t M, int64_t N, int64_t K, int group_size,

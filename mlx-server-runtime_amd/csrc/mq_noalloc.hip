@@ -5,10 +5,14 @@
 //
 // The array `scratch` below is a device global: every GPU the library runs on
 // holds its own copy (kScratchBytes) until the process ends.  Host code never
-// passes `scratch` itself (its host-side name is not a device address): the
-// first call on a device resolves that device's copy with
-// hipGetSymbolAddress, once, with the device current, and every later call
-// uses the resolved pointer.  Calls on one GPU share its copy, so calls that
+// passes `scratch` itself (its host-side name is not a device address): a
+// call with work to do on a device first resolves that device's copy with
+// hipGetSymbolAddress, with the device current, and keeps the pointer once
+// the lookup has succeeded (a failed lookup is returned and retried by the
+// next call); every later call uses the resolved pointer.  The lookup is a
+// runtime query, not stream work: callers that capture this entry point in a
+// HIP graph make one eager call on the device first, so that no lookup
+// happens during capture.  Calls on one GPU share its copy, so calls that
 // overlap on one GPU (different streams, no ordering between them) race;
 // calls ordered on one stream do not.  Nothing in the array needs clearing:
 // each split writes all of its partial sums before the reduce reads them.
@@ -24,27 +28,30 @@ constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-std::once_flag g_once[kMaxDevices];
-void* g_scratch[kMaxDevices];
-hipError_t g_status[kMaxDevices];
+std::mutex g_mu[kMaxDevices];
+void* g_scratch[kMaxDevices];  // non-null once resolved on that device
 
-// Device address of `scratch` on device `dev` (resolved once per device).
+// Device address of `scratch` on device `dev`: resolved on the first call
+// that succeeds, then reused.
 hipError_t scratch_on(int dev, void** out) {
-  std::call_once(g_once[dev], [dev] {
-    int cur = -1;
-    hipError_t e = hipGetDevice(&cur);
-    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
-    void* p = nullptr;
-    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (cur >= 0 && cur != dev) {
-      const hipError_t r = hipSetDevice(cur);
-      if (e == hipSuccess) e = r;
-    }
-    g_scratch[dev] = p;
-    g_status[dev] = e;
-  });
-  *out = g_scratch[dev];
-  return g_status[dev];
+  std::lock_guard<std::mutex> lock(g_mu[dev]);
+  if (g_scratch[dev]) {
+    *out = g_scratch[dev];
+    return hipSuccess;
+  }
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+  void* p = nullptr;
+  if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (cur >= 0 && cur != dev) {
+    const hipError_t r = hipSetDevice(cur);
+    if (e == hipSuccess) e = r;
+  }
+  if (e == hipSuccess && !p) e = hipErrorInvalidSymbol;
+  if (e == hipSuccess) g_scratch[dev] = p;
+  *out = p;
+  return e;
 }
 
 }  // namespace
@@ -68,7 +75,9 @@ extern "C" int mq_quantized_matmul_noalloc(const mq_bf16* x, const uint32_t* wq,
     return mq::set_last_error(MQ_ERR_INVALID, msg);
   }
   void* ws = nullptr;
-  if (need > 0) {
+  // Resolved whenever the call has work, even where this plan needs no
+  // scratch, so that one eager call of any size settles the lookup.
+  if (M > 0 && N > 0 && K > 0) {
     int dev = -1;
     hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
     if (e == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e = hipErrorInvalidDevice;
@@ -81,5 +90,5 @@ extern "C" int mq_quantized_matmul_noalloc(const mq_bf16* x, const uint32_t* wq,
     }
   }
   return mq_quantized_matmul_ws(x, wq, scales, biases, bias_vec, y, M, N, K, group_size, bits,
-                                transpose, ws, need, stream);
+                                transpose, need > 0 ? ws : nullptr, need, stream);
 }

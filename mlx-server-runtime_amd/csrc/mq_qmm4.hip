@@ -163,7 +163,10 @@ __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
   int* misc = pre + a.E + 1;    // [10]: lo, wave totals, the tile's expert
   const int tid = threadIdx.x;
   if (a.seg) {
-    for (int e = tid; e <= a.E; e += kThreads) start[e] = a.seg[e];
+    // Caller-supplied starts are clamped to [0, T], so every row and x batch
+    // a tile touches stays inside y and lhs; a start below its predecessor
+    // gives the predecessor an empty segment (rows = max(0, ...) below).
+    for (int e = tid; e <= a.E; e += kThreads) start[e] = min(max(a.seg[e], 0), a.T);
   } else {
     // start[e] = the first batch whose id is >= e: one coalesced pass over the
     // sorted ids, each boundary (ids u < v at batches p - 1, p) giving

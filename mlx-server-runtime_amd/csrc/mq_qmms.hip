@@ -452,9 +452,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_add_norm(
   float ss = 0.f;
   // Rows of at most 512 units (N <= 4096): the partial sums of both of a
   // thread's units are requested before the first add (one round trip); a
-  // thread without a second unit reads its first unit's twice.
+  // thread without a second unit reads its first unit's twice.  Threads past
+  // the row's units (N < 2048) read nothing: their first unit would lie past
+  // the row, and past the workspace on the last row of the last split.
   float acc2[2][8] = {};
-  const bool two = units <= 512;
+  const bool two = units <= 512 && (int)threadIdx.x < units;
   if (two) {
     const int u1 = threadIdx.x + 256 < units ? 256 * 8 : 0;
     float acc16[16] = {};

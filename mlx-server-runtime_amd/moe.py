@@ -27,6 +27,8 @@ sequence bit for bit.  There is no CPU fallback.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib, core
@@ -170,9 +172,12 @@ class QExperts:
         gather_qmm then silu_mul -- the same bits either way."""
         T, M, K = rhs.numel(), x.shape[-2], x.shape[-1]
         N = self.wq.shape[1] // 2
-        if offsets is not None and sorted_indices and T * M > 64 and self.group_size == 64:
-            # the expert-segment GEMM with SiLU * up in its epilogue (it reads one
-            # scale per 64-wide k step: group size 64 only)
+        n_x = math.prod(x.shape[:-2]) if x.ndim > 2 else 1
+        if (offsets is not None and sorted_indices and T * M > 64
+                and core.gather_segments_supported(T, M, N, K, self.num_experts, n_x,
+                                                   self.group_size, self.bits, swiglu=True)):
+            # the expert-segment GEMM with SiLU * up in its epilogue (where it
+            # takes the shape: group size 64, an even number of groups per row)
             return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
                                           self.group_size, self.bits, expert_offsets=offsets)
         if core.gather_swiglu_supported(T, M, N, K, self.group_size, self.bits):
@@ -189,6 +194,10 @@ class MoEBlock:
                  norm_topk_prob: bool = True, expert_bias: torch.Tensor | None = None):
         self.gate, self.gate_up, self.down = gate, gate_up, down
         self.top_k, self.norm_topk_prob, self.expert_bias = top_k, norm_topk_prob, expert_bias
+        # A list here receives a copy of every call's routed expert ids
+        # (int32 [T, k], token order): the routing trace, for eager calls
+        # only (a captured graph's replays do not append).
+        self.routing_log: list | None = None
 
     @property
     def num_experts(self) -> int:
@@ -204,7 +213,7 @@ class MoEBlock:
             # (<= 64 pairs) run per-pair GEMVs that do not read them
             sort = route_sort(logits, self.top_k, self.num_experts, self.norm_topk_prob,
                               self.expert_bias, with_offsets=T * self.top_k > 64)
-            _, sc, sorted_ids, _, inverse, rows = sort[:6]
+            idx, sc, sorted_ids, _, inverse, rows = sort[:6]
             offs = sort[6] if len(sort) > 6 else None
             act = self.gate_up.swiglu(xb, rows, sorted_ids, sorted_indices=True, offsets=offs)
             y = self.down(act, rhs=sorted_ids, sorted_indices=True, offsets=offs)
@@ -216,6 +225,8 @@ class MoEBlock:
             flat = idx.reshape(-1)
             act = self.gate_up.swiglu(xb, rows, flat)
             y = self.down(act, rhs=flat)
+        if self.routing_log is not None:
+            self.routing_log.append(idx.clone())
         return y.reshape(T * self.top_k, H), inverse, sc
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:

@@ -97,18 +97,22 @@ def moe_reference(mq, block, x, r=lambda t: t, indices=None):
 
 
 def reference_logits(mq, model, tokens: torch.Tensor, bf16_activations: bool = False,
-                     head_from: int = 0) -> torch.Tensor:
+                     head_from: int = 0, routing: dict | None = None) -> torch.Tensor:
     """tokens [B, S] (positions 0..S-1) -> float32 logits [B, S - head_from, vocab]
     of positions head_from..S-1, causal (the LM head on reference_hidden)."""
-    h = reference_hidden(mq, model, tokens, bf16_activations, head_from)
+    h = reference_hidden(mq, model, tokens, bf16_activations, head_from, routing)
     head = model.lm_head if model.lm_head is not None else model.embed
     return h @ _deq(mq, head).t()
 
 
 def reference_hidden(mq, model, tokens: torch.Tensor, bf16_activations: bool = False,
-                     head_from: int = 0) -> torch.Tensor:
+                     head_from: int = 0, routing: dict | None = None) -> torch.Tensor:
     """tokens [B, S] -> float32 final-normed hidden states [B, S - head_from, hidden]
     of positions head_from..S-1 (the LM head's input), causal.
+
+    routing {layer index: int [B, S, k]} teacher-forces the MoE layers'
+    expert choice (moe_reference's indices) to the model's own: the gates are
+    still computed here, so only the discrete choice is taken over.
 
     With bf16_activations, values are rounded to bfloat16 wherever the model
     under test -- and the reference's MLX graph -- stores bfloat16 (norm
@@ -127,7 +131,7 @@ def reference_hidden(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
                                 e.group_size, e.bits).float().reshape(B, S, c.hidden_size)
     else:
         h = e.weight.float()[tokens.reshape(-1).long()].reshape(B, S, c.hidden_size)
-    for layer in model.layers:
+    for li, layer in enumerate(model.layers):
         x = r(_rms(h, layer.input_norm, c.rms_norm_eps))
         qkv = r(_linear(mq, layer.qkv, x))
         q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
@@ -145,7 +149,8 @@ def reference_hidden(mq, model, tokens: torch.Tensor, bf16_activations: bool = F
         h = r(h + r(_linear(mq, layer.o, a)))
         x = r(_rms(h, layer.post_norm, c.rms_norm_eps))
         if layer.moe is not None:
-            h = r(h + r(moe_reference(mq, layer.moe, x, r)))
+            idx = None if routing is None else routing[li].reshape(B * S, -1)
+            h = r(h + r(moe_reference(mq, layer.moe, x, r, indices=idx)))
             continue
         gu = r(_linear(mq, layer.gate_up, x))
         act = r(r(F.silu(gu[..., :c.intermediate_size])) * gu[..., c.intermediate_size:])
@@ -167,3 +172,34 @@ def greedy_agreement(ref_logits: torch.Tensor, prompt_len: int, tokens: torch.Te
     margin = (lg.max(-1).values - chosen) / lg.std(-1)
     worst = float(margin[~match].max()) if (~match).any() else 0.0
     return int(match.sum()), B * n, worst
+
+
+class RoutingTrace:
+    """Records the expert ids every MoE layer of a model routes to, in eager
+    calls, and assembles them per layer as [B, S, k] over the positions of a
+    generate() call (its prompt prefill, then one position per decode step)
+    or of a single prefill: the routing= argument of reference_logits."""
+
+    def __init__(self, model):
+        self.layers = [i for i, l in enumerate(model.layers) if l.moe is not None]
+        self.model = model
+        self.logs = {i: [] for i in self.layers}
+
+    def __enter__(self):
+        for i in self.layers:
+            self.model.layers[i].moe.routing_log = self.logs[i]
+        return self
+
+    def __exit__(self, *exc):
+        for i in self.layers:
+            self.model.layers[i].moe.routing_log = None
+
+    def per_layer(self, B: int) -> dict:
+        """{layer: int [B, S, k]}: the calls' ids in call order, each call's
+        rows being B sequences of equal length."""
+        out = {}
+        for i in self.layers:
+            parts = [t.reshape(B, -1, t.shape[-1]) for t in self.logs[i]]
+            out[i] = torch.cat(parts, 1)
+        return out
+

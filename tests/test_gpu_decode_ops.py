@@ -178,7 +178,10 @@ def test_rms_norm_quantized_matmul_small_matrix_with_bias(ops):
 @pytest.mark.parametrize("M,N,K,bits,with_bias", [
     (32, 3584, 18944, 4, False), (32, 3584, 3584, 4, True), (32, 4096, 4096, 8, False),
     (27, 3584, 18944, 4, True), (16, 3584, 18944, 8, False), (16, 3584, 3584, 8, True),
-    (128, 3584, 18944, 4, False), (128, 3584, 18944, 8, True)])
+    (128, 3584, 18944, 4, False), (128, 3584, 18944, 8, True),
+    # rows of fewer than 256 8-element units (N < 2048): Qwen3-0.6B's o and
+    # down projections at decode batch sizes
+    (32, 1024, 3072, 4, False), (16, 1024, 2048, 4, True), (32, 1024, 2048, 8, False)])
 def test_quantized_matmul_add_rms_norm_equals_two_kernels(ops, M, N, K, bits, with_bias):
     """The skinny GEMM whose split-K reduce adds the residual and applies the
     RMSNorm: bit-equal to quantized_matmul (its workspace, the same split plan)

@@ -241,3 +241,54 @@ def test_continuous_batching_7b_widths_shared_prefix():
           f"{match}/{total}, worst margin {worst:.3f} std")
     assert e.max() <= 2 * e16.max() + 1e-2, (float(e.max()), float(e16.max()))
     assert match >= 0.9 * total and worst <= 0.1, (match, total, worst)
+
+
+@pytest.mark.timeout(900)
+def test_continuous_batching_7b_full_depth():
+    """The continuous-batching workload at full depth, as the bench decodes it:
+    the Qwen2.5-7B shape (28 layers), 32 sequences with 1024-token prompts whose
+    first 256 tokens are shared pages, page size 16, then 8 greedy decode steps.
+
+    Checked: graph replay equals eager decode; every decode step's logits and
+    the model's own prefill logits over the same tokens (one private prefill
+    of prompt + generated tokens) within 2 * e16 + 1e-2 of the float32
+    restatement (e16: the distance between the float32 restatement and one
+    that rounds to bfloat16 wherever the model stores bfloat16), so decode and
+    prefill agree within twice that; teacher-forced greedy tokens differ from
+    the restatement's argmax only where its top-2 margin is within twice the
+    bfloat16-storage error."""
+    mq = importlib.import_module("mlx-server-runtime_amd")
+    q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
+    cfg = q2.Qwen2Config.qwen25_7b()
+    assert cfg.num_hidden_layers == 28
+    m = q2.Qwen2Model.random(cfg, seed=0, device=DEV)
+    B, T, P, n = 32, 1024, 256, 8
+    print("config 4 full depth: 28 layers, batch 32, 1024-token prompts (256 shared), 8 steps",
+          flush=True)
+    prompt = torch.randint(0, cfg.vocab_size, (B, T),
+                           generator=torch.Generator(device=DEV).manual_seed(2), device=DEV)
+    prompt[:, :P] = prompt[0, :P]
+    steps = []
+    toks = m.generate(prompt, n, prefix_len=P, use_graph=False, logits_out=steps)
+    assert torch.equal(toks, m.generate(prompt, n, prefix_len=P))
+    full = torch.cat([prompt, toks], 1)[:, :-1]
+    dec = torch.stack(steps, 1)
+    r32 = reference_logits(mq, m, full, head_from=T - 1)
+    r16 = reference_logits(mq, m, full, bf16_activations=True, head_from=T - 1)
+    e = _per_position(dec, r32)
+    e16 = _per_position(r16, r32)
+    bound = 2 * e16.max() + 1e-2
+    ours = m.prefill(full, m.new_cache(B, full.shape[1]), all_positions=True)[:, T - 1:]
+    e_pre = _per_position(ours, r32)
+    e_dec = _per_position(dec, ours)
+    eps16 = (r16 - r32).abs().amax(-1)
+    top2 = r32.topk(2, -1).values
+    margin = top2[..., 0] - top2[..., 1]
+    differ = r32.argmax(-1) != toks
+    print(f"config-4 shape (28 layers): decode err max {e.max():.4f}, prefill err max "
+          f"{e_pre.max():.4f}, decode vs own prefill max {e_dec.max():.4f}; bf16-storage "
+          f"err max {e16.max():.4f}; {int(differ.sum())}/{differ.numel()} tokens differ from "
+          f"the restatement's argmax", flush=True)
+    assert e.max() <= bound and e_pre.max() <= bound, (float(e.max()), float(e_pre.max()))
+    assert e_dec.max() <= 2 * bound, float(e_dec.max())
+    assert bool((margin[differ] <= 2 * eps16[differ]).all()), (margin / eps16)[differ]

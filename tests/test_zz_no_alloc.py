@@ -84,3 +84,52 @@ def test_noalloc_refuses_beyond_the_array():
     rc = L.mq_quantized_matmul_noalloc(None, None, None, None, None, None, M, N, K, 64, 4, 1, None)
     assert rc == mq._lib.MQ_ERR_INVALID
     assert b"use mq_quantized_matmul_ws" in L.mq_last_error()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_noalloc_graph_replay_equals_eager(bits):
+    """The entry point's stated use: captured in a HIP graph (after one eager
+    call on the device, which resolves the array's address) and replayed
+    four times, with eager calls of other shapes -- which overwrite the
+    shared array -- and synchronisations between the replays; every replay is
+    bit-equal to the workspace entry's output.  M = 32, 3584 -> 18944 splits K
+    (partial sums in the array, then the fixed-order reduce)."""
+    mq, L = _lib()
+    core = importlib.import_module("mlx-server-runtime_amd.core")
+    M, N, K = 32, 3584, 18944
+    print(f"noalloc graph bits={bits}: M={M}, N={N}, K={K}", flush=True)
+    assert 0 < L.mq_quantized_matmul_workspace(M, N, K, 64, bits) <= SCRATCH_BYTES
+    g = torch.Generator(device=DEV).manual_seed(11 + bits)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = core.quantize(w, 64, bits)
+    x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    need = L.mq_quantized_matmul_workspace(M, N, K, 64, bits)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    ref = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    mq._lib.check(L.mq_quantized_matmul_ws(_ptr(x), _ptr(wq), _ptr(sc), _ptr(bi), None, _ptr(ref),
+                                           M, N, K, 64, bits, 1, _ptr(ws), ctypes.c_size_t(need),
+                                           cur), "ws")
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    # the eager call that resolves the array before any capture
+    mq._lib.check(L.mq_quantized_matmul_noalloc(_ptr(x), _ptr(wq), _ptr(sc), _ptr(bi), None,
+                                                _ptr(out), M, N, K, 64, bits, 1, cur), "eager")
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            rc = L.mq_quantized_matmul_noalloc(_ptr(x), _ptr(wq), _ptr(sc), _ptr(bi), None,
+                                               _ptr(out), M, N, K, 64, bits, 1, s)
+    torch.cuda.current_stream().wait_stream(side)
+    assert rc == 0, L.mq_last_error()
+    for i in range(4):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}"
+        # an eager call of another plan between replays: it rewrites the array
+        _case(mq, L, 16, 4608, 3584, bits, seed=20 + i, bias=True)
