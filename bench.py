@@ -69,10 +69,92 @@ def parse():
                     help="eager launches of quantized_matmul at one shape (rocprofv3 runs)")
     ap.add_argument("--profile-gather", action="store_true",
                     help="eager launches of the MoE-prefill expert GEMMs (rocprofv3 runs)")
+    ap.add_argument("--trace-qmv", action="store_true",
+                    help="per-wave timeline of the headline GEMV (mq_qmv_trace): one traced "
+                         "launch after 15 plain ones, in a graph")
     ap.add_argument("--decode-only", type=int, default=None, metavar="BATCH",
                     help="only one decode benchmark: 7B at batch 1 or 32, or the MoE model "
                          "at batch 8 (rocprofv3 runs)")
     return ap.parse_args()
+
+
+def trace_qmv(mq, torch, count: int = 16, replays: int = 20):
+    """Per-wave timeline of the headline GEMV (4-bit, K=3584, N=18944, M=1).
+
+    A HIP graph holds count - 1 plain launches and one traced launch
+    (mq_qmv_trace: the same kernel, with every wave's constant-clock time at
+    entry, after its block's prologue barrier and after its store, and its
+    CU), each on its own weight replica; after `replays` replays the last
+    traced launch is summarised: phase-time percentiles from the first wave's
+    entry, the last wave end on CUs by how many waves they ran, the blocks by
+    dispatch order, waves in flight per 0.25 us, and the part of the per-launch
+    time outside [first entry, last end] (dispatch and completion)."""
+    import ctypes
+
+    import numpy as np
+
+    K, N, bits = 3584, 18944, 4
+    reps = make_replicas(mq, torch, N, K, bits, count, seed=0)
+    x = torch.randn(1, K, generator=torch.Generator(device="cuda:0").manual_seed(1),
+                    device="cuda:0").to(torch.bfloat16)
+    y = torch.empty(count, N, dtype=torch.bfloat16, device="cuda:0")
+    waves = (N + 15) // 16 * 4
+    trace = torch.zeros(waves * 4, dtype=torch.int64, device="cuda:0")
+    L = mq._lib.lib()
+
+    def launch(i):
+        wq, s, b = reps[i % count]
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        if i % count == count - 1:
+            mq._lib.check(L.mq_qmv_trace(x.data_ptr(), wq.data_ptr(), s.data_ptr(), b.data_ptr(),
+                                         y[i % count].data_ptr(), N, K, trace.data_ptr(),
+                                         ctypes.c_size_t(trace.numel()), st), "qmv_trace")
+        else:
+            mq._lib.check(L.mq_quantized_matmul(x.data_ptr(), wq.data_ptr(), s.data_ptr(),
+                                                b.data_ptr(), None, y[i % count].data_ptr(), 1, N,
+                                                K, 64, bits, 1, st), "quantized_matmul")
+
+    ms, _ = time_graph(torch, launch, count, warmup=count, reps=replays)
+    ref = mq.quantized_matmul(x, *reps[count - 1], transpose=True, group_size=64, bits=bits)
+    assert torch.equal(y[count - 1], ref[0]), "traced GEMV differs from quantized_matmul"
+    a = trace.cpu().numpy().reshape(waves, 4).astype(np.int64)
+    t = (a[:, :3] - a[:, 0].min()) * 0.01  # us (10 ns ticks)
+    hw = a[:, 3]
+    cu = (((hw >> 32) & 0xF) * 1000 + ((hw >> 13) & 0x7) * 100 + ((hw >> 12) & 1) * 16
+          + ((hw >> 8) & 0xF))
+    keys, inv, cnt = np.unique(cu, return_inverse=True, return_counts=True)
+    cu_end = np.zeros(len(keys))
+    np.maximum.at(cu_end, inv, t[:, 2])
+    pct = lambda v: [round(float(q), 2) for q in np.percentile(v, [0, 10, 50, 90, 100])]
+    blk = np.arange(waves) // 4
+    nb = waves // 4
+    by_order = []
+    for lo in range(0, nb, 256):
+        m = (blk >= lo) & (blk < min(nb, lo + 256))
+        by_order.append({"blocks": [lo, int(min(nb, lo + 256)) - 1],
+                         "entry_median_us": round(float(np.median(t[m, 0])), 2),
+                         "prologue_median_us": round(float(np.median(t[m, 1])), 2),
+                         "end_median_us": round(float(np.median(t[m, 2])), 2),
+                         "end_max_us": round(float(t[m, 2].max()), 2)})
+    grid = np.arange(0.0, float(t[:, 2].max()) + 0.25, 0.25)
+    span = float(t[:, 2].max())
+    return {
+        "shape": {"M": 1, "K": K, "N": N, "bits": bits, "blocks": nb, "waves": waves,
+                  "cus": int(len(keys))},
+        "us_per_launch": round(ms * 1e3, 3),
+        "span_first_entry_to_last_end_us": round(span, 3),
+        "outside_waves_us": round(ms * 1e3 - span, 3),
+        "percentiles_us_0_10_50_90_100": {"entry": pct(t[:, 0]), "prologue_done": pct(t[:, 1]),
+                                          "end": pct(t[:, 2]), "wave_duration": pct(t[:, 2] - t[:, 0])},
+        "cu_last_end_by_waves_per_cu": {
+            str(int(c)): {"cus": int((cnt == c).sum()),
+                          "mean_us": round(float(cu_end[cnt == c].mean()), 2),
+                          "min_us": round(float(cu_end[cnt == c].min()), 2),
+                          "max_us": round(float(cu_end[cnt == c].max()), 2)}
+            for c in np.unique(cnt)},
+        "blocks_by_dispatch_order": by_order,
+        "waves_in_flight_per_0.25us": [int(((t[:, 0] <= g) & (t[:, 2] > g)).sum()) for g in grid],
+    }
 
 
 def make_replicas(mq, torch, N, K, bits, count, seed):
@@ -418,6 +500,10 @@ def main():
     if args.profile_gather:
         rows = gather_sweep(mq, torch, eager_launches=args.warmup + args.steps)
         print(json.dumps({"profile_gather": rows}))
+        return
+
+    if args.trace_qmv:
+        print(json.dumps({"qmv_trace": trace_qmv(mq, torch)}))
         return
 
     if args.decode_only is not None:

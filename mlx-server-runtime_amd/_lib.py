@@ -56,6 +56,7 @@ EXPORTS = (
     "mq_gather_qmm_segments",
     "mq_gather_qmm_segments_supported",
     "mq_hbm_read",          # include/mq_measure.h
+    "mq_qmv_trace",         # include/mq_measure.h
 )
 
 _lock = threading.Lock()
@@ -125,6 +126,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_gather_qmm_segments_supported.argtypes = [_i64, _i64, _i64, _i64, _i64, _i64, _int,
                                                    _int, _int]
     L.mq_hbm_read.argtypes = [_p, ctypes.c_size_t, _p, _p]
+    L.mq_qmv_trace.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _p, ctypes.c_size_t, _p]
     for name in EXPORTS[2:]:
         getattr(L, name).restype = _int
     L.mq_quantized_matmul_workspace.restype = ctypes.c_size_t

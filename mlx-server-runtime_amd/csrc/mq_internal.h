@@ -58,6 +58,18 @@ hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16
                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
                              int bits, hipStream_t stream);
 
+// The one-row 4-bit GEMV for rows of 16 lanes (K a multiple of 512, 1024 to
+// 4096, group size 64): where qmv1_fits(M, rows, K, bits, group_size) holds
+// (rows: 2N with swiglu), launch_qmv, launch_qmv_swiglu and launch_qmv_norm
+// run it instead of qmv_kernel, with bit-identical results.
+namespace qmv {
+struct NormIn;
+}
+bool qmv1_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
+hipError_t launch_qmv1(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t N,
+                       int64_t K, bool swiglu, const qmv::NormIn* nrm, hipStream_t stream);
+
 // Same contract on the matrix cores for M <= 8 (4-bit) / 16 (8-bit); valid
 // when qmvm_fits(M, N, K, bits, T) (K a multiple of 256, at most 12 chunks
 // per lane).

@@ -55,6 +55,8 @@ hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16
                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
                              int bits, hipStream_t stream) {
   if (N == 0 || M == 0) return hipSuccess;
+  if (qmv1_fits(M, 2 * N, K, bits, 64))
+    return launch_qmv1(x, wq, scales, biases, nullptr, y, N, K, true, nullptr, stream);
   const GatherMap g1{nullptr, nullptr, 1, 1, 1};
   const qmv::NormIn none{};
   if (bits == 4)
@@ -100,8 +102,10 @@ hipError_t launch_qmv_norm(const uint16_t* a, const uint16_t* res, uint16_t* res
                            uint16_t* y, int64_t N, int64_t K, int bits, bool swiglu,
                            hipStream_t stream) {
   if (N == 0) return hipSuccess;
-  const GatherMap g1{nullptr, nullptr, 1, 1, 1};
   const qmv::NormIn nrm{res, res_out, norm_w, eps};
+  if (qmv1_fits(1, swiglu ? 2 * N : N, K, bits, 64))
+    return launch_qmv1(a, wq, scales, biases, bias, y, N, K, swiglu, &nrm, stream);
+  const GatherMap g1{nullptr, nullptr, 1, 1, 1};
   if (swiglu)
     return bits == 4 ? qmv::run_bits<4, false, 1, true>(a, wq, scales, biases, nullptr, y, 1, N,
                                                         K, g1, nrm, 64, stream)
@@ -120,6 +124,8 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
   if (N == 0 || M == 0 || g.T == 0) return hipSuccess;
   // A plain matmul carries no tables: its kernels skip the index loads.
   const bool gather = g.lhs || g.rhs || g.T != 1;
+  if (!gather && qmv1_fits(M, N, K, bits, group_size))
+    return launch_qmv1(x, wq, scales, biases, bias, y, N, K, false, nullptr, stream);
   const qmv::NormIn none{};
   if (bits == 4)
     return gather ? qmv::run_bits<4, true, 0, false>(x, wq, scales, biases, bias, y, M, N, K, g,

@@ -44,7 +44,7 @@ def test_header_declares_the_abi():
         "mq_rms_norm_quantized_matmul", "mq_quantized_matmul_swiglu_workspace",
         "mq_quantized_matmul_swiglu_ws", "mq_quantized_matmul_add_rms_norm_supported",
         "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm",
-        "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu", "mq_hbm_read",
+        "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu", "mq_hbm_read", "mq_qmv_trace",
         "mq_quantized_matmul_noalloc", "mq_gather_qmm_segments",
         "mq_gather_qmm_segments_supported"])
 
