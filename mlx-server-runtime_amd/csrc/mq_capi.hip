@@ -190,6 +190,7 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
       (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0)
     return repack_bytes(N, K) + mq_quantized_matmul_workspace(M, N, K, group_size, 8);
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
+  if (mq::qmv1_fits(M, N, K, bits, 64)) return 0;
   if (use_skinny(M, N, K, bits, 64)) return mq::qmms_workspace_bytes(M, N, K, bits);
   if (dense_gemv(M, N, K, bits, 64) || mq::qmv_fits(M, N, K, bits, 1, 64)) return 0;
   if (mq::qmm4_fits(M, N, K, bits)) return mq::qmm4_workspace_bytes(M, N, K);
@@ -205,7 +206,8 @@ namespace mq {
 bool qmm_workspace_optional(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return false;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return false;
-  if (use_skinny(M, N, K, bits, 64) || dense_gemv(M, N, K, bits, 64) ||
+  if (mq::qmv1_fits(M, N, K, bits, 64) || use_skinny(M, N, K, bits, 64) ||
+      dense_gemv(M, N, K, bits, 64) ||
       mq::qmv_fits(M, N, K, bits, 1, 64))
     return false;
   return mq::qmm4_fits(M, N, K, bits) && mq::qmm4_stream_k(M, N, K);
@@ -222,6 +224,7 @@ namespace {
 int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
+  if (mq::qmv1_fits(M, 2 * N, K, bits, 64)) return 1;  // what mq_quantized_matmul runs
   if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
   if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
   if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
@@ -356,6 +359,7 @@ int mq_rms_norm_quantized_matmul_supported(int64_t M, int64_t N, int64_t K, int 
                                            int bits, int swiglu) {
   if (M != 1 || N <= 0 || K <= 0 || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
+  if (mq::qmv1_fits(1, swiglu ? 2 * N : N, K, bits, 64)) return 1;
   return mq::qmv_norm_fits(N, K, bits, swiglu != 0) ? 1 : 0;
 }
 
@@ -453,7 +457,9 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
   }
   hipError_t e;
   const mq::GatherMap g1{nullptr, nullptr, 1, 1, 1};
-  if (dense_gemv(M, N, K, bits, group_size) &&
+  if (mq::qmv1_fits(M, N, K, bits, group_size)) {
+    e = mq::launch_qmv1(x, wq, scales, biases, bias_vec, y, N, K, false, nullptr, stream);
+  } else if (dense_gemv(M, N, K, bits, group_size) &&
       (use_matrix_core_gemv(M, N, K) || !mq::qmv_fits(M, N, K, bits, 1, group_size))) {
     e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
   } else if (mq::qmv_fits(M, N, K, bits, 1, group_size)) {

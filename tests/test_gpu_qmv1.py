@@ -85,3 +85,39 @@ def test_norm_input_equals_norm_then_gemv(K, N, with_res):
     else:
         x = ops.rms_norm(a, nw, 1e-6)
     assert torch.equal(y, core.quantized_matmul(x, wq, sc, bi, True, 64, 4, bias=bias))
+
+
+@pytest.mark.parametrize("K,N", [(3584, 4608), (3584, 3584), (3584, 512), (2048, 4096),
+                                 (1024, 1000), (4096, 24)])
+def test_small_matrices_against_oracle(orc, K, N):
+    """Smaller one-row matmuls (where the matrix-core GEMV used to run) take
+    the one-row kernel too: against the oracle's float64 contraction with the
+    exactly dequantized weights (norm-wise 1e-2), with QuantizedLinear's
+    bias; the SwiGLU and RMSNorm forms on the same matrices bit-equal to the
+    unfused calls."""
+    import numpy as np
+    core, ops = _mods()
+    print(f"qmv1 small: K={K}, N={N}", flush=True)
+    rng = np.random.default_rng(K + 7 * N)
+    w = orc.f32_to_bf16(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+    wq, s, b = orc.quantize(w, 64, 4)
+    x = orc.f32_to_bf16(rng.normal(0, 1, (1, K)).astype(np.float32))
+    bias = orc.f32_to_bf16(rng.normal(0, 0.1, (N,)).astype(np.float32))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(DEV)
+    wqd = torch.from_numpy(wq.view(np.int32)).to(DEV)
+    y = core.quantized_matmul(dev(x), wqd, dev(s), dev(b), True, 64, 4, bias=dev(bias))
+    ref = orc.qmm(x, wq, s, b, 64, 4, bias=bias)
+    got = orc.bf16_to_f32(y.cpu().view(torch.int16).numpy().view(np.uint16))
+    assert float(np.abs(got - ref).max() / np.abs(ref).max()) <= 1e-2
+    if N % 16 == 0:  # silu_mul takes widths that are multiples of 8
+        h = N // 2
+        assert torch.equal(core.quantized_matmul_swiglu(dev(x), wqd, dev(s), dev(b), 64, 4),
+                           ops.silu_mul(core.quantized_matmul(dev(x), wqd, dev(s), dev(b), True,
+                                                              64, 4)))
+        assert core.swiglu_supported(1, h, K, 64, 4)
+    nw = dev(orc.f32_to_bf16((rng.random(K) + 0.5).astype(np.float32)))
+    yn, _ = core.rms_norm_quantized_matmul(dev(x), nw, 1e-6, wqd, dev(s), dev(b), dev(bias), None,
+                                           64, 4)
+    xn = ops.rms_norm(dev(x), nw, 1e-6)
+    assert torch.equal(yn, core.quantized_matmul(xn, wqd, dev(s), dev(b), True, 64, 4,
+                                                 bias=dev(bias)))
