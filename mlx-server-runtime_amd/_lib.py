@@ -11,7 +11,9 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmi355q.so")
+# MQ_LIBRARY_PATH names another build of the same library (the host-side
+# sanitizer build of tests/run_host_sanitizers.sh).
+LIB_PATH = os.environ.get("MQ_LIBRARY_PATH") or os.path.join(_HERE, "libmi355q.so")
 
 MQ_OK = 0
 MQ_ERR_INVALID = -1

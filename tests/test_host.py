@@ -314,3 +314,48 @@ def test_gather_swiglu_queries_and_validation(mq):
              null) == -1                           # no lhs: x must have T batches
     assert f(null, null, null, null, null, null, null, 64, 4, 768, 2048, 128, 64, 64, 4,
              null) == -2                           # a shape the kernel does not take
+
+
+def test_plan_queries_over_a_shape_grid(mq):
+    """Every host-side plan and support query over a grid of shapes -- row
+    counts from 0 to 65536 around the plan boundaries, the model widths and
+    odd ones, every width and group size -- answers without error and
+    consistently: support queries say 0 or 1; workspaces are whole float32
+    words (past any repacked codes); a fused entry that needs a workspace
+    asks for no more than the plain matmul of the same product plus that
+    product's repack.  (Run under tests/run_host_sanitizers.sh this sweeps
+    the plan arithmetic under ASan and UBSan.)"""
+    L = _L(mq)
+    rows = [0, 1, 2, 3, 8, 9, 16, 17, 31, 32, 33, 64, 127, 128, 129, 255, 256, 257, 300, 512,
+            1023, 1024, 2048, 4096, 8192, 65536]
+    shapes = [(3584, 18944), (18944, 3584), (3584, 4608), (2048, 768), (768, 2048), (4096, 14336),
+              (1024, 1000), (96, 24), (11008, 2048), (2048, 151936)]
+    checked = 0
+    for bits in (2, 3, 4, 5, 6, 8):
+        for gs in (32, 64, 128):
+            for K, N in shapes:
+                for M in rows:
+                    ws = L.mq_quantized_matmul_workspace(M, N, K, gs, bits)
+                    assert ws >= 0
+                    if bits in (4, 8):
+                        assert ws % 4 == 0
+                    sw = L.mq_quantized_matmul_swiglu_supported(M, N // 2, K, gs, bits)
+                    assert sw in (0, 1)
+                    sww = L.mq_quantized_matmul_swiglu_workspace(M, N // 2, K, gs, bits)
+                    if sw and sww:
+                        assert sww <= L.mq_quantized_matmul_workspace(M, 2 * (N // 2), K, gs, bits)
+                    an = L.mq_quantized_matmul_add_rms_norm_supported(M, N, K, gs, bits)
+                    assert an in (0, 1)
+                    anw = L.mq_quantized_matmul_add_rms_norm_workspace(M, N, K, gs, bits)
+                    assert (anw == 0) or an == 1
+                    for swg in (0, 1):
+                        assert L.mq_rms_norm_quantized_matmul_supported(M, N, K, gs, bits,
+                                                                        swg) in (0, 1)
+                    gq = L.mq_gather_qmm_swiglu_supported(max(M, 1), 1, N // 2, K, gs, bits)
+                    assert gq in (0, 1)
+                    for sg in (0, 1):
+                        assert L.mq_gather_qmm_segments_supported(M, 1, N // 2 if sg else N, K,
+                                                                  128, max(M, 1), gs, bits,
+                                                                  sg) in (0, 1)
+                    checked += 1
+    assert checked == 6 * 3 * len(shapes) * len(rows)
