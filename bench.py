@@ -47,9 +47,9 @@ METRIC = "decode tok/s (7B-shape 4-bit, bs=1/32); qmv HBM GB/s and qmm TFLOPS vs
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_4bit_K3584_N18944_traffic.txt")
 
 
-def alg_bytes(M: int, N: int, K: int, bits: int) -> int:
+def alg_bytes(M: int, N: int, K: int, bits: int, group_size: int = 64) -> int:
     """Packed codes + bf16 scales/biases + bf16 x + bf16 y."""
-    return N * K * bits // 8 + N * (K // 64) * 4 + 2 * M * K + 2 * M * N
+    return N * K * bits // 8 + N * (K // group_size) * 4 + 2 * M * K + 2 * M * N
 
 
 def parse():
@@ -157,14 +157,14 @@ def trace_qmv(mq, torch, count: int = 16, replays: int = 20):
     }
 
 
-def make_replicas(mq, torch, N, K, bits, count, seed):
+def make_replicas(mq, torch, N, K, bits, count, seed, group_size=64):
     """`count` independent quantized copies of W ~ N(0, 0.02), cast to bf16, quantized on GPU."""
     gen = torch.Generator(device="cuda:0")
     out = []
     for r in range(count):
         gen.manual_seed(seed + r)
         w = (torch.randn(N, K, generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16)
-        out.append(mq.quantize(w, 64, bits))
+        out.append(mq.quantize(w, group_size, bits))
         del w
     return out
 
@@ -411,6 +411,41 @@ def sweep(mq, torch):
     return rows
 
 
+def group_sweep(mq, torch):
+    """Group sizes 32 and 128 (group 64 is the sweep above) on the 7B gate|up
+    shape at 4 bits: the one-row GEMV, the skinny GEMM and the large-M GEMM
+    index their scales per group at every size."""
+    rows = []
+    K, N, bits = 3584, 18944, 4
+    for gs in (32, 128):
+        wbytes = alg_bytes(0, N, K, bits, gs)
+        reps = make_replicas(mq, torch, N, K, bits, max(1, min(16, math.ceil(640e6 / wbytes))),
+                             seed=300, group_size=gs)
+        for M in (1, 16, 128, 2048):
+            gen = torch.Generator(device="cuda:0").manual_seed(1)
+            x = torch.randn(M, K, generator=gen, device="cuda:0").to(torch.bfloat16)
+            flops = 2.0 * M * N * K
+            n_launch = 64 if flops < 2e11 else 8
+
+            def launch(i, x=x, reps=reps, gs=gs):
+                wq, s, b = reps[i % len(reps)]
+                mq.quantized_matmul(x, wq, s, b, transpose=True, group_size=gs, bits=bits)
+
+            ms, _ = time_graph(torch, launch, n_launch, warmup=2, reps=4)
+            by = alg_bytes(M, N, K, bits, gs)
+            gbs, tfl = by / (ms * 1e-3) / 1e9, flops / (ms * 1e-3) / 1e12
+            bound = "hbm" if flops / by < RIDGE else "mfma"
+            rows.append({"group_size": gs, "M": M, "K": K, "N": N, "bits": bits,
+                         "us": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                         "TFLOPs": round(tfl, 2), "bound": bound,
+                         "frac": round(gbs / HBM_PEAK_GBS if bound == "hbm"
+                                       else tfl / BF16_PEAK_TFLOPS, 4)})
+            del x
+        del reps
+        torch.cuda.empty_cache()
+    return rows
+
+
 def gather_sweep(mq, torch, eager_launches: int = 0):
     """The expert GEMMs of one MoE layer's prefill at the Qwen3-30B-A3B shape:
     8 x 512 tokens routed to 8 of 128 experts (uniform random), the 32768
@@ -583,6 +618,7 @@ def main():
                           decode_bench(torch, 8, 512, 128, model_name="qwen3_30b_a3b")]
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
+        line["group_sweep"] = group_sweep(mq, torch)
         line["gather_sweep"] = gather_sweep(mq, torch)
     if not args.no_cpu:
         wq, s, b = replicas[0]

@@ -28,10 +28,10 @@
  *     matrix once, e.g. at load time, to call them with bits = 8).  transpose
  *     = 0 returns MQ_ERR_UNSUPPORTED; anything MLX itself rejects returns
  *     MQ_ERR_INVALID.
- *     The fused entry points (SwiGLU, RMSNorm, add + RMSNorm, the SwiGLU
- *     epilogue of mq_gather_qmm_segments) take group_size 64 only (their
- *     *_supported queries say 0 otherwise); a matmul of more than 8 rows with
- *     group_size 32 needs K to be a multiple of 64 (else MQ_ERR_UNSUPPORTED).
+ *     Every matmul entry point, fused ones included, takes group sizes 32,
+ *     64 and 128 (the *_supported queries answer for each); a matmul of more
+ *     than 8 rows with group_size 32 needs K to be a multiple of 64 (else
+ *     MQ_ERR_UNSUPPORTED).
  *   - Pointers that feed 16-byte loads (x, wq, w, out, y rows) must be 16-byte
  *     aligned.
  *   - Return value: MQ_OK, or a negative code with a message available from

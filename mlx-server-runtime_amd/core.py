@@ -401,7 +401,10 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     xc = x.contiguous()
     y = torch.empty(tuple(out_batch) + (M, N), dtype=torch.bfloat16, device=dev)
     L = _lib.lib()
-    if expert_offsets is not None and sorted_indices:
+    if expert_offsets is not None and not sorted_indices:
+        raise ValueError(f"[{op}] expert_offsets are the segments of expert-sorted rows: pass "
+                         "sorted_indices=True with them")
+    if expert_offsets is not None:
         if expert_offsets.dtype != torch.int32 or expert_offsets.numel() != E + 1:
             raise ValueError(f"[{op}] expert_offsets must be int32 [{E + 1}]")
         _require_gpu(op, expert_offsets=expert_offsets)

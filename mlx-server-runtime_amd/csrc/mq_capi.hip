@@ -99,18 +99,34 @@ int check_dim(const char* op, const char* name, int64_t v) {
 // faster (M = 16, K = 3584: N = 18944 29.4 us against 34.6, N = 4608
 // 11.4 us against 14.1), so there it only serves shapes the skinny GEMM
 // does not fit.
-// The matrix-core GEMV, the skinny GEMM and the large-M GEMM read one scale
-// per 64-wide k step (group size 64); other group sizes run the dot2 GEMV
-// (M <= 8) or the 128 x 128 MFMA GEMM, which both index scales by group.
+// The matrix-core GEMV reads one scale per 64-wide k step (group size 64); the
+// other kernels take group sizes 32, 64 and 128.
 bool dense_gemv(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
   return group_size == 64 && mq::qmvm_fits(M, N, K, bits, 1) &&
          (M <= 8 || !mq::qmms_fits(M, N, K, bits));
 }
 
-// Skinny MFMA kernel for M above the GEMV range and up to two 128-row tiles.
-bool use_skinny(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
-  return group_size == 64 && M <= 256 && !dense_gemv(M, N, K, bits, 64) &&
-         !mq::qmv_fits(M, N, K, bits, 1, 64) && mq::qmms_fits(M, N, K, bits);
+// The kernel mq_quantized_matmul_ws runs for 4- or 8-bit codes (group size
+// 32, 64 or 128 dividing K), in its order of preference.
+enum class Dense { kNone, kQmv1, kQmvm, kQmv, kSkinny, kQmm4, kQmm };
+
+Dense dense_path(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+  if (mq::qmv1_fits(M, N, K, bits, group_size)) return Dense::kQmv1;
+  const bool qmv = mq::qmv_fits(M, N, K, bits, 1, group_size);
+  if (dense_gemv(M, N, K, bits, group_size) && (use_matrix_core_gemv(M, N, K) || !qmv))
+    return Dense::kQmvm;
+  if (qmv) return Dense::kQmv;
+  // the skinny MFMA kernel above the GEMV range, up to two 128-row tiles
+  if (M <= 256 && !dense_gemv(M, N, K, bits, group_size) && mq::qmms_fits(M, N, K, bits))
+    return Dense::kSkinny;
+  if (mq::qmm4_fits(M, N, K, bits, group_size)) return Dense::kQmm4;
+  return K % 64 ? Dense::kNone : Dense::kQmm;
+}
+
+// bits 4 or 8 and a group size that divides K (the matmul entries' checks)
+bool word_shape(int64_t K, int group_size, int bits) {
+  return (bits == 4 || bits == 8) && (group_size == 32 || group_size == 64 || group_size == 128) &&
+         K % group_size == 0;
 }
 
 }  // namespace
@@ -189,12 +205,12 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
   if ((bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
       (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0)
     return repack_bytes(N, K) + mq_quantized_matmul_workspace(M, N, K, group_size, 8);
-  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
-  if (mq::qmv1_fits(M, N, K, bits, 64)) return 0;
-  if (use_skinny(M, N, K, bits, 64)) return mq::qmms_workspace_bytes(M, N, K, bits);
-  if (dense_gemv(M, N, K, bits, 64) || mq::qmv_fits(M, N, K, bits, 1, 64)) return 0;
-  if (mq::qmm4_fits(M, N, K, bits)) return mq::qmm4_workspace_bytes(M, N, K);
-  return 0;
+  if (!word_shape(K, group_size, bits)) return 0;
+  switch (dense_path(M, N, K, group_size, bits)) {
+    case Dense::kSkinny: return mq::qmms_workspace_bytes(M, N, K, bits);
+    case Dense::kQmm4: return mq::qmm4_workspace_bytes(M, N, K, group_size);
+    default: return 0;
+  }
 }
 
 }  // extern "C"
@@ -205,12 +221,9 @@ namespace mq {
 // which without its workspace runs every tile whole.
 bool qmm_workspace_optional(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return false;
-  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return false;
-  if (mq::qmv1_fits(M, N, K, bits, 64) || use_skinny(M, N, K, bits, 64) ||
-      dense_gemv(M, N, K, bits, 64) ||
-      mq::qmv_fits(M, N, K, bits, 1, 64))
-    return false;
-  return mq::qmm4_fits(M, N, K, bits) && mq::qmm4_stream_k(M, N, K);
+  if (!word_shape(K, group_size, bits)) return false;
+  return dense_path(M, N, K, group_size, bits) == Dense::kQmm4 &&
+         mq::qmm4_stream_k(M, N, K, group_size);
 }
 }  // namespace mq
 
@@ -223,30 +236,35 @@ namespace {
 // (where mq_quantized_matmul runs that GEMM unsplit), 0 not fused.
 int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
-  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
-  if (mq::qmv1_fits(M, 2 * N, K, bits, 64)) return 1;  // what mq_quantized_matmul runs
-  if (!use_matrix_core_gemv(M, 2 * N, K) && mq::qmv_swiglu_fits(M, N, K, bits)) return 1;
-  if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_split_fusable(M, 2 * N, K, bits)) return 2;
-  if (use_skinny(M, 2 * N, K, bits, 64) && mq::qmms_swiglu_direct(M, N, K, bits)) return 3;
-  // route 4 only where mq_quantized_matmul_ws runs the large-M GEMM on the 2N
-  // rows with no even K split: the fused kernel runs every tile whole, as
-  // mq_quantized_matmul_ws does without a workspace (the same kernel, so the
-  // same bits; with one, a stream-K plan may sum a short last round of tiles
-  // in pieces)
+  if (!word_shape(K, group_size, bits)) return 0;
+  // what mq_quantized_matmul runs on the 2N rows
   const int64_t N2 = 2 * N;
-  if (!dense_gemv(M, N2, K, bits, 64) && !mq::qmv_fits(M, N2, K, bits, 1, 64) &&
-      !use_skinny(M, N2, K, bits, 64) && mq::qmm4_fits(M, N2, K, bits) &&
-      mq::qmm4_unsplit(M, N2, K) && mq::qmm4_swiglu_fits(M, N, K, bits))
-    return 4;
-  return 0;
+  switch (dense_path(M, N2, K, group_size, bits)) {
+    case Dense::kQmv1: return 1;
+    case Dense::kQmv: return mq::qmv_swiglu_fits(M, N, K, bits, group_size) ? 1 : 0;
+    case Dense::kSkinny:
+      if (mq::qmms_split_fusable(M, N2, K, bits)) return 2;
+      return mq::qmms_swiglu_direct(M, N, K, bits) ? 3 : 0;
+    case Dense::kQmm4:
+      // only with no even K split: the fused kernel runs every tile whole, as
+      // mq_quantized_matmul_ws does without a workspace (the same kernel, so
+      // the same bits; with one, a stream-K plan may sum a short last round
+      // of tiles in pieces)
+      return mq::qmm4_unsplit(M, N2, K, group_size) &&
+                     mq::qmm4_swiglu_fits(M, N, K, bits, group_size)
+                 ? 4
+                 : 0;
+    default: return 0;
+  }
 }
 
 // mq_quantized_matmul_add_rms_norm takes the skinny GEMM's split plans (the
 // reduce ends in the norm) for rows of at most 8192.
 bool add_norm_fusable(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return false;
-  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64 || N % 8 || N > 8192) return false;
-  return use_skinny(M, N, K, bits, 64) && mq::qmms_split_fusable(M, N, K, bits);
+  if (!word_shape(K, group_size, bits) || N % 8 || N > 8192) return false;
+  return dense_path(M, N, K, group_size, bits) == Dense::kSkinny &&
+         mq::qmms_split_fusable(M, N, K, bits);
 }
 }  // namespace
 
@@ -283,12 +301,16 @@ int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq
   if (!aligned16(x) || !aligned16(wq))
     return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
   if (route == 1)
-    return hip_status(mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+    return hip_status(
+        mq::launch_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, group_size, stream), op);
   if (route == 3)
     return hip_status(
-        mq::launch_qmms_swiglu_direct(x, wq, scales, biases, y, M, N, K, bits, stream), op);
+        mq::launch_qmms_swiglu_direct(x, wq, scales, biases, y, M, N, K, bits, group_size,
+                                      stream),
+        op);
   if (route == 4)
-    return hip_status(mq::launch_qmm4_swiglu(x, wq, scales, biases, y, M, N, K, bits, stream),
+    return hip_status(
+        mq::launch_qmm4_swiglu(x, wq, scales, biases, y, M, N, K, bits, group_size, stream),
                       op);
   const size_t need = mq::qmms_workspace_bytes(M, 2 * N, K, bits);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
@@ -296,8 +318,8 @@ int mq_quantized_matmul_swiglu_ws(const mq_bf16* x, const uint32_t* wq, const mq
                 "[%s] this shape needs a 16-byte aligned workspace of %zu bytes "
                 "(mq_quantized_matmul_swiglu_workspace).",
                 op, need);
-  return hip_status(mq::launch_qmms_swiglu(x, wq, scales, biases, y, M, N, K, bits, workspace,
-                                           workspace_bytes, stream),
+  return hip_status(mq::launch_qmms_swiglu(x, wq, scales, biases, y, M, N, K, bits, group_size,
+                                           workspace, workspace_bytes, stream),
                     op);
 }
 
@@ -351,16 +373,16 @@ int mq_quantized_matmul_add_rms_norm(const mq_bf16* x, const uint32_t* wq, const
                 op, need);
   return hip_status(mq::launch_qmms_add_norm(x, wq, scales, biases, bias_vec, residual,
                                              residual_out, norm_weight, eps, out, M, N, K, bits,
-                                             workspace, workspace_bytes, stream),
+                                             group_size, workspace, workspace_bytes, stream),
                     op);
 }
 
 int mq_rms_norm_quantized_matmul_supported(int64_t M, int64_t N, int64_t K, int group_size,
                                            int bits, int swiglu) {
   if (M != 1 || N <= 0 || K <= 0 || 2 * N >= kMaxDim || K >= kMaxDim) return 0;
-  if ((bits != 4 && bits != 8) || group_size != 64 || K % 64) return 0;
-  if (mq::qmv1_fits(1, swiglu ? 2 * N : N, K, bits, 64)) return 1;
-  return mq::qmv_norm_fits(N, K, bits, swiglu != 0) ? 1 : 0;
+  if (mq::qmv1_fits(1, swiglu ? 2 * N : N, K, bits, group_size)) return 1;
+  if (!word_shape(K, group_size, bits)) return 0;
+  return mq::qmv_norm_fits(N, K, bits, swiglu != 0, group_size) ? 1 : 0;
 }
 
 namespace {
@@ -401,7 +423,8 @@ int mq_rms_norm_quantized_matmul(const mq_bf16* a, const mq_bf16* residual, mq_b
   if (residual_out && (overlap(residual_out, residual, K * 2) || overlap(residual_out, a, K * 2)))
     return fail(MQ_ERR_INVALID, "[%s] residual_out may not overlap a or residual.", op);
   return hip_status(mq::launch_qmv_norm(a, residual, residual_out, norm_weight, eps, wq, scales,
-                                        biases, bias_vec, y, N, K, bits, swiglu != 0, stream),
+                                        biases, bias_vec, y, N, K, bits, swiglu != 0, group_size,
+                                        stream),
                     op);
 }
 
@@ -438,7 +461,7 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
     const size_t rb = repack_bytes(N, K);
     // the one refusal of the 8-bit path below, checked before the repack so
     // that a failed call enqueues nothing
-    if (group_size != 64 && K % 64 && !mq::qmv_fits(M, N, K, 8, 1, group_size))
+    if (dense_path(M, N, K, group_size, 8) == Dense::kNone)
       return fail(MQ_ERR_UNSUPPORTED,
                   "[%s] M=%lld rows with K=%lld (not a multiple of 64) are not implemented on "
                   "this backend.",
@@ -457,31 +480,37 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
   }
   hipError_t e;
   const mq::GatherMap g1{nullptr, nullptr, 1, 1, 1};
-  if (mq::qmv1_fits(M, N, K, bits, group_size)) {
-    e = mq::launch_qmv1(x, wq, scales, biases, bias_vec, y, N, K, false, nullptr, stream);
-  } else if (dense_gemv(M, N, K, bits, group_size) &&
-      (use_matrix_core_gemv(M, N, K) || !mq::qmv_fits(M, N, K, bits, 1, group_size))) {
-    e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
-  } else if (mq::qmv_fits(M, N, K, bits, 1, group_size)) {
-    e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, group_size,
-                       stream);
-  } else if (use_skinny(M, N, K, bits, group_size)) {
-    if (workspace && !aligned16(workspace))
-      return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
-    e = mq::launch_qmms(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
-                        workspace_bytes, stream);
-  } else if (group_size == 64 && mq::qmm4_fits(M, N, K, bits)) {
-    if (workspace && !aligned16(workspace))
-      return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
-    e = mq::launch_qmm4(x, wq, scales, biases, bias_vec, y, M, N, K, bits, workspace,
-                        workspace_bytes, stream);
-  } else {
-    if (K % 64)
+  const Dense path = dense_path(M, N, K, group_size, bits);
+  if ((path == Dense::kSkinny || path == Dense::kQmm4) && workspace && !aligned16(workspace))
+    return fail(MQ_ERR_INVALID, "[%s] the workspace must be 16-byte aligned.", op);
+  switch (path) {
+    case Dense::kQmv1:
+      e = mq::launch_qmv1(x, wq, scales, biases, bias_vec, y, N, K, group_size, false, nullptr,
+                          stream);
+      break;
+    case Dense::kQmvm:
+      e = mq::launch_qmvm(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, stream);
+      break;
+    case Dense::kQmv:
+      e = mq::launch_qmv(x, wq, scales, biases, bias_vec, y, M, N, K, bits, g1, group_size,
+                         stream);
+      break;
+    case Dense::kSkinny:
+      e = mq::launch_qmms(x, wq, scales, biases, bias_vec, y, M, N, K, bits, group_size,
+                          workspace, workspace_bytes, stream);
+      break;
+    case Dense::kQmm4:
+      e = mq::launch_qmm4(x, wq, scales, biases, bias_vec, y, M, N, K, bits, group_size,
+                          workspace, workspace_bytes, stream);
+      break;
+    case Dense::kQmm:
+      e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, group_size, bits, stream);
+      break;
+    default:
       return fail(MQ_ERR_UNSUPPORTED,
                   "[%s] M=%lld rows with K=%lld (not a multiple of 64) are not implemented on "
                   "this backend.",
                   op, (long long)M, (long long)K);
-    e = mq::launch_qmm(x, wq, scales, biases, bias_vec, y, M, N, K, group_size, bits, stream);
   }
   return hip_status(e, op);
 }
@@ -531,10 +560,9 @@ int mq_gather_qmm(const mq_bf16* x, const int32_t* lhs_indices, const int32_t* r
   } else if (few && mq::qmv_fits(M, N, K, bits, T, group_size)) {
     e = mq::launch_qmv(x, wq, scales, biases, nullptr, y, M, N, K, bits, g, group_size,
                        stream);
-  } else if (sorted_indices && group_size == 64 &&
-             mq::qmm4_gather_fits(T, M, N, K, E, x_batches, bits)) {
+  } else if (sorted_indices && mq::qmm4_gather_fits(T, M, N, K, E, x_batches, bits, group_size)) {
     e = mq::launch_qmm4_gather(x, lhs_indices, rhs_indices, nullptr, wq, scales, biases, y, T, M,
-                               N, K, E, x_batches, bits, false, stream);
+                               N, K, E, x_batches, bits, group_size, false, stream);
   } else {
     if (K % 64)
       return fail(MQ_ERR_UNSUPPORTED,
@@ -574,8 +602,8 @@ int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
     return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
   // Decode-sized batches run as mq_gather_qmm (or its SwiGLU GEMV) does: the
   // offsets are not needed there.
-  const bool fits = group_size == 64 &&
-                    mq::qmm4_gather_fits(T, M, swiglu ? 2 * N : N, K, E, x_batches, bits);
+  const bool fits =
+      mq::qmm4_gather_fits(T, M, swiglu ? 2 * N : N, K, E, x_batches, bits, group_size);
   if (T * M <= 64 || !fits) {
     if (!swiglu)
       return mq_gather_qmm(x, lhs_indices, rhs_indices, wq, scales, biases, y, T, M, N, K, E,
@@ -590,7 +618,7 @@ int mq_gather_qmm_segments(const mq_bf16* x, const int32_t* lhs_indices,
   }
   return hip_status(mq::launch_qmm4_gather(x, lhs_indices, rhs_indices, expert_offsets, wq,
                                            scales, biases, y, T, M, N, K, E, x_batches, bits,
-                                           swiglu != 0, stream),
+                                           group_size, swiglu != 0, stream),
                     op);
 }
 
@@ -604,18 +632,18 @@ int mq_gather_qmm_segments_supported(int64_t T, int64_t M, int64_t N, int64_t K,
     return 0;
   if (!swiglu) return bits == 4 || bits == 8;
   if (bits != 4 && bits != 8) return 0;
-  if (T * M > 64 && group_size == 64 && mq::qmm4_gather_fits(T, M, 2 * N, K, E, x_batches, bits))
+  if (T * M > 64 && mq::qmm4_gather_fits(T, M, 2 * N, K, E, x_batches, bits, group_size))
     return 1;
   return mq_gather_qmm_swiglu_supported(T, M, N, K, group_size, bits);
 }
 
 int mq_gather_qmm_swiglu_supported(int64_t T, int64_t M, int64_t N, int64_t K, int group_size,
                                    int bits) {
-  if ((bits != 4 && bits != 8) || group_size != 64 || K < 1 || K % 64) return 0;
+  if (K < 1 || !word_shape(K, group_size, bits)) return 0;
   // Only where mq_gather_qmm itself runs the per-pair GEMV (at most 64 rows in
   // all): more pairs go to the sorted gather GEMM, which reads each expert once.
   if (T * M > 64) return 0;
-  return mq::gather_qmv_swiglu_fits(M, N, K, bits, T) ? 1 : 0;
+  return mq::gather_qmv_swiglu_fits(M, N, K, bits, T, group_size) ? 1 : 0;
 }
 
 int mq_gather_qmm_swiglu(const mq_bf16* x, const int32_t* lhs_indices,
@@ -647,7 +675,9 @@ int mq_gather_qmm_swiglu(const mq_bf16* x, const int32_t* lhs_indices,
     return fail(MQ_ERR_INVALID, "[%s] x and wq must be 16-byte aligned.", op);
   const mq::GatherMap g{lhs_indices, rhs_indices, T, E, x_batches};
   return hip_status(
-      mq::launch_gather_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, g, stream), op);
+      mq::launch_gather_qmv_swiglu(x, wq, scales, biases, y, M, N, K, bits, g, group_size,
+                                   stream),
+      op);
 }
 
 int mq_rms_norm(const mq_bf16* x, const mq_bf16* residual, mq_bf16* residual_out,

@@ -42,33 +42,36 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
                       hipStream_t stream);
 // Gathered SwiGLU GEMV: y [T, M, N] per (batch, expert) pair of g; every
 // expert's matrix is 2N rows (gate rows, then up rows).
-bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T);
+bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T,
+                            int group_size);
 hipError_t launch_gather_qmv_swiglu(const uint16_t* x, const uint32_t* wq,
                                     const uint16_t* scales, const uint16_t* biases, uint16_t* y,
                                     int64_t M, int64_t N, int64_t K, int bits, const GatherMap& g,
-                                    hipStream_t stream);
-bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits);
-bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu);
+                                    int group_size, hipStream_t stream);
+bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu, int group_size);
 hipError_t launch_qmv_norm(const uint16_t* a, const uint16_t* res, uint16_t* res_out,
                            const uint16_t* norm_w, float eps, const uint32_t* wq,
                            const uint16_t* scales, const uint16_t* biases, const uint16_t* bias,
                            uint16_t* y, int64_t N, int64_t K, int bits, bool swiglu,
-                           hipStream_t stream);
+                           int group_size, hipStream_t stream);
 hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                             int bits, hipStream_t stream);
+                             int bits, int group_size, hipStream_t stream);
 
 // The one-row 4-bit GEMV for rows of 16 lanes (K a multiple of 512, 1024 to
-// 4096, group size 64): where qmv1_fits(M, rows, K, bits, group_size) holds
-// (rows: 2N with swiglu), launch_qmv, launch_qmv_swiglu and launch_qmv_norm
-// run it instead of qmv_kernel, with bit-identical results.
+// 4096, group size 32, 64 or 128): where qmv1_fits(M, rows, K, bits,
+// group_size) holds (rows: 2N with swiglu), mq_quantized_matmul and the
+// SwiGLU / RMSNorm fused entries run it (bit-identical to qmv_kernel where
+// that runs 16 lanes per row).
 namespace qmv {
 struct NormIn;
 }
 bool qmv1_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
 hipError_t launch_qmv1(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t N,
-                       int64_t K, bool swiglu, const qmv::NormIn* nrm, hipStream_t stream);
+                       int64_t K, int group_size, bool swiglu, const qmv::NormIn* nrm,
+                       hipStream_t stream);
 
 // Same contract on the matrix cores for M <= 8 (4-bit) / 16 (8-bit); valid
 // when qmvm_fits(M, N, K, bits, T) (K a multiple of 256, at most 12 chunks
@@ -79,24 +82,24 @@ hipError_t launch_qmvm(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
                        int64_t N, int64_t K, int bits, const GatherMap& g, hipStream_t stream);
 
 // 256x256-tile MFMA path with weights dequantized in registers (qmm4_fits:
-// K an even number of groups, >= 128 tiles or few tiles with K splits,
-// 32-bit offsets), two waves per SIMD, each owning the block's 256 rows for
+// group size 32, 64 or 128, K an even number of groups, >= 128 tiles or few
+// tiles with K splits, 32-bit offsets), two waves per SIMD, each owning the block's 256 rows for
 // 32 columns (every code dequantized once per block).  Few tiles and a long
 // K: K is split over blocks; a short last round of tiles: those tiles go to
 // stream-K blocks (qmm4_stream_k).  Both write float32 partial sums to a
 // workspace of qmm4_workspace_bytes; without it every tile runs whole.
 // qmm4_unsplit: the plan splits no tile's K evenly (the SwiGLU form's plan).
-bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits);
-size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K);
-bool qmm4_unsplit(int64_t M, int64_t N, int64_t K);
-bool qmm4_stream_k(int64_t M, int64_t N, int64_t K);
+bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
+bool qmm4_unsplit(int64_t M, int64_t N, int64_t K, int group_size);
+bool qmm4_stream_k(int64_t M, int64_t N, int64_t K, int group_size);
 // mq_quantized_matmul_ws takes the shape with less workspace than it asks for
 // (mq_capi.hip).
 bool qmm_workspace_optional(int64_t M, int64_t N, int64_t K, int group_size, int bits);
 hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream);
+                       int64_t N, int64_t K, int bits, int group_size, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
 // The same kernel over rows sorted by expert (gather_qmm with sorted
 // indices): rows = T * Mb, row p = (batch p / Mb, row p % Mb) reads x batch
 // lhs[batch] (the batch itself without lhs) and expert rhs[batch]; tiles are
@@ -105,18 +108,18 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
 // rows whose id names no expert are zero.  swiglu: every expert's matrix is
 // 2N rows (gate, then up) and y [T*Mb, N] = silu(gate) * up.
 bool qmm4_gather_fits(int64_t T, int64_t Mb, int64_t N, int64_t K, int64_t E,
-                      int64_t x_batches, int bits);
+                      int64_t x_batches, int bits, int group_size);
 hipError_t launch_qmm4_gather(const uint16_t* x, const int32_t* lhs, const int32_t* rhs,
                               const int32_t* seg, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t T, int64_t Mb,
                               int64_t N, int64_t K, int64_t E, int64_t x_batches, int bits,
-                              bool swiglu, hipStream_t stream);
+                              int group_size, bool swiglu, hipStream_t stream);
 // The dense kernel on a gate|up matrix [2N, K] (gate rows first) with
 // silu(gate) * up in its epilogue: y [M, N] (unsplit launches only).
-bool qmm4_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits);
+bool qmm4_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int group_size);
 hipError_t launch_qmm4_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t M, int64_t N,
-                              int64_t K, int bits, hipStream_t stream);
+                              int64_t K, int bits, int group_size, hipStream_t stream);
 // y[i] = bf16(sum over s < splits of partial[s * MN + i] (in order) + bias[i % N])
 hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t* bias,
                                 uint16_t* y, int64_t MN, int64_t N, hipStream_t stream);
@@ -124,7 +127,8 @@ hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t
 // Skinny MFMA path (M up to a few hundred): weights streamed once per M tile
 // of up to 128 rows; K split over blocks through a float32 workspace when the
 // tiles alone cannot fill the GPU (qmms_workspace_bytes > 0).  Without a large
-// enough workspace it runs unsplit.
+// enough workspace it runs unsplit.  Group sizes 32, 64 and 128 (the plans do
+// not depend on it).
 bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits);
 size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits);
 // Split plans of the skinny GEMM whose reduce can take an epilogue: SwiGLU of
@@ -136,21 +140,21 @@ bool qmms_swiglu_direct(int64_t M, int64_t Nout, int64_t K, int bits);
 hipError_t launch_qmms_swiglu_direct(const uint16_t* x, const uint32_t* wq,
                                      const uint16_t* scales, const uint16_t* biases, uint16_t* y,
                                      int64_t M, int64_t Nout, int64_t K, int bits,
-                                     hipStream_t stream);
+                                     int group_size, hipStream_t stream);
 hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t M, int64_t Nout,
-                              int64_t K, int bits, void* workspace, size_t workspace_bytes,
-                              hipStream_t stream);
+                              int64_t K, int bits, int group_size, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
 hipError_t launch_qmms_add_norm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                                 const uint16_t* biases, const uint16_t* bias,
                                 const uint16_t* residual, uint16_t* residual_out,
                                 const uint16_t* norm_w, float eps, uint16_t* out, int64_t M,
-                                int64_t N, int64_t K, int bits, void* workspace,
+                                int64_t N, int64_t K, int bits, int group_size, void* workspace,
                                 size_t workspace_bytes, hipStream_t stream);
 hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream);
+                       int64_t N, int64_t K, int bits, int group_size, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
 
 // MFMA path, any M, group size 32, 64 or 128.
 hipError_t launch_qmm(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,

@@ -34,6 +34,8 @@
 //   their MFMAs.
 // * Scales and biases for 8 groups of the block's 256 columns (16 bytes per
 //   column and array) are DMA-ed into LDS four steps before they are needed.
+//   Group sizes 32, 64 and 128: a chunk of 8 groups spans 4, 8 or 16 steps; in
+//   step u of a chunk lane half h reads group 2u + h, u or u / 2 of it.
 // * Tiles run in groups of 4 row blocks x every column block, the row blocks
 //   fastest: the 32 blocks an XCD runs at once cover 4 row blocks x 8 column
 //   blocks, so they share x rows and codes in that XCD's L2.
@@ -128,6 +130,7 @@ struct Qmm4Args {
   float* partial;
   int M, N, K;  // M: dense rows (gather: T * Mb)
   int tiles_m, tiles_n, tiles, chunks_per_split;
+  int chunks;  // scale/bias chunks (8 groups) along K
   // Dense K split: blocks below dp_blocks take (split, tile) pairs of
   // dp_tiles x (K / chunks_per_split) (partial != null: their float32 sums go
   // to partial[split][M][N]).  Blocks from dp_blocks on are stream-K blocks
@@ -265,8 +268,12 @@ __device__ __forceinline__ void dense_tile(const Qmm4Args& a, int tile, int& bm,
 // columns; the epilogue pairs them and writes y[., N] = silu(gate) * up, each
 // rounded to bfloat16 as the unfused kernels round (gate and up, then silu,
 // then the product).
-template <int BITS, bool GATHER, bool SB16, bool SWIGLU, int WAVES>
+// GSH: log2(group size / 32); a scale/bias chunk of 8 groups spans SPC steps.
+template <int BITS, bool GATHER, bool SB16, bool SWIGLU, int WAVES, int GSH>
 __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
+  constexpr int SPC = 4 << GSH;  // steps per chunk
+  constexpr int kRun = SPC < 8 ? SPC : 8;  // steps per unrolled run
+  static_assert(SPC >= 4 && kRun % kCodeRing == 0, "the chunk's DMA goes 4 steps ahead");
   constexpr int kThreads = 64 * WAVES;
   constexpr int NJ = 8 / WAVES;                     // 32-column MFMA tiles per wave
   constexpr int kXOps = kXStage / (kThreads * 16);  // x DMA operations per lane per step
@@ -284,9 +291,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
   const uint32_t* wbank = a.wq;
   const uint16_t* sbank = a.scales;
   const uint16_t* bbank = a.biases;
-  const int G = K / kGroup;
+  const int G = K >> (5 + GSH);  // groups per row
   const int KT = K / BK;
-  const int chunks = (KT + kSbChunk - 1) / kSbChunk;
+  const int chunks = (KT + SPC - 1) / SPC;
   // A K split writes float32 sums: element (m, c) of the tile (row m, block
   // column c) goes to pdst[(prow + m) * pld + pcol + c]; null: bfloat16 output
   float* pdst = nullptr;
@@ -373,8 +380,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
     // MFMA row tiles holding valid rows (the same for every wave of the block)
     const int live = __builtin_amdgcn_readfirstlane((rows_valid + 31) / 32);
 
-    const int kt0 = c_begin * kSbChunk;
-    const int kt_end = min(KT, c_end * kSbChunk);
+    const int kt0 = c_begin * SPC;
+    const int kt_end = min(KT, c_end * SPC);
     const int x_rows = GATHER ? a.x_batches * a.Mb : a.M;
     const rsrc_t xrs = make_rsrc(a.x, (uint64_t)x_rows * K * 2);
     const rsrc_t wrs = make_rsrc(wbank, (uint64_t)NW * K * BITS / 8);
@@ -481,6 +488,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
       if constexpr (BITS == 4) return dequant8<4>(w[ks], 0u, g.s, g.b);
       else return dequant8<8>(w[(ks & 1) * 2], w[(ks & 1) * 2 + 1], g.s, g.b);
     };
+    // the chunk's group of step u for this lane (half h of the step's 64 k)
+    auto group_of = [&](int u) { return GSH == 0 ? 2 * u + h : GSH == 1 ? u : u >> 1; };
     auto read_sb = [&](int buf, int grp, GroupAffine (&g)[NJ]) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
@@ -503,7 +512,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
     // B fragments of k-slice 0 are always dequantized one step early, at the end
     // of the previous step, so each step opens with MFMAs instead of VALU.
     GroupAffine ga[NJ];
-    read_sb(c_begin & 1, 0, ga);
+    read_sb(c_begin & 1, group_of(0), ga);
     bf16x8_t b0[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) b0[j] = dequant_frag(cw[0], j, 0, ga[j]);
@@ -515,20 +524,29 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
       constexpr bool MASKED = decltype(masked)::value;
       int st = 0;  // stage holding x of the current step
       for (int c = c_begin; c < c_end; ++c) {
+        // a 16-step chunk (group size 128) runs as two unrolled runs of 8
+        // (the compiler does not unroll 16 of these steps); ui, a multiple
+        // of the code ring's length away from u, indexes the ring
+#pragma unroll 1
+        for (int u0 = 0; u0 < SPC; u0 += kRun) {
 #pragma unroll
-        for (int u = 0; u < kSbChunk; ++u) {
-          const int kt = c * kSbChunk + u;
-          if constexpr (!SB16) {
-            if (kt >= kt_end) break;  // a K of G % 8 != 0 groups ends mid-chunk
+        for (int ui = 0; ui < kRun; ++ui) {
+          const int u = u0 + ui;
+          const int kt = c * SPC + u;
+          // a K of G % 8 != 0 groups ends mid-chunk; the runs of 16-step
+          // chunks keep the test too (without it the compiler spills the
+          // SB16 form's registers)
+          if constexpr (!SB16 || kRun < SPC) {
+            if (kt >= kt_end) break;
           }
           const uint32_t xa = st * kXStage + aoff;
           bf16x8_t a[kRowTiles];
 #pragma unroll
           for (int i = 0; i < kRowTiles; ++i)
             if (!MASKED || i < live) a[i] = *reinterpret_cast<const bf16x8_t*>(lds + xa + i * 4096);
-          load_codes(cw[(u + 2) % kCodeRing], kt + 2);
+          load_codes(cw[(ui + 2) % kCodeRing], kt + 2);
           dma_x(kt + 3, (st + 3) % kXStages);
-          if (u == kSbChunk - 4) dma_sb(c + 1, (c + 1) & 1);
+          if (u == SPC - 4) dma_sb(c + 1, (c + 1) & 1);
 
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
@@ -548,14 +566,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
               }
             if (ks < 3) {
 #pragma unroll
-              for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[u % kCodeRing], j, ks + 1, ga[j]);
+              for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[ui % kCodeRing], j, ks + 1, ga[j]);
             } else {
               // next step: its scales (the next chunk's buffer after the last
               // step of a chunk, DMA-ed four steps ago) and its first k-slice
-              if (u == kSbChunk - 1) read_sb((c + 1) & 1, 0, ga);
-              else read_sb(c & 1, u + 1, ga);
+              if (u == SPC - 1) read_sb((c + 1) & 1, group_of(0), ga);
+              else read_sb(c & 1, group_of(u + 1), ga);
 #pragma unroll
-              for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[(u + 1) % kCodeRing], j, 0, ga[j]);
+              for (int j = 0; j < NJ; ++j) bq[j] = dequant_frag(cw[(ui + 1) % kCodeRing], j, 0, ga[j]);
             }
 #pragma unroll
             for (int j = 0; j < NJ; ++j) b0[j] = bq[j];
@@ -567,9 +585,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
           // the DMAs of this step and the previous one may still be in flight
           // (more in the steps that load scales); x of the next step, issued two
           // steps ago, and the scales read next step have landed
-          if (u == kSbChunk - 4 || u == kSbChunk - 3) step_barrier<2 * kXOps + kSbOps>();
+          if (u == SPC - 4 || u == SPC - 3) step_barrier<2 * kXOps + kSbOps>();
           else step_barrier<2 * kXOps>();
           st = (st + 1) % kXStages;
+        }
         }
       }
     };
@@ -675,18 +694,23 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
   }
 }
 
+// Scale/bias chunks (8 groups each) along K.
+int64_t sb_chunks(int64_t K, int group_size) {
+  return (K / group_size + kSbChunk - 1) / kSbChunk;
+}
+
 // K splits for a launch: 1 when the tiles fill half a round of the GPU (one
 // block per CU); otherwise the most splits that keep the grid within one
-// round, each at least 2 scale chunks (1024 K) long.  Measured at M = 512
-// (7B prefill of one 512-token prompt): the down projection 18944 -> 3584 in
-// 28 tiles x 9 splits takes 81 us where the 128 x 128 GEMM took 431 us, and
-// q/k/v 3584 -> 4608 in 36 tiles x 3 splits 47 us (85 us).
-int qmm4_splits(int64_t M, int64_t N, int64_t K) {
+// round, each at least 1024 K long (whole scale chunks).  Measured at M = 512
+// (7B prefill of one 512-token prompt, group size 64): the down projection
+// 18944 -> 3584 in 28 tiles x 9 splits takes 81 us where the 128 x 128 GEMM
+// took 431 us, and q/k/v 3584 -> 4608 in 36 tiles x 3 splits 47 us (85 us).
+int qmm4_splits(int64_t M, int64_t N, int64_t K, int group_size) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   constexpr int64_t kRound = 256;
   if (tiles >= kRound / 2) return 1;
-  const int64_t chunks = (K / kGroup + kSbChunk - 1) / kSbChunk;
-  return (int)std::max<int64_t>(1, std::min(kRound / tiles, chunks / 2));
+  const int64_t cap = sb_chunks(K, group_size) * group_size / 128;  // 1024 K per split
+  return (int)std::max<int64_t>(1, std::min(kRound / tiles, cap));
 }
 
 constexpr int kWaves = 8;  // waves per block: two per SIMD
@@ -698,7 +722,7 @@ constexpr int kMaxPieces = 8;  // stream-K pieces per tile
 // adds 8 consecutive columns of tile row 8 * blockIdx.x + t / 32.
 __global__ __launch_bounds__(256) void qmm4_sk_reduce(const Qmm4Args a) {
   const int s = blockIdx.y;
-  const int chunks = (a.K / BK + kSbChunk - 1) / kSbChunk;
+  const int chunks = a.chunks;
   const int first = s * chunks / a.sk_w;
   const int pieces = (s * chunks + chunks - 1) / a.sk_w - first + 1;
   int bm, bn;
@@ -759,12 +783,12 @@ struct Plan {
   int sk_blocks, sk_pieces;
 };
 
-Plan qmm4_plan(int64_t M, int64_t N, int64_t K) {
+Plan qmm4_plan(int64_t M, int64_t N, int64_t K, int group_size) {
   constexpr int64_t kRound = 256;
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int64_t chunks = (K / kGroup + kSbChunk - 1) / kSbChunk;
+  const int64_t chunks = sb_chunks(K, group_size);
   Plan p{};
-  p.S = qmm4_splits(M, N, K);
+  p.S = qmm4_splits(M, N, K, group_size);
   const int64_t cps = (chunks + p.S - 1) / p.S;
   p.S = (int)((chunks + cps - 1) / cps);
   p.dp_tiles = (int)tiles;
@@ -791,16 +815,21 @@ size_t plan_workspace(const Plan& p, int64_t M, int64_t N) {
   return p.S > 1 ? (size_t)p.S * M * N * sizeof(float) : 0;
 }
 
-template <bool GATHER, bool SWIGLU>
-hipError_t launch(const Qmm4Args& a, int bits, dim3 grid, hipStream_t stream) {
-  const bool sb16 = (a.K / kGroup) % kSbChunk == 0;
-  void (*kern)(Qmm4Args);
+template <bool GATHER, bool SWIGLU, int GSH>
+void (*pick_kernel(int bits, bool sb16))(Qmm4Args) {
   if (bits == 4)
-    kern = sb16 ? qmm4_kernel<4, GATHER, true, SWIGLU, kWaves>
-                : qmm4_kernel<4, GATHER, false, SWIGLU, kWaves>;
-  else
-    kern = sb16 ? qmm4_kernel<8, GATHER, true, SWIGLU, kWaves>
-                : qmm4_kernel<8, GATHER, false, SWIGLU, kWaves>;
+    return sb16 ? qmm4_kernel<4, GATHER, true, SWIGLU, kWaves, GSH>
+                : qmm4_kernel<4, GATHER, false, SWIGLU, kWaves, GSH>;
+  return sb16 ? qmm4_kernel<8, GATHER, true, SWIGLU, kWaves, GSH>
+              : qmm4_kernel<8, GATHER, false, SWIGLU, kWaves, GSH>;
+}
+
+template <bool GATHER, bool SWIGLU>
+hipError_t launch(const Qmm4Args& a, int bits, int group_size, dim3 grid, hipStream_t stream) {
+  const bool sb16 = (a.K / group_size) % kSbChunk == 0;
+  void (*kern)(Qmm4Args) = group_size == 32  ? pick_kernel<GATHER, SWIGLU, 0>(bits, sb16)
+                           : group_size == 64 ? pick_kernel<GATHER, SWIGLU, 1>(bits, sb16)
+                                              : pick_kernel<GATHER, SWIGLU, 2>(bits, sb16);
   const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
   if (e != hipSuccess) return e;
@@ -809,42 +838,49 @@ hipError_t launch(const Qmm4Args& a, int bits, dim3 grid, hipStream_t stream) {
 }
 
 // 32-bit buffer offsets (with room for the kOutOfRange marker) for x, the
-// codes and the scales of one matrix; an even number of 64-element groups.
-bool offsets_fit(int64_t x_rows, int64_t N, int64_t K, int bits) {
+// codes and the scales of one matrix; an even number of groups (whole 64-wide
+// steps, 4-byte aligned scale rows) of 32, 64 or 128.
+bool offsets_fit(int64_t x_rows, int64_t N, int64_t K, int bits, int group_size) {
   const int64_t lim = (int64_t)1 << 31;
-  return K % (2 * kGroup) == 0 && (x_rows + BM) * K * 2 < lim && N * K * bits / 8 < lim &&
-         N * (K / kGroup) * 2 < lim;
+  return (group_size == 32 || group_size == 64 || group_size == 128) &&
+         K % (2 * group_size) == 0 && (x_rows + BM) * K * 2 < lim && N * K * bits / 8 < lim &&
+         N * (K / group_size) * 2 < lim;
 }
 
 }  // namespace
 
-bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits) {
+bool qmm4_fits(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
   // >= 128 tiles, or >= 8 whose K splits give >= 64 blocks
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  return offsets_fit(M, N, K, bits) && tiles < ((int64_t)1 << 31) &&
-         (tiles >= 128 || (tiles >= 8 && qmm4_splits(M, N, K) * tiles >= 64));
+  return offsets_fit(M, N, K, bits, group_size) && tiles < ((int64_t)1 << 31) &&
+         (tiles >= 128 || (tiles >= 8 && qmm4_splits(M, N, K, group_size) * tiles >= 64));
 }
 
-size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  return plan_workspace(qmm4_plan(M, N, K), M, N);
+size_t qmm4_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size) {
+  return plan_workspace(qmm4_plan(M, N, K, group_size), M, N);
 }
 
-bool qmm4_unsplit(int64_t M, int64_t N, int64_t K) { return qmm4_splits(M, N, K) == 1; }
+bool qmm4_unsplit(int64_t M, int64_t N, int64_t K, int group_size) {
+  return qmm4_splits(M, N, K, group_size) == 1;
+}
 
-bool qmm4_stream_k(int64_t M, int64_t N, int64_t K) { return qmm4_plan(M, N, K).sk_tiles > 0; }
+bool qmm4_stream_k(int64_t M, int64_t N, int64_t K, int group_size) {
+  return qmm4_plan(M, N, K, group_size).sk_tiles > 0;
+}
 
 hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream) {
+                       int64_t N, int64_t K, int bits, int group_size, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   Qmm4Args a{};
   a.x = x, a.wq = wq, a.scales = scales, a.biases = biases, a.bias = bias, a.y = y;
   a.M = (int)M, a.N = (int)N, a.K = (int)K;
   a.tiles_m = (int)((M + BM - 1) / BM), a.tiles_n = (int)((N + BN - 1) / BN);
   a.tiles = a.tiles_m * a.tiles_n;
-  const int chunks = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
-  Plan p = qmm4_plan(M, N, K);
+  const int chunks = (int)sb_chunks(K, group_size);
+  a.chunks = chunks;
+  Plan p = qmm4_plan(M, N, K, group_size);
   // without the workspace the plan needs: every tile whole
   if (!workspace || workspace_bytes < plan_workspace(p, M, N)) p = Plan{1, a.tiles, 0, 0, 0, 0};
   a.chunks_per_split = (chunks + p.S - 1) / p.S;
@@ -855,8 +891,8 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
   a.sk_units = p.sk_tiles * chunks;
   a.sk_pieces = p.sk_pieces;
   a.sk_partial = p.sk_tiles ? static_cast<float*>(workspace) : nullptr;
-  const hipError_t e =
-      launch<false, false>(a, bits, dim3((unsigned)(a.dp_blocks + p.sk_blocks)), stream);
+  const hipError_t e = launch<false, false>(a, bits, group_size,
+                                            dim3((unsigned)(a.dp_blocks + p.sk_blocks)), stream);
   if (e != hipSuccess) return e;
   if (p.sk_tiles) {
     hipLaunchKernelGGL(qmm4_sk_reduce, dim3(BM / 8, (unsigned)p.sk_tiles), dim3(256), 0, stream, a);
@@ -867,24 +903,24 @@ hipError_t launch_qmm4(const uint16_t* x, const uint32_t* wq, const uint16_t* sc
 }
 
 bool qmm4_gather_fits(int64_t T, int64_t Mb, int64_t N, int64_t K, int64_t E,
-                      int64_t x_batches, int bits) {
+                      int64_t x_batches, int bits, int group_size) {
   const int64_t lim = (int64_t)1 << 31;
   return E >= 1 && E <= 4 * 64 * kWaves && T * Mb < lim / 2 &&
-         offsets_fit(x_batches * Mb, N, K, bits);
+         offsets_fit(x_batches * Mb, N, K, bits, group_size);
 }
 
 hipError_t launch_qmm4_gather(const uint16_t* x, const int32_t* lhs, const int32_t* rhs,
                               const int32_t* seg, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t T, int64_t Mb,
                               int64_t N, int64_t K, int64_t E, int64_t x_batches, int bits,
-                              bool swiglu, hipStream_t stream) {
+                              int group_size, bool swiglu, hipStream_t stream) {
   if (T == 0 || Mb == 0 || N == 0) return hipSuccess;
   Qmm4Args a{};
   a.x = x, a.wq = wq, a.scales = scales, a.biases = biases, a.y = y;
   a.M = (int)(T * Mb), a.N = (int)N, a.K = (int)K;
   const int out_cols = swiglu ? BN / 2 : BN;
   a.tiles_n = (int)((N + out_cols - 1) / out_cols);
-  a.chunks_per_split = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
+  a.chunks = a.chunks_per_split = (int)sb_chunks(K, group_size);
   a.lhs = lhs, a.rhs = rhs, a.seg = seg;
   a.T = (int)T, a.Mb = (int)Mb, a.E = (int)E, a.x_batches = (int)x_batches;
   // every expert's segment adds at most one partial tile; one spare row tile
@@ -892,27 +928,29 @@ hipError_t launch_qmm4_gather(const uint16_t* x, const int32_t* lhs, const int32
   int64_t row_tiles = (T * Mb + BM - 1) / BM + std::min(E, T) + 1;
   row_tiles = (row_tiles + 7) / 8 * 8;  // whole runs of 8 row tiles (one per XCD)
   const dim3 grid((unsigned)(row_tiles * a.tiles_n));
-  return swiglu ? launch<true, true>(a, bits, grid, stream) : launch<true, false>(a, bits, grid, stream);
+  return swiglu ? launch<true, true>(a, bits, group_size, grid, stream)
+                : launch<true, false>(a, bits, group_size, grid, stream);
 }
 
-bool qmm4_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits) {
+bool qmm4_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
   // the gate|up matrix (2N rows) in 128-column output tiles, unsplit
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN / 2 - 1) / (BN / 2));
-  return offsets_fit(M, 2 * N, K, bits) && tiles >= 128 && tiles < ((int64_t)1 << 31);
+  return offsets_fit(M, 2 * N, K, bits, group_size) && tiles >= 128 &&
+         tiles < ((int64_t)1 << 31);
 }
 
 hipError_t launch_qmm4_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t M, int64_t N,
-                              int64_t K, int bits, hipStream_t stream) {
+                              int64_t K, int bits, int group_size, hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   Qmm4Args a{};
   a.x = x, a.wq = wq, a.scales = scales, a.biases = biases, a.y = y;
   a.M = (int)M, a.N = (int)N, a.K = (int)K;
   a.tiles_m = (int)((M + BM - 1) / BM), a.tiles_n = (int)((N + BN / 2 - 1) / (BN / 2));
   a.tiles = a.tiles_m * a.tiles_n;
-  a.chunks_per_split = (int)((K / kGroup + kSbChunk - 1) / kSbChunk);
+  a.chunks = a.chunks_per_split = (int)sb_chunks(K, group_size);
   a.dp_tiles = a.dp_blocks = a.tiles;
-  return launch<false, true>(a, bits, dim3((unsigned)a.tiles), stream);
+  return launch<false, true>(a, bits, group_size, dim3((unsigned)a.tiles), stream);
 }
 
 }  // namespace mq

@@ -29,6 +29,7 @@
 // split writes float32 partial sums to a caller-provided workspace and
 // splitk_reduce adds them in a fixed order (results do not depend on timing).
 #include <algorithm>
+#include <type_traits>
 
 #include "mq_common.h"
 #include "mq_internal.h"
@@ -113,7 +114,10 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, 
 // x, wq, scales and biases are deliberately not __restrict__: with it the
 // compiler may move their loads across the barriers' inline asm, and the
 // barriers' counts assume the issue order below.
-template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4>
+// GSH: log2(group size / 32) -- group sizes 32, 64, 128.  A lane's codes for
+// a 64-wide step are k = 32h .. 32h + 31 of it (both widths), all in one
+// group, (2 step + h) >> GSH within the chunk of 8 steps.
+template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4, int GSH = 1>
 __global__ __launch_bounds__(64 * W) void qmms_kernel(
     const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
@@ -142,7 +146,8 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   const int Nout = N / 2;  // EPI 1: output columns
   const int n0 = tn * (EPI == 1 ? 16 * W : 32 * W), m0 = tm * BM;
   const int KT = K / BK;
-  const int G = K / kGroup;
+  const int G = K >> (5 + GSH);  // groups per row
+  constexpr uint32_t kChunkSB = 32u >> GSH;  // scale (or bias) bytes per chunk of 8 steps
   const int c_begin = split * chunks_per_split;
   const int c_end = min(KT / kChunk, c_begin + chunks_per_split);
 
@@ -263,7 +268,39 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
 
   // ---- prologue: codes of the first kPrefetch steps, x of the first P ----
   const int kt0 = c_begin * kChunk;
-  u32x4_t sv = buf_load16(srs, soff + c_begin * 16), bv = buf_load16(brs, soff + c_begin * 16);
+  // a chunk's scales and biases for this lane's column: 16 (GSH 0), 8 or 4
+  // entries
+  auto load_sb = [&](u32x4_t (&v)[2], const rsrc_t& r, int c) {
+    const uint32_t o = soff + (uint32_t)c * kChunkSB;
+    if constexpr (GSH == 0) {
+      v[0] = buf_load16(r, o);
+      v[1] = buf_load16(r, o + 16);
+    } else if constexpr (GSH == 1) {
+      v[0] = buf_load16(r, o);
+    } else {
+      const u32x2_t t = buf_load8(r, o);
+      v[0] = u32x4_t{t[0], t[1], 0u, 0u};
+    }
+  };
+  // the entry of step u (a compile-time constant after unrolling) for lane half h
+  auto sb_entry = [&](const u32x4_t (&v)[2], int u) -> float {
+    uint32_t d;
+    int half;
+    if constexpr (GSH == 0) {
+      d = v[u >> 2][u & 3];
+      half = h;
+    } else if constexpr (GSH == 1) {
+      d = v[0][u >> 1];
+      half = u & 1;
+    } else {
+      d = v[0][u >> 2];
+      half = (u >> 1) & 1;
+    }
+    return half ? hi_bf16(d) : lo_bf16(d);
+  };
+  u32x4_t sv[2], bv[2];
+  load_sb(sv, srs, c_begin);
+  load_sb(bv, brs, c_begin);
   u32x4_t cw[kCodeDma<BITS> ? 1 : kPrefetch][NC];
   if constexpr (kCodeDma<BITS>) {
 #pragma unroll
@@ -281,20 +318,20 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
 
   int st = 0;  // stage of the current step's x tile
   for (int c = c_begin; c < c_end; ++c) {
-    u32x4_t svn, bvn;
+    u32x4_t svn[2], bvn[2];
 #pragma unroll
     for (int u = 0; u < kChunk; ++u) {
       const int kt = c * kChunk + u;
       if (u == 0) {
         __asm__ volatile("" ::: "memory");
-        svn = buf_load16(srs, soff + (c + 1) * 16);
-        bvn = buf_load16(brs, soff + (c + 1) * 16);
+        load_sb(svn, srs, c + 1);
+        load_sb(bvn, brs, c + 1);
         __asm__ volatile("" ::: "memory");
       }
       dma_x(kt + P, (st + P) & (S - 1));
 
-      const float s = bf16_bits_to_f32((sv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
-      const float b = bf16_bits_to_f32((bv[u >> 1] >> ((u & 1) * 16)) & 0xffffu);
+      const float s = sb_entry(sv, u);
+      const float b = sb_entry(bv, u);
       const uint32_t xa = st * kXStage + aoff;
       u32x4_t (&q)[NC] = cw[kCodeDma<BITS> ? 0 : u % kPrefetch];
 #pragma unroll
@@ -325,8 +362,12 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
       else step_barrier<kInFlight>();
       st = (st + 1) & (S - 1);
     }
-    sv = svn;
-    bv = bvn;
+    sv[0] = svn[0];
+    bv[0] = bvn[0];
+    if constexpr (GSH == 0) {
+      sv[1] = svn[1];
+      bv[1] = bvn[1];
+    }
   }
   // Prefetches past the split's range must land before the LDS is released.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -589,14 +630,14 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   return p;
 }
 
-template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4>
+template <int BITS, int MI, bool PARTIAL, int EPI, int W, int GSH>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
   const int lds =
       kXStages * 32 * MI * BK * 2 + (kCodeDma<BITS> ? W * kCodeSlots * kCodeBlock : 0);
-  auto kern = qmms_kernel<BITS, MI, PARTIAL, EPI, W>;
+  auto kern = qmms_kernel<BITS, MI, PARTIAL, EPI, W, GSH>;
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -609,29 +650,55 @@ hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
 }
 
 // one unsplit 32-row tile: the plan's block width
-template <int BITS, int EPI>
+template <int BITS, int EPI, int GSH>
 hipError_t run_wide(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                     const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                     int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   switch (p.waves) {
-    case 5: return run<BITS, 1, false, EPI, 5>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
-    case 6: return run<BITS, 1, false, EPI, 6>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
-    case 8: return run<BITS, 1, false, EPI, 8>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
-    default: return run<BITS, 1, false, EPI, 4>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    case 5: return run<BITS, 1, false, EPI, 5, GSH>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    case 6: return run<BITS, 1, false, EPI, 6, GSH>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    case 8: return run<BITS, 1, false, EPI, 8, GSH>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    default: return run<BITS, 1, false, EPI, 4, GSH>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
   }
 }
 
-template <int BITS, bool PARTIAL>
+template <int BITS, bool PARTIAL, int GSH>
 hipError_t run_mi(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                   const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                   int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   if constexpr (!PARTIAL)
-    if (p.mi == 1) return run_wide<BITS, 0>(x, wq, scales, biases, bias, y, M, N, K, p, stream);
+    if (p.mi == 1) return run_wide<BITS, 0, GSH>(x, wq, scales, biases, bias, y, M, N, K, p, stream);
   switch (p.mi) {
-    case 1: return run<BITS, 1, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
-    case 2: return run<BITS, 2, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
-    default: return run<BITS, 4, PARTIAL>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
+    case 1: return run<BITS, 1, PARTIAL, 0, 4, GSH>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
+    case 2: return run<BITS, 2, PARTIAL, 0, 4, GSH>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
+    default: return run<BITS, 4, PARTIAL, 0, 4, GSH>(x, wq, scales, biases, bias, y, partial, M, N, K, p, stream);
   }
+}
+
+// f(std::integral_constant<int, GSH>) for group size 32 << GSH
+template <class F>
+hipError_t by_group(int group_size, F&& f) {
+  switch (group_size) {
+    case 32: return f(std::integral_constant<int, 0>{});
+    case 64: return f(std::integral_constant<int, 1>{});
+    case 128: return f(std::integral_constant<int, 2>{});
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// the skinny kernel over the plan p (split or not) for 4- or 8-bit codes
+template <bool PARTIAL>
+hipError_t run_plan(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                    const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
+                    int64_t M, int64_t N, int64_t K, int bits, int group_size, const Plan& p,
+                    hipStream_t stream) {
+  return by_group(group_size, [&](auto g) {
+    constexpr int GSH = decltype(g)::value;
+    return bits == 4 ? run_mi<4, PARTIAL, GSH>(x, wq, scales, biases, bias, y, partial, M, N, K, p,
+                                               stream)
+                     : run_mi<8, PARTIAL, GSH>(x, wq, scales, biases, bias, y, partial, M, N, K, p,
+                                               stream);
+  });
 }
 
 }  // namespace
@@ -645,10 +712,10 @@ hipError_t launch_splitk_reduce(const float* partial, int splits, const uint16_t
 
 bool qmms_fits(int64_t M, int64_t N, int64_t K, int bits) {
   const int64_t lim = (int64_t)1 << 31;
-  // whole 8-group chunks; 32-bit offsets with room for the tiles' overhang
-  // (up to 256 columns for the widest blocks)
+  // whole 8-step chunks; 32-bit offsets with room for the tiles' overhang
+  // (up to 256 columns for the widest blocks), scales for group size 32
   return K % (BK * kChunk) == 0 && M >= 1 && (M + 128) * K * 2 < lim &&
-         (N + 256) * K * bits / 8 < lim && (N + 256) * (K / kGroup) * 2 < lim;
+         (N + 256) * K * bits / 8 < lim && (N + 256) * (K / 32) * 2 < lim;
 }
 
 size_t qmms_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits) {
@@ -671,30 +738,33 @@ bool qmms_swiglu_direct(int64_t M, int64_t Nout, int64_t K, int bits) {
 
 hipError_t launch_qmms_swiglu_direct(const uint16_t* x, const uint32_t* wq,
                                      const uint16_t* scales, const uint16_t* biases, uint16_t* y,
-                                     int64_t M, int64_t Nout, int64_t K, int bits,
+                                     int64_t M, int64_t Nout, int64_t K, int bits, int group_size,
                                      hipStream_t stream) {
   if (M == 0 || Nout == 0) return hipSuccess;
   Plan p = plan(M, 2 * Nout, K, bits, true);
   if (p.splits != 1 || p.mi != 1 || p.tiles_m != 1) return hipErrorInvalidValue;
   // 16 gate + 16 up columns per wave
   p.tiles_n = (int)((Nout + 16 * p.waves - 1) / (16 * p.waves));
-  return bits == 4 ? run_wide<4, 1>(x, wq, scales, biases, nullptr, y, M, 2 * Nout, K, p, stream)
-                   : run_wide<8, 1>(x, wq, scales, biases, nullptr, y, M, 2 * Nout, K, p, stream);
+  return by_group(group_size, [&](auto g) {
+    constexpr int GSH = decltype(g)::value;
+    return bits == 4
+               ? run_wide<4, 1, GSH>(x, wq, scales, biases, nullptr, y, M, 2 * Nout, K, p, stream)
+               : run_wide<8, 1, GSH>(x, wq, scales, biases, nullptr, y, M, 2 * Nout, K, p, stream);
+  });
 }
 
 hipError_t launch_qmms_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int64_t M, int64_t Nout,
-                              int64_t K, int bits, void* workspace, size_t workspace_bytes,
-                              hipStream_t stream) {
+                              int64_t K, int bits, int group_size, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
   if (M == 0 || Nout == 0) return hipSuccess;
   const int64_t N = 2 * Nout;
   const Plan p = plan(M, N, K, bits, true);
   if (p.splits < 2 || !workspace || workspace_bytes < (size_t)p.splits * M * N * sizeof(float))
     return hipErrorInvalidValue;  // excluded by the caller's checks
   float* part = static_cast<float*>(workspace);
-  const hipError_t e =
-      bits == 4 ? run_mi<4, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream)
-                : run_mi<8, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream);
+  const hipError_t e = run_plan<true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, bits,
+                                      group_size, p, stream);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(splitk_reduce_swiglu, dim3((unsigned)((M * Nout + 255) / 256)), dim3(256), 0,
                      stream, part, p.splits, y, M, (int)Nout);
@@ -705,16 +775,15 @@ hipError_t launch_qmms_add_norm(const uint16_t* x, const uint32_t* wq, const uin
                                 const uint16_t* biases, const uint16_t* bias,
                                 const uint16_t* residual, uint16_t* residual_out,
                                 const uint16_t* norm_w, float eps, uint16_t* out, int64_t M,
-                                int64_t N, int64_t K, int bits, void* workspace,
+                                int64_t N, int64_t K, int bits, int group_size, void* workspace,
                                 size_t workspace_bytes, hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   const Plan p = plan(M, N, K, bits, true);
   if (p.splits < 2 || !workspace || workspace_bytes < (size_t)p.splits * M * N * sizeof(float))
     return hipErrorInvalidValue;  // excluded by the caller's checks
   float* part = static_cast<float*>(workspace);
-  const hipError_t e =
-      bits == 4 ? run_mi<4, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream)
-                : run_mi<8, true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, p, stream);
+  const hipError_t e = run_plan<true>(x, wq, scales, biases, nullptr, nullptr, part, M, N, K, bits,
+                                      group_size, p, stream);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(splitk_reduce_add_norm, dim3((unsigned)M), dim3(256), 0, stream, part,
                      p.splits, bias, residual, residual_out, norm_w, out, M, (int)N, eps);
@@ -723,19 +792,18 @@ hipError_t launch_qmms_add_norm(const uint16_t* x, const uint32_t* wq, const uin
 
 hipError_t launch_qmms(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
-                       int64_t N, int64_t K, int bits, void* workspace, size_t workspace_bytes,
-                       hipStream_t stream) {
+                       int64_t N, int64_t K, int bits, int group_size, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
   if (M == 0 || N == 0) return hipSuccess;
   Plan p = plan(M, N, K, bits, true);
   if (p.splits > 1 && (!workspace || workspace_bytes < (size_t)p.splits * M * N * sizeof(float)))
     p = plan(M, N, K, bits, false);
   if (p.splits == 1)
-    return bits == 4 ? run_mi<4, false>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream)
-                     : run_mi<8, false>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+    return run_plan<false>(x, wq, scales, biases, bias, y, nullptr, M, N, K, bits, group_size, p,
+                           stream);
   float* part = static_cast<float*>(workspace);
-  hipError_t e = bits == 4
-                     ? run_mi<4, true>(x, wq, scales, biases, bias, y, part, M, N, K, p, stream)
-                     : run_mi<8, true>(x, wq, scales, biases, bias, y, part, M, N, K, p, stream);
+  hipError_t e = run_plan<true>(x, wq, scales, biases, bias, y, part, M, N, K, bits, group_size,
+                                p, stream);
   if (e != hipSuccess) return e;
   return launch_splitk_reduce(part, p.splits, bias, y, M * N, N, stream);
 }

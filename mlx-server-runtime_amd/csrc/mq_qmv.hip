@@ -45,33 +45,36 @@ bool qmv_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T, int group_si
 // The SwiGLU GEMV: N outputs from a 2N-row matrix, M <= 2, at most one wave
 // per row (a block pairs RPB/2 gate rows with their up rows), and every byte
 // offset of the block's rows within one buffer descriptor.
-bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits) {
-  if (M < 1 || M > 2 || N < 1 || !qmv_fits(M, 2 * N, K, bits, 1, 64)) return false;
+bool qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+  if (M < 1 || M > 2 || N < 1 || !qmv_fits(M, 2 * N, K, bits, 1, group_size)) return false;
   const int64_t C = K / (128 / bits);
   return qmv::pick_tpr(C, 2 * N, 1) <= 64 && 2 * N * C * 16 < (int64_t(1) << 32);
 }
 
 hipError_t launch_qmv_swiglu(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                              const uint16_t* biases, uint16_t* y, int64_t M, int64_t N, int64_t K,
-                             int bits, hipStream_t stream) {
+                             int bits, int group_size, hipStream_t stream) {
   if (N == 0 || M == 0) return hipSuccess;
-  if (qmv1_fits(M, 2 * N, K, bits, 64))
-    return launch_qmv1(x, wq, scales, biases, nullptr, y, N, K, true, nullptr, stream);
+  if (qmv1_fits(M, 2 * N, K, bits, group_size))
+    return launch_qmv1(x, wq, scales, biases, nullptr, y, N, K, group_size, true, nullptr,
+                       stream);
   const GatherMap g1{nullptr, nullptr, 1, 1, 1};
   const qmv::NormIn none{};
   if (bits == 4)
     return qmv::run_bits<4, false, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g1, none,
-                                             64, stream);
+                                             group_size, stream);
   return qmv::run_bits<8, false, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g1, none,
-                                           64, stream);
+                                           group_size, stream);
 }
 
 // The SwiGLU GEMV per gathered (batch, expert) pair: every expert's matrix is
 // 2N rows (gate rows, then up rows).  The lanes split each row exactly as the
 // plain gathered GEMV of the 2N-row matrix does, so the results are those of
 // that GEMV followed by silu_mul, bit for bit.
-bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T) {
-  if (M < 1 || M > 2 || N < 1 || T < 1 || !qmv_fits(M, 2 * N, K, bits, T, 64)) return false;
+bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T,
+                            int group_size) {
+  if (M < 1 || M > 2 || N < 1 || T < 1 || !qmv_fits(M, 2 * N, K, bits, T, group_size))
+    return false;
   const int64_t C = K / (128 / bits);
   return qmv::pick_tpr(C, 2 * N, T) <= 64 && 2 * N * C * 16 < (int64_t(1) << 32);
 }
@@ -79,42 +82,43 @@ bool gather_qmv_swiglu_fits(int64_t M, int64_t N, int64_t K, int bits, int64_t T
 hipError_t launch_gather_qmv_swiglu(const uint16_t* x, const uint32_t* wq,
                                     const uint16_t* scales, const uint16_t* biases, uint16_t* y,
                                     int64_t M, int64_t N, int64_t K, int bits, const GatherMap& g,
-                                    hipStream_t stream) {
+                                    int group_size, hipStream_t stream) {
   if (N == 0 || M == 0 || g.T == 0) return hipSuccess;
   const qmv::NormIn none{};
   if (bits == 4)
     return qmv::run_bits<4, true, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g, none,
-                                            64, stream);
+                                            group_size, stream);
   return qmv::run_bits<8, true, 1, false>(x, wq, scales, biases, nullptr, y, M, N, K, g, none,
-                                          64, stream);
+                                          group_size, stream);
 }
 
 // RMSNorm of one row, then the GEMV (or the SwiGLU GEMV over a 2N-row
 // matrix): the row's 8-element units must fit the norm's four per thread.
-bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu) {
+bool qmv_norm_fits(int64_t N, int64_t K, int bits, bool swiglu, int group_size) {
   if (K > 8192) return false;
-  return swiglu ? qmv_swiglu_fits(1, N, K, bits) : qmv_fits(1, N, K, bits, 1, 64);
+  return swiglu ? qmv_swiglu_fits(1, N, K, bits, group_size)
+                : qmv_fits(1, N, K, bits, 1, group_size);
 }
 
 hipError_t launch_qmv_norm(const uint16_t* a, const uint16_t* res, uint16_t* res_out,
                            const uint16_t* norm_w, float eps, const uint32_t* wq,
                            const uint16_t* scales, const uint16_t* biases, const uint16_t* bias,
                            uint16_t* y, int64_t N, int64_t K, int bits, bool swiglu,
-                           hipStream_t stream) {
+                           int group_size, hipStream_t stream) {
   if (N == 0) return hipSuccess;
   const qmv::NormIn nrm{res, res_out, norm_w, eps};
-  if (qmv1_fits(1, swiglu ? 2 * N : N, K, bits, 64))
-    return launch_qmv1(a, wq, scales, biases, bias, y, N, K, swiglu, &nrm, stream);
+  if (qmv1_fits(1, swiglu ? 2 * N : N, K, bits, group_size))
+    return launch_qmv1(a, wq, scales, biases, bias, y, N, K, group_size, swiglu, &nrm, stream);
   const GatherMap g1{nullptr, nullptr, 1, 1, 1};
   if (swiglu)
     return bits == 4 ? qmv::run_bits<4, false, 1, true>(a, wq, scales, biases, nullptr, y, 1, N,
-                                                        K, g1, nrm, 64, stream)
+                                                        K, g1, nrm, group_size, stream)
                      : qmv::run_bits<8, false, 1, true>(a, wq, scales, biases, nullptr, y, 1, N,
-                                                        K, g1, nrm, 64, stream);
+                                                        K, g1, nrm, group_size, stream);
   return bits == 4 ? qmv::run_bits<4, false, 0, true>(a, wq, scales, biases, bias, y, 1, N, K, g1,
-                                                      nrm, 64, stream)
+                                                      nrm, group_size, stream)
                    : qmv::run_bits<8, false, 0, true>(a, wq, scales, biases, bias, y, 1, N, K, g1,
-                                                      nrm, 64, stream);
+                                                      nrm, group_size, stream);
 }
 
 hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
@@ -125,7 +129,7 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
   // A plain matmul carries no tables: its kernels skip the index loads.
   const bool gather = g.lhs || g.rhs || g.T != 1;
   if (!gather && qmv1_fits(M, N, K, bits, group_size))
-    return launch_qmv1(x, wq, scales, biases, bias, y, N, K, false, nullptr, stream);
+    return launch_qmv1(x, wq, scales, biases, bias, y, N, K, group_size, false, nullptr, stream);
   const qmv::NormIn none{};
   if (bits == 4)
     return gather ? qmv::run_bits<4, true, 0, false>(x, wq, scales, biases, bias, y, M, N, K, g,

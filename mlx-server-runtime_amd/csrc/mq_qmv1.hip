@@ -57,11 +57,12 @@ __device__ __forceinline__ uint64_t realtime() {
   return t;
 }
 
-// S chunks per lane (C = 16 S), EPI 0 / 1, NORM as in qmv_kernel.  TRACE
+// S chunks per lane (C = 16 S), EPI 0 / 1, NORM as in qmv_kernel; 2^GSH
+// chunks per group (group sizes 32, 64, 128: GSH 0, 1, 2).  TRACE
 // (measurement only, mq_qmv_trace): every wave also records the constant
 // clock at entry, after the prologue's barrier and after its store, and the
 // CU it ran on, into trace[wave][4].
-template <int S, int EPI, bool NORM, bool TRACE = false>
+template <int S, int EPI, bool NORM, int GSH, bool TRACE = false>
 __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const uint32_t* wq,
                                                       const uint16_t* scales,
                                                       const uint16_t* biases,
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const u
                                                       qmv::NormIn nrm, uint64_t* trace) {
   uint64_t t0 = 0, t1 = 0;
   if constexpr (TRACE) t0 = realtime();
-  constexpr int C = 16 * S, G = C / 2;          // chunks, groups per row
+  constexpr int C = 16 * S, G = C >> GSH;       // chunks, groups per row
   constexpr int K = 32 * C;
   constexpr int XU = (4 * C + kBlock - 1) / kBlock;
   constexpr int HALF = RPB / 2;
@@ -240,14 +241,14 @@ __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const u
   wait_vm<0>();
   __syncthreads();  // every wave's share of the scales and biases has landed
   const float* xslane = xsum + lane;
-  const uint16_t* slane = sl + slot * G + (lane >> 1);
-  const uint16_t* blane = bl + slot * G + (lane >> 1);
+  const uint16_t* slane = sl + slot * G + (lane >> GSH);
+  const uint16_t* blane = bl + slot * G + (lane >> GSH);
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < S; ++j) {
     const float xs = xslane[j * TPR];
-    const float sc = bf16_bits_to_f32(slane[j * (TPR / 2)]);
-    const float bi = bf16_bits_to_f32(blane[j * (TPR / 2)]);
+    const float sc = bf16_bits_to_f32(slane[j * (TPR >> GSH)]);
+    const float bi = bf16_bits_to_f32(blane[j * (TPR >> GSH)]);
     acc = fmaf(sc, dd[j], acc);
     acc = fmaf(fmaf(-128.f, sc, bi), xs, acc);
   }
@@ -278,39 +279,51 @@ __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const u
   }
 }
 
-template <int S, int EPI, bool NORM, bool TRACE = false>
+template <int S, int EPI, bool NORM, int GSH, bool TRACE = false>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                const uint16_t* bias, uint16_t* y, int64_t N, const qmv::NormIn& nrm,
                hipStream_t stream, uint64_t* trace = nullptr) {
-  constexpr int C = 16 * S, G = C / 2;
+  constexpr int C = 16 * S, G = C >> GSH;
   constexpr int OPS = ((RPB * G + G + 1) / 2 + 63) / 64;
   const size_t lds = (size_t)C * 64 + C * 4 + 2 * OPS * 256;
   const int64_t rows = EPI == 1 ? RPB / 2 : RPB;
-  hipLaunchKernelGGL((qmv1_kernel<S, EPI, NORM, TRACE>),
+  hipLaunchKernelGGL((qmv1_kernel<S, EPI, NORM, GSH, TRACE>),
                      dim3((unsigned)((N + rows - 1) / rows)), dim3(kBlock), lds, stream, x, wq, s,
                      b, bias, y, (int)N, nrm, trace);
   return hipGetLastError();
 }
 
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, int GSH>
 hipError_t run_s(int S, const uint16_t* x, const uint32_t* wq, const uint16_t* s,
                  const uint16_t* b, const uint16_t* bias, uint16_t* y, int64_t N,
                  const qmv::NormIn& nrm, hipStream_t stream) {
   switch (S) {
-    case 2: return run<2, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
-    case 3: return run<3, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
-    case 4: return run<4, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
-    case 5: return run<5, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
-    case 6: return run<6, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
-    case 7: return run<7, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
-    case 8: return run<8, EPI, NORM>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 2: return run<2, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 3: return run<3, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 4: return run<4, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 5: return run<5, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 6: return run<6, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 7: return run<7, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    case 8: return run<8, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+    default: return hipErrorInvalidValue;  // excluded by qmv1_fits
+  }
+}
+
+template <int EPI, bool NORM>
+hipError_t run_gs(int S, int group_size, const uint16_t* x, const uint32_t* wq,
+                  const uint16_t* s, const uint16_t* b, const uint16_t* bias, uint16_t* y,
+                  int64_t N, const qmv::NormIn& nrm, hipStream_t stream) {
+  switch (group_size) {
+    case 32: return run_s<EPI, NORM, 0>(S, x, wq, s, b, bias, y, N, nrm, stream);
+    case 64: return run_s<EPI, NORM, 1>(S, x, wq, s, b, bias, y, N, nrm, stream);
+    case 128: return run_s<EPI, NORM, 2>(S, x, wq, s, b, bias, y, N, nrm, stream);
     default: return hipErrorInvalidValue;  // excluded by qmv1_fits
   }
 }
 
 }  // namespace qmv1
 
-// One activation row, 4-bit codes, group size 64, K a multiple of 512 from
+// One activation row, 4-bit codes, group size 32, 64 or 128, K a multiple of 512 from
 // 1024 to 4096 (2 to 8 chunks per lane), 32-bit code offsets.  Where
 // qmv_kernel itself would run 16 lanes per row (large matrices) the results
 // are its own, bit for bit; on smaller matrices (where the dispatch used to
@@ -319,21 +332,27 @@ hipError_t run_s(int S, const uint16_t* x, const uint32_t* wq, const uint16_t* s
 // 3584 -> 9216 7.7 -> 5.6 us.  rows: the rows of the matrix (2N for the
 // SwiGLU form).
 bool qmv1_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size) {
-  if (M != 1 || bits != 4 || group_size != 64 || K % 512 || K < 1024 || K > 4096) return false;
+  if (M != 1 || bits != 4 || K % 512 || K < 1024 || K > 4096) return false;
+  if (group_size != 32 && group_size != 64 && group_size != 128) return false;
   return rows >= 1 && rows * (K / 32) * 16 < (int64_t(1) << 32) && rows < (int64_t(1) << 30);
 }
 
 hipError_t launch_qmv1(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t N,
-                       int64_t K, bool swiglu, const qmv::NormIn* nrm, hipStream_t stream) {
+                       int64_t K, int group_size, bool swiglu, const qmv::NormIn* nrm,
+                       hipStream_t stream) {
   if (N == 0) return hipSuccess;
   const int S = (int)(K / 512);
   const qmv::NormIn none{};
   if (nrm)
-    return swiglu ? qmv1::run_s<1, true>(S, x, wq, scales, biases, nullptr, y, N, *nrm, stream)
-                  : qmv1::run_s<0, true>(S, x, wq, scales, biases, bias, y, N, *nrm, stream);
-  return swiglu ? qmv1::run_s<1, false>(S, x, wq, scales, biases, nullptr, y, N, none, stream)
-                : qmv1::run_s<0, false>(S, x, wq, scales, biases, bias, y, N, none, stream);
+    return swiglu ? qmv1::run_gs<1, true>(S, group_size, x, wq, scales, biases, nullptr, y, N,
+                                          *nrm, stream)
+                  : qmv1::run_gs<0, true>(S, group_size, x, wq, scales, biases, bias, y, N, *nrm,
+                                          stream);
+  return swiglu ? qmv1::run_gs<1, false>(S, group_size, x, wq, scales, biases, nullptr, y, N,
+                                         none, stream)
+                : qmv1::run_gs<0, false>(S, group_size, x, wq, scales, biases, bias, y, N, none,
+                                         stream);
 }
 
 // The traced plain form: 4 uint64 per wave (entry, after the prologue's
@@ -344,10 +363,10 @@ hipError_t launch_qmv1_trace(const uint16_t* x, const uint32_t* wq, const uint16
                              uint64_t* trace, hipStream_t stream) {
   const qmv::NormIn none{};
   switch (K / 512) {
-    case 7: return qmv1::run<7, 0, false, true>(x, wq, scales, biases, nullptr, y, N, none, stream,
-                                                 trace);
-    case 8: return qmv1::run<8, 0, false, true>(x, wq, scales, biases, nullptr, y, N, none, stream,
-                                                 trace);
+    case 7: return qmv1::run<7, 0, false, 1, true>(x, wq, scales, biases, nullptr, y, N, none,
+                                                    stream, trace);
+    case 8: return qmv1::run<8, 0, false, 1, true>(x, wq, scales, biases, nullptr, y, N, none,
+                                                    stream, trace);
     default: return hipErrorInvalidValue;
   }
 }

@@ -177,14 +177,14 @@ class QExperts:
                 and core.gather_segments_supported(T, M, N, K, self.num_experts, n_x,
                                                    self.group_size, self.bits, swiglu=True)):
             # the expert-segment GEMM with SiLU * up in its epilogue (where it
-            # takes the shape: group size 64, an even number of groups per row)
+            # takes the shape: an even number of groups per row)
             return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
                                           self.group_size, self.bits, expert_offsets=offsets)
         if core.gather_swiglu_supported(T, M, N, K, self.group_size, self.bits):
             return core.gather_qmm_swiglu(x, self.wq, self.scales, self.biases, lhs, rhs,
                                           self.group_size, self.bits)
         return silu_mul(self(x, lhs=lhs, rhs=rhs, sorted_indices=sorted_indices,
-                             offsets=offsets))
+                             offsets=offsets if sorted_indices else None))
 
 
 class MoEBlock:

@@ -208,7 +208,16 @@ def test_quantized_matmul_swiglu_refuses_other_shapes(ops):
     w = torch.zeros(2 * 1792, 18944 // 8, dtype=torch.int32, device=DEV)
     sc = torch.zeros(2 * 1792, 18944 // 64, dtype=torch.bfloat16, device=DEV)
     assert not core.swiglu_supported(1, 1792, 18944, 64, 4)  # rows of 128 lanes
-    assert not core.swiglu_supported(1, 4864, 896, 64, 4)    # small: the matrix-core GEMV
+    assert not core.swiglu_supported(1, 4864, 768, 64, 4)    # small: the matrix-core GEMV
+    # K = 896 (14 groups, not a multiple of the matrix-core GEMV's 4-group
+    # scale loads): quantized_matmul runs the dot2 GEMV there, so the fused
+    # form takes it
+    assert core.swiglu_supported(1, 4864, 896, 64, 4)
+    x = (torch.randn(1, 896, generator=_gen(896), device=DEV)).to(torch.bfloat16)
+    wt = (torch.randn(2 * 4864, 896, generator=_gen(4864), device=DEV) * 0.02).to(torch.bfloat16)
+    wq, s, b = core.quantize(wt, 64, 4)
+    assert torch.equal(core.quantized_matmul_swiglu(x, wq, s, b, 64, 4),
+                       ops.silu_mul(core.quantized_matmul(x, wq, s, b, True, 64, 4)))
     with pytest.raises(NotImplementedError, match="not a fused shape"):
         core.quantized_matmul_swiglu(torch.zeros(1, 18944, dtype=torch.bfloat16, device=DEV),
                                      w, sc, sc, 64, 4)

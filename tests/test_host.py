@@ -145,15 +145,16 @@ def test_decoder_entry_validation(mq):
     one = ctypes.c_void_p(16)  # never dereferenced: validation fails before any launch
     assert seg(null, null, null, one, null, null, null, null, 300, 1, 64, 512, 8, 300, 64, 4,
                0, null) == -1                                                   # null pointers
-    assert seg(one, null, one, one, one, one, one, one, 300, 1, 64, 512, 8, 300, 32, 4,
-               1, null) == -2                      # SiLU * up epilogue: group size 64 only
+    assert seg(one, null, one, one, one, one, one, one, 300, 1, 64, 512, 8, 300, 64, 3,
+               1, null) == -2                      # SiLU * up epilogue: 4- and 8-bit codes
     assert seg(null, null, null, one, null, null, null, null, 0, 1, 64, 512, 8, 0, 64, 4,
                1, null) == 0
     sup = L.mq_quantized_matmul_swiglu_supported
     assert sup(1, 18944, 3584, 64, 4) == 1 and sup(2, 18944, 3584, 64, 8) == 1
     assert sup(4, 18944, 3584, 64, 4) == 0                                      # M > 2
     assert sup(1, 1792, 18944, 64, 4) == 0                                      # 128-lane rows
-    assert sup(1, 18944, 3584, 32, 4) == 0 and sup(1, 18944, 3584, 64, 3) == 0
+    assert sup(1, 18944, 3584, 32, 4) == 1 and sup(1, 18944, 3584, 128, 8) == 1  # group sizes
+    assert sup(1, 18944, 3584, 64, 3) == 0 and sup(1, 18944, 3584, 16, 4) == 0
     sw = L.mq_quantized_matmul_swiglu
     assert sw(null, null, null, null, null, 4, 18944, 3584, 64, 4, null) == -2   # not fused
     assert sw(null, null, null, null, null, 1, 18944, 3584, 64, 4, null) == -1   # null pointers
@@ -302,7 +303,8 @@ def test_gather_swiglu_queries_and_validation(mq):
     assert sup(64, 1, 768, 2048, 64, 4) == 1 and sup(64, 1, 768, 2048, 64, 8) == 1
     assert sup(64, 4, 768, 2048, 64, 4) == 0       # more than 2 rows per pair
     assert sup(4096, 1, 768, 2048, 64, 4) == 0     # prefill: the sorted gather GEMM
-    assert sup(64, 1, 768, 2048, 32, 4) == 0       # group size
+    assert sup(64, 1, 768, 2048, 32, 4) == 1 and sup(64, 1, 768, 2048, 128, 8) == 1
+    assert sup(64, 1, 768, 2048, 16, 4) == 0       # group size
     assert sup(64, 1, 768, 2000, 64, 4) == 0       # K not a multiple of the group
     null = None
     f = L.mq_gather_qmm_swiglu
