@@ -111,7 +111,7 @@ bool dense_gemv(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
 enum class Dense { kNone, kQmv1, kQmvm, kQmv, kSkinny, kQmm4, kQmm };
 
 Dense dense_path(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
-  if (mq::qmv1_fits(M, N, K, bits, group_size)) return Dense::kQmv1;
+  if (mq::qmv1_plain_fits(M, N, K, bits, group_size)) return Dense::kQmv1;
   const bool qmv = mq::qmv_fits(M, N, K, bits, 1, group_size);
   if (dense_gemv(M, N, K, bits, group_size) && (use_matrix_core_gemv(M, N, K) || !qmv))
     return Dense::kQmvm;
@@ -240,7 +240,7 @@ int swiglu_route(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   // what mq_quantized_matmul runs on the 2N rows
   const int64_t N2 = 2 * N;
   switch (dense_path(M, N2, K, group_size, bits)) {
-    case Dense::kQmv1: return 1;
+    case Dense::kQmv1: return mq::qmv1_fits(M, N2, K, bits, group_size) ? 1 : 0;
     case Dense::kQmv: return mq::qmv_swiglu_fits(M, N, K, bits, group_size) ? 1 : 0;
     case Dense::kSkinny:
       if (mq::qmms_split_fusable(M, N2, K, bits)) return 2;

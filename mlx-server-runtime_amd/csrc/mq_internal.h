@@ -68,6 +68,9 @@ namespace qmv {
 struct NormIn;
 }
 bool qmv1_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
+// ... and where its plain form (no SwiGLU, no RMSNorm input) runs: also the
+// long rows of down projections.
+bool qmv1_plain_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
 hipError_t launch_qmv1(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t N,
                        int64_t K, int group_size, bool swiglu, const qmv::NormIn* nrm,

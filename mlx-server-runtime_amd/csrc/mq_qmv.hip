@@ -128,7 +128,7 @@ hipError_t launch_qmv(const uint16_t* x, const uint32_t* wq, const uint16_t* sca
   if (N == 0 || M == 0 || g.T == 0) return hipSuccess;
   // A plain matmul carries no tables: its kernels skip the index loads.
   const bool gather = g.lhs || g.rhs || g.T != 1;
-  if (!gather && qmv1_fits(M, N, K, bits, group_size))
+  if (!gather && qmv1_plain_fits(M, N, K, bits, group_size))
     return launch_qmv1(x, wq, scales, biases, bias, y, N, K, group_size, false, nullptr, stream);
   const qmv::NormIn none{};
   if (bits == 4)

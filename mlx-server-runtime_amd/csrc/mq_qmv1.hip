@@ -1,5 +1,6 @@
-// One-row 4-bit GEMV for rows of up to 128 chunks (K a multiple of 512, at
-// most 4096), group size 64, 16 lanes per row: y[n] = x . (s*q + b)[n], as every decode-time
+// One-row 4-bit GEMV, 16 lanes per row (K a multiple of 512, at most 4096, or
+// the long rows of down projections), group sizes 32, 64 and 128:
+// y[n] = x . (s*q + b)[n], as every decode-time
 // QuantizedLinear calls mx.quantized_matmul(x, w, scales, biases,
 // transpose=True) with one activation row
 // (python/mlx_worker/native_mlx/models/qwen2.py:76-78,115,134,227) -- gate and
@@ -31,7 +32,14 @@
 namespace mq {
 namespace qmv1 {
 
-constexpr int kBlock = 256, TPR = 16, RPB = kBlock / TPR, kLookahead = 2;
+constexpr int kBlock = 256, TPR = 16, RPB = kBlock / TPR;
+
+// Code loads a lane keeps in flight ahead of its contraction.  Rows of up to
+// 8 chunks per lane run 4-19 blocks per CU, whose loads together fill the
+// memory queue at 2; a down projection's long rows (K = 18944: 37 chunks per
+// lane, 224 blocks, at most one per CU) need more per lane: measured on
+// 3584 x 18944, 2 ahead 12.4 us, 4 ahead 10.1, 8 ahead 9.5, 12 ahead 9.9.
+constexpr int lookahead(int S) { return S > 8 ? 8 : 2; }
 
 template <int N_>
 __device__ __forceinline__ void wait_vm() {
@@ -74,7 +82,7 @@ __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const u
   constexpr int K = 32 * C;
   constexpr int XU = (4 * C + kBlock - 1) / kBlock;
   constexpr int HALF = RPB / 2;
-  constexpr int D = kLookahead < S ? kLookahead : S;  // codes issued before the loop
+  constexpr int D = lookahead(S) < S ? lookahead(S) : S;  // codes issued before the loop
   constexpr int SB_WORDS = (RPB * G + G + 1) / 2;     // qmv_kernel's LDS layout (GP = G)
   constexpr int OPS = (SB_WORDS + 63) / 64;           // DMA operations per array
   constexpr int NQ = (2 * OPS + kBlock / 64 - 1) / (kBlock / 64);  // per wave
@@ -305,8 +313,18 @@ hipError_t run_s(int S, const uint16_t* x, const uint32_t* wq, const uint16_t* s
     case 6: return run<6, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
     case 7: return run<7, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
     case 8: return run<8, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
-    default: return hipErrorInvalidValue;  // excluded by qmv1_fits
+    default: break;
   }
+  // long rows: the plain form at group size 64 or 128 (qmv1_plain_fits)
+  if constexpr (EPI == 0 && !NORM && GSH > 0) {
+    switch (S) {
+      case 27: return run<27, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+      case 28: return run<28, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+      case 37: return run<37, EPI, NORM, GSH>(x, wq, s, b, bias, y, N, nrm, stream);
+      default: break;
+    }
+  }
+  return hipErrorInvalidValue;  // excluded by qmv1_fits / qmv1_plain_fits
 }
 
 template <int EPI, bool NORM>
@@ -324,7 +342,7 @@ hipError_t run_gs(int S, int group_size, const uint16_t* x, const uint32_t* wq,
 }  // namespace qmv1
 
 // One activation row, 4-bit codes, group size 32, 64 or 128, K a multiple of 512 from
-// 1024 to 4096 (2 to 8 chunks per lane), 32-bit code offsets.  Where
+// 1024 to 4096 (2 to 8 chunks per lane), 32-bit code offsets: every form.  Where
 // qmv_kernel itself would run 16 lanes per row (large matrices) the results
 // are its own, bit for bit; on smaller matrices (where the dispatch used to
 // take the matrix-core GEMV or qmv_kernel with wider rows) this kernel is the
@@ -334,6 +352,20 @@ hipError_t run_gs(int S, int group_size, const uint16_t* x, const uint32_t* wq,
 bool qmv1_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size) {
   if (M != 1 || bits != 4 || K % 512 || K < 1024 || K > 4096) return false;
   if (group_size != 32 && group_size != 64 && group_size != 128) return false;
+  return rows >= 1 && rows * (K / 32) * 16 < (int64_t(1) << 32) && rows < (int64_t(1) << 30);
+}
+
+// The plain form also takes the long rows of decoders' down projections --
+// K = 13824, 14336, 18944 (27, 28, 37 chunks per lane) -- at group size 64 or
+// 128 (at group size 32, or 54 chunks, the kernel spills registers).  Measured on
+// 3584 x 18944 (the 7B down projection): 9.5 us against 11.7 for qmv_kernel
+// (128 lanes per row), group 128 9.2 against 11.5.
+bool qmv1_plain_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size) {
+  if (qmv1_fits(M, rows, K, bits, group_size)) return true;
+  const int64_t S = K / 512;
+  if (M != 1 || bits != 4 || K % 512 || (group_size != 64 && group_size != 128) ||
+      (S != 27 && S != 28 && S != 37))
+    return false;
   return rows >= 1 && rows * (K / 32) * 16 < (int64_t(1) << 32) && rows < (int64_t(1) << 30);
 }
 

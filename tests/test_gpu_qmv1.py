@@ -121,3 +121,33 @@ def test_small_matrices_against_oracle(orc, K, N):
     xn = ops.rms_norm(dev(x), nw, 1e-6)
     assert torch.equal(yn, core.quantized_matmul(xn, wqd, dev(s), dev(b), True, 64, 4,
                                                  bias=dev(bias)))
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("K,N", [(18944, 3584), (14336, 4096), (13824, 1000)])
+def test_long_rows_against_oracle(orc, gs, K, N):
+    """Down projections' long rows (27, 28 and 37 chunks per lane, codes 8
+    ahead) in the plain one-row form: every output against the oracle's
+    float64 contraction of the exactly dequantized weights -- norm-wise within
+    1e-2 and each element within its bfloat16 rounding (2^-8 relative) plus
+    2e-3 of the largest output (float32 accumulation over K terms) -- with
+    QuantizedLinear's bias; 1000 rows leave a partial last block.  The SwiGLU
+    and RMSNorm forms do not take these rows."""
+    import numpy as np
+    core, _ = _mods()
+    print(f"qmv1 long rows: K={K}, N={N}, group {gs}", flush=True)
+    rng = np.random.default_rng(K + N + gs)
+    w = orc.f32_to_bf16(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+    wq, s, b = orc.quantize(w, gs, 4)
+    x = orc.f32_to_bf16(rng.normal(0, 1, (1, K)).astype(np.float32))
+    bias = orc.f32_to_bf16(rng.normal(0, 0.1, (N,)).astype(np.float32))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(DEV)
+    y = core.quantized_matmul(dev(x), torch.from_numpy(wq.view(np.int32)).to(DEV), dev(s), dev(b),
+                              True, gs, 4, bias=dev(bias))
+    ref = orc.qmm(x, wq, s, b, gs, 4, bias=bias)
+    got = orc.bf16_to_f32(y.cpu().view(torch.int16).numpy().view(np.uint16))
+    scale = float(np.abs(ref).max())
+    assert float(np.abs(got - ref).max()) / scale <= 1e-2
+    assert bool((np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 2e-3 * scale).all())
+    assert not core.swiglu_supported(1, N // 2, K, gs, 4)
+    assert not core.rms_norm_qmm_supported(1, N, K, gs, 4)
