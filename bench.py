@@ -446,6 +446,33 @@ def group_sweep(mq, torch):
     return rows
 
 
+def bits_sweep(mq, torch):
+    """Codes of 2, 3, 5 and 6 bits on the headline shape, one row: the
+    one-row GEMV reads them at their width (32 codes = `bits` words); bytes
+    counted at that width.  The 4- and 8-bit rows are the sweep's."""
+    rows = []
+    K, N, M = 3584, 18944, 1
+    for bits in (2, 3, 5, 6):
+        wbytes = alg_bytes(0, N, K, bits)
+        reps = make_replicas(mq, torch, N, K, bits, max(1, min(16, math.ceil(640e6 / wbytes))),
+                             seed=400)
+        gen = torch.Generator(device="cuda:0").manual_seed(1)
+        x = torch.randn(M, K, generator=gen, device="cuda:0").to(torch.bfloat16)
+
+        def launch(i, x=x, reps=reps, bits=bits):
+            wq, s, b = reps[i % len(reps)]
+            mq.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits=bits)
+
+        ms, _ = time_graph(torch, launch, 64, warmup=2, reps=4)
+        by = alg_bytes(M, N, K, bits)
+        gbs = by / (ms * 1e-3) / 1e9
+        rows.append({"bits": bits, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2),
+                     "GBps": round(gbs, 1), "bound": "hbm", "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del reps, x
+        torch.cuda.empty_cache()
+    return rows
+
+
 def gather_sweep(mq, torch, eager_launches: int = 0):
     """The expert GEMMs of one MoE layer's prefill at the Qwen3-30B-A3B shape:
     8 x 512 tokens routed to 8 of 128 experts (uniform random), the 32768
@@ -619,6 +646,7 @@ def main():
     if not args.no_sweep:
         line["sweep"] = sweep(mq, torch)
         line["group_sweep"] = group_sweep(mq, torch)
+        line["bits_sweep"] = bits_sweep(mq, torch)
         line["gather_sweep"] = gather_sweep(mq, torch)
     if not args.no_cpu:
         wq, s, b = replicas[0]

@@ -19,13 +19,16 @@
  *     3 bytes, a code possibly straddling two words); scales and biases
  *     bfloat16 [rows, K/group_size]; w = scale*q + bias.
  *   - Supported here: bits 2, 3, 4, 5, 6 and 8 with group_size 32, 64 or 128
- *     for mq_quantize, mq_dequantize and mq_embedding_lookup.  The matmul
- *     kernels read 4- and 8-bit codes: mq_quantized_matmul_ws runs 2/3/5/6
- *     bits by rewriting the codes one byte each into its workspace
- *     (mq_quantized_matmul_workspace counts those bytes) and running the 8-bit
- *     kernels with the same scales and biases; the other matmul entry points
- *     return MQ_ERR_UNSUPPORTED for them (mq_repack_codes_u8 converts a
- *     matrix once, e.g. at load time, to call them with bits = 8).  transpose
+ *     for mq_quantize, mq_dequantize and mq_embedding_lookup.  At 2/3/5/6
+ *     bits mq_quantized_matmul[_ws] reads one-row products' codes at their
+ *     width (K a multiple of 512 from 1024 to 4096, or 13824/14336/18944 at
+ *     group size 64/128: no workspace); other shapes it runs by rewriting
+ *     the codes one byte each into its workspace
+ *     (mq_quantized_matmul_workspace counts those bytes) and running the
+ *     8-bit kernels with the same scales and biases.  The other matmul entry
+ *     points read 4- and 8-bit codes and return MQ_ERR_UNSUPPORTED for the
+ *     rest (mq_repack_codes_u8 converts a matrix once, e.g. at load time,
+ *     to call them with bits = 8).  transpose
  *     = 0 returns MQ_ERR_UNSUPPORTED; anything MLX itself rejects returns
  *     MQ_ERR_INVALID.
  *     Every matmul entry point, fused ones included, takes group sizes 32,

@@ -15,9 +15,11 @@ q/k norms; models/lfm2.py:569-591 for per-path quantization overrides):
   [N, K*bits/32], `{path}.scales` / `{path}.biases` [N, K/group_size];
   mixture-of-experts banks are stacked per expert,
   `mlp.switch_mlp.{gate,up,down}_proj.*` [E, N, ...] (or per-expert
-  `mlp.experts.{e}.*`, stacked on load); codes at 2, 3, 5 or 6 bits are
-  rewritten one byte each on a GPU device (the layer then runs at 8 bits with
-  the same scales and biases: the same dequantized weights).
+  `mlp.experts.{e}.*`, stacked on load); codes at 2, 3, 5 or 6 bits stay
+  packed in linear layers (one-row matmuls read them at their width, larger
+  ones rewrite them one byte each per call) and are rewritten one byte each
+  once, on a GPU device, in expert banks (the gather kernels read 4- and
+  8-bit codes; same scales and biases: the same dequantized weights).
 
 Tensors are read with safetensors (no pickle), straight to the target device.
 Modules stored without `{path}.scales` (and every module of a checkpoint
@@ -224,11 +226,6 @@ class _Builder:
             raise WeightArtifactValidationError(
                 f"{path}: weight {tuple(wq.shape)} does not hold {K} {bits}-bit codes per row")
         wq = wq.view(torch.int32) if wq.dtype == torch.uint32 else wq
-        if bits not in (4, 8) and wq.is_cuda:
-            # the matmul kernels read 4- and 8-bit codes: 2/3/5/6-bit codes are
-            # rewritten one byte each, once here (same scales and biases, so
-            # the same dequantized weights)
-            wq, bits = core.repack_codes_u8(wq.contiguous(), bits), 8
         return QLinear(wq.contiguous(), s, b, bias, gs, bits)
 
     def experts(self, path: str, proj: str) -> QExperts:
@@ -247,7 +244,12 @@ class _Builder:
             ql = QLinear(torch.stack([p.wq for p in parts]), torch.stack([p.scales for p in parts]),
                          torch.stack([p.biases for p in parts]), None, parts[0].group_size,
                          parts[0].bits)
-        return QExperts(ql.wq, ql.scales, ql.biases, ql.group_size, ql.bits)
+        wq, bits = ql.wq, ql.bits
+        if bits not in (4, 8) and wq.is_cuda:
+            # the gather kernels read 4- and 8-bit codes: a 2/3/5/6-bit bank is
+            # rewritten one byte each, once here
+            wq, bits = core.repack_codes_u8(wq.contiguous(), bits), 8
+        return QExperts(wq, ql.scales, ql.biases, ql.group_size, bits)
 
 
 def _qparams(ql) -> tuple[int, int] | None:

@@ -203,8 +203,10 @@ size_t mq_quantized_matmul_workspace(int64_t M, int64_t N, int64_t K, int group_
                                      int bits) {
   if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
   if ((bits == 2 || bits == 3 || bits == 5 || bits == 6) &&
-      (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0)
+      (group_size == 32 || group_size == 64 || group_size == 128) && K % group_size == 0) {
+    if (mq::qmvs_fits(M, N, K, bits, group_size)) return 0;  // read at their width
     return repack_bytes(N, K) + mq_quantized_matmul_workspace(M, N, K, group_size, 8);
+  }
   if (!word_shape(K, group_size, bits)) return 0;
   switch (dense_path(M, N, K, group_size, bits)) {
     case Dense::kSkinny: return mq::qmms_workspace_bytes(M, N, K, bits);
@@ -454,6 +456,10 @@ int mq_quantized_matmul_ws(const mq_bf16* x, const uint32_t* wq, const mq_bf16* 
   if ((M + 127) / 128 > 65535)
     return fail(MQ_ERR_UNSUPPORTED, "[%s] M=%lld exceeds the launch grid (8388480 rows).", op,
                 (long long)M);
+  if (stream_bits(bits) && mq::qmvs_fits(M, N, K, bits, group_size))
+    return hip_status(mq::launch_qmvs(x, wq, scales, biases, bias_vec, y, N, K, bits,
+                                      group_size, stream),
+                      op);
   if (stream_bits(bits)) {
     // codes rewritten one byte each into the workspace, then the 8-bit
     // kernels with the rest of it (same scales and biases: the dequantized

@@ -71,6 +71,13 @@ bool qmv1_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
 // ... and where its plain form (no SwiGLU, no RMSNorm input) runs: also the
 // long rows of down projections.
 bool qmv1_plain_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
+// The same kernel's plain form on 2, 3, 5 or 6-bit codes read at their width
+// (a 32-code chunk is `bits` whole words of the row's bit stream): one row,
+// the K values of qmv1_plain_fits.
+bool qmvs_fits(int64_t M, int64_t rows, int64_t K, int bits, int group_size);
+hipError_t launch_qmvs(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
+                       const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t N,
+                       int64_t K, int bits, int group_size, hipStream_t stream);
 hipError_t launch_qmv1(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                        const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t N,
                        int64_t K, int group_size, bool swiglu, const qmv::NormIn* nrm,

@@ -7,13 +7,14 @@ the oracle:
   the embedding lookup and the on-grid known-answer fixtures: bit-exact;
 * repack_codes_u8: the one-byte codes dequantize at 8 bits to exactly what the
   stream codes dequantize to;
-* quantized_matmul (the codes repacked into the call's workspace, then the
-  8-bit kernels) at GEMV, skinny and large-M rows, and gather_qmm sorted and
-  unsorted: norm-wise relative error <= 1e-2 against the oracle (bfloat16
-  output, float32 accumulation);
+* quantized_matmul at one row (the codes read at their width, no workspace)
+  and at skinny and large-M rows (the codes repacked into the call's
+  workspace, then the 8-bit kernels), and gather_qmm sorted and unsorted:
+  norm-wise relative error <= 1e-2 against the oracle (bfloat16 output,
+  float32 accumulation); the one-row kernel also per element;
 * a 2-layer Qwen2-shaped decoder and a Qwen3-MoE-shaped one at these widths
   against the float32 restatement, and a 3-bit checkpoint through the loader
-  (which repacks the codes once at load).
+  (which keeps linear layers' codes packed and repacks expert banks).
 """
 
 from __future__ import annotations
@@ -114,6 +115,34 @@ def test_quantized_matmul_parity(mq, orc, bits, M):
     assert_close(y, orc.qmm(x, wq, s, b, 64, bits, bias=bias))
 
 
+@pytest.mark.parametrize("bits", WIDTHS)
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("K,N", [(1024, 1000), (3584, 4608), (4096, 600), (18944, 512)])
+def test_one_row_at_code_width(mq, orc, bits, gs, K, N):
+    """One-row matmuls read the codes at their width -- 32 codes are `bits`
+    whole words of the row's bit stream -- with no workspace (K 1024-4096 at
+    every group size, the long row K = 18944 at group 64/128; K = 18944 at
+    group 32 takes the repacking path): every output against the oracle,
+    norm-wise within 1e-2 and each element within its bfloat16 rounding
+    (2^-8 relative) plus 2e-3 of the largest output; 1000 and 600 rows leave
+    partial blocks."""
+    L = mq._lib.lib()
+    native = not (K == 18944 and gs == 32)
+    assert (L.mq_quantized_matmul_workspace(1, N, K, gs, bits) == 0) == native
+    print(f"one row at {bits} bits: K={K}, N={N}, group {gs}", flush=True)
+    rng = np.random.default_rng(7000 + 10 * bits + gs + K + N)
+    wq, s, b = orc.quantize(rand_bf16(orc, rng, (N, K), 0.02), gs, bits)
+    x = rand_bf16(orc, rng, (1, K), 1.0)
+    bias = rand_bf16(orc, rng, (N,), 0.5)
+    y = mq.quantized_matmul(bf16_dev(x), u32_dev(wq), bf16_dev(s), bf16_dev(b), True, gs, bits,
+                            bias=bf16_dev(bias))
+    ref = orc.qmm(x, wq, s, b, gs, bits, bias=bias)
+    got = orc.bf16_to_f32(bits_host(y))
+    scale = float(np.abs(ref).max())
+    assert float(np.abs(got - ref).max()) / scale <= 1e-2
+    assert bool((np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 2e-3 * scale).all())
+
+
 @pytest.mark.parametrize("bits,gs", [(3, 32), (6, 128)])
 def test_quantized_matmul_group_sizes(mq, orc, bits, gs):
     rng = np.random.default_rng(950 + bits + gs)
@@ -203,11 +232,11 @@ def test_moe_decoder_bits():
     _forced_routing_check(mq, m, ids, 6, "qwen3-moe 3-bit")
 
 
-def test_three_bit_checkpoint_loads_repacked(tmp_path):
+def test_three_bit_checkpoint_loads(tmp_path):
     """A checkpoint whose config.json says bits 3 (and one path 6): the loader
-    rewrites the codes one byte each at load (the layers run the 8-bit
-    kernels, fused entries included); logits against the 3-bit model it was
-    saved from and against the float32 restatement."""
+    keeps the linear layers' codes packed (decode's one-row matmuls read them
+    at their width; prefill repacks them per call); logits against the 3-bit
+    model it was saved from and against the float32 restatement."""
     mq = importlib.import_module("mlx-server-runtime_amd")
     q2 = importlib.import_module("mlx-server-runtime_amd.qwen2")
     ck = importlib.import_module("mlx-server-runtime_amd.checkpoint")
@@ -220,7 +249,7 @@ def test_three_bit_checkpoint_loads_repacked(tmp_path):
     m.layers[1].down = q2.QLinear(*mq.quantize(w_d, 64, 6), None, 64, 6)
     ck.save(m, tmp_path)
     m2 = ck.load(tmp_path, device=DEV)
-    assert m2.layers[0].qkv.bits == 8 and m2.layers[1].down.bits == 8
+    assert m2.layers[0].qkv.bits == 3 and m2.layers[1].down.bits == 6
     ids = torch.randint(0, 1000, (2, 20), generator=gen, device=DEV)
     a = m.prefill(ids, m.new_cache(2, 20), all_positions=True)
     b = m2.prefill(ids, m2.new_cache(2, 20), all_positions=True)
