@@ -107,6 +107,31 @@ __device__ __forceinline__ uint32_t stream_pair(const uint32_t (&w)[BITS], int c
   return (stream_code<BITS>(w, c + 4) << 16) | stream_code<BITS>(w, c) | 0x43004300u;
 }
 
+// The four pairs (c, c + 4), c = 8g .. 8g + 3, of 8-code group g.  2 and 3
+// bits: the group's 16 / 24 bits are spread so that its upper four codes
+// sit 16 bits above the lower four (bits between them are never read), and
+// each pair is then one shift and one mask-and-magic, as for 4 bits.  5 and 6
+// bits: four codes are too wide for that, a bit-field extract per code.
+template <int BITS>
+__device__ __forceinline__ void stream_pairs(const uint32_t (&w)[BITS], int g, uint32_t (&p)[4]) {
+  if constexpr (BITS == 2) {
+    const uint32_t f = (g & 1) ? w[g >> 1] >> 16 : w[g >> 1] & 0xffffu;  // codes at 2i
+    const uint32_t v = (f << 8) | f;  // code i + 4 at bit 16 + 2i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = ((v >> (2 * i)) & 0x00030003u) | 0x43004300u;
+  } else if constexpr (BITS == 3) {
+    const int bit = 24 * g, wi = bit >> 5, sh = bit & 31;  // the group's 24 bits
+    const uint32_t f = sh + 24 <= 32 ? w[wi] >> sh : __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh);
+    // bits 0..11: codes 0..3; bits 16..27: codes 4..7 (f << 4's)
+    const uint32_t v = (f & 0xfffu) | ((f << 4) & 0xfffff000u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = ((v >> (3 * i)) & 0x00070007u) | 0x43004300u;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = stream_pair<BITS>(w, 8 * g + i);
+  }
+}
+
 // 100 MHz constant clock (s_memrealtime), read into scalar registers.
 __device__ __forceinline__ uint64_t realtime() {
   uint64_t t;
@@ -304,9 +329,10 @@ __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const u
         d = dot2_bf16(nib.pair(wd >> 8), xv[wi][2], d);
         d = dot2_bf16(nib.pair(wd >> 12), xv[wi][3], d);
       } else {
+        uint32_t pr[4];
+        stream_pairs<BITS>(ws[j % RING], wi, pr);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          d = dot2_bf16(stream_pair<BITS>(ws[j % RING], 8 * wi + i), xv[wi][i], d);
+        for (int i = 0; i < 4; ++i) d = dot2_bf16(pr[i], xv[wi][i], d);
       }
     }
     dd[j] = d;
