@@ -150,16 +150,21 @@ struct Qmm4Args {
 
 // Gather tile map, computed by each block from the expert segments: segment e
 // holds batches [start_e, start_(e+1)), i.e. ceil((start_(e+1) - start_e) * Mb
-// / BM) row tiles; the block's row tile rt is the (rt - pre_e)-th tile of the
-// expert e with pre_e <= rt < pre_(e+1) (exclusive prefix sums).  Out: e (-1
-// past the last tile), first row, valid rows, and lo/hi: the batches outside
-// [lo, hi) name no expert (ids < 0 sort first, ids >= E last) and give zeros.
+// / BM) row tiles, R in all; row tile rt is the (rt - pre_e)-th tile of the
+// expert e with pre_e <= rt < pre_(e+1) (exclusive prefix sums).  XCD x
+// takes the contiguous row tiles [x P, (x + 1) P), P = ceil(R / 8), in
+// expert order, so an expert's tiles share one L2 (its bank fetched once)
+// unless they straddle two ranges; the block is its XCD's row-tile slot
+// `slot`.  Out: e (-1 for a slot past its range), first row, valid rows,
+// and lo/hi: the batches outside [lo, hi) name no expert (ids < 0 sort
+// first, ids >= E last) and give zeros, written by XCD 0's slot P (`zero`).
 struct GatherTile {
-  int e, row0, rows, lo, hi, total;
+  int e, row0, rows, lo, hi;
+  bool zero;
 };
 
 template <int kThreads>
-__device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
+__device__ GatherTile gather_tile(const Qmm4Args& a, int xcd, int slot, int* sh) {
   // sh: LDS ints, 2 * (E + 1) + 10 of them; E <= 4 * kThreads
   int* start = sh;              // [E + 1] segment starts (batches)
   int* pre = sh + a.E + 1;      // [E + 1] exclusive tile prefix
@@ -231,6 +236,8 @@ __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
   if (tid == 0) misc[9] = -1;
   __syncthreads();
   const int total = pre[a.E];
+  const int per = (total + 7) / 8;  // row tiles per XCD
+  const int rt = slot < per ? xcd * per + slot : total;  // total: no tile
   for (int e = tid; e < a.E; e += kThreads)
     if (pre[e] <= rt && rt < pre[e + 1]) misc[9] = e;
   __syncthreads();
@@ -238,7 +245,7 @@ __device__ GatherTile gather_tile(const Qmm4Args& a, int rt, int* sh) {
   g.e = misc[9];
   g.lo = misc[0];
   g.hi = start[a.E];
-  g.total = total;
+  g.zero = xcd == 0 && slot == per;
   g.row0 = 0;
   g.rows = 0;
   if (g.e >= 0) {
@@ -303,17 +310,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
   const bool sk = !GATHER && (int)blockIdx.x >= a.dp_blocks;
   int sk_f = 0, sk_end = 0;
   if constexpr (GATHER) {
-    // Blocks go to the 8 XCDs round-robin.  Each run of 8 * tiles_n blocks
-    // covers 8 row tiles, row tile 8g + x on XCD x with all its column tiles
-    // (the same expert and gathered x rows in one L2); the row tiles past the
-    // last one (the grid reserves an upper bound) are spread over every XCD.
-    const int run = 8 * a.tiles_n;
-    const int rt = (blockIdx.x / run) * 8 + blockIdx.x % 8;
-    bn = (blockIdx.x % run) / 8;
-    const GatherTile g = gather_tile<kThreads>(a, rt, reinterpret_cast<int*>(lds));
+    // Blocks go to the 8 XCDs round-robin: block b runs on XCD b % 8 as its
+    // (b / 8)-th block there, i.e. row-tile slot (b / 8) / tiles_n, column
+    // tile (b / 8) % tiles_n -- each row tile's column tiles consecutive on
+    // one XCD, the XCD's row tiles a contiguous run of the expert order
+    // (gather_tile).  The grid reserves at least one slot per XCD past its
+    // run.
+    const int xcd = (int)blockIdx.x % 8, j = (int)blockIdx.x / 8;
+    bn = j % a.tiles_n;
+    const GatherTile g =
+        gather_tile<kThreads>(a, xcd, j / a.tiles_n, reinterpret_cast<int*>(lds));
     if (g.e < 0) {
-      // the first spare row tile zeroes the rows whose id names no expert
-      if (rt == g.total) {
+      // one spare slot zeroes the rows whose id names no expert
+      if (g.zero) {
         const int n = bn * kOutCols + tid;
         if (tid < kOutCols && n < N) {
           for (int p = 0; p < g.lo * a.Mb; ++p) a.y[(int64_t)p * N + n] = 0;
@@ -923,10 +932,11 @@ hipError_t launch_qmm4_gather(const uint16_t* x, const int32_t* lhs, const int32
   a.chunks = a.chunks_per_split = (int)sb_chunks(K, group_size);
   a.lhs = lhs, a.rhs = rhs, a.seg = seg;
   a.T = (int)T, a.Mb = (int)Mb, a.E = (int)E, a.x_batches = (int)x_batches;
-  // every expert's segment adds at most one partial tile; one spare row tile
-  // zeroes the rows whose id names no expert
-  int64_t row_tiles = (T * Mb + BM - 1) / BM + std::min(E, T) + 1;
-  row_tiles = (row_tiles + 7) / 8 * 8;  // whole runs of 8 row tiles (one per XCD)
+  // every expert's segment adds at most one partial tile: R <= bound row
+  // tiles in all; each XCD gets ceil(R / 8) of them and one more slot (the
+  // spare that zeroes the rows whose id names no expert)
+  const int64_t bound = (T * Mb + BM - 1) / BM + std::min(E, T);
+  const int64_t row_tiles = ((bound + 7) / 8 + 1) * 8;
   const dim3 grid((unsigned)(row_tiles * a.tiles_n));
   return swiglu ? launch<true, true>(a, bits, group_size, grid, stream)
                 : launch<true, false>(a, bits, group_size, grid, stream);
