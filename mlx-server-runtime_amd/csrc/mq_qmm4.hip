@@ -509,6 +509,104 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
       }
     };
 
+    // ---- short gather tiles: at most 64 valid rows (two MFMA row tiles) ----
+    // Such a tile (an expert segment's last few rows) does little MFMA work
+    // per step, so its steps wait on memory latency: with the loops below a
+    // 32-row tile cost 84 % of a full one.  It lays the LDS out differently:
+    // eight 8 KiB x stages of 64 rows, x six steps ahead, and per wave a ring
+    // of two 4-step code blocks (its 32 columns x 128 bytes, DMA'd as 8
+    // columns x 128 bytes per operation), the next block four steps ahead.
+    // Every load is a DMA, so each barrier's count is exact.  Dequantization
+    // and MFMA order are those of the loops below: bit-identical results.
+    auto short_tile = [&]() {
+      constexpr int XS = 8, XA = 6;      // x stages, x DMAs ahead
+      constexpr int kShX = 64 * BK * 2;  // an x stage: 64 rows
+      constexpr int kShCode = 32 * 128;  // a wave's 4-step code block
+      static_assert(XS * kShX + WAVES * 2 * kShCode <= kSbBase, "short-tile LDS");
+      char* const cring = lds + XS * kShX + wave * (2 * kShCode);
+      // x: wave w fills rows 8w .. 8w + 7 of a stage (the swizzle above)
+      uint32_t xo = kOutOfRange;
+      {
+        const int row = 8 * wave + (l >> 3);
+        const uint32_t chunk = (uint32_t)(((l & 7) ^ ((row >> 1) & 7)) * 8);
+        if (row < rows_valid) {
+          const int p = out_row0 + row;
+          const int t = p / a.Mb, m = p - t * a.Mb;
+          const int xb = a.lhs ? a.lhs[t] : t;
+          if (xb >= 0 && xb < a.x_batches)
+            xo = ((uint32_t)(xb * a.Mb + m) * (uint32_t)K + chunk) * 2u;
+        }
+      }
+      // codes: operation j fills columns 8j .. 8j + 7 of the wave's 32; lane l
+      // reads piece (l % 8) ^ f(c) of column c = 8j + l / 8, f(c) = (c >> 1) &
+      // 7, so column c holds logical piece p at c * 128 + 16 (p ^ f(c)) and 8
+      // lanes reading one piece of 8 columns hit 8 distinct bank groups
+      uint32_t cdo[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 8 * j + (l >> 3);
+        int oc;
+        const int n = wrow(wave * 32 + c, oc);
+        cdo[j] = oc < N ? (uint32_t)n * (uint32_t)(K / 2) + 16u * (uint32_t)((l & 7) ^ ((c >> 1) & 7))
+                        : kOutOfRange;
+      }
+      // this lane's 16 bytes of step s of a block: logical piece 2s + h
+      const uint32_t cread = (uint32_t)((l & 31) * 128 + 16 * (h ^ ((l >> 1) & 7)));
+      auto dma_code_block = [&](int b) {  // steps 4b .. 4b + 3 into slot b & 1
+        char* slot = cring + (b & 1) * kShCode;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16(wrs, (lds_t*)(slot + j * 1024), cdo[j] + (uint32_t)b * 128u);
+      };
+      auto dma_x_short = [&](int kt) {
+        dma16(xrs, (lds_t*)(lds + (kt % XS) * kShX + wave * 1024), xo + kt * (BK * 2));
+      };
+      // In issue order a step makes: the next code block's 4 DMAs (steps 4b),
+      // one x DMA, the next chunk's scale/bias DMAs (a chunk's first step).
+      // End of step kt: x of kt + 1 (issued at kt - 5) has at least 9
+      // operations after it; at 4b + 3 the block of 4b + 4 (issued at 4b) has
+      // 4, and a chunk's scales (issued at its first step) have SPC - 1 or
+      // more by the chunk's last step, where the next chunk's are read.
+      dma_sb(c_begin, c_begin & 1);
+      dma_code_block(kt0 / 4);
+#pragma unroll
+      for (int p = 0; p < XA; ++p) dma_x_short(kt0 + p);
+      step_barrier<XA - 1>();
+      for (int c = c_begin; c < c_end; ++c) {
+#pragma unroll 1
+        for (int u0 = 0; u0 < SPC; u0 += kRun) {
+#pragma unroll
+          for (int ui = 0; ui < kRun; ++ui) {
+            const int u = u0 + ui;
+            const int kt = c * SPC + u;
+            if (kt >= kt_end) break;
+            if (ui % 4 == 0) dma_code_block(kt / 4 + 1);
+            dma_x_short(kt + XA);
+            if (u == 0) dma_sb(c + 1, (c + 1) & 1);
+            GroupAffine g[NJ];
+            read_sb(c & 1, group_of(u), g);
+            const u32x4_t q = *reinterpret_cast<const u32x4_t*>(
+                cring + ((kt / 4) & 1) * kShCode + (cread ^ (32u * (uint32_t)(ui & 3))));
+            const uint32_t xa = (uint32_t)(kt % XS) * kShX + aoff;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+              const bf16x8_t bq = dequant8<4>(q[ks], 0u, g[0].s, g[0].b);
+#pragma unroll
+              for (int i = 0; i < 2; ++i)
+                if (i < live)
+                  acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                      *reinterpret_cast<const bf16x8_t*>(lds + (xa ^ (ks << 4)) + i * 4096), bq,
+                      acc[i][0], 0, 0, 0);
+            }
+            if ((ui & 3) == 3) step_barrier<SPC == 4 ? 3 : 4>();
+            else step_barrier<9>();
+          }
+        }
+      }
+    };
+
+    if (GATHER && BITS == 4 && NJ == 1 && live <= 2) {
+      if constexpr (GATHER && BITS == 4 && NJ == 1) short_tile();
+    } else {
     // ---- prologue: codes of this split's first two steps, its first scale
     // chunk, x of its first three steps ----
     load_codes(cw[0], kt0);
@@ -607,6 +705,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qmm4_kernel(const Qmm4Args a) {
     // 224-row masked tile 6 % slower than a full 256-row one).
     if (live <= kRowTiles - 2) k_loop(std::true_type{});
     else k_loop(std::false_type{});
+    }
     // The prefetches of the last steps (past K, unused) must land before the
     // block's LDS is released.
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
