@@ -460,6 +460,40 @@ def test_gather_segments_clamps_caller_offsets(moe, mq):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("K", [2048, 768])
+def test_gather_short_tiles_equal_long_tiles(mq, K):
+    """An expert segment of at most 64 rows runs the segment GEMM's short-tile
+    loop (its own LDS layout and prefetch); the same rows at the head of a
+    100-row segment run the masked full-tile loop.  Each output row depends
+    only on its own x row, so the two must agree bit for bit: segments of 20
+    and 64 rows against the first rows of a 100-row segment of expert 0 (the
+    x rows gathered through lhs), expert 1 keeping 100 rows in every call."""
+    E, N, T = 4, 512, 300
+    g = _gen(K + 5)
+    w = (torch.randn(E * N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wq, sc, bi = (t.reshape(E, N, -1) for t in mq.quantize(w, 64, 4))
+    x = torch.randn(T, 1, K, generator=g, device=DEV).to(torch.bfloat16)
+    src = torch.randperm(T, generator=torch.Generator().manual_seed(K))[:200].to(DEV)
+
+    def run(r0):
+        lhs = torch.cat([src[:r0], src[100:200]]).to(torch.int32).contiguous()
+        rhs = torch.cat([torch.zeros(r0, dtype=torch.int32, device=DEV),
+                         torch.ones(100, dtype=torch.int32, device=DEV)]).contiguous()
+        offs = torch.tensor([0, r0] + [r0 + 100] * (E - 1), dtype=torch.int32, device=DEV)
+        return mq.gather_qmm(x, wq, sc, bi, lhs_indices=lhs, rhs_indices=rhs,
+                             sorted_indices=True, expert_offsets=offs).reshape(-1, N)
+
+    print(f"gather short tiles: K={K}, segments of 100 / 64 / 20 rows", flush=True)
+    full = run(100)
+    ref = x[src[:100], 0].float() @ mq.dequantize(wq[0], sc[0], bi[0], 64, 4).float().t()
+    assert float((full[:100].float() - ref).norm() / ref.norm()) < 1e-2
+    for r0 in (64, 20):
+        short = run(r0)
+        torch.cuda.synchronize()
+        assert torch.equal(short[:r0], full[:r0]), r0
+        assert torch.equal(short[r0:], full[100:]), r0
+
+
 def test_moe_block_odd_group_count(moe, mq):
     """hidden 192 (3 groups of 64 per row): the expert-segment GEMM with the
     SiLU*up epilogue does not take an odd group count, so a sorted prefill
