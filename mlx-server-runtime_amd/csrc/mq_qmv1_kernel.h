@@ -156,7 +156,9 @@ __global__ __launch_bounds__(kBlock) void qmv1_kernel(const uint16_t* x, const u
   constexpr int K = 32 * C;
   constexpr int XU = (4 * C + kBlock - 1) / kBlock;
   constexpr int HALF = RPB / 2;
-  constexpr int D = lookahead(S) < S ? lookahead(S) : S;  // codes issued before the loop
+  // codes issued before the loop; the RMSNorm forms issue every chunk first,
+  // so the weight stream runs while the block reduces the norm
+  constexpr int D = NORM || lookahead(S) >= S ? S : lookahead(S);
   constexpr int SB_WORDS = (RPB * G + G + 1) / 2;     // qmv_kernel's LDS layout (GP = G)
   constexpr int OPS = (SB_WORDS + 63) / 64;           // DMA operations per array
   constexpr int NQ = (2 * OPS + kBlock / 64 - 1) / (kBlock / 64);  // per wave
