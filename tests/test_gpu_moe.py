@@ -460,18 +460,20 @@ def test_gather_segments_clamps_caller_offsets(moe, mq):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("K", [2048, 768])
-def test_gather_short_tiles_equal_long_tiles(mq, K):
+@pytest.mark.parametrize("K,gs", [(2048, 64), (768, 64), (2048, 32), (2048, 128), (768, 128)])
+def test_gather_short_tiles_equal_long_tiles(mq, K, gs):
     """An expert segment of at most 64 rows runs the segment GEMM's short-tile
     loop (its own LDS layout and prefetch); the same rows at the head of a
     100-row segment run the masked full-tile loop.  Each output row depends
     only on its own x row, so the two must agree bit for bit: segments of 20
     and 64 rows against the first rows of a 100-row segment of expert 0 (the
-    x rows gathered through lhs), expert 1 keeping 100 rows in every call."""
+    x rows gathered through lhs), expert 1 keeping 100 rows in every call;
+    group sizes 32/64/128 (8, 16 or 4 steps a scale chunk; K = 768 ends
+    mid-chunk)."""
     E, N, T = 4, 512, 300
-    g = _gen(K + 5)
+    g = _gen(K + gs)
     w = (torch.randn(E * N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
-    wq, sc, bi = (t.reshape(E, N, -1) for t in mq.quantize(w, 64, 4))
+    wq, sc, bi = (t.reshape(E, N, -1) for t in mq.quantize(w, gs, 4))
     x = torch.randn(T, 1, K, generator=g, device=DEV).to(torch.bfloat16)
     src = torch.randperm(T, generator=torch.Generator().manual_seed(K))[:200].to(DEV)
 
@@ -480,12 +482,12 @@ def test_gather_short_tiles_equal_long_tiles(mq, K):
         rhs = torch.cat([torch.zeros(r0, dtype=torch.int32, device=DEV),
                          torch.ones(100, dtype=torch.int32, device=DEV)]).contiguous()
         offs = torch.tensor([0, r0] + [r0 + 100] * (E - 1), dtype=torch.int32, device=DEV)
-        return mq.gather_qmm(x, wq, sc, bi, lhs_indices=lhs, rhs_indices=rhs,
+        return mq.gather_qmm(x, wq, sc, bi, lhs_indices=lhs, rhs_indices=rhs, group_size=gs,
                              sorted_indices=True, expert_offsets=offs).reshape(-1, N)
 
-    print(f"gather short tiles: K={K}, segments of 100 / 64 / 20 rows", flush=True)
+    print(f"gather short tiles: K={K}, group {gs}, segments of 100 / 64 / 20 rows", flush=True)
     full = run(100)
-    ref = x[src[:100], 0].float() @ mq.dequantize(wq[0], sc[0], bi[0], 64, 4).float().t()
+    ref = x[src[:100], 0].float() @ mq.dequantize(wq[0], sc[0], bi[0], gs, 4).float().t()
     assert float((full[:100].float() - ref).norm() / ref.norm()) < 1e-2
     for r0 in (64, 20):
         short = run(r0)
