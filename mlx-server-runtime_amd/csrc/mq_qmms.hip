@@ -28,6 +28,8 @@
 // down projection), K is split over blocks in whole 8-group chunks; each
 // split writes float32 partial sums to a caller-provided workspace and
 // splitk_reduce adds them in a fixed order (results do not depend on timing).
+// Unsplit 32-row plans too wide for one block per CU at 4 waves take blocks of
+// 5-8 column groups, each group's K steps split over two waves (4-bit).
 #include <algorithm>
 #include <type_traits>
 
@@ -63,7 +65,8 @@ __device__ __forceinline__ void dma16(rsrc_t r, lds_t* dst, uint32_t voff) {
 // (bit-identical results): 8-bit 11-25 % faster (M = 16 down projection
 // 26.1 -> 21.2 us, M = 32 3584 x 18944 28.4 -> 21.4 us, M = 128 40.6 ->
 // 36.1 us); 4-bit (32 columns x 32 bytes per instruction) 2-14 % slower at
-// M = 16..256, so 4-bit codes keep the per-lane register loads.
+// M = 16..256, so 4-bit codes keep the per-lane register loads -- except in
+// the K-sliced 10-wave blocks (qmms_kernel's KS), where the DMA is 5 % faster.
 constexpr int kCodeSlots = 4;
 constexpr int kCodeBlock = 32 * 128;
 template <int BITS>
@@ -117,7 +120,16 @@ __device__ __forceinline__ bf16x8_t dequant8(uint32_t w0, uint32_t w1, float s, 
 // GSH: log2(group size / 32) -- group sizes 32, 64, 128.  A lane's codes for
 // a 64-wide step are k = 32h .. 32h + 31 of it (both widths), all in one
 // group, (2 step + h) >> GSH within the chunk of 8 steps.
-template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4, int GSH = 1>
+// KS (2: 4-bit, one unsplit 32-row tile): the block's W waves are W / KS
+// column groups x KS K slices -- wave w takes column group w % (W / KS) and,
+// of every 8-step chunk, the 8 / KS steps of slice w / (W / KS), each slice
+// with x stages of its own; at the end the slices' sums meet in LDS and are
+// added in slice order.  Each code is still dequantized once, but the work of
+// a column group is spread over KS waves (more waves per SIMD, each with less
+// serial work).
+// CDMA: codes by DMA into the per-wave LDS ring (8-bit always; 4-bit with KS 2).
+template <int BITS, int MI, bool PARTIAL, int EPI = 0, int W = 4, int GSH = 1, int KS = 1,
+          bool CDMA = kCodeDma<BITS>>
 __global__ __launch_bounds__(64 * W) void qmms_kernel(
     const uint16_t* x, const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, float* __restrict__ partial,
@@ -132,10 +144,20 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   constexpr int NC = BITS == 4 ? 1 : 2;  // 16-byte code loads per lane per step
   static_assert(EPI == 0 || (MI == 1 && !PARTIAL), "SwiGLU epilogue: one tile, no split");
   static_assert(W == 4 || (MI == 1 && !PARTIAL), "wider blocks: one tile, no split");
+  constexpr int C = W / KS;  // column groups of 32 columns (EPI 1: 16 + 16)
+  static_assert(W % KS == 0 && C >= 4 && (KS == 1 || (KS == 2 && W > 4 && BITS == 4)),
+                "K slices: wide 4-bit plans");
+  static_assert(CDMA || BITS == 4, "8-bit codes come by DMA");
+  // A slice takes SPI consecutive steps of each 8-step chunk: slice sl the
+  // steps 8c + SPI sl .. + SPI - 1 of chunk c.
+  constexpr int SPI = kChunk / KS;
+  constexpr int CSL = KS > 1 ? 3 : kCodeSlots;  // code blocks in a wave's ring
   extern __shared__ u32x4_t smem[];
   char* const lds = reinterpret_cast<char*>(smem);
   const int l = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cg = KS == 1 ? wave : wave % C;  // column group
+  const int sl = KS == 1 ? 0 : wave / C;     // K slice
   const int h = l >> 5;
 
   int blk = blockIdx.x;
@@ -144,7 +166,7 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   const int tm = blk % tiles_m;
   const int split = blk / tiles_m;
   const int Nout = N / 2;  // EPI 1: output columns
-  const int n0 = tn * (EPI == 1 ? 16 * W : 32 * W), m0 = tm * BM;
+  const int n0 = tn * (EPI == 1 ? 16 * C : 32 * C), m0 = tm * BM;
   const int KT = K / BK;
   const int G = K >> (5 + GSH);  // groups per row
   constexpr uint32_t kChunkSB = 32u >> GSH;  // scale (or bias) bytes per chunk of 8 steps
@@ -156,18 +178,19 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   const rsrc_t srs = make_rsrc(scales, (uint64_t)N * G * 2);
   const rsrc_t brs = make_rsrc(biases, (uint64_t)N * G * 2);
 
-  // x DMA: op i of wave w fills rows (4i + w)*8 .. +7 (1 KiB); lane l writes
-  // physical chunk l % 8 of row l / 8, logical chunk (l % 8) ^ ((row >> 1) & 7).
-  // Rows past M lie beyond the descriptor and read as zeros.
+  // x DMA: op i of column group w < 4 fills rows (4i + w)*8 .. +7 (1 KiB) of
+  // its slice's tile; lane l writes physical chunk l % 8 of row l / 8,
+  // logical chunk (l % 8) ^ ((row >> 1) & 7).  Rows past M lie beyond the
+  // descriptor and read as zeros.
   uint32_t xoff[MI];
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-    const int row = (i * 4 + wave) * 8 + (l >> 3);
+    const int row = (i * 4 + cg) * 8 + (l >> 3);
     xoff[i] = (uint32_t)((m0 + row) * K + (((l & 7) ^ ((row >> 1) & 7)) * 8)) * 2;
   }
   // This lane's column; columns past N lie beyond the descriptors (zeros).
-  const int n = EPI == 1 ? ((l & 16) ? Nout : 0) + n0 + wave * 16 + (l & 15)
-                         : n0 + wave * 32 + (l & 31);
+  const int n = EPI == 1 ? ((l & 16) ? Nout : 0) + n0 + cg * 16 + (l & 15)
+                         : n0 + cg * 32 + (l & 31);
   const uint32_t coff = (uint32_t)n * (uint32_t)(K * BITS / 8) + h * CB;
   const uint32_t soff = (uint32_t)n * (uint32_t)G * 2;
   // A fragment: row 32i + l % 32, logical chunk 4h + ks at (4h + ks) ^ f(row).
@@ -182,40 +205,43 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   // at the end of the step before (ahead of its barrier), so no LDS latency
   // sits between a barrier and the next step's dequantization.
   constexpr int QS = 128 / (BK * BITS / 8);  // K steps per code block
+  // A slice's code blocks are numbered in its own order, BPC per chunk:
+  // slice block b of chunk b / BPC is K block KS b + sl (KS 1: b itself).
+  constexpr int BPC = SPI / QS;
   // blocks DMA'd ahead: QS * (DA - 1) > P, so the wait for step kt's x tile
   // (issued P steps before kt) also covers the code block of step kt + 1
   constexpr int DA = 1 + (P + QS) / QS;
-  static_assert(!kCodeDma<BITS> || (DA < kCodeSlots && kChunk % QS == 0 && QS * NC == 4),
-                "code ring");
-  char* const cring = lds + S * kXStage + wave * (kCodeSlots * kCodeBlock);
+  static_assert(!CDMA || (DA < CSL && SPI % QS == 0 && QS * NC == 4), "code ring");
+  char* const cring = lds + S * KS * kXStage + wave * (CSL * kCodeBlock);
   uint32_t cdoff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int c = 8 * j + (l >> 3);
-    const int col = EPI == 1 ? ((c & 16) ? Nout : 0) + n0 + wave * 16 + (c & 15) : n0 + wave * 32 + c;
+    const int col = EPI == 1 ? ((c & 16) ? Nout : 0) + n0 + cg * 16 + (c & 15) : n0 + cg * 32 + c;
     cdoff[j] = (uint32_t)col * (uint32_t)(K * BITS / 8) + 16u * (uint32_t)((l & 7) ^ ((c >> 1) & 7));
   }
   const uint32_t cread =
       (uint32_t)((l & 31) * 128 + 16 * ((BITS == 4 ? h : 2 * h) ^ ((l >> 1) & 7)));
-  auto read_codes = [&](u32x4_t (&q)[NC], int qb, int s) {  // step s of block qb
-    const char* slot = cring + (qb & (kCodeSlots - 1)) * kCodeBlock;
+  auto read_codes = [&](u32x4_t (&q)[NC], int qb, int s) {  // step s of slice block qb
+    const char* slot = cring + (qb % CSL) * kCodeBlock;
 #pragma unroll
     for (int e = 0; e < NC; ++e)
       q[e] = *reinterpret_cast<const u32x4_t*>(
           slot + (cread ^ (BITS == 4 ? 32 * s : 64 * s + 16 * e)));
   };
-  auto dma_codes = [&](int qb, int j0) {  // ops j0 .. j0 + NC - 1 of block qb
+  auto dma_codes = [&](int qb, int j0) {  // ops j0 .. j0 + NC - 1 of slice block qb
 #pragma unroll
     for (int p = 0; p < NC; ++p)
-      dma16<kBufNT>(wrs, (lds_t*)(cring + (qb & (kCodeSlots - 1)) * kCodeBlock + (j0 + p) * 1024),
-                    cdoff[j0 + p] + (uint32_t)qb * 128u);
+      dma16<kBufNT>(wrs, (lds_t*)(cring + (qb % CSL) * kCodeBlock + (j0 + p) * 1024),
+                    cdoff[j0 + p] + (uint32_t)(KS * qb + sl) * 128u);
   };
 
   auto dma_x = [&](int kt, int stage) {
-    if (W > 4 && wave >= 4) return;  // uniform
+    if (W > 4 && cg >= 4) return;  // uniform
 #pragma unroll
     for (int i = 0; i < MI; ++i)
-      dma16(xrs, (lds_t*)(lds + stage * kXStage + (i * 4 + wave) * 1024), xoff[i] + kt * (BK * 2));
+      dma16(xrs, (lds_t*)(lds + (stage * KS + sl) * kXStage + (i * 4 + cg) * 1024),
+            xoff[i] + kt * (BK * 2));
   };
   auto load_codes = [&](u32x4_t (&cw)[NC], int kt) {
     __asm__ volatile("" ::: "memory");
@@ -242,7 +268,7 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   // leaves at most the QS * (DA - 1) - 1 steps of NC ops after it in flight
   // (the prologue's blocks are followed by more).
   constexpr int kCodeOnly = (QS * (DA - 1) - 1) * NC;
-  static_assert(!kCodeDma<BITS> || W <= 4 || (P - 1) * MI <= (DA - 1) * 4,
+  static_assert(!CDMA || W <= 4 || (P - 1) * MI <= (DA - 1) * 4,
                 "prologue wait covers block 0");
   // the barrier of step u of a split's first chunk (u is a constant after
   // the unrolling, so the switch folds away)
@@ -267,7 +293,6 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
     for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
 
   // ---- prologue: codes of the first kPrefetch steps, x of the first P ----
-  const int kt0 = c_begin * kChunk;
   // a chunk's scales and biases for this lane's column: 16 (GSH 0), 8 or 4
   // entries
   auto load_sb = [&](u32x4_t (&v)[2], const rsrc_t& r, int c) {
@@ -282,58 +307,61 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
       v[0] = u32x4_t{t[0], t[1], 0u, 0u};
     }
   };
-  // the entry of step u (a compile-time constant after unrolling) for lane half h
+  // the entry of the slice's step u (a compile-time constant after
+  // unrolling) of a chunk -- step e = SPI sl + u of the chunk -- for lane
+  // half h: group 2e + h, e or e / 2
   auto sb_entry = [&](const u32x4_t (&v)[2], int u) -> float {
     uint32_t d;
     int half;
     if constexpr (GSH == 0) {
-      d = v[u >> 2][u & 3];
+      d = KS > 1 ? (sl ? v[1][u] : v[0][u]) : v[u >> 2][u & 3];
       half = h;
     } else if constexpr (GSH == 1) {
-      d = v[0][u >> 1];
+      d = KS > 1 ? (sl ? v[0][2 + (u >> 1)] : v[0][u >> 1]) : v[0][u >> 1];
       half = u & 1;
     } else {
-      d = v[0][u >> 2];
+      d = KS > 1 ? (sl ? v[0][1] : v[0][0]) : v[0][u >> 2];
       half = (u >> 1) & 1;
     }
     return half ? hi_bf16(d) : lo_bf16(d);
   };
+  // the slice's step u of chunk c (u past the chunk: of the chunks after it)
+  auto step_at = [&](int c, int u) { return (c + u / SPI) * kChunk + SPI * sl + u % SPI; };
   u32x4_t sv[2], bv[2];
   load_sb(sv, srs, c_begin);
   load_sb(bv, brs, c_begin);
-  u32x4_t cw[kCodeDma<BITS> ? 1 : kPrefetch][NC];
-  if constexpr (kCodeDma<BITS>) {
+  u32x4_t cw[CDMA ? 1 : kPrefetch][NC];
+  if constexpr (CDMA) {
 #pragma unroll
     for (int b = 0; b < DA; ++b)
 #pragma unroll
-      for (int j = 0; j < 4; j += NC) dma_codes(kt0 / QS + b, j);
+      for (int j = 0; j < 4; j += NC) dma_codes(c_begin * BPC + b, j);
   } else {
 #pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) load_codes(cw[p], kt0 + p);
+    for (int p = 0; p < kPrefetch; ++p) load_codes(cw[p], step_at(c_begin, p));
   }
 #pragma unroll
-  for (int p = 0; p < P; ++p) dma_x(kt0 + p, p);
+  for (int p = 0; p < P; ++p) dma_x(step_at(c_begin, p), p);
   step_barrier<(P - 1) * MI>();
-  if constexpr (kCodeDma<BITS>) read_codes(cw[0], kt0 / QS, 0);
+  if constexpr (CDMA) read_codes(cw[0], c_begin * BPC, 0);
 
   int st = 0;  // stage of the current step's x tile
   for (int c = c_begin; c < c_end; ++c) {
     u32x4_t svn[2], bvn[2];
 #pragma unroll
-    for (int u = 0; u < kChunk; ++u) {
-      const int kt = c * kChunk + u;
+    for (int u = 0; u < SPI; ++u) {
       if (u == 0) {
         __asm__ volatile("" ::: "memory");
         load_sb(svn, srs, c + 1);
         load_sb(bvn, brs, c + 1);
         __asm__ volatile("" ::: "memory");
       }
-      dma_x(kt + P, (st + P) & (S - 1));
+      dma_x(step_at(c, u + P), (st + P) & (S - 1));
 
       const float s = sb_entry(sv, u);
       const float b = sb_entry(bv, u);
-      const uint32_t xa = st * kXStage + aoff;
-      u32x4_t (&q)[NC] = cw[kCodeDma<BITS> ? 0 : u % kPrefetch];
+      const uint32_t xa = (st * KS + sl) * kXStage + aoff;
+      u32x4_t (&q)[NC] = cw[CDMA ? 0 : u % kPrefetch];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         bf16x8_t a[MI];
@@ -351,13 +379,13 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
       // refill the slot just consumed with the codes kPrefetch steps ahead
       // (by DMA: the next step's codes from the ring, then this step's share
       // of the block DA ahead)
-      if constexpr (kCodeDma<BITS>) {
-        read_codes(q, c * (kChunk / QS) + (u + 1) / QS, (u + 1) % QS);
-        dma_codes(c * (kChunk / QS) + u / QS + DA, (u % QS) * NC);
+      if constexpr (CDMA) {
+        read_codes(q, c * BPC + (u + 1) / QS, (u + 1) % QS);
+        dma_codes(c * BPC + u / QS + DA, (u % QS) * NC);
       } else {
-        load_codes(q, kt + kPrefetch);
+        load_codes(q, step_at(c, u + kPrefetch));
       }
-      if (kCodeDma<BITS> && W > 4 && wave >= 4) step_barrier<kCodeOnly>();  // uniform
+      if (CDMA && W > 4 && cg >= 4) step_barrier<kCodeOnly>();  // uniform
       else if (c == c_begin) first_barrier(u);
       else step_barrier<kInFlight>();
       st = (st + 1) & (S - 1);
@@ -371,11 +399,26 @@ __global__ __launch_bounds__(64 * W) void qmms_kernel(
   }
   // Prefetches past the split's range must land before the LDS is released.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (KS > 1) {
+    // slice 1's sums to LDS (over the x stages, read by every wave by now),
+    // added to slice 0's in that order; slice 0 stores
+    static_assert(C * 16 * 64 * 4 <= kXStages * KS * kXStage, "slice sums fit the x stages");
+    float* red = reinterpret_cast<float*>(lds) + cg * 16 * 64 + l;
+    __syncthreads();
+    if (sl == 1) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[v * 64] = acc[0][v];
+    }
+    __syncthreads();
+    if (sl != 0) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[0][v] += red[v * 64];
+  }
 
   // ---- epilogue: D[m][n], lane holds column l % 32, rows 8(v/4) + 4(l/32) + v%4 ----
   if constexpr (EPI == 1) {
     // lane l ^ 16 holds the up column of gate lane l (same rows)
-    const int cl = n0 + wave * 16 + (l & 15);
+    const int cl = n0 + cg * 16 + (l & 15);
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][v]));
@@ -567,6 +610,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_add_norm(
 
 struct Plan {
   int mi, waves, tiles_n, tiles_m, splits, chunks_per_split;
+  int ks;  // K slices per column group (qmms_kernel's KS): waves * ks waves a block
 };
 
 Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
@@ -617,12 +661,18 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   // 36.9 us, as 40 CUs run two blocks, where 32768 rows in 256 blocks take
   // 22.2 us.
   p.waves = 4;
+  p.ks = 1;
   if (p.mi == 1 && p.splits == 1 && base > 256) {
     for (const int w : {5, 6, 8}) {
       const int t = (int)((N + 32 * w - 1) / (32 * w));
       if (t <= 256) {
         p.waves = w;
         p.tiles_n = t;
+        // 4-bit: two waves per column group, each on half of every chunk's
+        // K steps, codes by DMA where the per-wave rings fit (5 groups):
+        // the 37888-row gate|up at M = 32 29.5 -> 26.5 us (M = 16 29.0 ->
+        // 26.2), of which 29.5 -> 27.9 from the slices alone
+        p.ks = bits == 4 ? 2 : 1;
         break;
       }
     }
@@ -630,14 +680,15 @@ Plan plan(int64_t M, int64_t N, int64_t K, int bits, bool can_split) {
   return p;
 }
 
-template <int BITS, int MI, bool PARTIAL, int EPI, int W, int GSH>
+template <int BITS, int MI, bool PARTIAL, int EPI, int W, int GSH, int KS = 1,
+          bool CDMA = kCodeDma<BITS>>
 hipError_t run(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, float* partial,
                int64_t M, int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
   const dim3 grid((unsigned)(p.tiles_n * p.tiles_m * p.splits));
   const int lds =
-      kXStages * 32 * MI * BK * 2 + (kCodeDma<BITS> ? W * kCodeSlots * kCodeBlock : 0);
-  auto kern = qmms_kernel<BITS, MI, PARTIAL, EPI, W, GSH>;
+      KS * kXStages * 32 * MI * BK * 2 + (CDMA ? W * (KS > 1 ? 3 : kCodeSlots) * kCodeBlock : 0);
+  auto kern = qmms_kernel<BITS, MI, PARTIAL, EPI, W, GSH, KS, CDMA>;
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -654,6 +705,16 @@ template <int BITS, int EPI, int GSH>
 hipError_t run_wide(const uint16_t* x, const uint32_t* wq, const uint16_t* scales,
                     const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M,
                     int64_t N, int64_t K, const Plan& p, hipStream_t stream) {
+  if constexpr (BITS == 4) {
+    if (p.ks == 2) {
+      switch (p.waves) {
+        case 5: return run<BITS, 1, false, EPI, 10, GSH, 2, true>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+        case 6: return run<BITS, 1, false, EPI, 12, GSH, 2>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+        case 8: return run<BITS, 1, false, EPI, 16, GSH, 2>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
+        default: return hipErrorInvalidValue;
+      }
+    }
+  }
   switch (p.waves) {
     case 5: return run<BITS, 1, false, EPI, 5, GSH>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
     case 6: return run<BITS, 1, false, EPI, 6, GSH>(x, wq, scales, biases, bias, y, nullptr, M, N, K, p, stream);
