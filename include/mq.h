@@ -62,7 +62,8 @@ typedef uint16_t mq_bf16; /* raw bfloat16 bits */
 #define MQ_ERR_HIP (-3)         /* the HIP runtime refused a launch */
 
 /* (major << 16) | minor.  2.0: mq_moe_sort and mq_moe_route_sort take an
- * expert_offsets output before the stream argument (1.0 had none). */
+ * expert_offsets output before the stream argument (1.0 had none).  2.1 adds
+ * mq_paged_prefill_attention and its _supported query. */
 int mq_version(void);
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -317,6 +318,34 @@ int mq_paged_decode_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq
                               int n_heads, int n_kv_heads, int head_dim, float scale,
                               void* workspace, size_t workspace_bytes, mq_bf16* out,
                               hipStream_t stream);
+
+/*
+ * Causal attention of a prefill chunk over the paged cache: query token j of
+ * row b sits at position starts[b] + min(j, lens[b] - 1) (tokens past
+ * lens[b] are padding that repeats the row's last position) and attends to
+ * the row's cached positions 0..that position (grouped-query: query head h
+ * reads KV head h / (n_heads / n_kv_heads)); the chunk's own k and v must
+ * already be in the pages.  Replaces PagedLayerAttentionContext
+ * .append_and_attend's dense gather of the pages, _dense_causal_mask and
+ * mx.fast.scaled_dot_product_attention for a prefill chunk
+ * (attention.py:215-261,404-425).  q bfloat16 [batch, tokens, n_heads,
+ * head_dim] (roped); starts, lens int64 [batch]; page_table int32 [batch,
+ * pages_per_seq] (the batch's rows); out bfloat16 [batch, tokens, n_heads,
+ * head_dim].  float32 scores, softmax and accumulation, the probabilities
+ * rounded to bfloat16 for the products with v.  head_dim 128; the pages of
+ * one layer under 2 GiB.
+ */
+/* 1 if mq_paged_prefill_attention takes these sizes, else 0.  Host-only; no
+ * counterpart in the reference. */
+int mq_paged_prefill_attention_supported(int n_heads, int n_kv_heads, int head_dim,
+                                         int64_t num_pages, int64_t page_size);
+
+int mq_paged_prefill_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq_bf16* v_pages,
+                               const int32_t* page_table, int64_t pages_per_seq,
+                               int64_t page_size, int64_t num_pages, const int64_t* starts,
+                               const int64_t* lens, int64_t batch, int64_t tokens, int n_heads,
+                               int n_kv_heads, int head_dim, float scale, mq_bf16* out,
+                               hipStream_t stream);
 
 /*
  * One decode step of a layer's attention after its QKV projection:

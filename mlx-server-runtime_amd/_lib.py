@@ -36,6 +36,8 @@ EXPORTS = (
     "mq_rope_kv_append",
     "mq_paged_decode_attention_workspace",
     "mq_paged_decode_attention",
+    "mq_paged_prefill_attention_supported",
+    "mq_paged_prefill_attention",
     "mq_decode_attention_step",
     "mq_silu_mul",
     "mq_moe_route",
@@ -97,6 +99,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_decode_attention_step.argtypes = [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p,
                                            ctypes.c_float, _p, _p, _i64, _int, _int, _int,
                                            ctypes.c_float, _p, ctypes.c_size_t, _p, _p]
+    L.mq_paged_prefill_attention_supported.argtypes = [_int, _int, _int, _i64, _i64]
+    L.mq_paged_prefill_attention.argtypes = [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
+                                             _int, _int, _int, ctypes.c_float, _p, _p]
     L.mq_silu_mul.argtypes = [_p, _p, _i64, _i64, _p]
     L.mq_moe_route.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p]
     L.mq_moe_sort.argtypes = [_p, _i64, _int, _int, _p, _p, _p, _p, _p, _p]

@@ -133,7 +133,7 @@ bool word_shape(int64_t K, int group_size, int bits) {
 
 extern "C" {
 
-int mq_version(void) { return (2 << 16) | 0; }
+int mq_version(void) { return (2 << 16) | 1; }
 
 const char* mq_last_error(void) { return g_err; }
 
@@ -821,6 +821,45 @@ int mq_decode_attention_step(const mq_bf16* qkv, const int64_t* positions,
                                               k_norm, norm_eps, k_pages, v_pages, batch, n_heads,
                                               n_kv_heads, head_dim, scale,
                                               static_cast<float*>(workspace), out, stream),
+                    op);
+}
+
+int mq_paged_prefill_attention_supported(int n_heads, int n_kv_heads, int head_dim,
+                                         int64_t num_pages, int64_t page_size) {
+  return n_heads > 0 && n_heads <= 65535 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 &&
+                 num_pages > 0 && page_size > 0 &&
+                 mq::prefill_attention_supported(n_heads, n_kv_heads, head_dim, num_pages,
+                                                 page_size)
+             ? 1
+             : 0;
+}
+
+int mq_paged_prefill_attention(const mq_bf16* q, const mq_bf16* k_pages, const mq_bf16* v_pages,
+                               const int32_t* page_table, int64_t pages_per_seq,
+                               int64_t page_size, int64_t num_pages, const int64_t* starts,
+                               const int64_t* lens, int64_t batch, int64_t tokens, int n_heads,
+                               int n_kv_heads, int head_dim, float scale, mq_bf16* out,
+                               hipStream_t stream) {
+  const char* op = "paged_prefill_attention";
+  if (int rc = check_pages(op, batch, n_heads, n_kv_heads, pages_per_seq, page_size, num_pages))
+    return rc;
+  if (int rc = check_dim(op, "tokens", tokens)) return rc;
+  if (n_heads > 65535)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] n_heads=%d > 65535.", op, n_heads);
+  if (!mq::prefill_attention_supported(n_heads, n_kv_heads, head_dim, num_pages, page_size))
+    return fail(MQ_ERR_UNSUPPORTED,
+                "[%s] head_dim=%d is not supported (128), or the pages of one layer exceed 2 GiB.",
+                op, head_dim);
+  if (batch == 0 || tokens == 0) return ok();
+  if (batch * tokens * n_heads * (int64_t)head_dim >= kMaxDim * (int64_t)64)
+    return fail(MQ_ERR_INVALID, "[%s] q is too large.", op);
+  if (!q || !k_pages || !v_pages || !page_table || !starts || !lens || !out)
+    return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(q) || !aligned16(k_pages) || !aligned16(v_pages))
+    return fail(MQ_ERR_INVALID, "[%s] q and the pages must be 16-byte aligned.", op);
+  return hip_status(mq::launch_prefill_attention(q, k_pages, v_pages, page_table, pages_per_seq,
+                                                 page_size, num_pages, starts, lens, batch,
+                                                 tokens, n_heads, n_kv_heads, scale, out, stream),
                     op);
 }
 

@@ -212,6 +212,15 @@ hipError_t launch_attention_step(const uint16_t* qkv, const int64_t* pos,
                                  float scale, float* workspace, uint16_t* out,
                                  hipStream_t stream);
 
+// Paged causal attention of prefill chunks (mq_prefill_attn.hip).
+bool prefill_attention_supported(int nh, int nkv, int d, int64_t num_pages, int64_t page_size);
+hipError_t launch_prefill_attention(const uint16_t* q, const uint16_t* k_pages,
+                                    const uint16_t* v_pages, const int32_t* page_table,
+                                    int64_t pages_per_seq, int64_t page_size, int64_t num_pages,
+                                    const int64_t* starts, const int64_t* lens, int64_t B,
+                                    int64_t T, int nh, int nkv, float scale, uint16_t* out,
+                                    hipStream_t stream);
+
 // Mixture-of-experts routing (mq_moe.hip).
 bool moe_route_supported(int E, int k);
 hipError_t launch_moe_route(const uint16_t* logits, const float* expert_bias, int64_t T, int E,

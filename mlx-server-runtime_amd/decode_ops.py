@@ -184,6 +184,41 @@ def paged_decode_attention(q: torch.Tensor, cache: PagedKV, layer: int, position
     return out
 
 
+def prefill_attention_supported(n_heads: int, cache: PagedKV) -> bool:
+    """Whether paged_prefill_attention takes this cache's shape."""
+    return bool(_lib.lib().mq_paged_prefill_attention_supported(
+        n_heads, cache.kv_heads, cache.head_dim, cache.num_pages, cache.page_size))
+
+
+def paged_prefill_attention(q: torch.Tensor, cache: PagedKV, layer: int, table: torch.Tensor,
+                            starts: torch.Tensor, lens: torch.Tensor, scale: float) -> torch.Tensor:
+    """Causal attention of a prefill chunk whose k and v are already in the pages
+    (attention.py:215-261 gathers the pages and runs scaled_dot_product_attention
+    under _dense_causal_mask, :404-425).  q bf16 [B, T, n_heads, head_dim] (roped);
+    table int32 [B, pages_per_seq] (the rows' page tables); starts, lens int64 [B]:
+    query j of row b sits at position starts[b] + min(j, lens[b] - 1) and attends to
+    positions 0..that -> bf16 [B, T, n_heads * head_dim]."""
+    op = "paged_prefill_attention"
+    _require_gpu(op, q=q, table=table, starts=starts, lens=lens)
+    _check_bf16(op, "q", q)
+    B, T, nh, d = q.shape
+    if d != cache.head_dim:
+        raise ValueError(f"[{op}] q {tuple(q.shape)} does not match the cache")
+    if table.dtype != torch.int32 or table.shape != (B, cache.pages_per_seq):
+        raise ValueError(f"[{op}] table must be int32 [{B}, {cache.pages_per_seq}]")
+    for name, t in (("starts", starts), ("lens", lens)):
+        if t.dtype != torch.int64 or t.shape != (B,):
+            raise ValueError(f"[{op}] {name} must be int64 [{B}]")
+    out = torch.empty(B, T, nh * d, dtype=torch.bfloat16, device=q.device)
+    L = _lib.lib()
+    _lib.check(L.mq_paged_prefill_attention(
+        _ptr(q.contiguous()), _ptr(cache.k[layer]), _ptr(cache.v[layer]), _ptr(table.contiguous()),
+        cache.pages_per_seq, cache.page_size, cache.num_pages, _ptr(starts.contiguous()),
+        _ptr(lens.contiguous()), B, T, nh, cache.kv_heads, d, float(scale), _ptr(out),
+        _stream(q)), op)
+    return out
+
+
 def attention_step(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, layer: int,
                    cos: torch.Tensor, sin: torch.Tensor, n_heads: int, scale: float,
                    q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,

@@ -29,9 +29,11 @@ add + RMSNorm + gate|up GEMV with SiLU * up in its epilogue; down GEMV; the
 norms run inside the GEMVs' input staging); batched, the residual adds, the
 norms and SiLU * up run in the skinny GEMMs' split-K reduces instead; captured
 once in a HIP graph and replayed per token (inputs live in static device
-buffers).  Prefill runs the same linears as GEMMs and float32 attention over
-the pages (the reference's dense-row gather, attention.py:264-298), so a
-prompt may start after a prefix already in the cache (prefix sharing).
+buffers).  Prefill runs the same linears as GEMMs and the paged prefill
+attention kernel over the pages (in place of the reference's dense-row gather
+and masked scaled_dot_product_attention, attention.py:215-298; head dims it
+does not take fall back to a float32 restatement of that), so a prompt may
+start after a prefix already in the cache (prefix sharing).
 Weights can be random-initialised at the reference's 7B shape
 (Qwen2Config.qwen25_7b) for benchmarking.
 """
@@ -45,7 +47,8 @@ import torch
 import torch.nn.functional as F
 
 from . import core
-from .decode_ops import PagedKV, attention_step, silu_mul
+from .decode_ops import (PagedKV, attention_step, paged_prefill_attention,
+                         prefill_attention_supported, silu_mul)
 from .moe import MoEBlock, QExperts
 from .decode_ops import rms_norm as fused_rms_norm
 
@@ -381,8 +384,15 @@ class Qwen2Model:
         cs, sn = cos[start:], sin[start:]
         pos = torch.arange(start, S, device=dev)
         slots = cache.slots(rows.repeat_interleave(T), pos.repeat(B))
-        # query i (position start + i) sees keys 0..start + i
-        causal = torch.full((T, S), float("-inf"), device=dev).triu(start + 1)
+        # query i (position start + i) sees keys 0..start + i: the paged
+        # prefill kernel, or (shapes it does not take) a float32 restatement
+        native = prefill_attention_supported(nh, cache)
+        if native:
+            table = cache.page_table[rows].contiguous()
+            starts = torch.full((B,), start, dtype=torch.int64, device=dev)
+            lens = torch.full((B,), T, dtype=torch.int64, device=dev)
+        else:
+            causal = torch.full((T, S), float("-inf"), device=dev).triu(start + 1)
         h = self._embed(ids.reshape(-1)).reshape(B, T, c.hidden_size)
         x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
@@ -398,14 +408,19 @@ class Qwen2Model:
             v = v.reshape(B, T, nkv, d).transpose(1, 2)
             cache.write(li, slots, k.transpose(1, 2).reshape(B * T, nkv, d),
                         v.transpose(1, 2).reshape(B * T, nkv, d))
-            if start:
-                k, v = cache.gather_rows(li, rows, S)
-            q = q.to(torch.bfloat16).float()
-            kk = k.float().repeat_interleave(rep, dim=1)
-            vv = v.float().repeat_interleave(rep, dim=1)
-            s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + causal
-            a = torch.matmul(torch.softmax(s, dim=-1), vv)
-            o = layer.o(a.transpose(1, 2).reshape(B, T, nh * d).to(torch.bfloat16))
+            if native:
+                a = paged_prefill_attention(q.to(torch.bfloat16).transpose(1, 2).contiguous(),
+                                            cache, li, table, starts, lens, d ** -0.5)
+            else:
+                if start:
+                    k, v = cache.gather_rows(li, rows, S)
+                q = q.to(torch.bfloat16).float()
+                kk = k.float().repeat_interleave(rep, dim=1)
+                vv = v.float().repeat_interleave(rep, dim=1)
+                s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + causal
+                a = torch.matmul(torch.softmax(s, dim=-1), vv).transpose(1, 2).reshape(
+                    B, T, nh * d).to(torch.bfloat16)
+            o = layer.o(a)
             x, h = self._ffn(li, h, o)
         return self._head(x if all_positions else x[:, -1])
 
@@ -434,9 +449,13 @@ class Qwen2Model:
         cs, sn = cos[pos][:, None], sin[pos][:, None]                       # [B, 1, T, d/2]
         # query (b, j) sees the keys of its row at positions <= pos[b, j]; a
         # padding query repeats the row's last valid one
-        keyp = torch.arange(S, device=dev)
-        mask = torch.zeros(B, 1, T, S, device=dev).masked_fill_(
-            (keyp[None, None, :] > pos[:, :, None])[:, None], float("-inf"))
+        native = prefill_attention_supported(nh, cache)
+        if native:
+            table = cache.page_table[rows].contiguous()
+        else:
+            keyp = torch.arange(S, device=dev)
+            mask = torch.zeros(B, 1, T, S, device=dev).masked_fill_(
+                (keyp[None, None, :] > pos[:, :, None])[:, None], float("-inf"))
         h = self._embed(ids.reshape(-1)).reshape(B, T, c.hidden_size)
         x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
@@ -450,13 +469,18 @@ class Qwen2Model:
             k = apply_rope(k.float().transpose(1, 2), cs, sn).to(torch.bfloat16)
             v = v.reshape(B, T, nkv, d)
             cache.write(li, slots, k.transpose(1, 2)[vb, vj], v[vb, vj])
-            kk, vv = cache.gather_rows(li, rows, S)
-            q = q.to(torch.bfloat16).float()
-            kk = kk.float().repeat_interleave(rep, dim=1)
-            vv = vv.float().repeat_interleave(rep, dim=1)
-            s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + mask
-            a = torch.matmul(torch.softmax(s, dim=-1), vv)
-            o = layer.o(a.transpose(1, 2).reshape(B, T, nh * d).to(torch.bfloat16))
+            if native:
+                a = paged_prefill_attention(q.to(torch.bfloat16).transpose(1, 2).contiguous(),
+                                            cache, li, table, starts, lens, d ** -0.5)
+            else:
+                kk, vv = cache.gather_rows(li, rows, S)
+                q = q.to(torch.bfloat16).float()
+                kk = kk.float().repeat_interleave(rep, dim=1)
+                vv = vv.float().repeat_interleave(rep, dim=1)
+                s = torch.matmul(q, kk.transpose(-1, -2).contiguous()) * (d ** -0.5) + mask
+                a = torch.matmul(torch.softmax(s, dim=-1), vv).transpose(1, 2).reshape(
+                    B, T, nh * d).to(torch.bfloat16)
+            o = layer.o(a)
             x, h = self._ffn(li, h, o)
         if all_positions:
             return self._head(x)

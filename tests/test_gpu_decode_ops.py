@@ -333,6 +333,74 @@ def test_paged_decode_attention(ops, B, nh, nkv, per, positions, d):
     assert torch.equal(out, again)
 
 
+def _prefill_ref(q, cache, layer, starts, lens, scale):
+    """float32 causal attention per row: query j of row b at position
+    starts[b] + min(j, lens[b] - 1) over the row's positions 0..that."""
+    B, T, nh, d = q.shape
+    rep = nh // cache.kv_heads
+    out = torch.empty(B, T, nh * d, device=DEV)
+    for b in range(B):
+        pos = int(starts[b]) + torch.clamp(torch.arange(T, device=DEV), max=int(lens[b]) - 1)
+        S = int(pos.max()) + 1
+        k, v = cache.gather_rows(layer, torch.tensor([b], device=DEV), S)
+        k = k[0].float().repeat_interleave(rep, 0)                      # [nh, S, d]
+        v = v[0].float().repeat_interleave(rep, 0)
+        s = torch.matmul(q[b].float().transpose(0, 1), k.transpose(1, 2).contiguous()) * scale
+        masked = torch.arange(S, device=DEV)[None, :] > pos[:, None]  # [T, S]
+        p = torch.softmax(s.masked_fill(masked[None], float("-inf")), -1)
+        out[b] = torch.matmul(p, v).transpose(0, 1).reshape(T, nh * d)
+    return out
+
+
+@pytest.mark.parametrize("B,T,nh,nkv,per,starts,lens", [
+    (1, 64, 28, 4, 4, [0], [64]),                        # one tile, no cache before it
+    (2, 100, 28, 4, 40, [256, 0], [100, 37]),            # a cached prefix; a ragged row
+    (3, 200, 32, 4, 50, [0, 500, 17], [200, 150, 1]),    # 8 per KV head; a one-token row
+    (1, 256, 8, 8, 80, [1000], [256]),                   # no grouping, 1000 cached positions
+    (4, 33, 16, 2, 10, [7, 64, 100, 0], [33, 20, 1, 9]),  # short chunks
+])
+def test_paged_prefill_attention(ops, B, T, nh, nkv, per, starts, lens):
+    """Prefill-chunk attention over shuffled pages against the float32
+    restatement (the probabilities are bfloat16 in the kernel's P.V, as in
+    the decode kernel: within 2^-7 of the largest output); each row alone
+    gives the same bits as in the batch."""
+    d, ps = 128, 16
+    cache = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=per + B + T)
+    g = _gen(31 + B + T + nh)
+    cache.k[0].copy_(torch.randn(cache.k[0].shape, generator=g, device=DEV).to(torch.bfloat16))
+    cache.v[0].copy_(torch.randn(cache.v[0].shape, generator=g, device=DEV).to(torch.bfloat16))
+    st = torch.tensor(starts, dtype=torch.int64, device=DEV)
+    ln = torch.tensor(lens, dtype=torch.int64, device=DEV)
+    q = (torch.randn(B, T, nh, d, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    scale = d ** -0.5
+    print(f"prefill attention B={B} T={T} nh={nh} nkv={nkv} starts={starts} lens={lens}",
+          flush=True)
+    assert ops.prefill_attention_supported(nh, cache)
+    out = ops.paged_prefill_attention(q, cache, 0, cache.page_table, st, ln, scale)
+    ref = _prefill_ref(q, cache, 0, st, ln, scale)
+    err = (out.float() - ref).abs().max() / ref.abs().max()
+    assert out.shape == (B, T, nh * d)
+    assert err < 2.0 ** -7, float(err)
+    assert torch.equal(out, ops.paged_prefill_attention(q, cache, 0, cache.page_table, st, ln,
+                                                        scale))
+    for b in range(B):
+        n = int(lens[b])
+        one = ops.paged_prefill_attention(q[b:b + 1, :n].contiguous(), cache, 0,
+                                          cache.page_table[b:b + 1].contiguous(), st[b:b + 1],
+                                          ln[b:b + 1], scale)
+        assert torch.equal(one[0], out[b, :n]), b
+
+
+def test_paged_prefill_attention_refusals(ops):
+    """head_dim 64 is not taken (the query says so and the call raises)."""
+    cache = _shuffled_cache(ops, 1, 1, 2, 16, 2, 64, seed=1)
+    assert not ops.prefill_attention_supported(8, cache)
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.bfloat16, device=DEV)
+    one = torch.zeros(1, dtype=torch.int64, device=DEV)
+    with pytest.raises(NotImplementedError):
+        ops.paged_prefill_attention(q, cache, 0, cache.page_table, one, one + 4, 0.125)
+
+
 def test_paged_decode_attention_shared_prefix_pages(ops):
     """Rows that share their first pages (a cached prompt prefix) read them
     through the table: equal to a cache holding private copies."""

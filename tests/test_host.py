@@ -46,7 +46,8 @@ def test_header_declares_the_abi():
         "mq_quantized_matmul_add_rms_norm_workspace", "mq_quantized_matmul_add_rms_norm",
         "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu", "mq_hbm_read", "mq_qmv_trace",
         "mq_quantized_matmul_noalloc", "mq_gather_qmm_segments",
-        "mq_gather_qmm_segments_supported"])
+        "mq_gather_qmm_segments_supported", "mq_paged_prefill_attention_supported",
+        "mq_paged_prefill_attention"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -54,7 +55,7 @@ def test_library_exports_every_declared_symbol(mq):
     for name in declared_functions():
         assert hasattr(L, name), name
     assert set(mq._lib.EXPORTS) == set(declared_functions())
-    assert mq.version() == (2, 0)
+    assert mq.version() == (2, 1)
 
 
 def _L(mq):
