@@ -126,11 +126,13 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
 def rope_kv_append(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, layer: int,
                    cos: torch.Tensor, sin: torch.Tensor, n_heads: int,
                    q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,
-                   norm_eps: float = 1e-6) -> torch.Tensor:
+                   norm_eps: float = 1e-6, table: torch.Tensor | None = None) -> torch.Tensor:
     """qkv bf16 [B, (n_heads + 2 kv_heads) * head_dim] of one token per sequence ->
     q bf16 [B, n_heads, head_dim] after RoPE; rope(k) and v go into the pages at
     each sequence's position (positions int64 [B], on the device).  q_norm /
-    k_norm (bf16 [head_dim]): Qwen3's per-head RMSNorm before RoPE."""
+    k_norm (bf16 [head_dim]): Qwen3's per-head RMSNorm before RoPE.  table (int32
+    [B, pages_per_seq], default the cache's own): each token's page-table row --
+    a prefill chunk's tokens, one entry per token, each with its row's table."""
     op = "rope_kv_append"
     _require_gpu(op, qkv=qkv, positions=positions, cos=cos, sin=sin)
     _check_bf16(op, "qkv", qkv)
@@ -141,8 +143,13 @@ def rope_kv_append(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, l
                          f"got {tuple(qkv.shape)}")
     if positions.dtype != torch.int64 or positions.shape != (B,):
         raise ValueError(f"[{op}] positions must be int64 [{B}]")
-    if cache.batch != B:
-        raise ValueError(f"[{op}] the page table has {cache.batch} rows, qkv {B}")
+    if table is None:
+        if cache.batch != B:
+            raise ValueError(f"[{op}] the page table has {cache.batch} rows, qkv {B}")
+        table = cache.page_table
+    elif table.dtype != torch.int32 or table.shape != (B, cache.pages_per_seq):
+        raise ValueError(f"[{op}] table must be int32 [{B}, {cache.pages_per_seq}], "
+                         f"got {tuple(table.shape)}")
     if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape[-1] != d // 2:
         raise ValueError(f"[{op}] cos/sin must be float32 [positions, {d // 2}]")
     if cos.shape[0] < cache.capacity or sin.shape != cos.shape:
@@ -153,7 +160,7 @@ def rope_kv_append(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, l
     q = torch.empty(B, n_heads, d, dtype=torch.bfloat16, device=qkv.device)
     L = _lib.lib()
     _lib.check(L.mq_rope_kv_append(
-        _ptr(qkv.contiguous()), _ptr(positions), _ptr(cache.page_table), cache.pages_per_seq,
+        _ptr(qkv.contiguous()), _ptr(positions), _ptr(table.contiguous()), cache.pages_per_seq,
         cache.page_size, cache.num_pages, _ptr(cos.contiguous()), _ptr(sin.contiguous()),
         _ptr(q_norm), _ptr(k_norm), float(norm_eps), _ptr(q), _ptr(cache.k[layer]),
         _ptr(cache.v[layer]), B, n_heads, nkv, d, _stream(qkv)), op)

@@ -48,7 +48,7 @@ import torch.nn.functional as F
 
 from . import core
 from .decode_ops import (PagedKV, attention_step, paged_prefill_attention,
-                         prefill_attention_supported, silu_mul)
+                         prefill_attention_supported, rope_kv_append, silu_mul)
 from .moe import MoEBlock, QExperts
 from .decode_ops import rms_norm as fused_rms_norm
 
@@ -203,6 +203,18 @@ def rope_tables(cfg: Qwen2Config, max_len: int, device) -> tuple[torch.Tensor, t
     pos = torch.arange(max_len, dtype=torch.float64, device=device) * cfg.rope_scale
     ang = pos[:, None] * inv[None, :]
     return torch.cos(ang).float(), torch.sin(ang).float()
+
+
+def _rope_append_tokens(qkv: torch.Tensor, positions: torch.Tensor, cache: PagedKV, layer: int,
+                        cos: torch.Tensor, sin: torch.Tensor, n_heads: int, lyr, eps: float,
+                        table: torch.Tensor, step: int = 32768) -> torch.Tensor:
+    """rope_kv_append over a prefill chunk's tokens (one row each, with its row's
+    page table), at most `step` tokens a call -> q bf16 [tokens, n_heads, head_dim]."""
+    n = qkv.shape[0]
+    parts = [rope_kv_append(qkv[a:a + step], positions[a:a + step], cache, layer, cos, sin,
+                            n_heads, lyr.q_norm, lyr.k_norm, eps, table=table[a:a + step])
+             for a in range(0, n, step)]
+    return parts[0] if len(parts) == 1 else torch.cat(parts)
 
 
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -380,38 +392,45 @@ class Qwen2Model:
         rep = nh // nkv
         S = start + T
         rows = torch.arange(B, device=dev) if rows is None else rows.to(dev).long()
-        cos, sin = rope_tables(c, S, dev)
-        cs, sn = cos[start:], sin[start:]
         pos = torch.arange(start, S, device=dev)
-        slots = cache.slots(rows.repeat_interleave(T), pos.repeat(B))
-        # query i (position start + i) sees keys 0..start + i: the paged
-        # prefill kernel, or (shapes it does not take) a float32 restatement
+        # query i (position start + i) sees keys 0..start + i: RoPE + append and
+        # the paged prefill kernel, or (shapes it does not take) a float32
+        # restatement
         native = prefill_attention_supported(nh, cache)
         if native:
+            cos, sin = rope_tables(c, cache.capacity, dev)
             table = cache.page_table[rows].contiguous()
+            tok_table = table.repeat_interleave(T, 0)   # token (b, i): row b's table
+            tok_pos = pos.repeat(B)
             starts = torch.full((B,), start, dtype=torch.int64, device=dev)
             lens = torch.full((B,), T, dtype=torch.int64, device=dev)
         else:
+            cos, sin = rope_tables(c, S, dev)
+            cs, sn = cos[start:], sin[start:]
+            slots = cache.slots(rows.repeat_interleave(T), pos.repeat(B))
             causal = torch.full((T, S), float("-inf"), device=dev).triu(start + 1)
         h = self._embed(ids.reshape(-1)).reshape(B, T, c.hidden_size)
         x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
             qkv = layer.qkv(x)
-            q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
-            q, k = q.reshape(B, T, nh, d), k.reshape(B, T, nkv, d)
-            if layer.q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
-                q = fused_rms_norm(q, layer.q_norm, c.rms_norm_eps)
-                k = fused_rms_norm(k, layer.k_norm, c.rms_norm_eps)
-            q = apply_rope(q.float().transpose(1, 2), cs, sn)
-            k = apply_rope(k.float().transpose(1, 2), cs, sn)
-            k = k.to(torch.bfloat16)
-            v = v.reshape(B, T, nkv, d).transpose(1, 2)
-            cache.write(li, slots, k.transpose(1, 2).reshape(B * T, nkv, d),
-                        v.transpose(1, 2).reshape(B * T, nkv, d))
             if native:
-                a = paged_prefill_attention(q.to(torch.bfloat16).transpose(1, 2).contiguous(),
-                                            cache, li, table, starts, lens, d ** -0.5)
+                q = _rope_append_tokens(qkv.reshape(B * T, -1), tok_pos, cache, li, cos, sin, nh,
+                                        layer, c.rms_norm_eps, tok_table)
+                a = paged_prefill_attention(q.reshape(B, T, nh, d), cache, li, table, starts, lens,
+                                            d ** -0.5)
             else:
+                q, k, v = (qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d],
+                           qkv[..., (nh + nkv) * d:])
+                q, k = q.reshape(B, T, nh, d), k.reshape(B, T, nkv, d)
+                if layer.q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
+                    q = fused_rms_norm(q, layer.q_norm, c.rms_norm_eps)
+                    k = fused_rms_norm(k, layer.k_norm, c.rms_norm_eps)
+                q = apply_rope(q.float().transpose(1, 2), cs, sn)
+                k = apply_rope(k.float().transpose(1, 2), cs, sn)
+                k = k.to(torch.bfloat16)
+                v = v.reshape(B, T, nkv, d).transpose(1, 2)
+                cache.write(li, slots, k.transpose(1, 2).reshape(B * T, nkv, d),
+                            v.transpose(1, 2).reshape(B * T, nkv, d))
                 if start:
                     k, v = cache.gather_rows(li, rows, S)
                 q = q.to(torch.bfloat16).float()
@@ -444,15 +463,20 @@ class Qwen2Model:
         valid = j[None, :] < lens[:, None]                                  # [B, T]
         pos = starts[:, None] + torch.minimum(j[None, :], lens[:, None] - 1)  # [B, T]
         vb, vj = valid.nonzero(as_tuple=True)
-        slots = cache.slots(rows[vb], pos[vb, vj])
-        cos, sin = rope_tables(c, S, dev)
-        cs, sn = cos[pos][:, None], sin[pos][:, None]                       # [B, 1, T, d/2]
         # query (b, j) sees the keys of its row at positions <= pos[b, j]; a
-        # padding query repeats the row's last valid one
+        # padding query repeats the row's last valid one.  Natively only the
+        # valid tokens are roped and appended, padding queries are zero (their
+        # outputs mean nothing either way)
         native = prefill_attention_supported(nh, cache)
         if native:
+            cos, sin = rope_tables(c, cache.capacity, dev)
             table = cache.page_table[rows].contiguous()
+            tok_table = table[vb].contiguous()
+            tok_pos = pos[vb, vj].contiguous()
         else:
+            slots = cache.slots(rows[vb], pos[vb, vj])
+            cos, sin = rope_tables(c, S, dev)
+            cs, sn = cos[pos][:, None], sin[pos][:, None]                   # [B, 1, T, d/2]
             keyp = torch.arange(S, device=dev)
             mask = torch.zeros(B, 1, T, S, device=dev).masked_fill_(
                 (keyp[None, None, :] > pos[:, :, None])[:, None], float("-inf"))
@@ -460,19 +484,23 @@ class Qwen2Model:
         x = fused_rms_norm(h, self.layers[0].input_norm, c.rms_norm_eps)
         for li, layer in enumerate(self.layers):
             qkv = layer.qkv(x)
-            q, k, v = qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d], qkv[..., (nh + nkv) * d:]
-            q, k = q.reshape(B, T, nh, d), k.reshape(B, T, nkv, d)
-            if layer.q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
-                q = fused_rms_norm(q, layer.q_norm, c.rms_norm_eps)
-                k = fused_rms_norm(k, layer.k_norm, c.rms_norm_eps)
-            q = apply_rope(q.float().transpose(1, 2), cs, sn)
-            k = apply_rope(k.float().transpose(1, 2), cs, sn).to(torch.bfloat16)
-            v = v.reshape(B, T, nkv, d)
-            cache.write(li, slots, k.transpose(1, 2)[vb, vj], v[vb, vj])
             if native:
-                a = paged_prefill_attention(q.to(torch.bfloat16).transpose(1, 2).contiguous(),
-                                            cache, li, table, starts, lens, d ** -0.5)
+                qv = _rope_append_tokens(qkv[vb, vj].contiguous(), tok_pos, cache, li, cos, sin,
+                                         nh, layer, c.rms_norm_eps, tok_table)
+                q = torch.zeros(B, T, nh, d, dtype=torch.bfloat16, device=dev)
+                q[vb, vj] = qv
+                a = paged_prefill_attention(q, cache, li, table, starts, lens, d ** -0.5)
             else:
+                q, k, v = (qkv[..., :nh * d], qkv[..., nh * d:(nh + nkv) * d],
+                           qkv[..., (nh + nkv) * d:])
+                q, k = q.reshape(B, T, nh, d), k.reshape(B, T, nkv, d)
+                if layer.q_norm is not None:  # Qwen3: per-head RMSNorm before RoPE
+                    q = fused_rms_norm(q, layer.q_norm, c.rms_norm_eps)
+                    k = fused_rms_norm(k, layer.k_norm, c.rms_norm_eps)
+                q = apply_rope(q.float().transpose(1, 2), cs, sn)
+                k = apply_rope(k.float().transpose(1, 2), cs, sn).to(torch.bfloat16)
+                v = v.reshape(B, T, nkv, d)
+                cache.write(li, slots, k.transpose(1, 2)[vb, vj], v[vb, vj])
                 kk, vv = cache.gather_rows(li, rows, S)
                 q = q.to(torch.bfloat16).float()
                 kk = kk.float().repeat_interleave(rep, dim=1)

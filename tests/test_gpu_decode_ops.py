@@ -285,6 +285,32 @@ def test_rope_kv_append(ops, B, nh, nkv, d):
     assert int((flat_v.abs().sum((1, 2)) > 0).sum()) == B
 
 
+def test_rope_kv_append_prefill_tokens(ops):
+    """A prefill chunk's tokens in one call, each with its row's page-table row
+    (the table argument): q roped, k roped and v written at each token's
+    position of its row, nothing else written."""
+    B, T, nh, nkv, d, ps, per = 2, 5, 28, 4, 128, 16, 4
+    cache = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=77)
+    cos, sin = _tables(d, cache.capacity)
+    g = _gen(78)
+    qkv = torch.randn(B * T, (nh + 2 * nkv) * d, generator=g, device=DEV).to(torch.bfloat16)
+    starts = torch.tensor([3, 40], device=DEV)
+    pos = (starts[:, None] + torch.arange(T, device=DEV)[None, :]).reshape(-1)
+    rows = torch.arange(B, device=DEV).repeat_interleave(T)
+    table = cache.page_table[rows].contiguous()
+    q = ops.rope_kv_append(qkv, pos, cache, 0, cos, sin, nh, table=table)
+    qf = qkv.float()
+    cs, sn = cos[pos][:, None, :], sin[pos][:, None, :]
+    assert _within_one_step(q, _rope_ref(qf[:, :nh * d].reshape(-1, nh, d), cs, sn))
+    slots = cache.slots(rows, pos)
+    flat_k = cache.k[0].view(-1, nkv, d)
+    flat_v = cache.v[0].view(-1, nkv, d)
+    k_ref = _rope_ref(qf[:, nh * d:(nh + nkv) * d].reshape(-1, nkv, d), cs, sn)
+    assert _within_one_step(flat_k[slots], k_ref)
+    assert torch.equal(flat_v[slots], qkv[:, (nh + nkv) * d:].reshape(-1, nkv, d))
+    assert int((flat_v.abs().sum((1, 2)) > 0).sum()) == B * T
+
+
 def _attention_ref(q, cache, layer, pos, scale):
     """float32 softmax(q k^T scale) v per row over its positions 0..pos."""
     B, nh, d = q.shape
