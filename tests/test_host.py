@@ -205,6 +205,38 @@ def test_decoder_entry_validation(mq):
     assert cn(null, null, null, null, null, null, null, 0, 8, 2048, 1e-6, null) == 0
 
 
+def test_prefill_attention_entry_validation(mq):
+    """The prefill attention entry: its support query and the argument checks,
+    all before any device access (null pointers are fine)."""
+    L = _L(mq)
+    null = None
+    sup = L.mq_paged_prefill_attention_supported
+    assert sup(28, 4, 128, 4096, 16) == 1
+    assert sup(32, 4, 128, 4096, 16) == 1
+    assert sup(28, 4, 64, 4096, 16) == 0                   # head_dim 128 only
+    assert sup(30, 4, 128, 4096, 16) == 0                  # heads not a multiple of KV heads
+    assert sup(28, 0, 128, 4096, 16) == 0
+    assert sup(28, 4, 128, 1 << 20, 16) == 0               # a layer's pages past 2 GiB
+    assert sup(28, 4, 128, 0, 16) == 0
+    pf = L.mq_paged_prefill_attention
+    #        q     k     v     table pps ps  pages starts lens B  T    nh  nkv d    scale
+    assert pf(null, null, null, null, 4, 16, 8, null, null, 2, 64, 30, 4, 128, 1.0, null,
+              null) == -1                                                   # 30 % 4
+    assert pf(null, null, null, null, 4, 16, 8, null, null, 2, 64, 28, 4, 64, 1.0, null,
+              null) == -2                                                   # head_dim
+    assert b"head_dim" in L.mq_last_error()
+    assert pf(null, null, null, null, 4, 16, 8, null, null, 2, 64, 28, 4, 128, 1.0, null,
+              null) == -1                                                   # null pointers
+    assert pf(null, null, null, null, 0, 16, 8, null, null, 2, 64, 28, 4, 128, 1.0, null,
+              null) == -1                                                   # no pages
+    assert pf(null, null, null, null, 4, 16, 8, null, null, 0, 64, 28, 4, 128, 1.0, null,
+              null) == 0                                                    # empty batch
+    assert pf(null, null, null, null, 4, 16, 8, null, null, 2, 0, 28, 4, 128, 1.0, null,
+              null) == 0                                                    # no tokens
+    assert pf(null, null, null, null, 4, 16, 8, null, null, 2, -1, 28, 4, 128, 1.0, null,
+              null) == -1                                                   # negative tokens
+
+
 def test_capi_invalid_and_unsupported_codes(mq):
     L = _L(mq)
     null = None
