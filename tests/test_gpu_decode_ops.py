@@ -378,19 +378,22 @@ def _prefill_ref(q, cache, layer, starts, lens, scale):
     return out
 
 
-@pytest.mark.parametrize("B,T,nh,nkv,per,starts,lens", [
-    (1, 64, 28, 4, 4, [0], [64]),                        # one tile, no cache before it
-    (2, 100, 28, 4, 40, [256, 0], [100, 37]),            # a cached prefix; a ragged row
-    (3, 200, 32, 4, 50, [0, 500, 17], [200, 150, 1]),    # 8 per KV head; a one-token row
-    (1, 256, 8, 8, 80, [1000], [256]),                   # no grouping, 1000 cached positions
-    (4, 33, 16, 2, 10, [7, 64, 100, 0], [33, 20, 1, 9]),  # short chunks
+@pytest.mark.parametrize("B,T,nh,nkv,per,starts,lens,ps", [
+    (1, 64, 28, 4, 4, [0], [64], 16),                        # one tile, no cache before it
+    (2, 100, 28, 4, 40, [256, 0], [100, 37], 16),            # a cached prefix; a ragged row
+    (3, 200, 32, 4, 50, [0, 500, 17], [200, 150, 1], 16),    # 8 per KV head; a one-token row
+    (1, 256, 8, 8, 80, [1000], [256], 16),                   # no grouping, 1000 cached positions
+    (4, 33, 16, 2, 10, [7, 64, 100, 0], [33, 20, 1, 9], 16),  # short chunks
+    (2, 70, 28, 4, 13, [0, 33], [70, 71 - 33], 8),           # page size 8, 104 positions: the
+                                                             # last key block runs past the table
+    (1, 130, 28, 4, 3, [61], [130], 64),                     # page size 64, a chunk over 3 pages
 ])
-def test_paged_prefill_attention(ops, B, T, nh, nkv, per, starts, lens):
+def test_paged_prefill_attention(ops, B, T, nh, nkv, per, starts, lens, ps):
     """Prefill-chunk attention over shuffled pages against the float32
     restatement (the probabilities are bfloat16 in the kernel's P.V, as in
     the decode kernel: within 2^-7 of the largest output); each row alone
     gives the same bits as in the batch."""
-    d, ps = 128, 16
+    d = 128
     cache = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=per + B + T)
     g = _gen(31 + B + T + nh)
     cache.k[0].copy_(torch.randn(cache.k[0].shape, generator=g, device=DEV).to(torch.bfloat16))
