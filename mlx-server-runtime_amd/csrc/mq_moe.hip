@@ -220,33 +220,42 @@ __global__ __launch_bounds__(64 * kRouteWaves) void moe_route_kernel(
 }
 
 // ---------------------------------------------------------------- sort
-// One block.  Entries are processed in chunks of kSortThreads, in order; an
-// entry's place is its expert's offset, plus the entries of that expert in
-// earlier chunks, earlier waves of this chunk and earlier lanes of its wave
-// (a match mask built from one ballot per id bit).  Ids outside [0, E) go to
-// a last bucket E, kept as they are (gather_qmm gives such rows zeros).
+// Blocks of kSortThreads, each placing one range of the entries.  An entry's
+// place is its expert's offset, plus the entries of that expert before the
+// block's range, in earlier chunks of the range, in earlier waves of its
+// chunk and in earlier lanes of its wave (a match mask built from one ballot
+// per id bit).  Every block counts all n ids itself -- the totals give the
+// experts' offsets, the ids before its range its start within each expert --
+// so the sort needs no memory beyond its outputs and one launch.  Ids outside
+// [0, E) go to a last bucket E, kept as they are (gather_qmm gives such rows
+// zeros).
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kMaxBuckets = kMaxExperts + 1;
+constexpr int kSortBlocks = 64;  // at most; a block's range is whole chunks
 
-// The whole sort, by one block of kSortThreads.
-__device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int E,
-                                           int32_t* __restrict__ sorted_ids,
+// Entries [lo, hi) of the sort of ids[0, n), by one block of kSortThreads;
+// the block with lo = 0 writes the segment offsets.
+__device__ __forceinline__ void sort_block(const int32_t* ids, int n, int lo, int hi, int k,
+                                           int E, int32_t* __restrict__ sorted_ids,
                                            int32_t* __restrict__ order,
                                            int32_t* __restrict__ inverse,
                                            int32_t* __restrict__ rows,
                                            int32_t* __restrict__ expert_offsets) {
   __shared__ int offset[kMaxBuckets];
+  __shared__ int prior[kMaxBuckets];  // entries of each expert before lo
   __shared__ int wave_count[kSortWaves][kMaxBuckets];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int buckets = E + 1;
   int bits = 0;
   while ((1 << bits) < buckets) ++bits;
-  for (int e = tid; e < buckets; e += kSortThreads) offset[e] = 0;
+  for (int e = tid; e < buckets; e += kSortThreads) offset[e] = prior[e] = 0;
   __syncthreads();
   for (int i = tid; i < n; i += kSortThreads) {
     const int id = ids[i];
-    atomicAdd(&offset[(id >= 0 && id < E) ? id : E], 1);
+    const int b = (id >= 0 && id < E) ? id : E;
+    atomicAdd(&offset[b], 1);
+    if (i < lo) atomicAdd(&prior[b], 1);
   }
   __syncthreads();
   if (tid < 64) {  // exclusive scan over at most 513 buckets: one wave, PB per lane
@@ -274,14 +283,18 @@ __device__ __forceinline__ void sort_block(const int32_t* ids, int n, int k, int
   }
   __syncthreads();
   // segment starts: expert e's pairs are sorted positions offset[e] ..
-  // offset[e + 1] - 1; offset[E] counts the pairs with a valid id
-  if (expert_offsets)
-    for (int e = tid; e < buckets; e += kSortThreads) expert_offsets[e] = offset[e];
+  // offset[e + 1] - 1; offset[E] counts the pairs with a valid id.  Then the
+  // block's own start within each expert (the chunk loop's first barrier
+  // orders these updates before any read of another bucket).
+  for (int e = tid; e < buckets; e += kSortThreads) {
+    if (expert_offsets && lo == 0) expert_offsets[e] = offset[e];
+    offset[e] += prior[e];
+  }
   const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-  for (int c0 = 0; c0 < n; c0 += kSortThreads) {
+  for (int c0 = lo; c0 < hi; c0 += kSortThreads) {
     for (int e = lane; e < buckets; e += 64) wave_count[wave][e] = 0;
     const int i = c0 + tid;
-    const bool valid = i < n;
+    const bool valid = i < hi;
     int bucket = E;
     int id = 0;
     if (valid) {
@@ -322,11 +335,16 @@ __global__ __launch_bounds__(256) void zero_i32_kernel(int32_t* __restrict__ p, 
   if (i < n) p[i] = 0;
 }
 
+// Block b places entries [b * per, min(n, (b + 1) * per)), per a multiple of
+// kSortThreads.
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
-    const int32_t* __restrict__ ids, int n, int k, int E, int32_t* __restrict__ sorted_ids,
-    int32_t* __restrict__ order, int32_t* __restrict__ inverse, int32_t* __restrict__ rows,
+    const int32_t* __restrict__ ids, int n, int per, int k, int E,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ order,
+    int32_t* __restrict__ inverse, int32_t* __restrict__ rows,
     int32_t* __restrict__ expert_offsets) {
-  sort_block(ids, n, k, E, sorted_ids, order, inverse, rows, expert_offsets);
+  const int lo = blockIdx.x * per;
+  sort_block(ids, n, lo, min(n, lo + per), k, E, sorted_ids, order, inverse, rows,
+             expert_offsets);
 }
 
 // Route (one wave per token) and then sort, in one block: a decode step's
@@ -350,7 +368,7 @@ __global__ __launch_bounds__(kSortThreads) void moe_route_sort_kernel(
                     rs[threadIdx.x >> 6], n <= 64 ? flat : nullptr);
   __syncthreads();
   if (n > 64) {
-    sort_block(indices, n, k, E, sorted_ids, order, inverse, rows, expert_offsets);
+    sort_block(indices, n, 0, n, k, E, sorted_ids, order, inverse, rows, expert_offsets);
     return;
   }
   // At most 64 pairs: one wave places each at its rank among the keys
@@ -584,8 +602,13 @@ hipError_t launch_moe_sort(const int32_t* ids, int64_t n, int k, int E, int32_t*
                        expert_offsets, E + 1);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, ids, (int)n, k, E,
-                     sorted_ids, order, inverse, rows, expert_offsets);
+  // whole chunks per block, at most kSortBlocks blocks, none empty
+  const int64_t chunks = (n + kSortThreads - 1) / kSortThreads;
+  const int64_t per_chunks = (chunks + kSortBlocks - 1) / kSortBlocks;
+  const unsigned blocks = (unsigned)((chunks + per_chunks - 1) / per_chunks);
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(blocks), dim3(kSortThreads), 0, stream, ids, (int)n,
+                     (int)(per_chunks * kSortThreads), k, E, sorted_ids, order, inverse, rows,
+                     expert_offsets);
   return hipGetLastError();
 }
 

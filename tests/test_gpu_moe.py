@@ -86,19 +86,31 @@ def test_route_ties_go_to_the_lower_id(moe, T, E, k):
     assert torch.equal(offs, torch.searchsorted(torch.sort(flat).values, torch.arange(E + 1)))
 
 
-@pytest.mark.parametrize("T,k,E", [(8, 8, 128), (4096, 8, 128), (77, 3, 17), (1, 1, 1),
-                                   (2000, 6, 512)])
-def test_expert_sort(moe, T, k, E):
+@pytest.mark.parametrize("T,k,E,bad", [(8, 8, 128, 0), (4096, 8, 128, 0), (77, 3, 17, 0),
+                                       (1, 1, 1, 0), (2000, 6, 512, 0),
+                                       (20000, 8, 128, 0),   # 157 chunks: 3 to a block
+                                       (1500, 3, 60, 40)])   # ids -1 and E in every block
+def test_expert_sort(moe, T, k, E, bad):
+    """The sort's blocks each place a range of whole 1024-entry chunks (up to
+    64 blocks): order, ids, inverse, rows and segment starts against a stable
+    argsort, with out-of-range ids (bucket E) spread over several blocks."""
     ids = torch.randint(0, E, (T, k), generator=_gen(T + k), device=DEV, dtype=torch.int32)
+    if bad:
+        flat_ids = ids.view(-1)
+        at = torch.randperm(flat_ids.numel(), generator=_gen(bad), device=DEV)[:bad]
+        flat_ids[at[::2]] = -1
+        flat_ids[at[1::2]] = E
     sorted_ids, order, inverse, rows, offs = moe.expert_sort(ids, E, with_offsets=True)
     flat = ids.reshape(-1).long()
-    ref_order = torch.argsort(flat, stable=True)
+    # out-of-range ids all sort last, in entry order, kept as they are
+    key = torch.where((flat >= 0) & (flat < E), flat, torch.full_like(flat, E))
+    ref_order = torch.argsort(key, stable=True)
     assert torch.equal(order.long(), ref_order)
     assert torch.equal(sorted_ids.long(), flat[ref_order])
     assert torch.equal(inverse.long(), torch.argsort(ref_order, stable=True))
     assert torch.equal(rows.long(), ref_order // k)
-    # segment starts: expert e's run begins after every smaller id
-    ref_offs = torch.searchsorted(flat[ref_order], torch.arange(E + 1, device=DEV))
+    # segment starts: expert e's run begins after every smaller valid id
+    ref_offs = torch.searchsorted(key[ref_order], torch.arange(E + 1, device=DEV))
     assert torch.equal(offs.long(), ref_offs)
 
 
