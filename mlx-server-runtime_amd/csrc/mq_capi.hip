@@ -120,6 +120,13 @@ Dense dense_path(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
   if (M <= 256 && !dense_gemv(M, N, K, bits, group_size) && mq::qmms_fits(M, N, K, bits))
     return Dense::kSkinny;
   if (mq::qmm4_fits(M, N, K, bits, group_size)) return Dense::kQmm4;
+  // Taller shapes with too few 256 x 256 tiles for the large-M GEMM: the
+  // skinny GEMM's 64- or 128-row tiles and K splits fill the GPU where the
+  // 128 x 128 tiles of the plain GEMM do not (M x N x K = 4096 x 128 x 2048,
+  // a MoE router at prefill: 35.1 -> 14.8 us a call; 2048 x 256 x 2048 35.1
+  // -> 14.5; 1024 x 1024 x 1024 20.1 -> 15.7).  Its partial sums take at
+  // most 256 tiles of 128 x 128 floats (16 MiB).
+  if (mq::qmms_fits(M, N, K, bits)) return Dense::kSkinny;
   return K % 64 ? Dense::kNone : Dense::kQmm;
 }
 
