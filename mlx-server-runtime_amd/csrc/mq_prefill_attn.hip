@@ -213,12 +213,14 @@ __global__ __launch_bounds__(kThreads, QW == 1 ? 3 : 2) void prefill_attn_kernel
     }
     // keys past query c's position masked (none where the whole block lies
     // at or before the wave's first query); key_of(t, 4g + r) is 8g plus a
-    // constant of (t, r).  The running max m is raised only when some query
-    // of the wave sees a score above m + kLazy (log2 units): P = exp2(x - m)
-    // then stays below 2^kLazy, and most blocks skip the output rescale.
+    // constant of (t, r).  A tile's running max m is raised only when one of
+    // its 16 queries sees a score above m + kLazy (log2 units): P = exp2(x -
+    // m) then stays below 2^kLazy, and most blocks skip the output rescale.
+    // The decision is per 16-query tile, so each query's arithmetic is the
+    // same for either QW.
     const bool full = key0 + kKB - 1 <= wmin;  // uniform
     float y[QW][4][4], mxs[QW];
-    bool grow = false;
+    bool rescale[QW];
 #pragma unroll
     for (int u = 0; u < QW; ++u) {
       float mx = -INFINITY;
@@ -243,14 +245,13 @@ __global__ __launch_bounds__(kThreads, QW == 1 ? 3 : 2) void prefill_attn_kernel
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       mxs[u] = mx * scale_log2;  // the scale is positive: the max of the scaled scores
-      grow = grow || mxs[u] > m[u] + kLazy;
+      rescale[u] = __ballot(mxs[u] > m[u] + kLazy) != 0ull;  // uniform
     }
-    const bool rescale = __ballot(grow) != 0ull;  // uniform
     float p[QW][4][4], f[QW];
 #pragma unroll
     for (int u = 0; u < QW; ++u) {
       f[u] = 1.f;
-      if (rescale) {
+      if (rescale[u]) {
         const float mn = fmaxf(m[u], mxs[u]);
         f[u] = __builtin_amdgcn_exp2f(m[u] - mn);  // argument <= 0
         m[u] = mn;
@@ -267,19 +268,15 @@ __global__ __launch_bounds__(kThreads, QW == 1 ? 3 : 2) void prefill_attn_kernel
       ps += __shfl_xor(ps, 32, 64);
       lsum[u] = fmaf(lsum[u], f[u], ps);
     }
-    if (rescale) {
+#pragma unroll
+    for (int u = 0; u < QW; ++u) {
+      if (!rescale[u]) continue;
       // the output rows are queries 4g + r: their factors through LDS
-      if (g == 0) {
-#pragma unroll
-        for (int u = 0; u < QW; ++u) sh.xch[wave][u][c] = f[u];
-      }
+      if (g == 0) sh.xch[wave][u][c] = f[u];
       __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const f32x4_t fr = *reinterpret_cast<const f32x4_t*>(&sh.xch[wave][u][4 * g]);
 #pragma unroll
-      for (int u = 0; u < QW; ++u) {
-        const f32x4_t fr = *reinterpret_cast<const f32x4_t*>(&sh.xch[wave][u][4 * g]);
-#pragma unroll
-        for (int t = 0; t < kD / 16; ++t) o[u][t] *= fr;
-      }
+      for (int t = 0; t < kD / 16; ++t) o[u][t] *= fr;
       __asm__ volatile("" ::: "memory");  // the exchange's read stays ahead of its next write
     }
     // P.V: two 32-key steps; A = P of tiles 2s, 2s + 1 (keys 32s + 8g .. +7)

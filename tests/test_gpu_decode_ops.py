@@ -387,12 +387,17 @@ def _prefill_ref(q, cache, layer, starts, lens, scale):
     (2, 70, 28, 4, 13, [0, 33], [70, 71 - 33], 8),           # page size 8, 104 positions: the
                                                              # last key block runs past the table
     (1, 130, 28, 4, 3, [61], [130], 64),                     # page size 64, a chunk over 3 pages
+    # 512+ blocks of 128 queries: two query tiles a wave (a row alone: one)
+    (8, 256, 32, 4, 30, [0, 100, 7, 200, 0, 33, 64, 150],
+     [256, 256, 200, 56, 1, 256, 129, 17], 16),
+    (4, 640, 28, 4, 60, [0, 300, 0, 17], [640, 600, 333, 640], 16),
 ])
 def test_paged_prefill_attention(ops, B, T, nh, nkv, per, starts, lens, ps):
     """Prefill-chunk attention over shuffled pages against the float32
     restatement (the probabilities are bfloat16 in the kernel's P.V, as in
     the decode kernel: within 2^-7 of the largest output); each row alone
-    gives the same bits as in the batch."""
+    gives the same bits as in the batch -- also where the batch runs two
+    query tiles a wave and the row alone one."""
     d = 128
     cache = _shuffled_cache(ops, 1, B, per, ps, nkv, d, seed=per + B + T)
     g = _gen(31 + B + T + nh)
