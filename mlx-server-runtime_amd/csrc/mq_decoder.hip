@@ -122,6 +122,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(
 // weight and rounded to bfloat16, as nn.RMSNorm stores it.
 constexpr int kRopeHeadsPerBlock = kThreads / 64;
 
+// The rotated pair (x1 c - x2 s, x2 c + x1 s), each with one product rounded
+// and the other fused, spelled out so that every kernel rounds it alike.
+__device__ __forceinline__ float rope_lo(float x1, float x2, float c, float s) {
+  return fmaf(x1, c, -(x2 * s));
+}
+__device__ __forceinline__ float rope_hi(float x1, float x2, float c, float s) {
+  return fmaf(x2, c, x1 * s);
+}
+
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(
     const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
     const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
@@ -162,10 +171,102 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(
     }
     if (i < half) {
       const float c = cos_t[p * half + i], sn = sin_t[p * half + i];
-      dst[i] = (uint16_t)f32_to_bf16_bits(x1 * c - x2 * sn);
-      dst[i + half] = (uint16_t)f32_to_bf16_bits(x2 * c + x1 * sn);
+      dst[i] = (uint16_t)f32_to_bf16_bits(rope_lo(x1, x2, c, sn));
+      dst[i + half] = (uint16_t)f32_to_bf16_bits(rope_hi(x1, x2, c, sn));
     }
   }
+}
+
+// The same for many rows at once (a prefill chunk's tokens), head_dim 32, 64
+// or 128 and 16-byte aligned operands: every (row, q/k head) pair is taken by
+// H = d / 16 adjacent lanes, lane j holding the rotated pairs 8j .. 8j + 7
+// (16-byte loads and stores of both halves; cos/sin 32 bytes each).  The
+// blocks after the pairs' copy the v heads, 16 bytes a lane.  The norm's sum
+// of squares is wave_sum's: its xor butterfly over lanes 0 .. d/2 - 1 (the
+// lanes past d/2 add exact zeros) is a balanced tree in lane order, which the
+// lane's own 8 pairs (three levels) and shuffles across the H lanes (xor 1, 2,
+// 4) reproduce -- so each (row, head) gets rope_append_kernel's bits.
+constexpr int64_t kRopeRowsMin = 1024;  // rows from which this grid is used
+
+__global__ __launch_bounds__(kThreads) void rope_append_rows_kernel(
+    const uint16_t* __restrict__ qkv, const int64_t* __restrict__ pos,
+    const int32_t* __restrict__ page_table, int pages_per_seq, int page_size, int num_pages,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, float eps,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages,
+    int64_t B, int nh, int nkv, int d, int64_t pair_blocks) {
+  const int H = d / 16, half = d / 2;
+  const int64_t row_elems = (int64_t)(nh + 2 * nkv) * d;
+  auto slot_of = [&](int64_t b, int64_t p) {
+    const int64_t page = clamp_index(page_table[b * pages_per_seq + p / page_size], num_pages);
+    return page * page_size + p % page_size;
+  };
+  if ((int64_t)blockIdx.x >= pair_blocks) {  // v rows: nkv * d / 8 lanes a row
+    const int per_row = nkv * d / 8;
+    const int64_t u = ((int64_t)blockIdx.x - pair_blocks) * kThreads + threadIdx.x;
+    const int64_t b = u / per_row;
+    if (b >= B) return;
+    const int e = (int)(u % per_row) * 8;
+    const int64_t p = clamp_index(pos[b], (int64_t)pages_per_seq * page_size);
+    *reinterpret_cast<u32x4_t*>(v_pages + slot_of(b, p) * nkv * (int64_t)d + e) =
+        *reinterpret_cast<const u32x4_t*>(qkv + b * row_elems + (int64_t)(nh + nkv) * d + e);
+    return;
+  }
+  const int64_t pair = (int64_t)blockIdx.x * (kThreads / H) + threadIdx.x / H;
+  const int j = threadIdx.x % H;
+  const int64_t npairs = B * (nh + nkv);
+  const bool live = pair < npairs;
+  const int64_t pr = live ? pair : npairs - 1;  // past the end: repeat the last (not stored)
+  const int64_t b = pr / (nh + nkv);
+  const int hh = (int)(pr % (nh + nkv));
+  const int64_t p = clamp_index(pos[b], (int64_t)pages_per_seq * page_size);
+  const uint16_t* src = qkv + b * row_elems + (int64_t)hh * d + 8 * j;
+  const u32x4_t v1 = *reinterpret_cast<const u32x4_t*>(src);
+  const u32x4_t v2 = *reinterpret_cast<const u32x4_t*>(src + half);
+  const float* cp = cos_t + p * half + 8 * j;
+  const float* sp = sin_t + p * half + 8 * j;
+  const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(cp), c1 = *reinterpret_cast<const f32x4_t*>(cp + 4);
+  const f32x4_t s0 = *reinterpret_cast<const f32x4_t*>(sp), s1 = *reinterpret_cast<const f32x4_t*>(sp + 4);
+  const uint16_t* norm = hh < nh ? q_norm : k_norm;
+  float x1[8], x2[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    x1[2 * q] = lo_bf16(v1[q]), x1[2 * q + 1] = hi_bf16(v1[q]);
+    x2[2 * q] = lo_bf16(v2[q]), x2[2 * q + 1] = hi_bf16(v2[q]);
+  }
+  if (norm) {  // uniform per pair (a pair's lanes are adjacent; the shuffles stay inside it)
+    const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(norm + 8 * j);
+    const u32x4_t w2 = *reinterpret_cast<const u32x4_t*>(norm + half + 8 * j);
+    float e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = fmaf(x1[i], x1[i], x2[i] * x2[i]);
+    float ss = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    for (int off = 1; off < H; off <<= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = rsqrtf(ss / (float)d + eps);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x1[2 * q] = bf16r(x1[2 * q] * inv * lo_bf16(w1[q]));
+      x1[2 * q + 1] = bf16r(x1[2 * q + 1] * inv * hi_bf16(w1[q]));
+      x2[2 * q] = bf16r(x2[2 * q] * inv * lo_bf16(w2[q]));
+      x2[2 * q + 1] = bf16r(x2[2 * q + 1] * inv * hi_bf16(w2[q]));
+    }
+  }
+  if (!live) return;
+  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float sn[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  u32x4_t o1, o2;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = 2 * q;
+    o1[q] = pack_bf16x2(rope_lo(x1[i], x2[i], c[i], sn[i]),
+                        rope_lo(x1[i + 1], x2[i + 1], c[i + 1], sn[i + 1]));
+    o2[q] = pack_bf16x2(rope_hi(x1[i], x2[i], c[i], sn[i]),
+                        rope_hi(x1[i + 1], x2[i + 1], c[i + 1], sn[i + 1]));
+  }
+  uint16_t* dst = hh < nh ? q_out + (b * nh + hh) * (int64_t)d
+                          : k_pages + (slot_of(b, p) * nkv + (hh - nh)) * (int64_t)d;
+  *reinterpret_cast<u32x4_t*>(dst + 8 * j) = o1;
+  *reinterpret_cast<u32x4_t*>(dst + half + 8 * j) = o2;
 }
 
 // ---------------------------------------------------------------- attention
@@ -517,8 +618,8 @@ __global__ __launch_bounds__(kThreads, kAttnWaves[REP]) void attn_step_kernel(
     if (lane < HALF) {
       const float c = cos_t[(int64_t)p * HALF + lane], sn = sin_t[(int64_t)p * HALF + lane];
       uint16_t* dst = is_k ? sh.fresh[0] : qs[hh];
-      dst[lane] = (uint16_t)f32_to_bf16_bits(x1 * c - x2 * sn);
-      dst[lane + HALF] = (uint16_t)f32_to_bf16_bits(x2 * c + x1 * sn);
+      dst[lane] = (uint16_t)f32_to_bf16_bits(rope_lo(x1, x2, c, sn));
+      dst[lane + HALF] = (uint16_t)f32_to_bf16_bits(rope_hi(x1, x2, c, sn));
     }
   }
   if (owner && threadIdx.x < LANES)  // the new v row, as is
@@ -667,6 +768,19 @@ hipError_t launch_rope_append(const uint16_t* qkv, const int64_t* pos, const int
                               hipStream_t stream) {
   if (B == 0) return hipSuccess;
   const unsigned head_blocks = (unsigned)((nh + nkv + kRopeHeadsPerBlock - 1) / kRopeHeadsPerBlock);
+  auto a16 = [](const void* ptr) { return ((uintptr_t)ptr & 15) == 0; };
+  if (B >= kRopeRowsMin && (d == 32 || d == 64 || d == 128) && a16(qkv) && a16(cos_t) &&
+      a16(sin_t) && a16(q_out) && a16(k_pages) && a16(v_pages) && (!q_norm || a16(q_norm)) &&
+      (!k_norm || a16(k_norm))) {
+    const int64_t pairs_per_block = kThreads / (d / 16);
+    const int64_t pair_blocks = (B * (nh + nkv) + pairs_per_block - 1) / pairs_per_block;
+    const int64_t v_blocks = (B * (nkv * d / 8) + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(rope_append_rows_kernel, dim3((unsigned)(pair_blocks + v_blocks)),
+                       dim3(kThreads), 0, stream, qkv, pos, page_table, (int)pages_per_seq,
+                       (int)page_size, (int)num_pages, cos_t, sin_t, q_norm, k_norm, eps, q_out,
+                       k_pages, v_pages, B, nh, nkv, d, pair_blocks);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)B, head_blocks + 1), dim3(kThreads), 0,
                      stream, qkv, pos,
                      page_table, (int)pages_per_seq, (int)page_size, (int)num_pages, cos_t, sin_t,

@@ -311,6 +311,41 @@ def test_rope_kv_append_prefill_tokens(ops):
     assert int((flat_v.abs().sum((1, 2)) > 0).sum()) == B * T
 
 
+@pytest.mark.parametrize("d,norms", [(128, False), (128, True), (64, True)])
+def test_rope_kv_append_many_rows_equal_row_chunks(ops, d, norms):
+    """1027 rows in one call take the row-batched grid (4 rows a block, the
+    last block partial); the same rows appended in chunks of under 1024 take
+    one row a block.  q, the k pages and the v pages agree bit for bit, with
+    and without the q/k norms."""
+    nh, nkv, ps, per = 16, 2, 16, 25
+    lens = [300, 300, 300, 127]
+    starts = [0, 50, 99, 200]
+    R = len(lens)
+    g = _gen(901 + d + norms)
+    qkv = torch.randn(sum(lens), (nh + 2 * nkv) * d, generator=g, device=DEV).to(torch.bfloat16)
+    pos = torch.cat([torch.arange(s0, s0 + n, device=DEV) for s0, n in zip(starts, lens)])
+    rows = torch.cat([torch.full((n,), r, device=DEV) for r, n in enumerate(lens)])
+    qn = kn = None
+    if norms:
+        qn = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(torch.bfloat16)
+        kn = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).to(torch.bfloat16)
+    caches = [_shuffled_cache(ops, 1, R, per, ps, nkv, d, seed=5) for _ in range(2)]
+    cos, sin = _tables(d, caches[0].capacity)
+    table = caches[0].page_table[rows].contiguous()
+    q_all = ops.rope_kv_append(qkv, pos, caches[0], 0, cos, sin, nh, q_norm=qn, k_norm=kn,
+                               table=table)
+    parts = []
+    for a in range(0, qkv.shape[0], 500):
+        b = min(a + 500, qkv.shape[0])
+        parts.append(ops.rope_kv_append(qkv[a:b].contiguous(), pos[a:b].contiguous(), caches[1],
+                                        0, cos, sin, nh, q_norm=qn, k_norm=kn,
+                                        table=table[a:b].contiguous()))
+    assert torch.equal(q_all, torch.cat(parts))
+    assert torch.equal(caches[0].k[0], caches[1].k[0])
+    assert torch.equal(caches[0].v[0], caches[1].v[0])
+    assert int((caches[0].v[0].abs().sum((2, 3)) > 0).sum()) == sum(lens)
+
+
 def _attention_ref(q, cache, layer, pos, scale):
     """float32 softmax(q k^T scale) v per row over its positions 0..pos."""
     B, nh, d = q.shape
