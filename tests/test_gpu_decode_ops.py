@@ -311,13 +311,15 @@ def test_rope_kv_append_prefill_tokens(ops):
     assert int((flat_v.abs().sum((1, 2)) > 0).sum()) == B * T
 
 
-@pytest.mark.parametrize("d,norms", [(128, False), (128, True), (64, True)])
-def test_rope_kv_append_many_rows_equal_row_chunks(ops, d, norms):
+@pytest.mark.parametrize("d,norms,ps", [(128, False, 16), (128, True, 16), (64, True, 16),
+                                        (128, True, 24)])
+def test_rope_kv_append_many_rows_equal_row_chunks(ops, d, norms, ps):
     """1027 rows in one call take the row-batched grid (4 rows a block, the
     last block partial); the same rows appended in chunks of under 1024 take
     one row a block.  q, the k pages and the v pages agree bit for bit, with
     and without the q/k norms."""
-    nh, nkv, ps, per = 16, 2, 16, 25
+    nh, nkv = 16, 2
+    per = -(-400 // ps)  # at least 400 positions a row
     lens = [300, 300, 300, 127]
     starts = [0, 50, 99, 200]
     R = len(lens)
@@ -422,6 +424,7 @@ def _prefill_ref(q, cache, layer, starts, lens, scale):
     (2, 70, 28, 4, 13, [0, 33], [70, 71 - 33], 8),           # page size 8, 104 positions: the
                                                              # last key block runs past the table
     (1, 130, 28, 4, 3, [61], [130], 64),                     # page size 64, a chunk over 3 pages
+    (2, 90, 28, 4, 8, [0, 50], [90, 77], 24),                # page size 24 (not a power of two)
     # 512+ blocks of 128 queries: two query tiles a wave (a row alone: one)
     (8, 256, 32, 4, 30, [0, 100, 7, 200, 0, 33, 64, 150],
      [256, 256, 200, 56, 1, 256, 129, 17], 16),
