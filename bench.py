@@ -336,14 +336,14 @@ def decode_bench(torch, batch: int, prompt_len: int, n_new: int, prefix_len: int
     torch.cuda.synchronize()
     t_prefill = time.perf_counter() - t0
     cos, sin = q2.rope_tables(cfg, cache.capacity, "cuda:0")
-    tok = logits.float().argmax(-1)
+    tok = q2.greedy_tokens(logits)
     pos = torch.full((batch,), prompt_len, dtype=torch.int64, device="cuda:0")
     g, static_logits = model._capture(lambda: model.decode_step(tok, pos, cache, cos, sin))
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(n_new):
         g.replay()
-        tok.copy_(static_logits.float().argmax(-1))
+        tok.copy_(q2.greedy_tokens(static_logits))
         pos.add_(1)
     end.record()
     torch.cuda.synchronize()

@@ -63,7 +63,7 @@ typedef uint16_t mq_bf16; /* raw bfloat16 bits */
 
 /* (major << 16) | minor.  2.0: mq_moe_sort and mq_moe_route_sort take an
  * expert_offsets output before the stream argument (1.0 had none).  2.1 adds
- * mq_paged_prefill_attention and its _supported query. */
+ * mq_paged_prefill_attention and its _supported query, 2.2 mq_argmax_rows. */
 int mq_version(void);
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -507,6 +507,16 @@ int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t t
                       int num_experts, int top_k, int norm_topk_prob, int32_t* indices,
                       mq_bf16* scores, int32_t* sorted_ids, int32_t* order, int32_t* inverse,
                       int32_t* rows, int32_t* expert_offsets, hipStream_t stream);
+
+/*
+ * Greedy decoding's next token: out int64 [rows] = the first index of each
+ * row's largest value, x bfloat16 [rows, cols] (cols % 8 == 0, x 16-byte
+ * aligned; -0 equals +0, NaN counts as the largest, as torch.argmax returns
+ * the first NaN).  Replaces mx.argmax over the last logits of each row, as
+ * the reference's executor takes the next tokens (executor.py:406-414).
+ */
+int mq_argmax_rows(const mq_bf16* x, int64_t rows, int64_t cols, int64_t* out,
+                   hipStream_t stream);
 
 /*
  * mq_moe_combine, then the residual add and the RMSNorm that follow the MoE

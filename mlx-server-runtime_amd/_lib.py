@@ -44,6 +44,7 @@ EXPORTS = (
     "mq_moe_sort",
     "mq_moe_combine",
     "mq_moe_route_sort",
+    "mq_argmax_rows",
     "mq_moe_combine_rms_norm",
     "mq_quantized_matmul_swiglu_supported",
     "mq_quantized_matmul_swiglu",
@@ -108,6 +109,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.mq_moe_combine.argtypes = [_p, _p, _p, _p, _i64, _int, _i64, _p]
     L.mq_moe_route_sort.argtypes = [_p, _p, _i64, _int, _int, _int, _p, _p, _p, _p, _p, _p, _p,
                                     _p]
+    L.mq_argmax_rows.argtypes = [_p, _i64, _i64, _p, _p]
     L.mq_quantized_matmul_swiglu_supported.argtypes = [_i64, _i64, _i64, _int, _int]
     L.mq_quantized_matmul_swiglu.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _p]
     L.mq_rms_norm_quantized_matmul_supported.argtypes = [_i64, _i64, _i64, _int, _int, _int]

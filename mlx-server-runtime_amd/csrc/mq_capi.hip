@@ -140,7 +140,7 @@ bool word_shape(int64_t K, int group_size, int bits) {
 
 extern "C" {
 
-int mq_version(void) { return (2 << 16) | 1; }
+int mq_version(void) { return (2 << 16) | 2; }
 
 const char* mq_last_error(void) { return g_err; }
 
@@ -955,6 +955,21 @@ int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t t
                                               norm_topk_prob != 0, indices, scores, sorted_ids,
                                               order, inverse, rows, expert_offsets, stream),
                     op);
+}
+
+int mq_argmax_rows(const mq_bf16* x, int64_t rows, int64_t cols, int64_t* out,
+                   hipStream_t stream) {
+  const char* op = "argmax_rows";
+  if (int rc = check_dim(op, "rows", rows)) return rc;
+  if (cols < 1 || cols >= kMaxDim)
+    return fail(MQ_ERR_INVALID, "[%s] cols=%lld is out of range.", op, (long long)cols);
+  if (cols % 8)
+    return fail(MQ_ERR_UNSUPPORTED, "[%s] cols=%lld: rows of whole 8-element units only.", op,
+                (long long)cols);
+  if (rows == 0) return ok();
+  if (!x || !out) return fail(MQ_ERR_INVALID, "[%s] null pointer.", op);
+  if (!aligned16(x)) return fail(MQ_ERR_INVALID, "[%s] x must be 16-byte aligned.", op);
+  return hip_status(mq::launch_argmax_rows(x, rows, cols, out, stream), op);
 }
 
 int mq_moe_combine_rms_norm(const mq_bf16* y, const int32_t* inverse, const mq_bf16* scores,

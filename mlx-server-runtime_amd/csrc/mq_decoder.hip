@@ -695,6 +695,60 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(const float* part, cons
   out[(b * nkv * REP + hh) * (int64_t)D + threadIdx.x] = (uint16_t)f32_to_bf16_bits(num / den);
 }
 
+// ---------------------------------------------------------------- argmax
+// Greedy decoding's argmax over each bfloat16 row (the next token, as the
+// reference takes mx.argmax of each row's last logits, executor.py:406-414):
+// one block per row, 16-byte loads, every element's (value, index) packed
+// into a 64-bit key whose maximum is the first index of the largest value --
+// the value as an order-preserving 16-bit key (-0 as +0, NaN above every
+// number, as torch.argmax returns the first NaN) over the complemented index.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ uint64_t argmax_key(uint32_t u, uint32_t idx) {
+  u &= 0xffffu;
+  const uint32_t mag = u & 0x7fffu;
+  const uint32_t key = mag > 0x7f80u ? 0xffffu          // NaN
+                       : mag == 0     ? 0x8000u         // -0 and +0
+                       : (u & 0x8000u) ? (~u & 0xffffu) // negative: larger magnitude lower
+                                       : (u | 0x8000u);
+  return ((uint64_t)key << 32) | (0xffffffffu - idx);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const uint16_t* __restrict__ x,
+                                                                     int64_t cols,
+                                                                     int64_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const rsrc_t rs = make_rsrc(x + r * cols, (uint64_t)cols * 2);
+  const uint32_t units = (uint32_t)(cols / 8);  // 16-byte units (cols % 8 == 0)
+  uint64_t best = 0;                             // below every element's key
+#pragma unroll 4
+  for (uint32_t u = threadIdx.x; u < units; u += kArgmaxThreads) {
+    const u32x4_t v = buf_load16(rs, u * 16u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint64_t a = argmax_key(v[q], 8u * u + 2u * q);
+      const uint64_t b = argmax_key(v[q] >> 16, 8u * u + 2u * q + 1u);
+      best = a > best ? a : best;
+      best = b > best ? b : best;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, off, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), off, 64);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    best = o > best ? o : best;
+  }
+  __shared__ uint64_t wave_best[kArgmaxThreads / 64];
+  if ((threadIdx.x & 63) == 0) wave_best[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < kArgmaxThreads / 64; ++w) best = wave_best[w] > best ? wave_best[w] : best;
+    out[r] = (int64_t)(0xffffffffu - (uint32_t)best);
+  }
+}
+
 // ---------------------------------------------------------------- SiLU * up
 // gu bf16 [rows, 2 * inter] = (gate | up) -> out bf16 [rows, inter]
 //   = bf16(bf16(silu(gate)) * up)
@@ -903,6 +957,14 @@ hipError_t launch_attention_step(const uint16_t* qkv, const int64_t* pos,
                               (int)num_pages, cos_t, sin_t, q_norm, k_norm, eps, k_pages,
                               v_pages, B, nh, nkv, scale, workspace, out, chunk, splits, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_argmax_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t* out,
+                              hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(kArgmaxThreads), 0, stream, x,
+                     cols, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter,

@@ -200,6 +200,10 @@ hipError_t launch_decode_attention(const uint16_t* q, const uint16_t* k_pages,
                                    const int64_t* pos, int64_t B, int nh, int nkv, int d,
                                    float scale, float* workspace, uint16_t* out,
                                    hipStream_t stream);
+// out int64 [rows] = the first index of each bfloat16 row's largest value
+// (cols % 8 == 0, x 16-byte aligned; NaN counts as the largest).
+hipError_t launch_argmax_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t* out,
+                              hipStream_t stream);
 hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter,
                            hipStream_t stream);
 // RoPE + append fused into the split attention kernel, then the combine.

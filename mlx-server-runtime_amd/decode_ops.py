@@ -197,6 +197,20 @@ def prefill_attention_supported(n_heads: int, cache: PagedKV) -> bool:
         n_heads, cache.kv_heads, cache.head_dim, cache.num_pages, cache.page_size))
 
 
+def argmax_rows(x: torch.Tensor) -> torch.Tensor:
+    """Greedy next tokens: x bf16 [..., C] (C % 8 == 0) -> int64 [...], the first
+    index of each row's largest value (NaN as the largest), as torch.argmax(-1)
+    of the same values."""
+    op = "argmax_rows"
+    _require_gpu(op, x=x)
+    _check_bf16(op, "x", x)
+    C = x.shape[-1]
+    x2 = x.contiguous().reshape(-1, C)
+    out = torch.empty(x2.shape[0], dtype=torch.int64, device=x.device)
+    _lib.check(_lib.lib().mq_argmax_rows(_ptr(x2), x2.shape[0], C, _ptr(out), _stream(x)), op)
+    return out.reshape(x.shape[:-1])
+
+
 def paged_prefill_attention(q: torch.Tensor, cache: PagedKV, layer: int, table: torch.Tensor,
                             starts: torch.Tensor, lens: torch.Tensor, scale: float) -> torch.Tensor:
     """Causal attention of a prefill chunk whose k and v are already in the pages
@@ -278,4 +292,4 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
 
 
 __all__ = ["PagedKV", "rms_norm", "rope_kv_append", "paged_decode_attention", "attention_step",
-           "silu_mul"]
+           "silu_mul", "argmax_rows"]

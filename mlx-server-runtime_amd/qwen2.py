@@ -47,7 +47,7 @@ import torch
 import torch.nn.functional as F
 
 from . import core
-from .decode_ops import (PagedKV, attention_step, paged_prefill_attention,
+from .decode_ops import (PagedKV, argmax_rows, attention_step, paged_prefill_attention,
                          prefill_attention_supported, rope_kv_append, silu_mul)
 from .moe import MoEBlock, QExperts
 from .decode_ops import rms_norm as fused_rms_norm
@@ -193,6 +193,16 @@ def _random_experts(gen, E, n_out, n_in, cfg, device, std=0.02) -> QExperts:
     del w
     return QExperts(wq.reshape(E, n_out, -1), s.reshape(E, n_out, -1), b.reshape(E, n_out, -1),
                     cfg.group_size, cfg.bits)
+
+
+def greedy_tokens(logits: torch.Tensor) -> torch.Tensor:
+    """The next tokens of greedy decoding (executor.py:406-414): the first index
+    of each row's largest logit, int64 [...] -- the library's row argmax over the
+    bfloat16 logits (torch.argmax's result on the same values) where the
+    vocabulary is whole 8-element units."""
+    if logits.dtype == torch.bfloat16 and logits.shape[-1] % 8 == 0:
+        return argmax_rows(logits)
+    return logits.float().argmax(-1)
 
 
 def rope_tables(cfg: Qwen2Config, max_len: int, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -588,7 +598,7 @@ class Qwen2Model:
             pos = lens.clone()
         if logits_out is not None:
             logits_out.append(logits.clone())
-        out[:, 0] = logits.float().argmax(-1)
+        out[:, 0] = greedy_tokens(logits)
         tok = out[:, 0].clone()
         step = lambda: self.decode_step(tok, pos, cache, cos, sin)  # noqa: E731
         if use_graph and n_new > 1:
@@ -601,7 +611,7 @@ class Qwen2Model:
                 logits = step()
             if logits_out is not None:
                 logits_out.append(logits.clone())
-            nxt = logits.float().argmax(-1)
+            nxt = greedy_tokens(logits)
             out[:, i] = nxt
             tok.copy_(nxt)
             pos.add_(1)

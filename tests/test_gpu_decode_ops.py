@@ -348,6 +348,33 @@ def test_rope_kv_append_many_rows_equal_row_chunks(ops, d, norms, ps):
     assert int((caches[0].v[0].abs().sum((2, 3)) > 0).sum()) == sum(lens)
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 152064), (32, 152064), (5, 8), (6, 1000)])
+def test_argmax_rows_equals_torch_argmax(ops, rows, cols):
+    """The greedy next token: the first index of each row's largest bfloat16
+    value, as torch.argmax over the same values -- random rows, a row of ties
+    (the first of two maxima), -0 before +0 among -inf, a NaN (the largest)."""
+    g = _gen(rows * 7 + cols)
+    x = torch.randn(rows, cols, generator=g, device=DEV).to(torch.bfloat16)
+    if rows >= 2:
+        x[1] = 0.5
+        x[1, cols // 3] = 2.0
+        x[1, cols - 1] = 2.0
+    if rows >= 3:
+        x[2] = -float("inf")
+        x[2, cols // 2] = -0.0
+        x[2, cols // 2 + 1] = 0.0
+    if rows >= 4:
+        x[3, cols // 2 - 1] = float("nan")
+    got = ops.argmax_rows(x)
+    ref = x.float().argmax(-1)
+    assert got.dtype == torch.int64 and got.shape == (rows,)
+    assert torch.equal(got, ref), (got, ref)
+    if rows >= 3:
+        assert int(got[1]) == cols // 3 and int(got[2]) == cols // 2
+    if rows >= 4:
+        assert int(got[3]) == cols // 2 - 1
+
+
 def _attention_ref(q, cache, layer, pos, scale):
     """float32 softmax(q k^T scale) v per row over its positions 0..pos."""
     B, nh, d = q.shape

@@ -47,7 +47,7 @@ def test_header_declares_the_abi():
         "mq_gather_qmm_swiglu_supported", "mq_gather_qmm_swiglu", "mq_hbm_read", "mq_qmv_trace",
         "mq_quantized_matmul_noalloc", "mq_gather_qmm_segments",
         "mq_gather_qmm_segments_supported", "mq_paged_prefill_attention_supported",
-        "mq_paged_prefill_attention"])
+        "mq_paged_prefill_attention", "mq_argmax_rows"])
 
 
 def test_library_exports_every_declared_symbol(mq):
@@ -55,7 +55,7 @@ def test_library_exports_every_declared_symbol(mq):
     for name in declared_functions():
         assert hasattr(L, name), name
     assert set(mq._lib.EXPORTS) == set(declared_functions())
-    assert mq.version() == (2, 1)
+    assert mq.version() == (2, 2)
 
 
 def _L(mq):
@@ -203,6 +203,18 @@ def test_decoder_entry_validation(mq):
     assert cn(null, null, null, null, null, null, null, 4, 8, 8200, 1e-6, null) == -2  # > 8192
     assert cn(null, null, null, null, null, null, null, 4, 0, 2048, 1e-6, null) == -1  # top_k
     assert cn(null, null, null, null, null, null, null, 0, 8, 2048, 1e-6, null) == 0
+
+
+def test_argmax_rows_entry_validation(mq):
+    """Rows of whole 8-element units only; null pointers and a misaligned x
+    refused; no rows a no-op."""
+    L = _L(mq)
+    f = L.mq_argmax_rows
+    assert f(None, 2, 12, None, None) == -2      # cols % 8
+    assert f(None, 2, 0, None, None) == -1       # no columns
+    assert f(None, 0, 16, None, None) == 0
+    assert f(None, 2, 16, None, None) == -1      # null
+    assert f(8, 2, 16, 64, None) == -1           # x not 16-byte aligned
 
 
 def test_prefill_attention_entry_validation(mq):
