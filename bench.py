@@ -65,6 +65,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", action="store_true",
                     help="eager launches of the headline kernel + a 128 MiB copy (rocprofv3 runs)")
+    ap.add_argument("--profile-prefill-attention", default=None, metavar="B,T,START,HEADS,KV",
+                    help="only launch the paged prefill attention (B rows of T new tokens over "
+                         "START cached positions, page size 16) warmup + steps times, for "
+                         "rocprofv3")
     ap.add_argument("--profile-shape", default=None, metavar="M,K,N,BITS",
                     help="eager launches of quantized_matmul at one shape (rocprofv3 runs)")
     ap.add_argument("--profile-gather", action="store_true",
@@ -557,6 +561,23 @@ def main():
             mq.quantized_matmul(px, wq, s, b, transpose=True, group_size=64, bits=pbits)
         torch.cuda.synchronize()
         print(json.dumps({"profile_shape": [pM, pK, pN, pbits], "launches": args.warmup + args.steps}))
+        return
+
+    if args.profile_prefill_attention:
+        pB, pT, pS, pH, pKV = (int(v) for v in args.profile_prefill_attention.split(","))
+        ops = importlib.import_module("mlx-server-runtime_amd.decode_ops")
+        gen = torch.Generator(device="cuda:0").manual_seed(pB * pT)
+        cache = ops.PagedKV.contiguous(1, pB, pS + pT, pKV, 128, "cuda:0")
+        cache.k[0].normal_(generator=gen)
+        cache.v[0].normal_(generator=gen)
+        q = torch.randn(pB, pT, pH, 128, generator=gen, device="cuda:0").to(torch.bfloat16)
+        starts = torch.full((pB,), pS, dtype=torch.int64, device="cuda:0")
+        lens = torch.full((pB,), pT, dtype=torch.int64, device="cuda:0")
+        for _ in range(args.warmup + args.steps):
+            ops.paged_prefill_attention(q, cache, 0, cache.page_table, starts, lens, 128 ** -0.5)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_prefill_attention": [pB, pT, pS, pH, pKV],
+                          "launches": args.warmup + args.steps}))
         return
 
     if args.profile_gather:
