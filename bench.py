@@ -342,13 +342,22 @@ def decode_bench(torch, batch: int, prompt_len: int, n_new: int, prefix_len: int
     cos, sin = q2.rope_tables(cfg, cache.capacity, "cuda:0")
     tok = q2.greedy_tokens(logits)
     pos = torch.full((batch,), prompt_len, dtype=torch.int64, device="cuda:0")
-    g, static_logits = model._capture(lambda: model.decode_step(tok, pos, cache, cos, sin))
+    def step():
+        # one greedy step in the graph: the logits, the next tokens fed back,
+        # the positions advanced
+        lg = model.decode_step(tok, pos, cache, cos, sin)
+        tok.copy_(q2.greedy_tokens(lg))
+        pos.add_(1)
+        return lg
+
+    tok0, pos0 = tok.clone(), pos.clone()
+    g, static_logits = model._capture(step)  # its warm-up runs one step: undo its feedback
+    tok.copy_(tok0)
+    pos.copy_(pos0)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(n_new):
         g.replay()
-        tok.copy_(q2.greedy_tokens(static_logits))
-        pos.add_(1)
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
