@@ -510,8 +510,8 @@ int mq_moe_route_sort(const mq_bf16* logits, const float* expert_bias, int64_t t
 
 /*
  * Greedy decoding's next token: out int64 [rows] = the first index of each
- * row's largest value, x bfloat16 [rows, cols] (cols % 8 == 0, x 16-byte
- * aligned; -0 equals +0, NaN counts as the largest, as torch.argmax returns
+ * row's largest value, x bfloat16 [rows, cols] (cols % 8 == 0, cols <= 2^28,
+ * x 16-byte aligned; -0 equals +0, NaN counts as the largest, as torch.argmax returns
  * the first NaN).  Replaces mx.argmax over the last logits of each row, as
  * the reference's executor takes the next tokens (executor.py:406-414).
  */

@@ -961,8 +961,10 @@ int mq_argmax_rows(const mq_bf16* x, int64_t rows, int64_t cols, int64_t* out,
                    hipStream_t stream) {
   const char* op = "argmax_rows";
   if (int rc = check_dim(op, "rows", rows)) return rc;
-  if (cols < 1 || cols >= kMaxDim)
-    return fail(MQ_ERR_INVALID, "[%s] cols=%lld is out of range.", op, (long long)cols);
+  // a row's byte offsets are 32-bit: at most 2^28 elements
+  if (cols < 1 || cols > ((int64_t)1 << 28))
+    return fail(MQ_ERR_INVALID, "[%s] cols=%lld is out of range (1..2^28).", op,
+                (long long)cols);
   if (cols % 8)
     return fail(MQ_ERR_UNSUPPORTED, "[%s] cols=%lld: rows of whole 8-element units only.", op,
                 (long long)cols);

@@ -212,6 +212,7 @@ def test_argmax_rows_entry_validation(mq):
     f = L.mq_argmax_rows
     assert f(None, 2, 12, None, None) == -2      # cols % 8
     assert f(None, 2, 0, None, None) == -1       # no columns
+    assert f(None, 2, (1 << 28) + 8, None, None) == -1   # past 32-bit row offsets
     assert f(None, 0, 16, None, None) == 0
     assert f(None, 2, 16, None, None) == -1      # null
     assert f(8, 2, 16, 64, None) == -1           # x not 16-byte aligned
